@@ -1,0 +1,412 @@
+"""Pins the CPU oracle (oracle/oracle.c) against mathematics, not against itself.
+
+The reference (hobby-rs) is Rust and cannot be built here, and it ships no golden
+vectors for this path, so every oracle function is checked against something fixed
+independently of it: exhaustive enumeration (fp16), format closed forms (Q8_0),
+invariants (requantization is the identity on GGML blocks), brute force with exact
+rational arithmetic (activation rounding, int8 dots, the FMA lane order of
+qrow_dot_avx2 and of ops::dot), textbook forms evaluated in float64 (RMSNorm,
+softmax, RoPE as a complex rotation, attention, routing by sorting) and an
+independent float64 model (tests/refmodel.py) that reads the GGUF with its own parser.
+"""
+import math
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import exactfp as X
+from hobbylm_amd import gguf_synth as gs
+
+
+# ---------------------------------------------------------------- fp16 / Q8_0
+def test_half_to_f32_exhaustive(orc):
+    h = np.arange(65536, dtype=np.uint16)
+    got = np.empty(65536, np.float32)
+    orc.lib().orc_dequant_f16(h.view(np.uint8), 65536, got)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_dequant_q8_0_closed_form(orc):
+    rng = np.random.default_rng(5)
+    nb = 4096
+    blk = np.empty(nb, gs.Q8_BLOCK)
+    blk["d"] = rng.standard_normal(nb).astype(np.float16)
+    blk["qs"] = rng.integers(-128, 128, size=(nb, 32), dtype=np.int8)
+    got = orc.dequant_q8_0(blk.view(np.uint8), nb * 32)
+    want = blk["qs"].astype(np.float32) * blk["d"].astype(np.float32)[:, None]
+    assert np.array_equal(got.view(np.uint32), want.reshape(-1).view(np.uint32))
+
+
+def test_requant_is_identity_on_ggml_blocks(orc):
+    """Q8Tensor::quantize of a dequantized GGML block returns the same q and d (max|q| = 127)."""
+    rng = np.random.default_rng(6)
+    w = (rng.standard_normal((64, 1024)) * 0.02).astype(np.float32)
+    w[3, 64:96] = 0.0  # an all-zero block
+    blk = gs.quantize_q8_0(w)
+    deq = orc.dequant_q8_0(blk.view(np.uint8), w.size).reshape(w.shape)
+    sc, qs = orc.q8_quantize(deq)
+    assert np.array_equal(qs.reshape(-1, 32), blk["qs"])
+    assert np.array_equal(sc.reshape(-1), blk["d"].astype(np.float32))
+    mx = np.abs(blk["qs"].astype(np.int32)).max(axis=1)
+    assert set(np.unique(mx)) <= {0, 127}
+
+
+def _round_away(v: np.float32) -> int:
+    f = X.F(v)
+    n = math.floor(abs(f) + X.Fraction(1, 2))
+    return int(n if f >= 0 else -n)
+
+
+def _act_quant_exact(x):
+    """quant.rs:114-122 evaluated with exact rationals and explicit binary32 rounding."""
+    q = np.empty(x.size, np.int8)
+    d = np.empty(x.size // 32, np.float32)
+    for b in range(x.size // 32):
+        blk = x[b * 32:(b + 1) * 32]
+        amax = max(abs(float(v)) for v in blk)
+        db = X.round_f32(X.Fraction(amax) / 127)
+        idv = X.round_f32(1 / X.F(db)) if db > 0 else np.float32(0.0)
+        d[b] = db
+        for j in range(32):
+            r = _round_away(X.mul(blk[j], idv))
+            q[b * 32 + j] = max(-127, min(127, r))
+    return q, d
+
+
+def test_act_quant_bruteforce(orc):
+    rng = np.random.default_rng(7)
+    x = np.concatenate([
+        (rng.standard_normal(256) * 10 ** rng.uniform(-6, 3)).astype(np.float32),
+        np.zeros(32, np.float32),                                   # d = 0 -> q = 0
+        np.array([127, 2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5] + [0.25] * 24, np.float32),  # ties
+        rng.uniform(-1e-30, 1e-30, 32).astype(np.float32),          # subnormal-ish scales
+    ])
+    qx, dx = orc.quantize_act(x)
+    q2, d2 = _act_quant_exact(x)
+    assert np.array_equal(dx.view(np.uint32), d2.view(np.uint32))
+    assert np.array_equal(qx, q2)
+    tie = qx[288:296]
+    assert list(tie) == [127, 3, -3, 1, -1, 2, -2, 127]  # half away from zero, never to even
+
+
+def test_int8_block_dot_exact(orc):
+    rng = np.random.default_rng(8)
+    for _ in range(50):
+        qw = rng.integers(-127, 128, 32, dtype=np.int8)
+        qa = rng.integers(-127, 128, 32, dtype=np.int8)
+        got = orc.qrow_dot(qw, qa, np.ones(1, np.float32), np.ones(1, np.float32))
+        assert got == float(np.dot(qw.astype(np.int64), qa.astype(np.int64)))
+    ext = np.full(32, 127, np.int8)
+    assert orc.qrow_dot(ext, -ext, np.ones(1, np.float32), np.ones(1, np.float32)) == -32 * 127 * 127
+
+
+def _qrow_dot_lanes(qw, qa, sw, dx, fused=True, lane_order=True):
+    """qrow_dot_avx2: lane j of block b is sum_{m<4} qw[32b+4j+m]*qa[32b+4j+m]; lane j
+    accumulates fma(sw[b]*dx[b], p, acc_j) over blocks; hsum ((0+4)+(2+6))+((1+5)+(3+7))."""
+    nb = len(sw)
+    acc = [np.float32(0.0)] * 8
+    seq = np.float32(0.0)
+    for b in range(nb):
+        d = X.mul(sw[b], dx[b])
+        p = [int(np.dot(qw[32 * b + 4 * j:32 * b + 4 * j + 4].astype(np.int64),
+                        qa[32 * b + 4 * j:32 * b + 4 * j + 4].astype(np.int64))) for j in range(8)]
+        for j in range(8):
+            acc[j] = X.fma(d, p[j], acc[j]) if fused else X.add(X.mul(d, p[j]), acc[j])
+        seq = X.add(seq, X.mul(d, sum(p)))
+    if not lane_order:
+        return seq
+    a = acc
+    return X.add(X.add(X.add(a[0], a[4]), X.add(a[2], a[6])), X.add(X.add(a[1], a[5]), X.add(a[3], a[7])))
+
+
+def test_qrow_dot_lane_order(orc):
+    rng = np.random.default_rng(9)
+    n_unfused_differs = n_seq_differs = 0
+    for nb in (1, 3, 8, 32):
+        for _ in range(6):
+            qw = rng.integers(-127, 128, 32 * nb, dtype=np.int8)
+            qa = rng.integers(-127, 128, 32 * nb, dtype=np.int8)
+            sw = (rng.uniform(0.5, 2.0, nb) * 1e-4).astype(np.float32)
+            dx = rng.uniform(0.001, 0.05, nb).astype(np.float32)
+            got = np.float32(orc.qrow_dot(qw, qa, sw, dx))
+            want = _qrow_dot_lanes(qw, qa, sw, dx)
+            assert got.view(np.uint32) == want.view(np.uint32), (nb, got, want)
+            n_unfused_differs += _qrow_dot_lanes(qw, qa, sw, dx, fused=False) != got
+            n_seq_differs += _qrow_dot_lanes(qw, qa, sw, dx, lane_order=False) != got
+            exact = sum(float(sw[b]) * float(dx[b]) * float(np.dot(qw[32 * b:32 * b + 32].astype(np.int64),
+                        qa[32 * b:32 * b + 32].astype(np.int64))) for b in range(nb))
+            assert abs(float(got) - exact) <= 1e-5 * (abs(exact) + 1e-12) + 1e-9
+    # the check distinguishes the specified order from the two nearest mistakes
+    assert n_unfused_differs > 0 and n_seq_differs > 0
+
+
+def _dot_wide(a, b, fused=True):
+    """ops::dot: 4 f32x8 FMA accumulators over 32-wide steps, 8-wide tail into a0,
+    reduce_add((a0+a1)+(a2+a3)) with the lo/hi, movehl, lane-1 order, scalar tail."""
+    n = a.size
+    acc = [[np.float32(0.0)] * 8 for _ in range(4)]
+    op = X.fma if fused else (lambda x, y, z: X.add(X.mul(x, y), z))
+    i, main = 0, n - n % 32
+    while i < main:
+        for r in range(4):
+            for l in range(8):
+                acc[r][l] = op(a[i + 8 * r + l], b[i + 8 * r + l], acc[r][l])
+        i += 32
+    while i + 8 <= n:
+        for l in range(8):
+            acc[0][l] = op(a[i + l], b[i + l], acc[0][l])
+        i += 8
+    v = [X.add(X.add(acc[0][l], acc[1][l]), X.add(acc[2][l], acc[3][l])) for l in range(8)]
+    s = X.add(X.add(X.add(v[0], v[4]), X.add(v[2], v[6])), X.add(X.add(v[1], v[5]), X.add(v[3], v[7])))
+    while i < n:
+        s = X.add(s, X.mul(a[i], b[i]))
+        i += 1
+    return s
+
+
+def test_dot_wide_order(orc):
+    rng = np.random.default_rng(10)
+    differs = 0
+    for n in (8, 37, 64, 100, 1024):
+        a = rng.standard_normal(n).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        got = np.float32(orc.dot(a, b))
+        assert got.view(np.uint32) == _dot_wide(a, b).view(np.uint32), n
+        differs += _dot_wide(a, b, fused=False) != got
+        assert abs(float(got) - float(np.dot(a.astype(np.float64), b.astype(np.float64)))) < 1e-5 * n ** 0.5
+    assert differs > 0
+
+
+def test_q8_matmul_scalar_order(orc):
+    """quant.rs:171-184: acc += (sw*dx)*isum, blocks in order, one accumulator."""
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((5, 96)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((3, 96)).astype(np.float32)
+    sc, qs = orc.q8_quantize(w)
+    y = orc.q8_matmul(sc, qs, x)
+    for t in range(3):
+        qx, dx = orc.quantize_act(x[t])
+        for o in range(5):
+            acc = np.float32(0.0)
+            for b in range(3):
+                isum = int(np.dot(qs[o, 32 * b:32 * b + 32].astype(np.int64), qx[32 * b:32 * b + 32].astype(np.int64)))
+                acc = X.add(acc, X.mul(X.mul(sc[o, b], dx[b]), isum))
+            assert y[t, o].view(np.uint32) == acc.view(np.uint32)
+
+
+def test_q8_matvec_rows_and_f64(orc):
+    rng = np.random.default_rng(12)
+    for (n, k) in ((1024, 1024), (70, 512), (5, 192)):
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        x = rng.standard_normal(k).astype(np.float32)
+        sc, qs = orc.q8_quantize(w)
+        y = orc.q8_matvec(sc, qs, x)
+        qx, dx = orc.quantize_act(x)
+        for o in rng.integers(0, n, 8):
+            assert y[o] == np.float32(orc.qrow_dot(qs[o], qx, sc[o], dx))
+        deq = qs.astype(np.float64) * np.repeat(sc.astype(np.float64), 32, axis=1)
+        xq = qx.astype(np.float64) * np.repeat(dx.astype(np.float64), 32)
+        np.testing.assert_allclose(y, deq @ xq, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- f32 ops
+def test_expf_sigmoid_silu(orc):
+    xs = np.concatenate([np.linspace(-103, 88, 20001), np.random.default_rng(13).standard_normal(5000)])
+    for x in xs.astype(np.float32):
+        e = np.float32(orc.lib().orc_expf(float(x)))
+        want = np.float32(math.exp(float(x)))
+        assert abs(int(e.view(np.int32)) - int(want.view(np.int32))) <= 1
+    for x in np.linspace(-30, 30, 601).astype(np.float32):
+        s = 1 / (1 + math.exp(-float(x)))
+        assert abs(orc.lib().orc_sigmoid(float(x)) - s) <= 2e-7 * s + 1e-38
+        assert abs(orc.lib().orc_silu(float(x)) - float(x) * s) <= 1e-6 * abs(float(x) * s) + 1e-30
+
+
+def test_rmsnorm_norm_head_softmax_vs_float64(orc):
+    rng = np.random.default_rng(14)
+    for n in (64, 1024):
+        x = rng.standard_normal(n).astype(np.float32) * 3
+        w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        x64 = x.astype(np.float64)
+        want = x64 / np.sqrt(np.mean(x64 ** 2) + 1e-5) * w
+        np.testing.assert_allclose(orc.rmsnorm(x, w, 1e-5), want, rtol=2e-6, atol=1e-7)
+        np.testing.assert_allclose(orc.norm_head(x, w, 1e-5), want, rtol=2e-6, atol=1e-7)
+        s = x * 4
+        p = np.exp(s.astype(np.float64) - s.max())
+        np.testing.assert_allclose(orc.softmax(s), p / p.sum(), rtol=1e-5, atol=1e-9)
+
+
+def test_rope_table_and_rotation(orc):
+    hd, P, theta = 64, 300, 10000.0
+    c, s = orc.rope_table(hd, P, theta)
+    i = np.arange(hd // 2)
+    ang = np.arange(P)[:, None] * theta ** (-(2.0 * i) / hd)[None, :]
+    np.testing.assert_array_equal(c, np.cos(ang).astype(np.float32))
+    np.testing.assert_array_equal(s, np.sin(ang).astype(np.float32))
+    v = np.random.default_rng(15).standard_normal(hd).astype(np.float32)
+    for pos in (0, 1, 17, 299):
+        r = orc.rope_apply(c, s, v, pos)
+        z = (v[:32].astype(np.float64) + 1j * v[32:]) * np.exp(1j * ang[pos])
+        np.testing.assert_allclose(r, np.concatenate([z.real, z.imag]), rtol=1e-6, atol=1e-6)
+    assert np.array_equal(orc.rope_apply(c, s, v, 0), v)
+
+
+def test_argmax_first_max_and_nan(orc):
+    assert orc.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
+    assert orc.argmax(np.array([np.nan, 1, 5, np.nan, 5], np.float32)) == 2
+    assert orc.argmax(np.full(4, -np.inf, np.float32)) == 0
+    assert orc.argmax(np.array([-np.inf, -1e30, -np.inf], np.float32)) == 1
+
+
+def test_route_bruteforce(orc):
+    rng = np.random.default_rng(16)
+    for trial in range(200):
+        ne, k = (36, 6) if trial % 2 else (8, 3)
+        lg = (rng.standard_normal(ne) * 0.1).astype(np.float32)
+        bias = (rng.standard_normal(ne) * 0.01).astype(np.float32)
+        if trial % 7 == 0:
+            bias[:] = 0
+            lg[1] = lg[4]  # an exact tie: the lower expert id ranks first
+        idx, w, gap = orc.route(lg, bias, k)
+        sc = np.array([np.float32(orc.lib().orc_sigmoid(float(v))) for v in lg], np.float32)
+        sel = sc + bias
+        want = np.argsort(-sel.astype(np.float64), kind="stable")[:k]
+        assert list(idx) == list(want)
+        assert np.array_equal(w, sc[want])
+        assert gap == np.float32(sel[want[-1]] - sel[np.argsort(-sel.astype(np.float64), kind="stable")[k]])
+        idx2, w2, _ = orc.route(lg, bias, k, weights_norm=True)
+        np.testing.assert_allclose(w2, w / (w.sum() + 1e-9), rtol=1e-6)
+
+
+def test_attention_decode_vs_float64(orc):
+    rng = np.random.default_rng(17)
+    nh, nkv, hd, pos = 16, 4, 64, 40
+    cos_t, sin_t = orc.rope_table(hd, 64, 10000.0)
+    kc = np.zeros((64, nkv * hd), np.float32)
+    vc = np.zeros((64, nkv * hd), np.float32)
+    kc[:pos] = rng.standard_normal((pos, nkv * hd))
+    vc[:pos] = rng.standard_normal((pos, nkv * hd))
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(nkv * hd).astype(np.float32)
+    v = rng.standard_normal(nkv * hd).astype(np.float32)
+    ones = np.ones(hd, np.float32)
+    out, qr, kr = orc.attention_decode(q, k, v, ones, ones, cos_t, sin_t, 1e-5, nh, nkv, hd, pos, kc, vc)
+    assert np.array_equal(kc[pos], kr) and np.array_equal(vc[pos], v)
+    K = kc[:pos + 1].reshape(pos + 1, nkv, hd).astype(np.float64)
+    V = vc[:pos + 1].reshape(pos + 1, nkv, hd).astype(np.float64)
+    for h in range(nh):
+        s = K[:, h // 4] @ qr[h * hd:(h + 1) * hd] / 8.0
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        np.testing.assert_allclose(out[h * hd:(h + 1) * hd], p @ V[:, h // 4], rtol=1e-4, atol=1e-5)
+    # the normalisation + rotation of q/k against the closed form
+    qh = q[:hd].astype(np.float64)
+    qn = qh / np.sqrt(np.mean(qh ** 2) + 1e-5)
+    ang = pos * 10000.0 ** (-(2.0 * np.arange(32)) / hd)
+    z = (qn[:32] + 1j * qn[32:]) * np.exp(1j * ang)
+    np.testing.assert_allclose(qr[:hd], np.concatenate([z.real, z.imag]), rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- model level
+@pytest.fixture(scope="module")
+def tiny_path():
+    return gs.synth_path("tiny", 3, norm_jitter=0.1)
+
+
+def test_model_vs_float64_reexpression(orc, tiny_path):
+    from refmodel import RefModel
+    m = orc.Model(tiny_path)
+    kv = m.new_cache()
+    ref = RefModel(tiny_path)
+    toks = gs.prompt_ids(4, 12, m.cfg.vocab_size)
+    for pos, t in enumerate(toks):
+        got = m.forward(int(t), pos, kv)
+        want = ref.forward(int(t), pos)
+        rng_ = want.max() - want.min()
+        assert np.max(np.abs(got - want)) <= 2e-3 * rng_, pos
+    k, v = kv.read(1)
+    np.testing.assert_allclose(k, np.stack(ref.k[1]).reshape(len(toks), -1), rtol=1e-2, atol=2e-3)
+    np.testing.assert_allclose(v, np.stack(ref.v[1]).reshape(len(toks), -1), rtol=1e-2, atol=2e-3)
+
+
+def test_prefill_matches_stepwise_forward(orc, tiny_path):
+    m = orc.Model(tiny_path)
+    toks = gs.prompt_ids(5, 10, m.cfg.vocab_size)
+    kv1, kv2 = m.new_cache(), m.new_cache()
+    emb = np.stack([m.token_embedding(int(t)) for t in toks])
+    lp = m.prefill(emb, kv1)
+    for pos, t in enumerate(toks):
+        lf = m.forward(int(t), pos, kv2)
+    assert kv1.len == kv2.len == len(toks)
+    assert np.max(np.abs(lp - lf)) <= 1e-3 * (lf.max() - lf.min())
+    for l in range(m.cfg.n_layers):
+        np.testing.assert_allclose(kv1.read(l)[0], kv2.read(l)[0], rtol=1e-3, atol=1e-3)
+
+
+def test_generate_greedy_is_argmax_chain(orc, tiny_path):
+    m = orc.Model(tiny_path)
+    toks = gs.prompt_ids(6, 8, m.cfg.vocab_size)
+    ids = m.generate_greedy(toks, 12, m.new_cache(), eos=2 ** 32 - 1)
+    kv = m.new_cache()
+    emb = np.stack([m.token_embedding(int(t)) for t in toks])
+    lg = m.prefill(emb, kv)
+    pos = len(toks)
+    for i in range(12):
+        nxt = int(np.argmax(lg))  # vocab 1000 < 50257: nothing masked
+        assert ids[i] == nxt
+        lg = m.forward(nxt, pos, kv)
+        pos += 1
+
+
+def test_weight_bytes(orc, tiny_path):
+    m = orc.Model(tiny_path)
+    c = m.cfg
+    mats = (c.vocab_size * c.d_model + c.n_layers * (
+        (c.n_heads + 2 * c.n_kv_heads) * c.head_dim * c.d_model + c.d_model * c.n_heads * c.head_dim))
+    mats += c.n_dense * 3 * c.dense_ffn * c.d_model
+    mats += (c.n_layers - c.n_dense) * (c.n_experts + 1) * 3 * c.expert_ffn * c.d_model
+    assert m.weight_bytes() == mats + mats // 32 * 4  # 1 B per weight + one f32 scale per 32
+
+
+# ---------------------------------------------------------------- load errors (gguf.rs / config.rs)
+def _write(tmp_path, name, data):
+    p = tmp_path / name
+    p.write_bytes(data)
+    return str(p)
+
+
+def test_load_errors(orc, tmp_path, tiny_path):
+    good = open(tiny_path, "rb").read()
+    cases = {
+        "magic.gguf": (b"XXXX" + good[4:], "bad magic"),
+        "ver.gguf": (good[:4] + struct.pack("<I", 2) + good[8:], "unsupported GGUF version 2"),
+        "trunc.gguf": (good[:100], "unexpected end of file"),
+        "empty.gguf": (b"", "unexpected end of file"),
+    }
+    for name, (data, msg) in cases.items():
+        with pytest.raises(orc.OracleError, match=msg):
+            orc.Model(_write(tmp_path, name, data))
+    with pytest.raises(orc.OracleError, match="opening"):
+        orc.Model(str(tmp_path / "missing.gguf"))
+    # a missing tensor: rename one in the directory
+    bad = good.replace(b"blk.1.attn_norm.weight", b"blk.1.attn_norm.weighX", 1)
+    with pytest.raises(orc.OracleError, match="attn_norm.weight` not found"):
+        orc.Model(_write(tmp_path, "missing_t.gguf", bad))
+    # a missing required metadata key
+    bad = good.replace(b"hobbylm.block_count", b"hobbylm.block_counX", 1)
+    with pytest.raises(orc.OracleError, match="missing metadata `hobbylm.block_count`"):
+        orc.Model(_write(tmp_path, "missing_k.gguf", bad))
+
+
+def test_pos_and_token_errors(orc, tiny_path):
+    m = orc.Model(tiny_path)
+    kv = m.new_cache()
+    with pytest.raises(orc.OracleError, match="out of range"):
+        m.forward(m.cfg.vocab_size, 0, kv)
+    with pytest.raises(orc.OracleError, match="does not continue"):
+        m.forward(1, 3, kv)
