@@ -1,0 +1,299 @@
+"""hobbylm_amd -- MI355X (gfx950) backend for hobby-rs's single-sequence decode step.
+
+Python mirror of the hobby-rs engine API (hobby-rs/src/lib.rs, model.rs, quant.rs) over the
+C ABI of include/hobby_gpu.h (libhobby_gpu.so, built in-tree by hobbylm_amd/build.py):
+
+    Engine.load(path, quant)          lib.rs:85-92
+    Engine.weight_bytes()             lib.rs:100-102
+    Engine.generate_greedy(...)       lib.rs:107-162 at temp 0, over token ids
+    Model.forward(token, pos, cache)  model.rs:152-156
+    Model.forward_x(x, pos, cache)    model.rs:160-184
+    Model.prefill(inputs, cache)      model.rs:340-370
+    Model.token_embedding(id)         model.rs:332-335
+    KvCache(model) / .len             model.rs:60-75
+    Q8Tensor.quantize / .matvec / .matmul   quant.rs:78-194
+
+There is no CPU fallback: every call goes to the HIP library, and importing the module
+raises if libhobby_gpu.so has not been built.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libhobby_gpu.so")
+
+HG_OK = 0
+HG_KV_EXACT = 1
+GPT2_VALID = 50257
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_vp = C.c_void_p
+
+
+class HgConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in (
+        "d_model", "n_layers", "n_dense", "n_heads", "n_kv_heads", "head_dim", "dense_ffn",
+        "expert_ffn", "n_experts", "top_k", "n_shared", "vocab_size", "context_length")] + [
+        ("rms_eps", C.c_float), ("rope_theta", C.c_float), ("expert_weights_scale", C.c_float),
+        ("expert_weights_norm", C.c_int32), ("gating_sigmoid", C.c_int32)]
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
+# name -> (restype, argtypes); the complete export list of include/hobby_gpu.h
+SIGNATURES = {
+    "hg_last_error": (C.c_char_p, []),
+    "hg_model_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(_vp)]),
+    "hg_model_free": (None, [_vp]),
+    "hg_model_config": (C.c_int, [_vp, C.POINTER(HgConfig)]),
+    "hg_weight_bytes": (C.c_uint64, [_vp]),
+    "hg_device_weight_bytes": (C.c_uint64, [_vp]),
+    "hg_token_embedding": (C.c_int, [_vp, C.c_uint32, _f32p]),
+    "hg_kv_new": (C.c_int, [_vp, C.c_uint32, C.c_uint32, C.POINTER(_vp)]),
+    "hg_kv_free": (None, [_vp]),
+    "hg_kv_len": (C.c_uint32, [_vp]),
+    "hg_kv_read": (C.c_int, [_vp, C.c_uint32, _f32p, _f32p]),
+    "hg_forward": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, _vp, C.POINTER(C.c_uint32)]),
+    "hg_forward_x": (C.c_int, [_vp, _vp, _f32p, C.c_uint32, _vp, C.POINTER(C.c_uint32)]),
+    "hg_prefill": (C.c_int, [_vp, _vp, _f32p, C.c_uint32, _vp, C.POINTER(C.c_uint32)]),
+    "hg_decode_greedy": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, _u32p]),
+    "hg_generate_greedy": (C.c_int, [_vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32,
+                                     _u32p, C.POINTER(C.c_uint32)]),
+    "hg_last_routing": (C.c_int, [_vp, _u32p, _f32p]),
+    "hg_q8_tensor_quantize": (C.c_int, [_f32p, C.c_uint32, C.c_uint32, C.POINTER(_vp)]),
+    "hg_q8_tensor_from_q8_0": (C.c_int, [_u8p, C.c_uint32, C.c_uint32, C.POINTER(_vp)]),
+    "hg_q8_tensor_free": (None, [_vp]),
+    "hg_q8_tensor_bytes": (C.c_uint64, [_vp]),
+    "hg_q8_tensor_matvec": (C.c_int, [_vp, _f32p, _f32p]),
+    "hg_q8_tensor_matmul": (C.c_int, [_vp, _f32p, _f32p, C.c_uint32]),
+    "hg_q8_tensor_matvec_gather": (C.c_int, [_vp, C.c_uint32, _u32p, C.c_uint32, _f32p, _f32p]),
+    "hg_attention_decode": (C.c_int, [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_float, C.c_float, C.c_uint32,
+                                      C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _f32p, _f32p, _f32p,
+                                      C.c_uint32]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded libhobby_gpu.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `python -m hobbylm_amd.build` "
+                              "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+class HgError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+def _check(rc: int):
+    if rc != HG_OK:
+        raise HgError(rc, lib().hg_last_error().decode())
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class Model:
+    """A loaded hobbylm model resident on the GPU (Model::load, model.rs:79-131)."""
+
+    def __init__(self, path: str, quant: bool = True):
+        h = _vp()
+        _check(lib().hg_model_load(str(path).encode(), 1 if quant else 0, C.byref(h)))
+        self.h = h
+        cfg = HgConfig()
+        _check(lib().hg_model_config(h, C.byref(cfg)))
+        self.cfg = cfg
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().hg_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def weight_bytes(self) -> int:
+        return int(lib().hg_weight_bytes(self.h))
+
+    def device_weight_bytes(self) -> int:
+        return int(lib().hg_device_weight_bytes(self.h))
+
+    def new_cache(self, max_ctx: int = 0, exact: bool = False) -> "KvCache":
+        return KvCache(self, max_ctx, exact)
+
+    def token_embedding(self, tok: int) -> np.ndarray:
+        out = np.empty(self.cfg.d_model, np.float32)
+        _check(lib().hg_token_embedding(self.h, tok, out))
+        return out
+
+    def forward(self, tok: int, pos: int, cache: "KvCache", want_logits: bool = True):
+        """Returns (logits or None, greedy next token)."""
+        lg = np.empty(self.cfg.vocab_size, np.float32) if want_logits else None
+        nxt = C.c_uint32()
+        _check(lib().hg_forward(self.h, cache.h, tok, pos, _ptr(lg), C.byref(nxt)))
+        return lg, int(nxt.value)
+
+    def forward_x(self, x: np.ndarray, pos: int, cache: "KvCache", want_logits: bool = True):
+        lg = np.empty(self.cfg.vocab_size, np.float32) if want_logits else None
+        nxt = C.c_uint32()
+        _check(lib().hg_forward_x(self.h, cache.h, np.ascontiguousarray(x, np.float32), pos, _ptr(lg),
+                                  C.byref(nxt)))
+        return lg, int(nxt.value)
+
+    def prefill(self, inputs: np.ndarray, cache: "KvCache", want_logits: bool = True):
+        inputs = np.ascontiguousarray(inputs, np.float32)
+        lg = np.empty(self.cfg.vocab_size, np.float32) if want_logits else None
+        nxt = C.c_uint32()
+        _check(lib().hg_prefill(self.h, cache.h, inputs.reshape(-1), inputs.shape[0], _ptr(lg), C.byref(nxt)))
+        return lg, int(nxt.value)
+
+    def decode_greedy(self, first_token: int, n_steps: int, cache: "KvCache") -> np.ndarray:
+        out = np.empty(max(n_steps, 1), np.uint32)
+        _check(lib().hg_decode_greedy(self.h, cache.h, first_token, n_steps, out))
+        return out[:n_steps]
+
+    def generate_greedy(self, prompt, max_new: int, cache: "KvCache", rep_penalty: float = 1.0,
+                        eos: int = 50256) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.empty(max(max_new, 1), np.uint32)
+        n = C.c_uint32()
+        _check(lib().hg_generate_greedy(self.h, cache.h, p, p.size, max_new, rep_penalty, eos, out, C.byref(n)))
+        return out[: n.value].copy()
+
+
+class KvCache:
+    """Device KV cache (KvCache, model.rs:60-75); exact=True selects reference-order reductions."""
+
+    def __init__(self, model: Model, max_ctx: int = 0, exact: bool = False):
+        self.model = model
+        h = _vp()
+        _check(lib().hg_kv_new(model.h, max_ctx, HG_KV_EXACT if exact else 0, C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().hg_kv_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def len(self) -> int:
+        return int(lib().hg_kv_len(self.h))
+
+    def read(self, layer: int):
+        c = self.model.cfg
+        kvd = c.n_kv_heads * c.head_dim
+        k = np.empty((self.len, kvd), np.float32)
+        v = np.empty((self.len, kvd), np.float32)
+        _check(lib().hg_kv_read(self.h, layer, k.reshape(-1), v.reshape(-1)))
+        return k, v
+
+    def routing(self):
+        c = self.model.cfg
+        idx = np.empty(c.n_layers * c.top_k, np.uint32)
+        w = np.empty(c.n_layers * c.top_k, np.float32)
+        _check(lib().hg_last_routing(self.h, idx, w))
+        return idx.reshape(c.n_layers, c.top_k), w.reshape(c.n_layers, c.top_k)
+
+
+class Engine(Model):
+    """Engine::load (lib.rs:85-92): the model without the tokenizer (token ids cross the boundary)."""
+
+    @classmethod
+    def load(cls, path: str, quant: bool = True) -> "Engine":
+        return cls(path, quant)
+
+
+class Q8Tensor:
+    """Q8Tensor (quant.rs:69-194) resident on the GPU."""
+
+    def __init__(self, h, out: int, inn: int):
+        self.h, self.out, self.inn = h, out, inn
+
+    @classmethod
+    def quantize(cls, w: np.ndarray) -> "Q8Tensor":
+        out, inn = w.shape
+        h = _vp()
+        _check(lib().hg_q8_tensor_quantize(np.ascontiguousarray(w, np.float32).reshape(-1), out, inn, C.byref(h)))
+        return cls(h, out, inn)
+
+    @classmethod
+    def from_q8_0(cls, blocks: np.ndarray, out: int, inn: int) -> "Q8Tensor":
+        h = _vp()
+        _check(lib().hg_q8_tensor_from_q8_0(np.ascontiguousarray(blocks).view(np.uint8).reshape(-1), out, inn,
+                                            C.byref(h)))
+        return cls(h, out, inn)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().hg_q8_tensor_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def bytes(self) -> int:
+        return int(lib().hg_q8_tensor_bytes(self.h))
+
+    def matvec(self, x: np.ndarray) -> np.ndarray:
+        y = np.empty(self.out, np.float32)
+        _check(lib().hg_q8_tensor_matvec(self.h, np.ascontiguousarray(x, np.float32), y))
+        return y
+
+    def matmul(self, x: np.ndarray) -> np.ndarray:
+        tn = x.shape[0]
+        y = np.empty((tn, self.out), np.float32)
+        _check(lib().hg_q8_tensor_matmul(self.h, np.ascontiguousarray(x, np.float32).reshape(-1), y.reshape(-1), tn))
+        return y
+
+    def matvec_gather(self, rows_per_mat: int, ids, x: np.ndarray) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, np.uint32)
+        y = np.empty((ids.size, rows_per_mat), np.float32)
+        _check(lib().hg_q8_tensor_matvec_gather(self.h, rows_per_mat, ids, ids.size,
+                                                np.ascontiguousarray(x, np.float32), y.reshape(-1)))
+        return y
+
+
+def attention_decode(q, k, v, q_norm, k_norm, eps, theta, rope_len, n_heads, n_kv, hd, pos, kcache, vcache,
+                     exact=False):
+    """One decode-attention layer (model.rs:199-233); kcache/vcache [pos+1][n_kv*hd] are updated in place."""
+    out = np.empty(n_heads * hd, np.float32)
+    assert kcache.flags["C_CONTIGUOUS"] and vcache.flags["C_CONTIGUOUS"]
+    _check(lib().hg_attention_decode(np.ascontiguousarray(q, np.float32), np.ascontiguousarray(k, np.float32),
+                                     np.ascontiguousarray(v, np.float32), np.ascontiguousarray(q_norm, np.float32),
+                                     np.ascontiguousarray(k_norm, np.float32), eps, theta, rope_len, n_heads, n_kv,
+                                     hd, pos, kcache.reshape(-1), vcache.reshape(-1), out,
+                                     HG_KV_EXACT if exact else 0))
+    return out

@@ -1,0 +1,819 @@
+// hg_engine.hip -- model load, device residency, KV cache and the decode step behind the
+// C ABI of include/hobby_gpu.h.
+//
+// One decode step is a fixed sequence of kernels per layer (norm+quant, QKV, attention,
+// attn_output+residual, norm+router or norm, gate/up, down+residual) plus the lm_head tail.
+// The sequence reads its token and position from a device StepParams block, so it is
+// captured once per cache as a HIP graph and replayed per token; in the greedy loop the
+// argmax kernel advances StepParams itself and steps chain on the device.
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/hobby_gpu.h"
+#include "hg_common.h"
+#include "hg_gguf.h"
+#include "hg_kernels.h"
+
+using namespace hg;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string &msg) {
+    g_err = msg;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                              \
+    do {                                                                                           \
+        hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess)                                                                      \
+            return fail(e_ == hipErrorOutOfMemory ? HG_ERR_NOMEM : HG_ERR_DEVICE,                  \
+                        std::string(#expr) + ": " + hipGetErrorString(e_));                        \
+    } while (0)
+
+// Device allocation that frees itself.
+struct DevBuf {
+    void *p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    int alloc(size_t bytes) {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = bytes;
+        if (bytes == 0) return HG_OK;
+        HIP_TRY(hipMalloc(&p, bytes));
+        return HG_OK;
+    }
+    int upload(const void *src, size_t bytes) {
+        int rc = alloc(bytes);
+        if (rc) return rc;
+        if (bytes) HIP_TRY(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice));
+        return HG_OK;
+    }
+    template <class T>
+    T *as() const { return static_cast<T *>(p); }
+};
+
+int check_device() {
+    static std::once_flag once;
+    static int status = HG_OK;
+    static std::string msg;
+    std::call_once(once, [] {
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+            status = HG_ERR_DEVICE;
+            msg = "no HIP device available";
+            return;
+        }
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+            status = HG_ERR_DEVICE;
+            msg = "hipGetDeviceProperties failed";
+            return;
+        }
+        if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+            status = HG_ERR_DEVICE;
+            msg = std::string("this build targets gfx950; device is ") + prop.gcnArchName;
+        }
+    });
+    if (status) g_err = msg;
+    return status;
+}
+
+struct DevQ8 {
+    DevBuf qs, sc;
+    Q8Mat m{};
+    uint64_t ref_bytes = 0;
+    int upload(const PackedQ8 &p) {
+        int rc = qs.upload(p.qs.data(), p.qs.size());
+        if (!rc) rc = sc.upload(p.sc.data(), p.sc.size());
+        if (rc) return rc;
+        m.qs = qs.as<uint8_t>();
+        m.sc = sc.p;
+        m.N = p.N;
+        m.K = p.K;
+        m.nb = p.nb;
+        m.nc = p.nc;
+        m.sc_f32 = p.f32sc;
+        ref_bytes = p.ref_bytes();
+        return HG_OK;
+    }
+    uint64_t dev_bytes() const { return qs.n + sc.n; }
+};
+
+struct Layer {
+    bool moe = false;
+    DevBuf attn_norm, q_norm, k_norm, ffn_norm, router, bias;
+    DevQ8 qkv, o, gate, up, down, gate_e, up_e, down_e, gate_sh, up_sh, down_sh;
+};
+
+}  // namespace
+
+struct hg_model {
+    hg_config c{};
+    std::vector<std::unique_ptr<Layer>> layers;
+    DevBuf token_embd, output_norm, rope_cos, rope_sin;
+    DevQ8 output;
+    uint64_t ref_bytes = 0, dev_bytes = 0;
+    uint32_t n_slots = 0;  // routed top-k + shared expert slot
+};
+
+struct hg_kv {
+    const hg_model *m = nullptr;
+    hipStream_t st = nullptr;
+    uint32_t cap = 0, len = 0, flags = 0;
+    bool exact = false;
+    uint32_t S = 0;         // attention context splits
+    uint32_t lm_threads = 256, n_part = 0;
+    DevBuf kc, vc;          // [L][n_kv][cap][hd]
+    DevBuf x, qkv, part, scores, a, logits, pv, pi, qa, da, topk_idx, topk_w, order, rec_idx, rec_w, params,
+        out_ids, inputs;
+    uint32_t inputs_rows = 0;
+    StepParams *h_params = nullptr;
+    uint32_t *h_ids = nullptr;
+    float *h_logits = nullptr;
+    hipGraphExec_t g_decode = nullptr, g_body = nullptr, g_tail = nullptr;
+    bool use_graph = true;
+    ~hg_kv();
+};
+
+namespace {
+
+uint32_t slots_of(const hg_config &c) { return c.top_k + (c.n_shared > 0 ? 1 : 0); }
+
+int load_norm(const Gguf &g, const std::string &name, size_t want, DevBuf &dst) {
+    std::vector<float> v;
+    int rc = g.f32(name, v, g_err);
+    if (rc) return rc;
+    if (v.size() != want)
+        return fail(HG_ERR_FORMAT, "tensor `" + name + "` has " + std::to_string(v.size()) + " elements, expected " +
+                                       std::to_string(want));
+    return dst.upload(v.data(), v.size() * 4);
+}
+
+// Gguf::load + Mat::build(.., quant = true) (model.rs:87-89, 121): requantize and upload.
+int load_q8(const Gguf &g, const std::string &name, uint32_t N, uint32_t K, DevQ8 &dst, hg_model *m) {
+    const TensorInfo *t;
+    const uint8_t *raw;
+    size_t nbytes;
+    int rc = g.raw(name, t, raw, nbytes, g_err);
+    if (rc) return rc;
+    if (t->n_elems() != (uint64_t)N * K)
+        return fail(HG_ERR_FORMAT, "tensor `" + name + "` has " + std::to_string(t->n_elems()) + " elements, expected " +
+                                       std::to_string((uint64_t)N * K));
+    if (K % QK) return fail(HG_ERR_UNSUPPORTED, "Q8_0 needs in_ divisible by 32 (got " + std::to_string(K) + ")");
+    PackedQ8 p;
+    if (t->type == 8) pack_q8_from_q8_0(raw, N, K, p);
+    else {
+        std::vector<float> w;
+        rc = g.load(name, w, g_err);
+        if (rc) return rc;
+        pack_q8_from_f32(w.data(), N, K, p);
+    }
+    rc = dst.upload(p);
+    if (rc) return rc;
+    m->ref_bytes += dst.ref_bytes;
+    m->dev_bytes += dst.dev_bytes();
+    return HG_OK;
+}
+
+int validate(const hg_config &c) {
+    auto bad = [](const std::string &s) { return fail(HG_ERR_UNSUPPORTED, s); };
+    if (!c.d_model || !c.n_layers || !c.n_heads || !c.n_kv_heads || c.n_heads % c.n_kv_heads)
+        return bad("unsupported head configuration");
+    if (c.head_dim != 32 && c.head_dim != 64 && c.head_dim != 128)
+        return bad("head_dim " + std::to_string(c.head_dim) + " not in {32, 64, 128}");
+    if (c.n_heads / c.n_kv_heads > 8) return bad("more than 8 query heads per kv head");
+    if (c.d_model % QK || c.expert_ffn % QK || c.dense_ffn % QK)
+        return bad("Q8_0 needs in_ divisible by 32");
+    if (c.n_experts > 256 || c.top_k > 64 || c.top_k > c.n_experts) return bad("expert count out of range");
+    if (c.n_dense < c.n_layers && (slots_of(c) == 0 || slots_of(c) > 16)) return bad("more than 16 expert slots");
+    if (!c.context_length) return bad("context_length is 0");
+    return HG_OK;
+}
+
+}  // namespace
+
+// ======================================================================= C ABI
+extern "C" {
+
+const char *hg_last_error(void) { return g_err.c_str(); }
+
+int hg_model_load(const char *path, int quant, hg_model **out) {
+    if (!out) return fail(HG_ERR_ARG, "out is NULL");
+    *out = nullptr;
+    if (!quant) return fail(HG_ERR_UNSUPPORTED, "F32 matrices (quant = false) are not supported by the GPU backend");
+    int rc = check_device();
+    if (rc) return rc;
+    Gguf g;
+    rc = g.open(path, g_err);
+    if (rc) return rc;
+    auto m = std::make_unique<hg_model>();
+    rc = config_from_gguf(g, m->c, g_err);
+    if (rc) return rc;
+    rc = validate(m->c);
+    if (rc) return rc;
+    const hg_config &c = m->c;
+    const uint32_t d = c.d_model, f = c.expert_ffn, hd = c.head_dim;
+    const uint32_t qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+    m->n_slots = slots_of(c);
+    for (uint32_t i = 0; i < c.n_layers; ++i) {
+        auto L = std::make_unique<Layer>();
+        const std::string p = "blk." + std::to_string(i) + ".";
+        L->moe = i >= c.n_dense;
+        if (L->moe) {
+            std::vector<float> rw;
+            if ((rc = g.load(p + "ffn_gate_inp.weight", rw, g_err))) return rc;
+            if (rw.size() != (size_t)c.n_experts * d)
+                return fail(HG_ERR_FORMAT, "tensor `" + p + "ffn_gate_inp.weight` has wrong size");
+            if ((rc = L->router.upload(rw.data(), rw.size() * 4))) return rc;
+            if ((rc = load_norm(g, p + "exp_probs_b.bias", c.n_experts, L->bias))) return rc;
+            if ((rc = load_q8(g, p + "ffn_gate_exps.weight", c.n_experts * f, d, L->gate_e, m.get()))) return rc;
+            if ((rc = load_q8(g, p + "ffn_up_exps.weight", c.n_experts * f, d, L->up_e, m.get()))) return rc;
+            if ((rc = load_q8(g, p + "ffn_down_exps.weight", c.n_experts * d, f, L->down_e, m.get()))) return rc;
+            if ((rc = load_q8(g, p + "ffn_gate_shexp.weight", f, d, L->gate_sh, m.get()))) return rc;
+            if ((rc = load_q8(g, p + "ffn_up_shexp.weight", f, d, L->up_sh, m.get()))) return rc;
+            if ((rc = load_q8(g, p + "ffn_down_shexp.weight", d, f, L->down_sh, m.get()))) return rc;
+        } else {
+            if ((rc = load_q8(g, p + "ffn_gate.weight", c.dense_ffn, d, L->gate, m.get()))) return rc;
+            if ((rc = load_q8(g, p + "ffn_up.weight", c.dense_ffn, d, L->up, m.get()))) return rc;
+            if ((rc = load_q8(g, p + "ffn_down.weight", d, c.dense_ffn, L->down, m.get()))) return rc;
+        }
+        if ((rc = load_norm(g, p + "attn_norm.weight", d, L->attn_norm))) return rc;
+        if ((rc = load_q8(g, p + "attn_qkv.weight", qd + 2 * kvd, d, L->qkv, m.get()))) return rc;
+        if ((rc = load_norm(g, p + "attn_q_norm.weight", hd, L->q_norm))) return rc;
+        if ((rc = load_norm(g, p + "attn_k_norm.weight", hd, L->k_norm))) return rc;
+        if ((rc = load_q8(g, p + "attn_output.weight", d, qd, L->o, m.get()))) return rc;
+        if ((rc = load_norm(g, p + "ffn_norm.weight", d, L->ffn_norm))) return rc;
+        m->layers.push_back(std::move(L));
+    }
+    if ((rc = load_q8(g, "output.weight", c.vocab_size, d, m->output, m.get()))) return rc;
+    {
+        std::vector<float> emb;
+        if ((rc = g.load("token_embd.weight", emb, g_err))) return rc;
+        if (emb.size() != (size_t)c.vocab_size * d) return fail(HG_ERR_FORMAT, "tensor `token_embd.weight` has wrong size");
+        if ((rc = m->token_embd.upload(emb.data(), emb.size() * 4))) return rc;
+    }
+    if ((rc = load_norm(g, "output_norm.weight", d, m->output_norm))) return rc;
+    std::vector<float> cs, sn;
+    rope_table(hd, c.context_length, c.rope_theta, cs, sn);
+    if ((rc = m->rope_cos.upload(cs.data(), cs.size() * 4))) return rc;
+    if ((rc = m->rope_sin.upload(sn.data(), sn.size() * 4))) return rc;
+    *out = m.release();
+    return HG_OK;
+}
+
+void hg_model_free(hg_model *m) { delete m; }
+
+int hg_model_config(const hg_model *m, hg_config *out) {
+    if (!m || !out) return fail(HG_ERR_ARG, "NULL argument");
+    *out = m->c;
+    return HG_OK;
+}
+
+uint64_t hg_weight_bytes(const hg_model *m) { return m ? m->ref_bytes : 0; }
+uint64_t hg_device_weight_bytes(const hg_model *m) { return m ? m->dev_bytes : 0; }
+
+int hg_token_embedding(const hg_model *m, uint32_t id, float *out) {
+    if (!m || !out) return fail(HG_ERR_ARG, "NULL argument");
+    if (id >= m->c.vocab_size) return fail(HG_ERR_ARG, "token " + std::to_string(id) + " out of range");
+    HIP_TRY(hipMemcpy(out, m->token_embd.as<float>() + (size_t)id * m->c.d_model, m->c.d_model * 4,
+                      hipMemcpyDeviceToHost));
+    return HG_OK;
+}
+
+}  // extern "C"
+
+// ======================================================================= step enqueue
+namespace {
+
+float *layer_k(const hg_kv *kv, uint32_t l) {
+    const hg_config &c = kv->m->c;
+    return kv->kc.as<float>() + (size_t)l * c.n_kv_heads * kv->cap * c.head_dim;
+}
+float *layer_v(const hg_kv *kv, uint32_t l) {
+    const hg_config &c = kv->m->c;
+    return kv->vc.as<float>() + (size_t)l * c.n_kv_heads * kv->cap * c.head_dim;
+}
+
+void enqueue_layers(hg_kv *kv, int order) {
+    const hg_model *m = kv->m;
+    const hg_config &c = m->c;
+    hipStream_t st = kv->st;
+    const uint32_t d = c.d_model;
+    float *x = kv->x.as<float>();
+    uint8_t *qa = kv->qa.as<uint8_t>();
+    float *da = kv->da.as<float>();
+    StepParams *p = kv->params.as<StepParams>();
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        const Layer &L = *m->layers[l];
+        launch_rmsnorm_quant(st, kv->exact, x, L.attn_norm.as<float>(), c.rms_eps, d, nullptr, qa, da);
+        launch_matvec(st, order, EPI_STORE, L.qkv.m, qa, da, kv->qkv.as<float>(), 64, 0, nullptr, nullptr);
+        launch_attn(st, kv->exact, c.head_dim, kv->qkv.as<float>(), L.q_norm.as<float>(), L.k_norm.as<float>(),
+                    c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), p, layer_k(kv, l), layer_v(kv, l),
+                    kv->cap, c.n_heads, c.n_kv_heads, kv->S, kv->part.as<float>(), kv->scores.as<float>(), nullptr,
+                    qa, da);
+        launch_matvec(st, order, EPI_RESID, L.o.m, qa, da, x, 64, 0, nullptr, nullptr);
+        if (L.moe) {
+            launch_ffn_router(st, kv->exact, x, L.ffn_norm.as<float>(), c.rms_eps, d, L.router.as<float>(),
+                              L.bias.as<float>(), c.n_experts, c.top_k, c.gating_sigmoid, c.expert_weights_norm,
+                              c.expert_weights_scale, qa, da, kv->topk_idx.as<uint32_t>(), kv->topk_w.as<float>(),
+                              kv->order.as<uint32_t>(), kv->rec_idx.as<uint32_t>() + (size_t)l * c.top_k,
+                              kv->rec_w.as<float>() + (size_t)l * c.top_k);
+            launch_ffn_gateup(st, order, L.gate_e.m, L.up_e.m, L.gate_sh.m, L.up_sh.m, kv->topk_idx.as<uint32_t>(),
+                              c.top_k, m->n_slots, c.expert_ffn, qa, da, kv->a.as<float>());
+            launch_ffn_down(st, order, L.down_e.m, L.down_sh.m, kv->topk_idx.as<uint32_t>(), kv->topk_w.as<float>(),
+                            kv->order.as<uint32_t>(), c.top_k, m->n_slots, 0, d, c.expert_ffn, kv->a.as<float>(), x);
+        } else {
+            launch_rmsnorm_quant(st, kv->exact, x, L.ffn_norm.as<float>(), c.rms_eps, d, nullptr, qa, da);
+            launch_ffn_gateup(st, order, L.gate.m, L.up.m, L.gate.m, L.up.m, nullptr, 0, 1, c.dense_ffn, qa, da,
+                              kv->a.as<float>());
+            launch_ffn_down(st, order, L.down.m, L.down.m, nullptr, nullptr, nullptr, 0, 1, 1, d, c.dense_ffn,
+                            kv->a.as<float>(), x);
+        }
+    }
+}
+
+// output_norm + lm_head + greedy argmax (model.rs:180-183, lib.rs:132-142).
+void enqueue_tail(hg_kv *kv) {
+    const hg_model *m = kv->m;
+    const hg_config &c = m->c;
+    const uint32_t valid = c.vocab_size < 50257 ? c.vocab_size : 50257;
+    launch_rmsnorm_quant(kv->st, kv->exact, kv->x.as<float>(), m->output_norm.as<float>(), c.rms_eps, c.d_model,
+                         nullptr, kv->qa.as<uint8_t>(), kv->da.as<float>());
+    launch_matvec(kv->st, ORDER_DECODE, EPI_LOGITS, m->output.m, kv->qa.as<uint8_t>(), kv->da.as<float>(),
+                  kv->logits.as<float>(), kv->lm_threads, valid, kv->pv.as<float>(), kv->pi.as<uint32_t>());
+    launch_argmax_final(kv->st, kv->pv.as<float>(), kv->pi.as<uint32_t>(), kv->n_part, kv->params.as<StepParams>(),
+                        kv->out_ids.as<uint32_t>());
+}
+
+void enqueue_decode(hg_kv *kv) {
+    launch_embed(kv->st, kv->m->token_embd.as<float>(), kv->m->c.d_model, kv->params.as<StepParams>(),
+                 kv->x.as<float>());
+    enqueue_layers(kv, ORDER_DECODE);
+    enqueue_tail(kv);
+}
+
+void enqueue_body(hg_kv *kv) {
+    launch_load_row(kv->st, kv->inputs.as<float>(), kv->m->c.d_model, kv->params.as<StepParams>(), kv->x.as<float>());
+    enqueue_layers(kv, ORDER_PREFILL);
+    launch_advance(kv->st, kv->params.as<StepParams>());
+}
+
+// Run `fn`'s kernels on the cache's stream: replay its captured graph (capturing it on
+// first use) or, with HG_GRAPH=0, launch eagerly.
+template <class F>
+int run(hg_kv *kv, hipGraphExec_t &exec, F fn) {
+    if (!kv->use_graph) {
+        fn(kv);
+        HIP_TRY(hipGetLastError());
+        return HG_OK;
+    }
+    if (!exec) {
+        hipGraph_t graph = nullptr;
+        HIP_TRY(hipStreamBeginCapture(kv->st, hipStreamCaptureModeThreadLocal));
+        fn(kv);
+        hipError_t e = hipStreamEndCapture(kv->st, &graph);
+        if (e != hipSuccess) return fail(HG_ERR_DEVICE, std::string("graph capture: ") + hipGetErrorString(e));
+        e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (e != hipSuccess) {
+            exec = nullptr;
+            return fail(HG_ERR_DEVICE, std::string("graph instantiate: ") + hipGetErrorString(e));
+        }
+    }
+    HIP_TRY(hipGraphLaunch(exec, kv->st));
+    return HG_OK;
+}
+
+int set_params(hg_kv *kv, uint32_t token, uint32_t pos, uint32_t feedback, uint32_t embed, uint32_t base) {
+    StepParams &hp = *kv->h_params;
+    hp = StepParams{};
+    hp.token = token;
+    hp.pos = pos;
+    hp.step = 0;
+    hp.feedback = feedback;
+    hp.embed = embed;
+    hp.base = base;
+    HIP_TRY(hipMemcpyAsync(kv->params.p, kv->h_params, sizeof(StepParams), hipMemcpyHostToDevice, kv->st));
+    return HG_OK;
+}
+
+int finish(hg_kv *kv, float *logits, uint32_t *next) {
+    const hg_config &c = kv->m->c;
+    if (logits)
+        HIP_TRY(hipMemcpyAsync(kv->h_logits, kv->logits.p, (size_t)c.vocab_size * 4, hipMemcpyDeviceToHost, kv->st));
+    HIP_TRY(hipMemcpyAsync(kv->h_ids, kv->out_ids.p, 4, hipMemcpyDeviceToHost, kv->st));
+    HIP_TRY(hipStreamSynchronize(kv->st));
+    if (logits) memcpy(logits, kv->h_logits, (size_t)c.vocab_size * 4);
+    if (next) *next = kv->h_ids[0];
+    return HG_OK;
+}
+
+int check_step(const hg_model *m, const hg_kv *kv, uint32_t pos, uint32_t n) {
+    if (!m || !kv || kv->m != m) return fail(HG_ERR_ARG, "cache does not belong to this model");
+    if (pos != kv->len)
+        return fail(HG_ERR_ARG, "pos " + std::to_string(pos) + " does not continue the cache (len " +
+                                    std::to_string(kv->len) + ")");
+    if ((uint64_t)pos + n > kv->cap)
+        return fail(HG_ERR_ARG, "pos " + std::to_string(pos) + " + " + std::to_string(n) + " exceeds the cache (" +
+                                    std::to_string(kv->cap) + " positions)");
+    return HG_OK;
+}
+
+}  // namespace
+
+hg_kv::~hg_kv() {
+    if (st) (void)hipStreamSynchronize(st);
+    if (g_decode) (void)hipGraphExecDestroy(g_decode);
+    if (g_body) (void)hipGraphExecDestroy(g_body);
+    if (g_tail) (void)hipGraphExecDestroy(g_tail);
+    if (h_params) (void)hipHostFree(h_params);
+    if (h_ids) (void)hipHostFree(h_ids);
+    if (h_logits) (void)hipHostFree(h_logits);
+    if (st) (void)hipStreamDestroy(st);
+}
+
+extern "C" {
+
+int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out) {
+    if (!m || !out) return fail(HG_ERR_ARG, "NULL argument");
+    *out = nullptr;
+    const hg_config &c = m->c;
+    if (max_ctx == 0 || max_ctx > c.context_length) max_ctx = c.context_length;
+    auto kv = std::make_unique<hg_kv>();
+    kv->m = m;
+    kv->cap = max_ctx;
+    kv->flags = flags;
+    kv->exact = (flags & HG_KV_EXACT) != 0;
+    const char *ge = getenv("HG_GRAPH");
+    kv->use_graph = !(ge && ge[0] == '0');
+    kv->S = std::max(64u, div_up(kv->cap, 256));  // splits of at most 256 positions (LDS bound)
+    HIP_TRY(hipStreamCreateWithFlags(&kv->st, hipStreamNonBlocking));
+    const size_t kvsz = (size_t)c.n_layers * c.n_kv_heads * kv->cap * c.head_dim * 4;
+    int rc;
+    if ((rc = kv->kc.alloc(kvsz)) || (rc = kv->vc.alloc(kvsz))) return rc;
+    const uint32_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    const uint32_t maxk = std::max(std::max(c.d_model, qd), std::max(c.dense_ffn, c.expert_ffn));
+    const uint32_t maxnc = div_up(maxk / QK, 4);
+    const uint32_t ffw = std::max(c.dense_ffn, c.expert_ffn) * std::max(m->n_slots, 1u);
+    kv->n_part = matvec_blocks(c.vocab_size, kv->lm_threads);
+    if ((rc = kv->x.alloc(c.d_model * 4)) || (rc = kv->qkv.alloc((size_t)(qd + 2 * kvd) * 4)) ||
+        (rc = kv->part.alloc((size_t)c.n_heads * kv->S * (c.head_dim + 2) * 4)) ||
+        (rc = kv->scores.alloc(kv->exact ? (size_t)c.n_heads * kv->cap * 4 : 4)) ||
+        (rc = kv->a.alloc((size_t)ffw * 4)) || (rc = kv->logits.alloc((size_t)c.vocab_size * 4)) ||
+        (rc = kv->pv.alloc((size_t)kv->n_part * 4)) || (rc = kv->pi.alloc((size_t)kv->n_part * 4)) ||
+        (rc = kv->qa.alloc((size_t)maxnc * CHUNK_BYTES)) || (rc = kv->da.alloc((size_t)maxnc * 4 * 4)) ||
+        (rc = kv->topk_idx.alloc(64 * 4)) || (rc = kv->topk_w.alloc(64 * 4)) || (rc = kv->order.alloc(64 * 4)) ||
+        (rc = kv->rec_idx.alloc((size_t)c.n_layers * std::max(c.top_k, 1u) * 4)) ||
+        (rc = kv->rec_w.alloc((size_t)c.n_layers * std::max(c.top_k, 1u) * 4)) ||
+        (rc = kv->params.alloc(sizeof(StepParams))) || (rc = kv->out_ids.alloc((size_t)(kv->cap + 1) * 4)))
+        return rc;
+    HIP_TRY(hipMemset(kv->rec_idx.p, 0xff, kv->rec_idx.n));
+    HIP_TRY(hipMemset(kv->rec_w.p, 0, kv->rec_w.n));
+    HIP_TRY(hipMemset(kv->kc.p, 0, kv->kc.n));
+    HIP_TRY(hipMemset(kv->vc.p, 0, kv->vc.n));
+    HIP_TRY(hipHostMalloc((void **)&kv->h_params, sizeof(StepParams), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&kv->h_ids, (size_t)(kv->cap + 1) * 4, hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&kv->h_logits, (size_t)c.vocab_size * 4, hipHostMallocDefault));
+    HIP_TRY(hipDeviceSynchronize());
+    *out = kv.release();
+    return HG_OK;
+}
+
+void hg_kv_free(hg_kv *kv) { delete kv; }
+
+uint32_t hg_kv_len(const hg_kv *kv) { return kv ? kv->len : 0; }
+
+int hg_kv_read(const hg_kv *kv, uint32_t layer, float *k, float *v) {
+    if (!kv || !k || !v) return fail(HG_ERR_ARG, "NULL argument");
+    const hg_config &c = kv->m->c;
+    if (layer >= c.n_layers) return fail(HG_ERR_ARG, "layer out of range");
+    const uint32_t hd = c.head_dim, nkv = c.n_kv_heads, len = kv->len;
+    std::vector<float> kb((size_t)nkv * kv->cap * hd), vb(kb.size());
+    HIP_TRY(hipStreamSynchronize(kv->st));
+    HIP_TRY(hipMemcpy(kb.data(), layer_k(kv, layer), kb.size() * 4, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(vb.data(), layer_v(kv, layer), vb.size() * 4, hipMemcpyDeviceToHost));
+    for (uint32_t t = 0; t < len; ++t)
+        for (uint32_t g = 0; g < nkv; ++g) {
+            memcpy(k + ((size_t)t * nkv + g) * hd, kb.data() + ((size_t)g * kv->cap + t) * hd, hd * 4);
+            memcpy(v + ((size_t)t * nkv + g) * hd, vb.data() + ((size_t)g * kv->cap + t) * hd, hd * 4);
+        }
+    return HG_OK;
+}
+
+int hg_forward(const hg_model *m, hg_kv *kv, uint32_t token, uint32_t pos, float *logits, uint32_t *next) {
+    int rc = check_step(m, kv, pos, 1);
+    if (rc) return rc;
+    if (token >= m->c.vocab_size)
+        return fail(HG_ERR_ARG, "token " + std::to_string(token) + " out of range (vocab " +
+                                    std::to_string(m->c.vocab_size) + ")");
+    if ((rc = set_params(kv, token, pos, 0, 1, pos))) return rc;
+    if ((rc = run(kv, kv->g_decode, enqueue_decode))) return rc;
+    if ((rc = finish(kv, logits, next))) return rc;
+    kv->len = pos + 1;
+    return HG_OK;
+}
+
+int hg_forward_x(const hg_model *m, hg_kv *kv, const float *x, uint32_t pos, float *logits, uint32_t *next) {
+    int rc = check_step(m, kv, pos, 1);
+    if (rc) return rc;
+    if (!x) return fail(HG_ERR_ARG, "x is NULL");
+    HIP_TRY(hipMemcpyAsync(kv->x.p, x, (size_t)m->c.d_model * 4, hipMemcpyHostToDevice, kv->st));
+    if ((rc = set_params(kv, 0, pos, 0, 0, pos))) return rc;
+    if ((rc = run(kv, kv->g_decode, enqueue_decode))) return rc;
+    if ((rc = finish(kv, logits, next))) return rc;
+    kv->len = pos + 1;
+    return HG_OK;
+}
+
+int hg_prefill(const hg_model *m, hg_kv *kv, const float *inputs, uint32_t tn, float *logits, uint32_t *next) {
+    if (!kv) return fail(HG_ERR_ARG, "NULL argument");
+    if (tn == 0) return fail(HG_ERR_ARG, "prefill needs at least one input row");
+    if (!inputs) return fail(HG_ERR_ARG, "inputs is NULL");
+    const uint32_t base = kv->len;
+    int rc = check_step(m, kv, base, tn);
+    if (rc) return rc;
+    const size_t rowb = (size_t)m->c.d_model * 4;
+    if (tn > kv->inputs_rows) {
+        HIP_TRY(hipStreamSynchronize(kv->st));
+        if ((rc = kv->inputs.alloc(rowb * tn))) return rc;
+        kv->inputs_rows = tn;
+        if (kv->g_body) {  // the captured body reads the old buffer
+            (void)hipGraphExecDestroy(kv->g_body);
+            kv->g_body = nullptr;
+        }
+    }
+    HIP_TRY(hipMemcpyAsync(kv->inputs.p, inputs, rowb * tn, hipMemcpyHostToDevice, kv->st));
+    if ((rc = set_params(kv, 0, base, 0, 0, base))) return rc;
+    for (uint32_t t = 0; t < tn; ++t)
+        if ((rc = run(kv, kv->g_body, enqueue_body))) return rc;
+    if ((rc = run(kv, kv->g_tail, enqueue_tail))) return rc;
+    if ((rc = finish(kv, logits, next))) return rc;
+    kv->len = base + tn;
+    return HG_OK;
+}
+
+int hg_decode_greedy(const hg_model *m, hg_kv *kv, uint32_t first_token, uint32_t n_steps, uint32_t *out_ids) {
+    if (!kv) return fail(HG_ERR_ARG, "NULL argument");
+    const uint32_t pos = kv->len;
+    int rc = check_step(m, kv, pos, n_steps);
+    if (rc) return rc;
+    if (first_token >= m->c.vocab_size) return fail(HG_ERR_ARG, "token out of range");
+    if (n_steps == 0) return HG_OK;
+    if (!out_ids) return fail(HG_ERR_ARG, "out_ids is NULL");
+    if ((rc = set_params(kv, first_token, pos, 1, 1, pos))) return rc;
+    for (uint32_t i = 0; i < n_steps; ++i)
+        if ((rc = run(kv, kv->g_decode, enqueue_decode))) return rc;
+    HIP_TRY(hipMemcpyAsync(kv->h_ids, kv->out_ids.p, (size_t)n_steps * 4, hipMemcpyDeviceToHost, kv->st));
+    HIP_TRY(hipStreamSynchronize(kv->st));
+    memcpy(out_ids, kv->h_ids, (size_t)n_steps * 4);
+    kv->len = pos + n_steps;
+    return HG_OK;
+}
+
+int hg_generate_greedy(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_new,
+                       float rep_penalty, uint32_t eos, uint32_t *out_ids, uint32_t *n_out) {
+    if (!m || !kv || !n_out) return fail(HG_ERR_ARG, "NULL argument");
+    *n_out = 0;
+    if (n_prompt == 0) return HG_OK;
+    const hg_config &c = m->c;
+    const uint32_t d = c.d_model, V = c.vocab_size, valid = V < 50257 ? V : 50257;
+    std::vector<float> in((size_t)n_prompt * d);
+    int rc;
+    for (uint32_t i = 0; i < n_prompt; ++i)
+        if ((rc = hg_token_embedding(m, prompt[i], in.data() + (size_t)i * d))) return rc;
+    const bool host_sample = rep_penalty != 1.0f;
+    std::vector<float> logits(host_sample ? V : 0);
+    uint32_t next = 0, pos = kv->len + n_prompt;
+    if ((rc = hg_prefill(m, kv, in.data(), n_prompt, host_sample ? logits.data() : nullptr, &next))) return rc;
+    const uint32_t stop = std::min(c.context_length, kv->cap);
+    uint32_t n = 0;
+    for (uint32_t it = 0; it < max_new; ++it) {
+        if (host_sample) {
+            for (uint32_t i = valid; i < V; ++i) logits[i] = -INFINITY;
+            for (uint32_t q = 0; q < n; ++q) {
+                float &l = logits[out_ids[q]];
+                l = l > 0.0f ? l / rep_penalty : l * rep_penalty;
+            }
+            uint32_t best = 0;
+            float bv = -INFINITY;
+            for (uint32_t i = 0; i < V; ++i)
+                if (logits[i] > bv) { bv = logits[i]; best = i; }
+            next = best;
+        }
+        if (next == eos) break;
+        out_ids[n++] = next;
+        if (pos + 1 >= stop) break;
+        if ((rc = hg_forward(m, kv, next, pos, host_sample ? logits.data() : nullptr, &next))) {
+            *n_out = n;
+            return rc;
+        }
+        ++pos;
+    }
+    *n_out = n;
+    return HG_OK;
+}
+
+int hg_last_routing(const hg_kv *kv, uint32_t *idx, float *w) {
+    if (!kv) return fail(HG_ERR_ARG, "NULL argument");
+    const size_t n = (size_t)kv->m->c.n_layers * kv->m->c.top_k;
+    HIP_TRY(hipStreamSynchronize(kv->st));
+    if (idx) HIP_TRY(hipMemcpy(idx, kv->rec_idx.p, n * 4, hipMemcpyDeviceToHost));
+    if (w) HIP_TRY(hipMemcpy(w, kv->rec_w.p, n * 4, hipMemcpyDeviceToHost));
+    return HG_OK;
+}
+
+}  // extern "C"
+
+// ======================================================================= operator level
+struct hg_q8_tensor {
+    DevQ8 w;
+    hipStream_t st = nullptr;
+    ~hg_q8_tensor() {
+        if (st) (void)hipStreamDestroy(st);
+    }
+};
+
+namespace {
+
+int make_tensor(const PackedQ8 &p, hg_q8_tensor **t) {
+    auto q = std::make_unique<hg_q8_tensor>();
+    int rc = q->w.upload(p);
+    if (rc) return rc;
+    HIP_TRY(hipStreamCreateWithFlags(&q->st, hipStreamNonBlocking));
+    *t = q.release();
+    return HG_OK;
+}
+
+// Quantize x (host) into device (qa, da); then run `body`.
+template <class F>
+int with_act(const hg_q8_tensor *t, const float *x, uint32_t rows, F body) {
+    const Q8Mat &W = t->w.m;
+    DevBuf dx, qa, da;
+    int rc;
+    if ((rc = dx.upload(x, (size_t)rows * W.K * 4))) return rc;
+    if ((rc = qa.alloc((size_t)rows * W.nc * CHUNK_BYTES)) || (rc = da.alloc((size_t)rows * W.nc * 16))) return rc;
+    for (uint32_t r = 0; r < rows; ++r)
+        launch_quant_vec(t->st, dx.as<float>() + (size_t)r * W.K, W.K, qa.as<uint8_t>() + (size_t)r * W.nc * CHUNK_BYTES,
+                         da.as<float>() + (size_t)r * W.nc * 4);
+    return body(qa, da);
+}
+
+}  // namespace
+
+extern "C" {
+
+int hg_q8_tensor_quantize(const float *w, uint32_t out, uint32_t in, hg_q8_tensor **t) {
+    if (!w || !t) return fail(HG_ERR_ARG, "NULL argument");
+    if (in % QK || !out || !in) return fail(HG_ERR_ARG, "Q8_0 needs in_ divisible by 32 (got " + std::to_string(in) + ")");
+    int rc = check_device();
+    if (rc) return rc;
+    PackedQ8 p;
+    pack_q8_from_f32(w, out, in, p);
+    return make_tensor(p, t);
+}
+
+int hg_q8_tensor_from_q8_0(const void *blocks, uint32_t out, uint32_t in, hg_q8_tensor **t) {
+    if (!blocks || !t) return fail(HG_ERR_ARG, "NULL argument");
+    if (in % QK || !out || !in) return fail(HG_ERR_ARG, "Q8_0 needs in_ divisible by 32 (got " + std::to_string(in) + ")");
+    int rc = check_device();
+    if (rc) return rc;
+    PackedQ8 p;
+    pack_q8_from_q8_0(static_cast<const uint8_t *>(blocks), out, in, p);
+    return make_tensor(p, t);
+}
+
+void hg_q8_tensor_free(hg_q8_tensor *t) { delete t; }
+
+uint64_t hg_q8_tensor_bytes(const hg_q8_tensor *t) { return t ? t->w.ref_bytes : 0; }
+
+int hg_q8_tensor_matvec(const hg_q8_tensor *t, const float *x, float *y) {
+    if (!t || !x || !y) return fail(HG_ERR_ARG, "NULL argument");
+    const Q8Mat &W = t->w.m;
+    return with_act(t, x, 1, [&](DevBuf &qa, DevBuf &da) -> int {
+        DevBuf dy;
+        int rc = dy.alloc((size_t)W.N * 4);
+        if (rc) return rc;
+        launch_matvec(t->st, ORDER_DECODE, EPI_STORE, W, qa.as<uint8_t>(), da.as<float>(), dy.as<float>(), 64, 0,
+                      nullptr, nullptr);
+        HIP_TRY(hipGetLastError());
+        HIP_TRY(hipMemcpyAsync(y, dy.p, (size_t)W.N * 4, hipMemcpyDeviceToHost, t->st));
+        HIP_TRY(hipStreamSynchronize(t->st));
+        return HG_OK;
+    });
+}
+
+int hg_q8_tensor_matmul(const hg_q8_tensor *t, const float *x, float *y, uint32_t tn) {
+    if (!t || !x || !y) return fail(HG_ERR_ARG, "NULL argument");
+    if (tn == 0) return HG_OK;
+    const Q8Mat &W = t->w.m;
+    return with_act(t, x, tn, [&](DevBuf &qa, DevBuf &da) -> int {
+        DevBuf dy;
+        int rc = dy.alloc((size_t)W.N * tn * 4);
+        if (rc) return rc;
+        for (uint32_t r = 0; r < tn; ++r)
+            launch_matvec(t->st, ORDER_PREFILL, EPI_STORE, W, qa.as<uint8_t>() + (size_t)r * W.nc * CHUNK_BYTES,
+                          da.as<float>() + (size_t)r * W.nc * 4, dy.as<float>() + (size_t)r * W.N, 64, 0, nullptr,
+                          nullptr);
+        HIP_TRY(hipGetLastError());
+        HIP_TRY(hipMemcpyAsync(y, dy.p, (size_t)W.N * tn * 4, hipMemcpyDeviceToHost, t->st));
+        HIP_TRY(hipStreamSynchronize(t->st));
+        return HG_OK;
+    });
+}
+
+int hg_q8_tensor_matvec_gather(const hg_q8_tensor *t, uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids,
+                               const float *x, float *y) {
+    if (!t || !ids || !x || !y) return fail(HG_ERR_ARG, "NULL argument");
+    const Q8Mat &W = t->w.m;
+    if (rows_per_mat == 0 || W.N % rows_per_mat) return fail(HG_ERR_ARG, "rows_per_mat does not divide the rows");
+    const uint32_t n_mat = W.N / rows_per_mat;
+    for (uint32_t i = 0; i < n_ids; ++i)
+        if (ids[i] >= n_mat) return fail(HG_ERR_ARG, "expert id " + std::to_string(ids[i]) + " out of range");
+    return with_act(t, x, 1, [&](DevBuf &qa, DevBuf &da) -> int {
+        DevBuf dy;
+        int rc = dy.alloc((size_t)rows_per_mat * n_ids * 4);
+        if (rc) return rc;
+        const size_t sc_elem = W.sc_f32 ? 4 : 2;
+        for (uint32_t i = 0; i < n_ids; ++i) {
+            Q8Mat v = W;
+            v.N = rows_per_mat;
+            v.qs = W.qs + (size_t)ids[i] * rows_per_mat * W.nc * CHUNK_BYTES;
+            v.sc = static_cast<const uint8_t *>(W.sc) + (size_t)ids[i] * rows_per_mat * W.nc * 4 * sc_elem;
+            launch_matvec(t->st, ORDER_DECODE, EPI_STORE, v, qa.as<uint8_t>(), da.as<float>(),
+                          dy.as<float>() + (size_t)i * rows_per_mat, 64, 0, nullptr, nullptr);
+        }
+        HIP_TRY(hipGetLastError());
+        HIP_TRY(hipMemcpyAsync(y, dy.p, (size_t)rows_per_mat * n_ids * 4, hipMemcpyDeviceToHost, t->st));
+        HIP_TRY(hipStreamSynchronize(t->st));
+        return HG_OK;
+    });
+}
+
+int hg_attention_decode(const float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
+                        float eps, float theta, uint32_t rope_len, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
+                        uint32_t pos, float *kc, float *vc, float *out, uint32_t flags) {
+    if (!q || !k || !v || !q_norm || !k_norm || !kc || !vc || !out) return fail(HG_ERR_ARG, "NULL argument");
+    if (hd != 32 && hd != 64 && hd != 128) return fail(HG_ERR_UNSUPPORTED, "head_dim not in {32, 64, 128}");
+    if (!n_kv || n_heads % n_kv || n_heads / n_kv > 8) return fail(HG_ERR_UNSUPPORTED, "unsupported head grouping");
+    if (pos >= rope_len) return fail(HG_ERR_ARG, "pos beyond the RoPE table");
+    int rc = check_device();
+    if (rc) return rc;
+    const bool exact = flags & HG_KV_EXACT;
+    const uint32_t qd = n_heads * hd, kvd = n_kv * hd, n = pos + 1, cap = n, S = std::max(64u, div_up(n, 256));
+    std::vector<float> qkv(qd + 2 * kvd);
+    memcpy(qkv.data(), q, qd * 4);
+    memcpy(qkv.data() + qd, k, kvd * 4);
+    memcpy(qkv.data() + qd + kvd, v, kvd * 4);
+    std::vector<float> kh((size_t)n_kv * cap * hd, 0.0f), vh(kh.size(), 0.0f);
+    for (uint32_t t = 0; t < pos; ++t)
+        for (uint32_t g = 0; g < n_kv; ++g) {
+            memcpy(&kh[((size_t)g * cap + t) * hd], kc + ((size_t)t * n_kv + g) * hd, hd * 4);
+            memcpy(&vh[((size_t)g * cap + t) * hd], vc + ((size_t)t * n_kv + g) * hd, hd * 4);
+        }
+    std::vector<float> cs, sn;
+    rope_table(hd, rope_len, theta, cs, sn);
+    StepParams hp{};
+    hp.pos = pos;
+    DevBuf dqkv, dqn, dkn, dcs, dsn, dk, dv, dp, dpart, dscr, dout, dq, dd;
+    if ((rc = dqkv.upload(qkv.data(), qkv.size() * 4)) || (rc = dqn.upload(q_norm, hd * 4)) ||
+        (rc = dkn.upload(k_norm, hd * 4)) || (rc = dcs.upload(cs.data(), cs.size() * 4)) ||
+        (rc = dsn.upload(sn.data(), sn.size() * 4)) || (rc = dk.upload(kh.data(), kh.size() * 4)) ||
+        (rc = dv.upload(vh.data(), vh.size() * 4)) || (rc = dp.upload(&hp, sizeof hp)) ||
+        (rc = dpart.alloc((size_t)n_heads * S * (hd + 2) * 4)) || (rc = dscr.alloc((size_t)n_heads * cap * 4)) ||
+        (rc = dout.alloc((size_t)qd * 4)) || (rc = dq.alloc((size_t)div_up(qd / QK, 4) * CHUNK_BYTES)) ||
+        (rc = dd.alloc((size_t)div_up(qd / QK, 4) * 16)))
+        return rc;
+    if (!launch_attn(nullptr, exact, hd, dqkv.as<float>(), dqn.as<float>(), dkn.as<float>(), eps, dcs.as<float>(),
+                     dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap, n_heads, n_kv, S,
+                     dpart.as<float>(), dscr.as<float>(), dout.as<float>(), dq.as<uint8_t>(), dd.as<float>()))
+        return fail(HG_ERR_UNSUPPORTED, "head_dim not supported");
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(out, dout.p, (size_t)qd * 4, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(kh.data(), dk.p, kh.size() * 4, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(vh.data(), dv.p, vh.size() * 4, hipMemcpyDeviceToHost));
+    for (uint32_t g = 0; g < n_kv; ++g) {
+        memcpy(kc + ((size_t)pos * n_kv + g) * hd, &kh[((size_t)g * cap + pos) * hd], hd * 4);
+        memcpy(vc + ((size_t)pos * n_kv + g) * hd, &vh[((size_t)g * cap + pos) * hd], hd * 4);
+    }
+    return HG_OK;
+}
+
+}  // extern "C"

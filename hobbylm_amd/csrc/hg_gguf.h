@@ -1,0 +1,78 @@
+// hg_gguf.h -- GGUF v3 reader, hobbylm config and the Q8 load path (host side).
+#pragma once
+#include <stdint.h>
+
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/hobby_gpu.h"
+
+namespace hg {
+
+// A parsed metadata value, typed as Gguf::open keeps it (gguf.rs:16-28, 109-163).
+struct Meta {
+    enum Kind { U32, I32, F32, U64, BOOL, STR, ARR_STR, ARR_I32, ARR_F32, OTHER } kind = OTHER;
+    uint64_t u = 0;
+    int32_t i = 0;
+    float f = 0.0f;
+    std::string s;
+};
+
+struct TensorInfo {
+    std::vector<uint64_t> ne;  // fastest-varying first (gguf.rs:32-34)
+    uint32_t type = 0;
+    uint64_t offset = 0;
+    uint64_t n_elems() const;
+};
+
+class Gguf {
+  public:
+    ~Gguf();
+    // Gguf::open (gguf.rs:166-212).  Returns HG_OK or a negative HG_ERR_* with `err` set.
+    int open(const char *path, std::string &err);
+    const TensorInfo *info(const std::string &name) const;
+    bool get_u32(const std::string &key, uint32_t &v) const;   // gguf.rs:272-279
+    bool get_f32(const std::string &key, float &v) const;      // gguf.rs:280-286
+    bool get_bool(const std::string &key, bool &v) const;      // gguf.rs:287-292
+    bool get_str(const std::string &key, std::string &v) const;
+    // Gguf::f32 (gguf.rs:215-235): an F32 tensor, any other type is an error.
+    int f32(const std::string &name, std::vector<float> &out, std::string &err) const;
+    // Raw bytes of a tensor of a supported ggml type (F32, F16, Q8_0), bounds-checked.
+    int raw(const std::string &name, const TensorInfo *&t, const uint8_t *&data, size_t &nbytes,
+            std::string &err) const;
+    // Gguf::load (gguf.rs:250-269) for F32, F16 and Q8_0: the tensor as f32.
+    int load(const std::string &name, std::vector<float> &out, std::string &err) const;
+
+  private:
+    const uint8_t *map_ = nullptr;
+    size_t size_ = 0;
+    size_t data_start_ = 0;
+    std::unordered_map<std::string, Meta> meta_;
+    std::unordered_map<std::string, TensorInfo> tensors_;
+};
+
+float half_to_f32(uint16_t h);  // gguf.rs:329-341
+
+// Config::from_gguf (config.rs:35-97)
+int config_from_gguf(const Gguf &g, hg_config &c, std::string &err);
+
+// A Q8_0 matrix after Q8Tensor::quantize (quant.rs:78-102), packed in the device row
+// layout of hg_common.h (lane-major 128-byte chunks, scales per row).
+struct PackedQ8 {
+    uint32_t N = 0, K = 0, nb = 0, nc = 0;
+    bool f32sc = false;
+    std::vector<uint8_t> qs;  // N * nc * 128
+    std::vector<uint8_t> sc;  // N * nc * 4 * (2 or 4)
+    uint64_t ref_bytes() const { return (uint64_t)N * K + (uint64_t)N * nb * 4; }  // Q8Tensor::bytes
+};
+
+// Requantize f32 rows (Q8Tensor::quantize) and pack them.
+void pack_q8_from_f32(const float *w, uint32_t N, uint32_t K, PackedQ8 &out);
+// dequant_q8_0 (gguf.rs:365-375) fused with Q8Tensor::quantize, block by block.
+void pack_q8_from_q8_0(const uint8_t *blocks, uint32_t N, uint32_t K, PackedQ8 &out);
+
+// Rope::new (ops.rs:139-152): cos/sin[max_pos][hd/2] from f64 angles.
+void rope_table(uint32_t head_dim, uint32_t max_pos, float theta, std::vector<float> &cs, std::vector<float> &sn);
+
+}  // namespace hg

@@ -1,0 +1,34 @@
+// hg_kernels.h -- host-side launchers of the gfx950 decode kernels (hg_kernels.hip).
+#pragma once
+#include "hg_common.h"
+
+namespace hg {
+
+void launch_embed(hipStream_t st, const float *emb, uint32_t d, const StepParams *p, float *x);
+void launch_load_row(hipStream_t st, const float *inputs, uint32_t d, const StepParams *p, float *x);
+void launch_advance(hipStream_t st, StepParams *p);
+void launch_rmsnorm_quant(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,
+                          float *h, uint8_t *q, float *dq);
+void launch_quant_vec(hipStream_t st, const float *x, uint32_t n, uint8_t *q, float *dq);
+uint32_t matvec_blocks(uint32_t N, uint32_t threads);
+void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uint8_t *q, const float *dq, float *y,
+                   uint32_t threads, uint32_t valid, float *pv, uint32_t *pi);
+void launch_argmax_final(hipStream_t st, const float *pv, const uint32_t *pi, uint32_t n, StepParams *p,
+                         uint32_t *out_ids);
+size_t attn_fast_shm(uint32_t hd, uint32_t rep, uint32_t cap, uint32_t S);
+bool launch_attn(hipStream_t st, bool exact, uint32_t hd, const float *qkv, const float *qn, const float *kn,
+                 float eps, const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
+                 uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,
+                 float *o_out, uint8_t *q_out, float *d_out);
+void launch_ffn_router(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,
+                       const float *Wr, const float *bias, uint32_t E, uint32_t top_k, int gating_sigmoid,
+                       int weights_norm, float weights_scale, uint8_t *q, float *dq, uint32_t *topk_idx,
+                       float *topk_w, uint32_t *order, uint32_t *rec_idx, float *rec_w);
+void launch_ffn_gateup(hipStream_t st, int order, const Q8Mat &Wg, const Q8Mat &Wu, const Q8Mat &Sg,
+                       const Q8Mat &Su, const uint32_t *topk_idx, uint32_t top_k, uint32_t n_slots, uint32_t f,
+                       const uint8_t *q, const float *dq, float *a);
+void launch_ffn_down(hipStream_t st, int order, const Q8Mat &Wd, const Q8Mat &Sd, const uint32_t *topk_idx,
+                     const float *topk_w, const uint32_t *ord, uint32_t top_k, uint32_t n_slots, int dense,
+                     uint32_t d, uint32_t f, const float *a, float *x);
+
+}  // namespace hg

@@ -1,0 +1,991 @@
+// hg_kernels.hip -- gfx950 kernels of the hobbylm single-sequence decode step.
+//
+// Every kernel restates one piece of hobby-rs's arithmetic (file:line given at each) in the
+// same floating-point operation order, except where a comment says "tree": those
+// reductions (RMSNorm sum of squares and attention softmax / P.V in the fast path) are
+// reassociated.  The build uses -ffp-contract=off; each fmaf() stands where the reference
+// issues an FMA.  Wavefronts are 64 wide; a Q8 row is owned by 8 adjacent lanes (see
+// hg_common.h for the device row layout).
+#include "hg_common.h"
+#include "hg_expf.h"
+#include "hg_kernels.h"
+
+namespace hg {
+
+// ------------------------------------------------------------------ small helpers
+__device__ inline float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+__device__ inline int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
+
+__device__ inline int sdot4(int a, int b) { return __builtin_amdgcn_sdot4(a, b, 0, false); }
+
+// One 32-block of activation quantization (quant.rs:114-122), lanes j = 0..7 of 8 adjacent
+// threads each holding v[0..3] = x[32b + 4j + 0..3].  d = amax/127, id = 1/d (0 if d == 0),
+// q = clamp(round_half_away(x*id), +-127).  Writes q into the lane-major chunk layout.
+__device__ inline void quant_block_lane(const float v[4], int j, uint32_t b, uint8_t *q, float *d) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, shfl_xor(amax, 1));
+    amax = fmaxf(amax, shfl_xor(amax, 2));
+    amax = fmaxf(amax, shfl_xor(amax, 4));
+    const float dd = amax / 127.0f;
+    const float id = dd > 0.0f ? 1.0f / dd : 0.0f;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        float r = roundf(v[m] * id);
+        if (r != r) r = 0.0f;
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        packed |= (uint32_t)(uint8_t)(int8_t)(int)r << (8 * m);
+    }
+    *reinterpret_cast<uint32_t *>(q + (b / 4) * CHUNK_BYTES + j * 16 + (b % 4) * 4) = packed;
+    if (j == 0) d[b] = dd;
+}
+
+// Zero the padding blocks of a partial last chunk so padded lanes contribute 0.
+__device__ inline void zero_pad(uint32_t nb, uint32_t nc, uint8_t *q, float *d, int tid, int nthr) {
+    for (uint32_t b = nb + tid; b < nc * 4; b += nthr) {
+        for (int j = 0; j < 8; ++j)
+            *reinterpret_cast<uint32_t *>(q + (b / 4) * CHUNK_BYTES + j * 16 + (b % 4) * 4) = 0;
+        d[b] = 0.0f;
+    }
+}
+
+// Stage a quantized activation (nc chunks + scales) from global into LDS.
+__device__ inline void stage_act(const uint8_t *gq, const float *gd, uint32_t nc, uint8_t *sq,
+                                 float *sd, int tid, int nthr) {
+    const int4 *src = reinterpret_cast<const int4 *>(gq);
+    int4 *dst = reinterpret_cast<int4 *>(sq);
+    for (uint32_t i = tid; i < nc * 8; i += nthr) dst[i] = src[i];
+    for (uint32_t i = tid; i < nc * 4; i += nthr) sd[i] = gd[i];
+}
+
+// Row dot of the Q8 matvec, lane j of the 8 lanes owning the row.
+//   ORDER_DECODE: qrow_dot_avx2 (quant.rs:44-67).  Lane j keeps accumulator lane j:
+//     acc_j = fma(sw[b]*dx[b], (float)sum_{m<4} w[32b+4j+m]*x[32b+4j+m], acc_j) over b,
+//     then ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) (the hsum of quant.rs:61-65) by xor 4/2/1.
+//   ORDER_PREFILL: Q8Tensor::matmul (quant.rs:171-184).  isum over the whole block (exact),
+//     acc += (sw[b]*dx[b]) * isum in block order, one accumulator.
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// The four scales of chunk c of a row (f16 or f32 storage).
+__device__ inline v4f load_scales4(const void *srow, uint32_t c, uint32_t f32) {
+    if (f32) return __builtin_nontemporal_load(reinterpret_cast<const v4f *>(srow) + c);
+    const v2u h = __builtin_nontemporal_load(reinterpret_cast<const v2u *>(srow) + c);
+    v4f r;
+    r.x = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.x & 0xffffu));
+    r.y = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.x >> 16));
+    r.z = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.y & 0xffffu));
+    r.w = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.y >> 16));
+    return r;
+}
+
+template <int ORDER>
+__device__ inline float q8_row_dot(const uint8_t *__restrict__ wrow, const void *__restrict__ srow,
+                                   uint32_t sc_f32, const uint8_t *qx, const float *dx, uint32_t nb,
+                                   uint32_t nc, int j) {
+    float acc = 0.0f;
+    constexpr uint32_t U = 8;
+    for (uint32_t c0 = 0; c0 < nc; c0 += U) {
+        v4i w[U];
+        v4f sw[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u)
+            if (c0 + u < nc) {
+                w[u] = __builtin_nontemporal_load(
+                    reinterpret_cast<const v4i *>(wrow + (c0 + u) * CHUNK_BYTES + j * 16));
+                sw[u] = load_scales4(srow, c0 + u, sc_f32);
+            }
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t c = c0 + u;
+            if (c >= nc) break;
+            const v4i x = *reinterpret_cast<const v4i *>(qx + c * CHUNK_BYTES + j * 16);
+            const v4f dxc = *reinterpret_cast<const v4f *>(dx + c * 4);
+            const int p[4] = {sdot4(w[u].x, x.x), sdot4(w[u].y, x.y), sdot4(w[u].z, x.z),
+                              sdot4(w[u].w, x.w)};
+            const float sv[4] = {sw[u].x, sw[u].y, sw[u].z, sw[u].w};
+            const float dv[4] = {dxc.x, dxc.y, dxc.z, dxc.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t b = c * 4 + t;
+                const float d = sv[t] * dv[t];
+                if (ORDER == ORDER_DECODE) {
+                    if (b < nb) acc = fmaf(d, (float)p[t], acc);
+                } else {
+                    int is = p[t];
+                    is += shfl_xor_i(is, 1);
+                    is += shfl_xor_i(is, 2);
+                    is += shfl_xor_i(is, 4);
+                    if (b < nb) acc = acc + d * (float)is;
+                }
+            }
+        }
+    }
+    if (ORDER == ORDER_DECODE) {
+        acc = acc + shfl_xor(acc, 4);
+        acc = acc + shfl_xor(acc, 2);
+        acc = acc + shfl_xor(acc, 1);
+    }
+    return acc;
+}
+
+__device__ inline const uint8_t *row_qs(const Q8Mat &W, uint32_t r) {
+    return W.qs + (size_t)r * W.nc * CHUNK_BYTES;
+}
+__device__ inline const void *row_sc(const Q8Mat &W, uint32_t r) {
+    return W.sc_f32 ? (const void *)(reinterpret_cast<const float *>(W.sc) + (size_t)r * W.nc * 4)
+                    : (const void *)(reinterpret_cast<const _Float16 *>(W.sc) + (size_t)r * W.nc * 4);
+}
+
+// ------------------------------------------------------------------ embedding
+// Model::forward (model.rs:154): x = token_embd[token] (F32 table, dequantized at load).
+__global__ void k_embed(const float *__restrict__ emb, uint32_t d, const StepParams *p, float *x) {
+    if (!p->embed) return;
+    const float *row = emb + (size_t)p->token * d;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x) x[i] = row[i];
+}
+
+// Prefill: x = inputs[pos - base].
+__global__ void k_load_row(const float *__restrict__ inputs, uint32_t d, const StepParams *p, float *x) {
+    const float *row = inputs + (size_t)(p->pos - p->base) * d;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x) x[i] = row[i];
+}
+
+__global__ void k_advance(StepParams *p) {
+    if (threadIdx.x == 0) p->pos += 1;
+}
+
+// ------------------------------------------------------------------ RMSNorm + quantize
+// rmsnorm (ops.rs:85-96): ss = sum x^2; scale = 1/sqrt(ss/n + eps); h = x*scale*w; then
+// the activation quantization of the consuming matvec (quant.rs:111-123).
+// EXACT: ss accumulated sequentially as in the reference; otherwise a tree.
+template <bool EXACT>
+__global__ __launch_bounds__(256) void k_rmsnorm_quant(const float *__restrict__ x, const float *__restrict__ w,
+                                                       float eps, uint32_t d, float *h_out, uint8_t *q_out,
+                                                       float *d_out) {
+    extern __shared__ float xs[];
+    __shared__ float red[4];
+    __shared__ float s_scale;
+    const int tid = threadIdx.x;
+    for (uint32_t i = tid; i < d; i += 256) xs[i] = x[i];
+    __syncthreads();
+    if (EXACT) {
+        if (tid == 0) {
+            float ss = 0.0f;
+            for (uint32_t i = 0; i < d; ++i) ss = ss + xs[i] * xs[i];
+            s_scale = 1.0f / sqrtf(ss / (float)d + eps);
+        }
+    } else {
+        float ss = 0.0f;
+        for (uint32_t i = tid; i < d; i += 256) ss += xs[i] * xs[i];
+        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        if (tid == 0) s_scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)d + eps);
+    }
+    __syncthreads();
+    const float scale = s_scale;
+    const uint32_t nb = d / QK, nc = div_up(nb, 4);
+    const int j = tid & 7;
+    for (uint32_t b0 = 0; b0 < nb; b0 += 32) {
+        const uint32_t b = b0 + (tid >> 3);
+        if (b < nb) {
+            float v[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const uint32_t i = b * QK + j * 4 + m;
+                v[m] = xs[i] * scale * w[i];
+                if (h_out) h_out[i] = v[m];
+            }
+            quant_block_lane(v, j, b, q_out, d_out);
+        }
+    }
+    zero_pad(nb, nc, q_out, d_out, tid, 256);
+}
+
+// Quantize a plain f32 vector (the activation of Q8Tensor::matvec, quant.rs:111-123).
+__global__ __launch_bounds__(256) void k_quant_vec(const float *__restrict__ x, uint32_t n, uint8_t *q_out,
+                                                   float *d_out) {
+    const int tid = threadIdx.x, j = tid & 7;
+    const uint32_t nb = n / QK, nc = div_up(nb, 4);
+    for (uint32_t b0 = blockIdx.x * 32; b0 < nb; b0 += gridDim.x * 32) {
+        const uint32_t b = b0 + (tid >> 3);
+        if (b < nb) {
+            float v[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) v[m] = x[b * QK + j * 4 + m];
+            quant_block_lane(v, j, b, q_out, d_out);
+        }
+    }
+    if (blockIdx.x == 0) zero_pad(nb, nc, q_out, d_out, tid, 256);
+}
+
+// ------------------------------------------------------------------ Q8 matvec
+// Q8Tensor::matvec / matmul row loop (quant.rs:125-135, 168-185) over a pre-quantized
+// activation.  8 lanes per row; blockDim.x/8 rows per workgroup.
+//   EPI_STORE:  y[r] = v
+//   EPI_RESID:  y[r] = y[r] + v     (x[i] += attn[i], model.rs:169-171)
+//   EPI_LOGITS: y[r] = v, plus a per-workgroup (max, first index) over rows < valid for
+//               the greedy argmax (sample.rs:53-63 on logits masked per lib.rs:132-134).
+template <int ORDER, int EPI>
+__global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restrict__ gq,
+                                                const float *__restrict__ gd, float *y, uint32_t valid,
+                                                float *part_v, uint32_t *part_i) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint8_t *sq = smem;
+    float *sd = reinterpret_cast<float *>(smem + W.nc * CHUNK_BYTES);
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    stage_act(gq, gd, W.nc, sq, sd, tid, nthr);
+    __syncthreads();
+    const uint32_t row = blockIdx.x * (nthr >> 3) + (tid >> 3);
+    const int j = tid & 7;
+    float v = 0.0f;
+    if (row < W.N) {
+        v = q8_row_dot<ORDER>(row_qs(W, row), row_sc(W, row), W.sc_f32, sq, sd, W.nb, W.nc, j);
+        if (j == 0) {
+            if (EPI == EPI_RESID) y[row] = y[row] + v;
+            else y[row] = v;
+        }
+    }
+    if (EPI == EPI_LOGITS) {
+        __shared__ float bv[32];
+        __shared__ uint32_t bi[32];
+        float mv = -__builtin_huge_valf();
+        uint32_t mi = 0xffffffffu;
+        if (j == 0 && row < W.N && row < valid && v > mv) { mv = v; mi = row; }
+        // wave reduce: larger value wins, equal values keep the lower row
+        for (int m = 8; m < 64; m <<= 1) {
+            const float ov = shfl_xor(mv, m);
+            const uint32_t oi = (uint32_t)shfl_xor_i((int)mi, m);
+            if (ov > mv || (ov == mv && oi < mi)) { mv = ov; mi = oi; }
+        }
+        if ((tid & 63) == 0) { bv[tid >> 6] = mv; bi[tid >> 6] = mi; }
+        __syncthreads();
+        if (tid == 0) {
+            for (int wv = 1; wv < (nthr >> 6); ++wv)
+                if (bv[wv] > mv || (bv[wv] == mv && bi[wv] < mi)) { mv = bv[wv]; mi = bi[wv]; }
+            part_v[blockIdx.x] = mv;
+            part_i[blockIdx.x] = mi;
+        }
+    }
+}
+
+// Final greedy argmax over the per-workgroup partials; writes out_ids[step] and, in
+// feedback mode, chains the next step (token = next, pos += 1).
+__global__ __launch_bounds__(1024) void k_argmax_final(const float *__restrict__ pv, const uint32_t *__restrict__ pi,
+                                                       uint32_t n, StepParams *p, uint32_t *out_ids) {
+    __shared__ float bv[16];
+    __shared__ uint32_t bi[16];
+    const int tid = threadIdx.x;
+    float mv = -__builtin_huge_valf();
+    uint32_t mi = 0xffffffffu;
+    for (uint32_t i = tid; i < n; i += 1024) {
+        const float v = pv[i];
+        const uint32_t ix = pi[i];
+        if (ix != 0xffffffffu && (v > mv || (v == mv && ix < mi))) { mv = v; mi = ix; }
+    }
+    for (int m = 1; m < 64; m <<= 1) {
+        const float ov = shfl_xor(mv, m);
+        const uint32_t oi = (uint32_t)shfl_xor_i((int)mi, m);
+        if (ov > mv || (ov == mv && oi < mi)) { mv = ov; mi = oi; }
+    }
+    if ((tid & 63) == 0) { bv[tid >> 6] = mv; bi[tid >> 6] = mi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int wv = 1; wv < 16; ++wv)
+            if (bv[wv] > mv || (bv[wv] == mv && bi[wv] < mi)) { mv = bv[wv]; mi = bi[wv]; }
+        // sample::argmax returns 0 when no logit exceeds -inf
+        const uint32_t next = (mi == 0xffffffffu) ? 0u : mi;
+        out_ids[p->step] = next;
+        p->step += 1;
+        if (p->feedback) {
+            p->token = next;
+            p->pos += 1;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ QK-norm + RoPE
+// norm_head (model.rs:753-763) then Rope::apply (ops.rs:155-166) of one head vector held in
+// LDS `u` (hd floats); result in `o`.  The sum of squares is sequential (as the reference);
+// called by one wave, lane 0 doing the sum.
+__device__ inline void norm_rope_head(const float *u, float *o, const float *__restrict__ w, float eps, uint32_t hd,
+                                      const float *__restrict__ cs, const float *__restrict__ sn, uint32_t pos,
+                                      float *tmp, int lane) {
+    float scale = 0.0f;
+    if (lane == 0) {
+        float ss = 0.0f;
+        for (uint32_t i = 0; i < hd; ++i) ss = ss + u[i] * u[i];
+        scale = 1.0f / sqrtf(ss / (float)hd + eps);
+    }
+    scale = __shfl(scale, 0, 64);
+    for (uint32_t i = lane; i < hd; i += 64) tmp[i] = u[i] * scale * w[i];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    const uint32_t half = hd / 2;
+    for (uint32_t i = lane; i < half; i += 64) {
+        const float c = cs[(size_t)pos * half + i], s = sn[(size_t)pos * half + i];
+        const float x1 = tmp[i], x2 = tmp[half + i];
+        o[i] = x1 * c - x2 * s;
+        o[half + i] = x2 * c + x1 * s;
+    }
+}
+
+// ------------------------------------------------------------------ attention (fast)
+// Longest split of a cache of `cap` positions cut in S parts, rounded to whole float4s.
+__host__ __device__ inline uint32_t attn_maxchunk(uint32_t cap, uint32_t S) { return div_up(div_up(cap, S), 4) * 4; }
+
+// Decode attention of model.rs:212-233, split over the context (flash-decoding): workgroup
+// (g, s) handles kv head g and positions [t0, t1) of split s for the rep = n_heads/n_kv query
+// heads of the group, and writes an unnormalised partial (max, sum, o[hd]) per head.  Every
+// workgroup redoes the QK-norm + RoPE of its q heads and of k (reference order, exact);
+// the split holding `pos` appends k and v to the cache (model.rs:210-211).  Softmax and
+// P.V are reduced as trees across lanes and splits.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_fast(const float *__restrict__ qkv, const float *__restrict__ qn,
+                                                   const float *__restrict__ kn, float eps,
+                                                   const float *__restrict__ cs, const float *__restrict__ sn,
+                                                   const StepParams *p, float *kc, float *vc, uint32_t cap,
+                                                   uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part) {
+    constexpr int MAXREP = 8;
+    constexpr int TPT = HD / 4;       // threads per token (one float4 each)
+    constexpr int TOK = 256 / TPT;    // tokens per pass
+    extern __shared__ __align__(16) float sm[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t g = blockIdx.x, s = blockIdx.y;
+    const uint32_t rep = n_heads / n_kv;
+    const uint32_t pos = p->pos, n = pos + 1;
+    const uint32_t chunk = div_up(n, S);
+    const uint32_t t0 = s * chunk, t1 = min(n, t0 + chunk);
+    const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
+    float *raw = sm;                         // (rep+2)*HD : q heads, k, v as produced
+    float *rot = raw + (rep + 2) * HD;       // (rep+1)*HD : normalised + rotated q heads, k
+    float *tmp = rot + (rep + 1) * HD;       // 4*HD scratch (one per wave)
+    float *sc = tmp + 4 * HD;                // rep * chunk scores
+    const uint32_t maxchunk = attn_maxchunk(cap, S);
+    float *red = sc + rep * maxchunk;        // TOK * rep * HD partial P.V sums
+    float *stat = red + TOK * rep * HD;      // 2*rep (max, sum)
+    for (uint32_t i = tid; i < rep * HD; i += 256) raw[i] = qkv[g * rep * HD + i];
+    for (uint32_t i = tid; i < HD; i += 256) {
+        raw[rep * HD + i] = qkv[qd + g * HD + i];
+        raw[(rep + 1) * HD + i] = qkv[qd + kvd + g * HD + i];
+    }
+    __syncthreads();
+    for (uint32_t vi = wave; vi <= rep; vi += 4)
+        norm_rope_head(raw + vi * HD, rot + vi * HD, vi < rep ? qn : kn, eps, HD, cs, sn, pos, tmp + wave * HD, lane);
+    __syncthreads();
+    const float *krot = rot + rep * HD;
+    const float *vnew = raw + (rep + 1) * HD;
+    float *kcg = kc + (size_t)g * cap * HD;
+    float *vcg = vc + (size_t)g * cap * HD;
+    if (t0 <= pos && pos < t1) {
+        for (uint32_t i = tid; i < HD; i += 256) {
+            kcg[(size_t)pos * HD + i] = krot[i];
+            vcg[(size_t)pos * HD + i] = vnew[i];
+        }
+    }
+    float *pout = part + (size_t)(g * rep) * S * (HD + 2);
+    if (t0 >= t1) {
+        for (uint32_t r = 0; r < rep; ++r) {
+            float *pr = pout + ((size_t)r * S + s) * (HD + 2);
+            for (uint32_t i = tid; i < HD + 2; i += 256) pr[i] = (i == 0) ? -__builtin_huge_valf() : 0.0f;
+        }
+        return;
+    }
+    const uint32_t len = t1 - t0;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int tl = tid % TPT, tg = tid / TPT;
+    // scores
+    for (uint32_t tt = tg; tt < len; tt += TOK) {
+        const uint32_t t = t0 + tt;
+        const float4 k4 = (t == pos) ? *reinterpret_cast<const float4 *>(krot + tl * 4)
+                                     : *reinterpret_cast<const float4 *>(kcg + (size_t)t * HD + tl * 4);
+        float acc[MAXREP];
+#pragma unroll
+        for (int r = 0; r < MAXREP; ++r) {
+            if (r < (int)rep) {
+                const float4 q4 = *reinterpret_cast<const float4 *>(rot + r * HD + tl * 4);
+                acc[r] = q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < MAXREP; ++r) {
+            if (r < (int)rep) {
+                float a = acc[r];
+                for (int m = 1; m < TPT; m <<= 1) a += shfl_xor(a, m);
+                if (tl == 0) sc[r * maxchunk + tt] = a * scale;
+            }
+        }
+    }
+    __syncthreads();
+    // softmax statistics per head: one wave per head
+    for (uint32_t r = wave; r < rep; r += 4) {
+        float m = -__builtin_huge_valf();
+        for (uint32_t tt = lane; tt < len; tt += 64) m = fmaxf(m, sc[r * maxchunk + tt]);
+        for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
+        float l = 0.0f;
+        for (uint32_t tt = lane; tt < len; tt += 64) {
+            const float e = __expf(sc[r * maxchunk + tt] - m);
+            sc[r * maxchunk + tt] = e;
+            l += e;
+        }
+        for (int k = 32; k >= 1; k >>= 1) l += shfl_xor(l, k);
+        if (lane == 0) { stat[2 * r] = m; stat[2 * r + 1] = l; }
+    }
+    __syncthreads();
+    // P.V
+    float4 o[MAXREP];
+#pragma unroll
+    for (int r = 0; r < MAXREP; ++r) o[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t tt = tg; tt < len; tt += TOK) {
+        const uint32_t t = t0 + tt;
+        const float4 v4 = (t == pos) ? *reinterpret_cast<const float4 *>(vnew + tl * 4)
+                                     : *reinterpret_cast<const float4 *>(vcg + (size_t)t * HD + tl * 4);
+#pragma unroll
+        for (int r = 0; r < MAXREP; ++r) {
+            if (r < (int)rep) {
+                const float pr = sc[r * maxchunk + tt];
+                o[r].x += pr * v4.x; o[r].y += pr * v4.y; o[r].z += pr * v4.z; o[r].w += pr * v4.w;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < MAXREP; ++r)
+        if (r < (int)rep) *reinterpret_cast<float4 *>(red + ((size_t)tg * rep + r) * HD + tl * 4) = o[r];
+    __syncthreads();
+    for (uint32_t i = tid; i < rep * HD; i += 256) {
+        float a = 0.0f;
+        for (int q = 0; q < TOK; ++q) a += red[(size_t)q * rep * HD + i];
+        const uint32_t r = i / HD, di = i % HD;
+        float *pr = pout + ((size_t)r * S + s) * (HD + 2);
+        pr[2 + di] = a;
+        if (di == 0) { pr[0] = stat[2 * r]; pr[1] = stat[2 * r + 1]; }
+    }
+}
+
+// Merge the split partials of every head into o = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M),
+// write o (optional) and its quantization for the attn_output matvec (quant.rs:111-123).
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part, uint32_t n_heads, uint32_t S,
+                                                      float *o_out, uint8_t *q_out, float *d_out) {
+    const int tid = threadIdx.x;
+    const uint32_t total4 = n_heads * HD / 4;
+    const uint32_t nb = n_heads * HD / QK, nc = div_up(nb, 4);
+    for (uint32_t base = 0; base < total4; base += 256) {
+        const uint32_t t = base + tid;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (t < total4) {
+            const uint32_t h = (t * 4) / HD, di = (t * 4) % HD;
+            const float *ph = part + (size_t)h * S * (HD + 2);
+            float M = -__builtin_huge_valf();
+            for (uint32_t s = 0; s < S; ++s) M = fmaxf(M, ph[(size_t)s * (HD + 2)]);
+            float L = 0.0f;
+            for (uint32_t s = 0; s < S; ++s) {
+                const float *pr = ph + (size_t)s * (HD + 2);
+                if (pr[1] == 0.0f) continue;
+                const float f = __expf(pr[0] - M);
+                L += pr[1] * f;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) v[m] += pr[2 + di + m] * f;
+            }
+            const float inv = 1.0f / L;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) v[m] *= inv;
+            if (o_out)
+#pragma unroll
+                for (int m = 0; m < 4; ++m) o_out[t * 4 + m] = v[m];
+        }
+        const uint32_t b = t / 8;
+        if (b < nb) quant_block_lane(v, t & 7, b, q_out, d_out);
+    }
+    zero_pad(nb, nc, q_out, d_out, tid, 256);
+}
+
+// ------------------------------------------------------------------ attention (exact)
+// ops::dot (ops.rs:7-36) of two hd-vectors in the reference order: four 8-lane FMA
+// accumulators over 32-wide steps, 8-wide tail on accumulator 0, then
+// ((a0+a1)+(a2+a3)) reduced as ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)), then a scalar tail.
+__device__ inline float dot_wide_serial(const float *a, const float *b, uint32_t n) {
+    float acc[4][8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) acc[r][l] = 0.0f;
+    uint32_t i = 0;
+    const uint32_t main = n - n % 32;
+    for (; i < main; i += 32)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int l = 0; l < 8; ++l) acc[r][l] = fmaf(a[i + 8 * r + l], b[i + 8 * r + l], acc[r][l]);
+    for (; i + 8 <= n; i += 8)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) acc[0][l] = fmaf(a[i + l], b[i + l], acc[0][l]);
+    float v[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) v[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+    float s = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+    for (; i < n; ++i) s = s + a[i] * b[i];
+    return s;
+}
+
+// Reference-order attention of one query head (model.rs:218-233, ops.rs:112-128): scores
+// in parallel, softmax with glibc-exact exp and a sequential sum, o accumulated
+// sequentially over positions, then the quantization of o for attn_output.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_exact(const float *__restrict__ qkv, const float *__restrict__ qn,
+                                                    const float *__restrict__ kn, float eps,
+                                                    const float *__restrict__ cs, const float *__restrict__ sn,
+                                                    const StepParams *p, float *kc, float *vc, uint32_t cap,
+                                                    uint32_t n_heads, uint32_t n_kv, float *scratch,
+                                                    float *o_out, uint8_t *q_out, float *d_out) {
+    constexpr uint32_t CH = 2048;
+    __shared__ __align__(16) float raw[3 * HD];
+    __shared__ __align__(16) float rot[2 * HD];
+    __shared__ float tmp[2 * HD];
+    __shared__ float buf[CH];
+    __shared__ float red[4];
+    __shared__ float s_m, s_sum;
+    __shared__ __align__(16) float ov[HD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t hq = blockIdx.x, rep = n_heads / n_kv, g = hq / rep;
+    const uint32_t pos = p->pos, n = pos + 1;
+    const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
+    for (uint32_t i = tid; i < HD; i += 256) {
+        raw[i] = qkv[hq * HD + i];
+        raw[HD + i] = qkv[qd + g * HD + i];
+        raw[2 * HD + i] = qkv[qd + kvd + g * HD + i];
+    }
+    __syncthreads();
+    if (wave < 2) norm_rope_head(raw + wave * HD, rot + wave * HD, wave == 0 ? qn : kn, eps, HD, cs, sn, pos, tmp + wave * HD, lane);
+    __syncthreads();
+    const float *q = rot, *knew = rot + HD, *vnew = raw + 2 * HD;
+    float *kcg = kc + (size_t)g * cap * HD;
+    float *vcg = vc + (size_t)g * cap * HD;
+    if (hq % rep == 0)
+        for (uint32_t i = tid; i < HD; i += 256) {
+            kcg[(size_t)pos * HD + i] = knew[i];
+            vcg[(size_t)pos * HD + i] = vnew[i];
+        }
+    float *sc = scratch + (size_t)hq * cap;
+    const float scale = 1.0f / sqrtf((float)HD);
+    float m = -__builtin_huge_valf();
+    for (uint32_t t = tid; t < n; t += 256) {
+        const float *kt = (t == pos) ? knew : kcg + (size_t)t * HD;
+        const float v = dot_wide_serial(q, kt, HD) * scale;
+        sc[t] = v;
+        m = fmaxf(m, v);
+    }
+    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    if (tid == 0) s_m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    m = s_m;
+    for (uint32_t t = tid; t < n; t += 256) sc[t] = hg_expf(sc[t] - m);
+    __syncthreads();
+    // sum = e_0 + e_1 + ... in order (ops.rs:120-123), staged through LDS
+    float sum = 0.0f;
+    for (uint32_t c0 = 0; c0 < n; c0 += CH) {
+        const uint32_t cl = min(CH, n - c0);
+        for (uint32_t i = tid; i < cl; i += 256) buf[i] = sc[c0 + i];
+        __syncthreads();
+        if (tid == 0)
+            for (uint32_t i = 0; i < cl; ++i) sum = sum + buf[i];
+        __syncthreads();
+    }
+    if (tid == 0) s_sum = sum;
+    __syncthreads();
+    const float inv = 1.0f / s_sum;
+    for (uint32_t t = tid; t < n; t += 256) sc[t] = sc[t] * inv;
+    __syncthreads();
+    // o[di] += p_t * v_t[di] over t in order (model.rs:227-232)
+    float o = 0.0f;
+    for (uint32_t c0 = 0; c0 < n; c0 += CH) {
+        const uint32_t cl = min(CH, n - c0);
+        for (uint32_t i = tid; i < cl; i += 256) buf[i] = sc[c0 + i];
+        __syncthreads();
+        if (tid < (int)HD)
+            for (uint32_t i = 0; i < cl; ++i) {
+                const uint32_t t = c0 + i;
+                const float vt = (t == pos) ? vnew[tid] : vcg[(size_t)t * HD + tid];
+                o = o + buf[i] * vt;
+            }
+        __syncthreads();
+    }
+    if (tid < (int)HD) {
+        ov[tid] = o;
+        if (o_out) o_out[hq * HD + tid] = o;
+    }
+    __syncthreads();
+    const uint32_t nbh = HD / QK;
+    if ((uint32_t)tid < nbh * 8) {
+        const uint32_t bl = tid >> 3;
+        const int j = tid & 7;
+        float v[4];
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) v[mm] = ov[bl * QK + j * 4 + mm];
+        quant_block_lane(v, j, hq * nbh + bl, q_out, d_out);
+    }
+    if (hq == 0) {
+        const uint32_t nb = n_heads * HD / QK;
+        zero_pad(nb, div_up(nb, 4), q_out, d_out, tid, 256);
+    }
+}
+
+// ------------------------------------------------------------------ MoE router
+// ffn_norm RMSNorm + quantization of h, then the F32 router of Model::ffn (model.rs:270-293):
+// logits = W_r h with ops::dot's order (32 lanes per expert row: lane 8a+l is accumulator a,
+// lane l), sigmoid (or softmax) gate, sel = score + bias, descending rank (equal keys:
+// lower expert first), top-k in rank order, optional renormalisation, x weights_scale.
+// One workgroup of 1024 threads.
+template <bool EXACT>
+__global__ __launch_bounds__(1024) void k_ffn_router(const float *__restrict__ x, const float *__restrict__ w,
+                                                     float eps, uint32_t d, const float *__restrict__ Wr,
+                                                     const float *__restrict__ bias, uint32_t E, uint32_t top_k,
+                                                     int gating_sigmoid, int weights_norm, float weights_scale,
+                                                     uint8_t *q_out, float *d_out, uint32_t *topk_idx,
+                                                     float *topk_w, uint32_t *order, uint32_t *rec_idx,
+                                                     float *rec_w) {
+    extern __shared__ float hs[];  // d floats
+    __shared__ float red[16];
+    __shared__ float s_scale;
+    __shared__ float lg[256], scr[256], sel[256];
+    __shared__ uint32_t tk[64];
+    __shared__ float tw[64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (uint32_t i = tid; i < d; i += 1024) hs[i] = x[i];
+    __syncthreads();
+    if (EXACT) {
+        if (tid == 0) {
+            float ss = 0.0f;
+            for (uint32_t i = 0; i < d; ++i) ss = ss + hs[i] * hs[i];
+            s_scale = 1.0f / sqrtf(ss / (float)d + eps);
+        }
+    } else {
+        float ss = 0.0f;
+        for (uint32_t i = tid; i < d; i += 1024) ss += hs[i] * hs[i];
+        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        if (tid == 0) {
+            float t = 0.0f;
+            for (int i = 0; i < 16; ++i) t += red[i];
+            s_scale = 1.0f / sqrtf(t / (float)d + eps);
+        }
+    }
+    __syncthreads();
+    const float scale = s_scale;
+    for (uint32_t i = tid; i < d; i += 1024) hs[i] = hs[i] * scale * w[i];
+    __syncthreads();
+    {
+        const uint32_t nb = d / QK, nc = div_up(nb, 4);
+        const int j = tid & 7;
+        for (uint32_t b0 = 0; b0 < nb; b0 += 128) {
+            const uint32_t b = b0 + (tid >> 3);
+            if (b < nb) {
+                float v[4];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) v[m] = hs[b * QK + j * 4 + m];
+                quant_block_lane(v, j, b, q_out, d_out);
+            }
+        }
+        zero_pad(nb, nc, q_out, d_out, tid, 1024);
+    }
+    // router logits, 32 lanes per expert
+    const int grp = tid >> 5, l32 = tid & 31;
+    const uint32_t main = d - d % 32;
+    for (uint32_t e = grp; e < E; e += 32) {
+        const float *row = Wr + (size_t)e * d;
+        float acc = 0.0f;
+        uint32_t i = 0;
+        for (; i < main; i += 32) acc = fmaf(row[i + l32], hs[i + l32], acc);
+        for (; i + 8 <= d; i += 8)
+            if (l32 < 8) acc = fmaf(row[i + l32], hs[i + l32], acc);
+        acc = acc + shfl_xor(acc, 8);
+        acc = acc + shfl_xor(acc, 16);
+        acc = acc + shfl_xor(acc, 4);
+        acc = acc + shfl_xor(acc, 2);
+        acc = acc + shfl_xor(acc, 1);
+        if (l32 == 0) {
+            for (; i < d; ++i) acc = acc + row[i] * hs[i];
+            lg[e] = acc;
+        }
+    }
+    __syncthreads();
+    if (gating_sigmoid) {
+        if ((uint32_t)tid < E) scr[tid] = hg_sigmoid(lg[tid]);
+    } else if (tid == 0) {
+        float mx = -__builtin_huge_valf();
+        for (uint32_t e = 0; e < E; ++e)
+            if (lg[e] > mx) mx = lg[e];
+        float sum = 0.0f;
+        for (uint32_t e = 0; e < E; ++e) {
+            scr[e] = hg_expf(lg[e] - mx);
+            sum = sum + scr[e];
+        }
+        const float inv = 1.0f / sum;
+        for (uint32_t e = 0; e < E; ++e) scr[e] = scr[e] * inv;
+    }
+    __syncthreads();
+    if ((uint32_t)tid < E) sel[tid] = scr[tid] + bias[tid];
+    __syncthreads();
+    if ((uint32_t)tid < E) {
+        const float me = sel[tid];
+        uint32_t rank = 0;
+        for (uint32_t e = 0; e < E; ++e) rank += (sel[e] > me) || (sel[e] == me && e < (uint32_t)tid);
+        if (rank < top_k) { tk[rank] = tid; tw[rank] = scr[tid]; }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        if (weights_norm) {
+            float s = 0.0f;
+            for (uint32_t r = 0; r < top_k; ++r) s = s + tw[r];
+            s = s + 1e-9f;
+            for (uint32_t r = 0; r < top_k; ++r) tw[r] = tw[r] / s;
+        }
+        for (uint32_t r = 0; r < top_k; ++r) {
+            const float wr = tw[r] * weights_scale;
+            topk_idx[r] = tk[r];
+            topk_w[r] = wr;
+            rec_idx[r] = tk[r];
+            rec_w[r] = wr;
+        }
+        // slot order by ascending expert id (the prompt path's accumulation order)
+        uint32_t ord[64];
+        for (uint32_t r = 0; r < top_k; ++r) ord[r] = r;
+        for (uint32_t a = 1; a < top_k; ++a) {
+            const uint32_t v = ord[a];
+            uint32_t b = a;
+            while (b > 0 && tk[ord[b - 1]] > tk[v]) { ord[b] = ord[b - 1]; --b; }
+            ord[b] = v;
+        }
+        for (uint32_t r = 0; r < top_k; ++r) order[r] = ord[r];
+    }
+}
+
+// ------------------------------------------------------------------ experts
+// Gate and up rows of every active expert slot and a = silu(g)*u (model.rs:301-305,
+// 314-318; dense: 247-251).  blockIdx.y = slot: slots < top_k are routed experts
+// (topk_idx), the next one the shared expert (or the dense FFN).  8 rows per workgroup.
+template <int ORDER>
+__global__ __launch_bounds__(64) void k_ffn_gateup(Q8Mat Wg, Q8Mat Wu, Q8Mat Sg, Q8Mat Su,
+                                                   const uint32_t *__restrict__ topk_idx, uint32_t top_k,
+                                                   uint32_t f, const uint8_t *__restrict__ gq,
+                                                   const float *__restrict__ gd, float *a_out) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint8_t *sq = smem;
+    float *sd = reinterpret_cast<float *>(smem + Wg.nc * CHUNK_BYTES);
+    const int tid = threadIdx.x;
+    stage_act(gq, gd, Wg.nc, sq, sd, tid, 64);
+    __syncthreads();
+    const uint32_t slot = blockIdx.y;
+    const uint32_t i = blockIdx.x * 8 + (tid >> 3);
+    const int j = tid & 7;
+    if (i >= f) return;
+    float g, u;
+    if (slot < top_k) {
+        const uint32_t r = topk_idx[slot] * f + i;
+        g = q8_row_dot<ORDER>(row_qs(Wg, r), row_sc(Wg, r), Wg.sc_f32, sq, sd, Wg.nb, Wg.nc, j);
+        u = q8_row_dot<ORDER>(row_qs(Wu, r), row_sc(Wu, r), Wu.sc_f32, sq, sd, Wu.nb, Wu.nc, j);
+    } else {
+        g = q8_row_dot<ORDER>(row_qs(Sg, i), row_sc(Sg, i), Sg.sc_f32, sq, sd, Sg.nb, Sg.nc, j);
+        u = q8_row_dot<ORDER>(row_qs(Su, i), row_sc(Su, i), Su.sc_f32, sq, sd, Su.nb, Su.nc, j);
+    }
+    if (j == 0) a_out[(size_t)slot * f + i] = hg_silu(g) * u;
+}
+
+// Down rows of every slot and the fixed-order combination (model.rs:306-323; dense:
+// 253-254), then the residual add x += ffn (model.rs:173-176).  One wave per slot; each
+// wave first quantizes its slot's activation a[slot] (quant.rs:111-123) into LDS.
+//   decode:  out = ((0 + w_0 y_0) + w_1 y_1 ...) + y_shared    (rank order)
+//   prefill: the same sum in ascending expert-id order (model.rs:707-731)
+//   dense:   x += y
+template <int ORDER>
+__global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uint32_t *__restrict__ topk_idx,
+                                                   const float *__restrict__ topk_w,
+                                                   const uint32_t *__restrict__ order, uint32_t top_k,
+                                                   uint32_t n_slots, int dense, uint32_t d, uint32_t f,
+                                                   const float *__restrict__ a, float *x) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t nc = Sd.nc, nb = Sd.nb;
+    const size_t per = (size_t)nc * CHUNK_BYTES + (size_t)nc * 4 * sizeof(float);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float *ys = reinterpret_cast<float *>(smem + per * n_slots);  // [n_slots][8]
+    const uint32_t slot = wave;
+    uint8_t *sq = smem + per * slot;
+    float *sd = reinterpret_cast<float *>(sq + (size_t)nc * CHUNK_BYTES);
+    if (slot < n_slots) {
+        const float *as = a + (size_t)slot * f;
+        const int j = lane & 7;
+        for (uint32_t b0 = 0; b0 < nb; b0 += 8) {
+            const uint32_t b = b0 + (lane >> 3);
+            if (b < nb) {
+                float v[4];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) v[m] = as[b * QK + j * 4 + m];
+                quant_block_lane(v, j, b, sq, sd);
+            }
+        }
+        zero_pad(nb, nc, sq, sd, lane, 64);
+    }
+    __syncthreads();
+    const uint32_t r = blockIdx.x * 8 + (lane >> 3);
+    const int j = lane & 7;
+    if (slot < n_slots && r < d) {
+        float y;
+        if (slot < top_k) {
+            const uint32_t row = topk_idx[slot] * d + r;
+            y = q8_row_dot<ORDER>(row_qs(Wd, row), row_sc(Wd, row), Wd.sc_f32, sq, sd, nb, nc, j);
+        } else {
+            y = q8_row_dot<ORDER>(row_qs(Sd, r), row_sc(Sd, r), Sd.sc_f32, sq, sd, nb, nc, j);
+        }
+        if (j == 0) ys[slot * 8 + (lane >> 3)] = y;
+    }
+    __syncthreads();
+    if (tid < 8) {
+        const uint32_t rr = blockIdx.x * 8 + tid;
+        if (rr < d) {
+            if (dense) {
+                x[rr] = x[rr] + ys[tid];
+            } else {
+                float acc = 0.0f;
+                for (uint32_t q = 0; q < top_k; ++q) {
+                    const uint32_t s = (ORDER == ORDER_PREFILL) ? order[q] : q;
+                    acc = acc + topk_w[s] * ys[s * 8 + tid];
+                }
+                if (n_slots > top_k) acc = acc + ys[top_k * 8 + tid];
+                x[rr] = x[rr] + acc;
+            }
+        }
+    }
+}
+
+// ====================================================================== launchers
+#define LAUNCH(kern, grid, block, shm, st, ...) hipLaunchKernelGGL(kern, grid, block, shm, st, __VA_ARGS__)
+
+void launch_embed(hipStream_t st, const float *emb, uint32_t d, const StepParams *p, float *x) {
+    LAUNCH(k_embed, dim3(div_up(d, 256)), dim3(256), 0, st, emb, d, p, x);
+}
+void launch_load_row(hipStream_t st, const float *inputs, uint32_t d, const StepParams *p, float *x) {
+    LAUNCH(k_load_row, dim3(div_up(d, 256)), dim3(256), 0, st, inputs, d, p, x);
+}
+void launch_advance(hipStream_t st, StepParams *p) { LAUNCH(k_advance, dim3(1), dim3(64), 0, st, p); }
+
+void launch_rmsnorm_quant(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,
+                          float *h, uint8_t *q, float *dq) {
+    const size_t shm = d * sizeof(float);
+    if (exact) LAUNCH(k_rmsnorm_quant<true>, dim3(1), dim3(256), shm, st, x, w, eps, d, h, q, dq);
+    else LAUNCH(k_rmsnorm_quant<false>, dim3(1), dim3(256), shm, st, x, w, eps, d, h, q, dq);
+}
+
+void launch_quant_vec(hipStream_t st, const float *x, uint32_t n, uint8_t *q, float *dq) {
+    LAUNCH(k_quant_vec, dim3(div_up(n / QK, 32)), dim3(256), 0, st, x, n, q, dq);
+}
+
+uint32_t matvec_blocks(uint32_t N, uint32_t threads) { return div_up(N, threads / 8); }
+
+void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uint8_t *q, const float *dq, float *y,
+                   uint32_t threads, uint32_t valid, float *pv, uint32_t *pi) {
+    const dim3 grid(matvec_blocks(W.N, threads)), block(threads);
+    const size_t shm = (size_t)W.nc * CHUNK_BYTES + (size_t)W.nc * 4 * sizeof(float);
+#define MV(O, E) LAUNCH((k_matvec<O, E>), grid, block, shm, st, W, q, dq, y, valid, pv, pi)
+    if (order == ORDER_DECODE) {
+        if (epi == EPI_STORE) MV(ORDER_DECODE, EPI_STORE);
+        else if (epi == EPI_RESID) MV(ORDER_DECODE, EPI_RESID);
+        else MV(ORDER_DECODE, EPI_LOGITS);
+    } else {
+        if (epi == EPI_STORE) MV(ORDER_PREFILL, EPI_STORE);
+        else if (epi == EPI_RESID) MV(ORDER_PREFILL, EPI_RESID);
+        else MV(ORDER_PREFILL, EPI_LOGITS);
+    }
+#undef MV
+}
+
+void launch_argmax_final(hipStream_t st, const float *pv, const uint32_t *pi, uint32_t n, StepParams *p,
+                         uint32_t *out_ids) {
+    LAUNCH(k_argmax_final, dim3(1), dim3(1024), 0, st, pv, pi, n, p, out_ids);
+}
+
+size_t attn_fast_shm(uint32_t hd, uint32_t rep, uint32_t cap, uint32_t S) {
+    const uint32_t tok = 256 / (hd / 4);
+    const size_t floats = (size_t)(rep + 2) * hd + (size_t)(rep + 1) * hd + 4 * hd + (size_t)rep * attn_maxchunk(cap, S) +
+                          (size_t)tok * rep * hd + 2 * rep;
+    return floats * sizeof(float);
+}
+
+bool launch_attn(hipStream_t st, bool exact, uint32_t hd, const float *qkv, const float *qn, const float *kn,
+                 float eps, const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
+                 uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,
+                 float *o_out, uint8_t *q_out, float *d_out) {
+    const uint32_t rep = n_heads / n_kv;
+    if (exact) {
+        if (hd == 64)
+            LAUNCH(k_attn_exact<64>, dim3(n_heads), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
+                   n_kv, scratch, o_out, q_out, d_out);
+        else if (hd == 128)
+            LAUNCH(k_attn_exact<128>, dim3(n_heads), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap,
+                   n_heads, n_kv, scratch, o_out, q_out, d_out);
+        else if (hd == 32)
+            LAUNCH(k_attn_exact<32>, dim3(n_heads), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap,
+                   n_heads, n_kv, scratch, o_out, q_out, d_out);
+        else return false;
+        return true;
+    }
+    const size_t shm = attn_fast_shm(hd, rep, cap, S);
+    const dim3 grid(n_kv, S);
+    if (hd == 64) {
+        LAUNCH(k_attn_fast<64>, grid, dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part);
+        LAUNCH(k_attn_combine<64>, dim3(1), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
+    } else if (hd == 128) {
+        LAUNCH(k_attn_fast<128>, grid, dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part);
+        LAUNCH(k_attn_combine<128>, dim3(1), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
+    } else if (hd == 32) {
+        LAUNCH(k_attn_fast<32>, grid, dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part);
+        LAUNCH(k_attn_combine<32>, dim3(1), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
+    } else {
+        return false;
+    }
+    return true;
+}
+
+void launch_ffn_router(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,
+                       const float *Wr, const float *bias, uint32_t E, uint32_t top_k, int gating_sigmoid,
+                       int weights_norm, float weights_scale, uint8_t *q, float *dq, uint32_t *topk_idx,
+                       float *topk_w, uint32_t *order, uint32_t *rec_idx, float *rec_w) {
+    const size_t shm = d * sizeof(float);
+    if (exact)
+        LAUNCH(k_ffn_router<true>, dim3(1), dim3(1024), shm, st, x, w, eps, d, Wr, bias, E, top_k, gating_sigmoid,
+               weights_norm, weights_scale, q, dq, topk_idx, topk_w, order, rec_idx, rec_w);
+    else
+        LAUNCH(k_ffn_router<false>, dim3(1), dim3(1024), shm, st, x, w, eps, d, Wr, bias, E, top_k, gating_sigmoid,
+               weights_norm, weights_scale, q, dq, topk_idx, topk_w, order, rec_idx, rec_w);
+}
+
+void launch_ffn_gateup(hipStream_t st, int order, const Q8Mat &Wg, const Q8Mat &Wu, const Q8Mat &Sg,
+                       const Q8Mat &Su, const uint32_t *topk_idx, uint32_t top_k, uint32_t n_slots, uint32_t f,
+                       const uint8_t *q, const float *dq, float *a) {
+    const dim3 grid(div_up(f, 8), n_slots);
+    const size_t shm = (size_t)Wg.nc * CHUNK_BYTES + (size_t)Wg.nc * 4 * sizeof(float);
+    if (order == ORDER_DECODE)
+        LAUNCH(k_ffn_gateup<ORDER_DECODE>, grid, dim3(64), shm, st, Wg, Wu, Sg, Su, topk_idx, top_k, f, q, dq, a);
+    else
+        LAUNCH(k_ffn_gateup<ORDER_PREFILL>, grid, dim3(64), shm, st, Wg, Wu, Sg, Su, topk_idx, top_k, f, q, dq, a);
+}
+
+void launch_ffn_down(hipStream_t st, int order, const Q8Mat &Wd, const Q8Mat &Sd, const uint32_t *topk_idx,
+                     const float *topk_w, const uint32_t *ord, uint32_t top_k, uint32_t n_slots, int dense,
+                     uint32_t d, uint32_t f, const float *a, float *x) {
+    const size_t per = (size_t)Sd.nc * CHUNK_BYTES + (size_t)Sd.nc * 4 * sizeof(float);
+    const size_t shm = per * n_slots + (size_t)n_slots * 8 * sizeof(float);
+    const dim3 grid(div_up(d, 8)), block(64 * n_slots);
+    if (order == ORDER_DECODE)
+        LAUNCH(k_ffn_down<ORDER_DECODE>, grid, block, shm, st, Wd, Sd, topk_idx, topk_w, ord, top_k, n_slots, dense, d,
+               f, a, x);
+    else
+        LAUNCH(k_ffn_down<ORDER_PREFILL>, grid, block, shm, st, Wd, Sd, topk_idx, topk_w, ord, top_k, n_slots, dense, d,
+               f, a, x);
+}
+
+}  // namespace hg

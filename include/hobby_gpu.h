@@ -1,0 +1,159 @@
+/*
+ * hobby_gpu.h -- C ABI of the MI355X (gfx950) decode backend for hobbylm GGUF models.
+ *
+ * Drop-in boundary for hobby-rs's model-load / forward-token API.  Every entry point
+ * names the reference item it replaces (paths relative to the HobbyLM repository root).
+ *
+ * Conventions
+ *   - Functions returning int return HG_OK (0) or a negative HG_ERR_* code; the message
+ *     of the last failure on the calling thread is hg_last_error().  Nothing aborts or
+ *     throws across this boundary (the reference panics with panic=abort instead,
+ *     hobby-rs/Cargo.toml:23).
+ *   - Caller buffers are host memory; the library owns all device memory.
+ *   - An hg_model is immutable after load and may be shared by threads (the reference
+ *     shares Arc<Engine>, hobby-chat/src-tauri/src/server.rs:15,28-30).  An hg_kv owns a
+ *     HIP stream, its KV cache and its scratch, and must be used by one thread at a time
+ *     (the reference's &mut KvCache).
+ *   - Numerics: the Q8_0 matvec reproduces qrow_dot_avx2's lane order and FMAs
+ *     (quant.rs:44-67) and every other operation of the step except two follows the
+ *     reference's operation order; RMSNorm's sum of squares and attention's softmax sum
+ *     and P.V sum are reduced as trees, unless the cache is created with HG_KV_EXACT, in
+ *     which case they run in the reference's sequential order and the logits, routing and
+ *     cache contents are bit-identical to hobby-rs's AVX2 path.
+ */
+#ifndef HOBBY_GPU_H
+#define HOBBY_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HG_OK 0
+#define HG_ERR_IO (-1)          /* file cannot be opened / mapped */
+#define HG_ERR_FORMAT (-2)      /* malformed or truncated GGUF, missing tensor or metadata */
+#define HG_ERR_UNSUPPORTED (-3) /* a ggml type or shape this backend does not handle */
+#define HG_ERR_ARG (-4)         /* bad argument: token >= vocab, pos out of order or >= context */
+#define HG_ERR_DEVICE (-5)      /* HIP runtime failure or no gfx950 device */
+#define HG_ERR_NOMEM (-6)       /* device or host allocation failed */
+
+/* hg_kv_new flags */
+#define HG_KV_EXACT 1u /* reference-order (sequential) reductions: bit-identical to hobby-rs */
+
+typedef struct hg_model hg_model;
+typedef struct hg_kv hg_kv;
+typedef struct hg_q8_tensor hg_q8_tensor;
+
+/* Model hyperparameters; mirrors Config (hobby-rs/src/config.rs:8-32, diffusion fields
+ * omitted). */
+typedef struct hg_config {
+    uint32_t d_model, n_layers, n_dense, n_heads, n_kv_heads, head_dim;
+    uint32_t dense_ffn, expert_ffn, n_experts, top_k, n_shared;
+    uint32_t vocab_size, context_length;
+    float rms_eps, rope_theta, expert_weights_scale;
+    int32_t expert_weights_norm, gating_sigmoid;
+} hg_config;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *hg_last_error(void);
+
+/* ---- model (hobby-rs/src/lib.rs, model.rs) ------------------------------------------ */
+
+/* Engine::load(path, quant) (lib.rs:85-92) -> Gguf::open (gguf.rs:166-212),
+ * Config::from_gguf (config.rs:35-97), Model::load (model.rs:79-131).  quant != 0 keeps
+ * every matrix as Q8_0 after the load-time requantization of Q8Tensor::quantize
+ * (quant.rs:78-102); quant == 0 (F32 matrices) returns HG_ERR_UNSUPPORTED.  The tokenizer
+ * is not built: token ids cross this boundary. */
+int hg_model_load(const char *path, int quant, hg_model **out);
+void hg_model_free(hg_model *m);
+/* Engine.cfg (lib.rs:79) */
+int hg_model_config(const hg_model *m, hg_config *out);
+/* Engine::weight_bytes (lib.rs:100-102) -> Model::weight_bytes (model.rs:134-149): bytes
+ * the reference holds for the matrices (one f32 scale + 32 int8 per block).  The device
+ * copy stores each scale as the f16 it came from when that is exact (34 B per block). */
+uint64_t hg_weight_bytes(const hg_model *m);
+/* Device bytes actually resident for the matrices. */
+uint64_t hg_device_weight_bytes(const hg_model *m);
+/* Model::token_embedding (model.rs:332-335) */
+int hg_token_embedding(const hg_model *m, uint32_t id, float *out);
+
+/* ---- KV cache + decode step ---------------------------------------------------------- */
+
+/* KvCache::new (model.rs:67-74): a device-resident cache for max_ctx positions
+ * (0 = context_length), layer-major, head-major within a layer. */
+int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out);
+void hg_kv_free(hg_kv *kv);
+/* KvCache.len (model.rs:63) */
+uint32_t hg_kv_len(const hg_kv *kv);
+/* Cache rows [0, len) of one layer in the reference layout KvCache.k[layer] /
+ * KvCache.v[layer] ([len][n_kv_heads*head_dim], model.rs:60-64, 210-211). */
+int hg_kv_read(const hg_kv *kv, uint32_t layer, float *k, float *v);
+
+/* Model::forward(token, pos, cache) (model.rs:152-156).  pos must equal hg_kv_len(kv)
+ * and be < max_ctx.  logits (may be NULL) receives vocab_size floats; next (may be NULL)
+ * receives the greedy token of Engine::generate at temp 0 (lib.rs:132-142 with
+ * rep_penalty 1: ids >= min(50257, vocab) masked, then sample::argmax, sample.rs:53-63). */
+int hg_forward(const hg_model *m, hg_kv *kv, uint32_t token, uint32_t pos, float *logits,
+               uint32_t *next);
+/* Model::forward_x(x, pos, cache) (model.rs:160-184): x is d_model floats. */
+int hg_forward_x(const hg_model *m, hg_kv *kv, const float *x, uint32_t pos, float *logits,
+                 uint32_t *next);
+/* Model::prefill(inputs, cache) (model.rs:340-370): tn rows of d_model floats appended at
+ * positions len..len+tn-1 with the prompt path's arithmetic (Q8Tensor::matmul order,
+ * quant.rs:171-184; experts accumulated in expert-id order, model.rs:707-731); logits and
+ * next are those of the last row. */
+int hg_prefill(const hg_model *m, hg_kv *kv, const float *inputs, uint32_t tn, float *logits,
+               uint32_t *next);
+/* n_steps greedy decode steps without a host round trip per token: step i forwards the
+ * previous step's greedy token (first_token for i = 0) at pos = len and writes the greedy
+ * token it produces to out_ids[i].  Equivalent to n_steps calls of hg_forward with
+ * token = previous *next, which is the loop of Engine::generate (lib.rs:131-160) at temp 0
+ * with no EOS stop. */
+int hg_decode_greedy(const hg_model *m, hg_kv *kv, uint32_t first_token, uint32_t n_steps,
+                     uint32_t *out_ids);
+/* Engine::generate (lib.rs:107-162) at temp 0 over token ids: prefill of the prompt, then
+ * greedy steps with the 50257 mask, the repetition penalty of lib.rs:136-141 (1.0 = off),
+ * the EOS stop (lib.rs:143-145) and the context stop (lib.rs:155-157).  Writes at most
+ * max_new ids; *n_out receives the count. */
+int hg_generate_greedy(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uint32_t n_prompt,
+                       uint32_t max_new, float rep_penalty, uint32_t eos, uint32_t *out_ids,
+                       uint32_t *n_out);
+/* Routing of the last processed row, per layer in rank order (model.rs:282-293):
+ * idx[L*top_k] (UINT32_MAX for dense layers) and the scaled weights w[L*top_k]. */
+int hg_last_routing(const hg_kv *kv, uint32_t *idx, float *w);
+
+/* ---- operator level (hobby-rs/src/quant.rs, model.rs:199-233) ------------------------ */
+
+/* Q8Tensor::quantize(w, out, in) (quant.rs:78-102) from f32 weights [out][in]. */
+int hg_q8_tensor_quantize(const float *w, uint32_t out, uint32_t in, hg_q8_tensor **t);
+/* The GGUF load path of one Q8_0 matrix: dequant_q8_0 (gguf.rs:365-375) then
+ * Q8Tensor::quantize.  blocks: out*in/32 GGML blocks {f16 d; int8 q[32]}. */
+int hg_q8_tensor_from_q8_0(const void *blocks, uint32_t out, uint32_t in, hg_q8_tensor **t);
+void hg_q8_tensor_free(hg_q8_tensor *t);
+/* Q8Tensor::bytes (quant.rs:138-140) */
+uint64_t hg_q8_tensor_bytes(const hg_q8_tensor *t);
+/* Q8Tensor::matvec (quant.rs:106-136): y[out] = W x[in]. */
+int hg_q8_tensor_matvec(const hg_q8_tensor *t, const float *x, float *y);
+/* Q8Tensor::matmul (quant.rs:144-194): y[tn][out] = x[tn][in] W^T. */
+int hg_q8_tensor_matmul(const hg_q8_tensor *t, const float *x, float *y, uint32_t tn);
+/* The routed-expert matvec: t holds n_mat stacked matrices of rows_per_mat rows each
+ * (split_experts, model.rs:17-21); y[i][rows_per_mat] = W[ids[i]] x for i < n_ids. */
+int hg_q8_tensor_matvec_gather(const hg_q8_tensor *t, uint32_t rows_per_mat, const uint32_t *ids,
+                               uint32_t n_ids, const float *x, float *y);
+
+/* One decode-attention layer of Model::attention (model.rs:199-233) after the QKV
+ * projection: QK-norm (model.rs:753-763) and RoPE (ops.rs:139-166, theta, table of
+ * rope_len positions) on q[n_heads*hd] and k[n_kv*hd], append of k and v at row pos of
+ * the caches kc/vc ([pos+1][n_kv*hd] host arrays; rows < pos are inputs, row pos is
+ * written), GQA attention over rows 0..pos, output out[n_heads*hd].  flags: HG_KV_EXACT. */
+int hg_attention_decode(const float *q, const float *k, const float *v, const float *q_norm,
+                        const float *k_norm, float eps, float theta, uint32_t rope_len,
+                        uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t pos, float *kc,
+                        float *vc, float *out, uint32_t flags);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,128 @@
+"""Model-level parity of the HIP decode path against the CPU oracle.
+
+Exact caches (HG_KV_EXACT: reference-order reductions) must reproduce the oracle bit for
+bit: logits, greedy tokens, per-layer routing and every KV-cache row.  Fast caches (tree
+reductions in RMSNorm and attention) must keep logits within 1e-3 of the logit range,
+routing identical, and greedy tokens identical.
+"""
+import numpy as np
+import pytest
+
+from hobbylm_amd import gguf_synth as gs
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hg():
+    import hobbylm_amd
+    hobbylm_amd.lib()
+    return hobbylm_amd
+
+
+def _bits_equal(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+def _run_pair(hg, orc, path, n_prompt, n_steps, exact, seed=7, forced=False):
+    """Prefill a seeded prompt then decode n_steps on both paths; return per-step records."""
+    gm = hg.Model(path)
+    om = orc.Model(path)
+    V = gm.cfg.vocab_size
+    gkv = gm.new_cache(exact=exact)
+    okv = om.new_cache()
+    prompt = gs.prompt_ids(seed, n_prompt, min(V, 50257))
+    emb = np.stack([om.token_embedding(int(t)) for t in prompt])
+    assert _bits_equal(emb, np.stack([gm.token_embedding(int(t)) for t in prompt]))
+    gl, gnext = gm.prefill(emb, gkv)
+    ol = om.prefill(emb, okv)
+    recs = [(gl, ol, gnext, gkv.routing(), okv.routing())]
+    forced_toks = gs.prompt_ids(seed + 1, n_steps, min(V, 50257))
+    valid = min(V, 50257)
+    tok = gnext
+    for i in range(n_steps):
+        otok = int(np.argmax(np.where(np.arange(V) < valid, ol, -np.inf)))
+        assert tok == otok, f"greedy token differs at step {i}"
+        if forced:
+            tok = int(forced_toks[i])
+        pos = n_prompt + i
+        gl, gnext = gm.forward(tok, pos, gkv)
+        ol = om.forward(tok, pos, okv)
+        recs.append((gl, ol, gnext, gkv.routing(), okv.routing()))
+        tok = gnext
+    return gm, om, gkv, okv, recs
+
+
+@pytest.mark.parametrize("preset", ["tiny", "tiny_noshared"])
+def test_exact_mode_bit_exact(hg, orc, preset):
+    path = gs.synth_path(preset, 11, norm_jitter=0.1)
+    gm, om, gkv, okv, recs = _run_pair(hg, orc, path, 9, 12, exact=True, forced=True)
+    for i, (gl, ol, gnext, (gi, gw), (oi, ow, _)) in enumerate(recs):
+        assert _bits_equal(gl, ol), f"logits differ at step {i}"
+        assert np.array_equal(gi[gm.cfg.n_dense:], oi[gm.cfg.n_dense:]), i
+        assert _bits_equal(gw[gm.cfg.n_dense:], ow[gm.cfg.n_dense:]), i
+    for layer in range(gm.cfg.n_layers):
+        gk, gv = gkv.read(layer)
+        ok, ov = okv.read(layer)
+        assert _bits_equal(gk, ok) and _bits_equal(gv, ov), layer
+
+
+@pytest.mark.parametrize("preset", ["tiny", "tiny_noshared"])
+def test_fast_mode_within_tolerance(hg, orc, preset):
+    path = gs.synth_path(preset, 12, norm_jitter=0.1)
+    gm, om, gkv, okv, recs = _run_pair(hg, orc, path, 9, 24, exact=False, forced=True)
+    for i, (gl, ol, gnext, (gi, gw), (oi, ow, gap)) in enumerate(recs):
+        assert np.max(np.abs(gl - ol)) <= 1e-3 * (ol.max() - ol.min()), i
+        moe = slice(gm.cfg.n_dense, None)
+        assert np.array_equal(gi[moe], oi[moe]), i
+
+
+def test_130m_exact_bit_exact(hg, orc):
+    """The 130M preset: K = 192 expert rows (partial chunk), top-8 of 32, vocab 50304 (masked ids)."""
+    path = gs.synth_path("130M", 0)
+    gm, om, gkv, okv, recs = _run_pair(hg, orc, path, 16, 6, exact=True)
+    for i, (gl, ol, gnext, (gi, gw), (oi, ow, _)) in enumerate(recs):
+        assert _bits_equal(gl, ol), i
+        assert np.array_equal(gi[1:], oi[1:]), i
+
+
+def test_greedy_device_loop_matches_forward(hg, orc):
+    path = gs.synth_path("tiny", 13, norm_jitter=0.1)
+    gm = hg.Model(path)
+    om = orc.Model(path)
+    prompt = gs.prompt_ids(3, 6, gm.cfg.vocab_size)
+    kv1 = gm.new_cache(exact=True)
+    emb = np.stack([gm.token_embedding(int(t)) for t in prompt])
+    _, first = gm.prefill(emb, kv1)
+    ids = gm.decode_greedy(first, 20, kv1)
+    ref = om.generate_greedy(prompt, 21, om.new_cache(), eos=2 ** 32 - 1)
+    assert list(ref) == [first] + list(ids)
+    gen = gm.generate_greedy(prompt, 21, gm.new_cache(exact=True), eos=2 ** 32 - 1)
+    assert list(gen) == list(ref)
+    # repetition penalty path (logits on the host) and the EOS stop
+    ref_rp = om.generate_greedy(prompt, 15, om.new_cache(), rep_penalty=1.3, eos=2 ** 32 - 1)
+    gen_rp = gm.generate_greedy(prompt, 15, gm.new_cache(exact=True), rep_penalty=1.3, eos=2 ** 32 - 1)
+    assert list(gen_rp) == list(ref_rp)
+    eos = int(ref[3])
+    assert list(gm.generate_greedy(prompt, 21, gm.new_cache(exact=True), eos=eos)) == \
+        list(om.generate_greedy(prompt, 21, om.new_cache(), eos=eos))
+
+
+def test_forward_x_and_errors(hg, orc):
+    path = gs.synth_path("tiny", 14)
+    gm = hg.Model(path)
+    om = orc.Model(path)
+    kv, okv = gm.new_cache(exact=True), om.new_cache()
+    x = np.random.default_rng(0).standard_normal(gm.cfg.d_model).astype(np.float32)
+    gl, _ = gm.forward_x(x, 0, kv)
+    assert _bits_equal(gl, om.forward_x(x, 0, okv))
+    with pytest.raises(hg.HgError):
+        gm.forward(gm.cfg.vocab_size, 1, kv)      # token out of range
+    with pytest.raises(hg.HgError):
+        gm.forward(1, 5, kv)                      # pos does not continue the cache
+    small = gm.new_cache(max_ctx=2)
+    gm.forward(1, 0, small)
+    gm.forward(1, 1, small)
+    with pytest.raises(hg.HgError):
+        gm.forward(1, 2, small)                   # beyond the cache
+    assert gm.weight_bytes() == om.weight_bytes()
