@@ -28,7 +28,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libhobby_gpu.so")
 
 HG_OK = 0
-HG_KV_EXACT = 1
+HG_KV_FAST = 1
 GPT2_VALID = 50257
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
@@ -142,8 +142,8 @@ class Model:
     def device_weight_bytes(self) -> int:
         return int(lib().hg_device_weight_bytes(self.h))
 
-    def new_cache(self, max_ctx: int = 0, exact: bool = False) -> "KvCache":
-        return KvCache(self, max_ctx, exact)
+    def new_cache(self, max_ctx: int = 0, fast: bool = False) -> "KvCache":
+        return KvCache(self, max_ctx, fast)
 
     def token_embedding(self, tok: int) -> np.ndarray:
         out = np.empty(self.cfg.d_model, np.float32)
@@ -186,12 +186,13 @@ class Model:
 
 
 class KvCache:
-    """Device KV cache (KvCache, model.rs:60-75); exact=True selects reference-order reductions."""
+    """Device KV cache (KvCache, model.rs:60-75).  fast=True reassociates the RMSNorm and
+    attention sums as trees (not bit-identical to the reference; routing may differ)."""
 
-    def __init__(self, model: Model, max_ctx: int = 0, exact: bool = False):
+    def __init__(self, model: Model, max_ctx: int = 0, fast: bool = False):
         self.model = model
         h = _vp()
-        _check(lib().hg_kv_new(model.h, max_ctx, HG_KV_EXACT if exact else 0, C.byref(h)))
+        _check(lib().hg_kv_new(model.h, max_ctx, HG_KV_FAST if fast else 0, C.byref(h)))
         self.h = h
 
     def close(self):
@@ -287,7 +288,7 @@ class Q8Tensor:
 
 
 def attention_decode(q, k, v, q_norm, k_norm, eps, theta, rope_len, n_heads, n_kv, hd, pos, kcache, vcache,
-                     exact=False):
+                     fast=False):
     """One decode-attention layer (model.rs:199-233); kcache/vcache [pos+1][n_kv*hd] are updated in place."""
     out = np.empty(n_heads * hd, np.float32)
     assert kcache.flags["C_CONTIGUOUS"] and vcache.flags["C_CONTIGUOUS"]
@@ -295,5 +296,5 @@ def attention_decode(q, k, v, q_norm, k_norm, eps, theta, rope_len, n_heads, n_k
                                      np.ascontiguousarray(v, np.float32), np.ascontiguousarray(q_norm, np.float32),
                                      np.ascontiguousarray(k_norm, np.float32), eps, theta, rope_len, n_heads, n_kv,
                                      hd, pos, kcache.reshape(-1), vcache.reshape(-1), out,
-                                     HG_KV_EXACT if exact else 0))
+                                     HG_KV_FAST if fast else 0))
     return out

@@ -89,6 +89,11 @@ int check_device() {
         if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
             status = HG_ERR_DEVICE;
             msg = std::string("this build targets gfx950; device is ") + prop.gcnArchName;
+            return;
+        }
+        if (init_kernel_attributes() != hipSuccess) {
+            status = HG_ERR_DEVICE;
+            msg = "hipFuncSetAttribute failed";
         }
     });
     if (status) g_err = msg;
@@ -101,7 +106,7 @@ struct DevQ8 {
     uint64_t ref_bytes = 0;
     int upload(const PackedQ8 &p) {
         int rc = qs.upload(p.qs.data(), p.qs.size());
-        if (!rc) rc = sc.upload(p.sc.data(), p.sc.size());
+        if (!rc) rc = sc.upload(p.sc_bytes(), p.sc_size());
         if (rc) return rc;
         m.qs = qs.as<uint8_t>();
         m.sc = sc.p;
@@ -109,7 +114,7 @@ struct DevQ8 {
         m.K = p.K;
         m.nb = p.nb;
         m.nc = p.nc;
-        m.sc_f32 = p.f32sc;
+        m.sc_f32 = p.f32sc ? 1u : 0u;
         ref_bytes = p.ref_bytes();
         return HG_OK;
     }
@@ -166,7 +171,13 @@ int load_norm(const Gguf &g, const std::string &name, size_t want, DevBuf &dst) 
     return dst.upload(v.data(), v.size() * 4);
 }
 
-// Gguf::load + Mat::build(.., quant = true) (model.rs:87-89, 121): requantize and upload.
+// Matrices packed on the host, uploaded together once the model-wide scale storage is known.
+struct Pending {
+    std::vector<std::pair<PackedQ8, DevQ8 *>> mats;
+};
+thread_local Pending *g_pending = nullptr;
+
+// Gguf::load + Mat::build(.., quant = true) (model.rs:87-89, 121): requantize and pack.
 int load_q8(const Gguf &g, const std::string &name, uint32_t N, uint32_t K, DevQ8 &dst, hg_model *m) {
     const TensorInfo *t;
     const uint8_t *raw;
@@ -185,10 +196,24 @@ int load_q8(const Gguf &g, const std::string &name, uint32_t N, uint32_t K, DevQ
         if (rc) return rc;
         pack_q8_from_f32(w.data(), N, K, p);
     }
-    rc = dst.upload(p);
-    if (rc) return rc;
-    m->ref_bytes += dst.ref_bytes;
-    m->dev_bytes += dst.dev_bytes();
+    m->ref_bytes += p.ref_bytes();
+    g_pending->mats.emplace_back(std::move(p), &dst);
+    return HG_OK;
+}
+
+// Upload the pending matrices with f16 scales if every scale of every matrix is an exact
+// f16 value (GGUF Q8_0 files: the on-disk 34 bytes per block), else all with f32 scales.
+int upload_pending(hg_model *m) {
+    bool all_f16 = true;
+    for (auto &pm : g_pending->mats) all_f16 = all_f16 && pm.first.f16_exact;
+    for (auto &pm : g_pending->mats) {
+        pm.first.set_scale_storage(!all_f16);
+        int rc = pm.second->upload(pm.first);
+        if (rc) return rc;
+        m->dev_bytes += pm.second->dev_bytes();
+        pm.first = PackedQ8();
+    }
+    g_pending->mats.clear();
     return HG_OK;
 }
 
@@ -223,6 +248,9 @@ int hg_model_load(const char *path, int quant, hg_model **out) {
     Gguf g;
     rc = g.open(path, g_err);
     if (rc) return rc;
+    Pending pending;
+    g_pending = &pending;
+    struct Reset { ~Reset() { g_pending = nullptr; } } reset;
     auto m = std::make_unique<hg_model>();
     rc = config_from_gguf(g, m->c, g_err);
     if (rc) return rc;
@@ -263,6 +291,7 @@ int hg_model_load(const char *path, int quant, hg_model **out) {
         m->layers.push_back(std::move(L));
     }
     if ((rc = load_q8(g, "output.weight", c.vocab_size, d, m->output, m.get()))) return rc;
+    if ((rc = upload_pending(m.get()))) return rc;
     {
         std::vector<float> emb;
         if ((rc = g.load("token_embd.weight", emb, g_err))) return rc;
@@ -460,7 +489,7 @@ int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out) 
     kv->m = m;
     kv->cap = max_ctx;
     kv->flags = flags;
-    kv->exact = (flags & HG_KV_EXACT) != 0;
+    kv->exact = (flags & HG_KV_FAST) == 0;
     const char *ge = getenv("HG_GRAPH");
     kv->use_graph = !(ge && ge[0] == '0');
     kv->S = std::max(64u, div_up(kv->cap, 256));  // splits of at most 256 positions (LDS bound)
@@ -652,7 +681,8 @@ struct hg_q8_tensor {
 
 namespace {
 
-int make_tensor(const PackedQ8 &p, hg_q8_tensor **t) {
+int make_tensor(PackedQ8 &p, hg_q8_tensor **t) {
+    p.set_scale_storage(!p.f16_exact);
     auto q = std::make_unique<hg_q8_tensor>();
     int rc = q->w.upload(p);
     if (rc) return rc;
@@ -775,7 +805,7 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
     if (pos >= rope_len) return fail(HG_ERR_ARG, "pos beyond the RoPE table");
     int rc = check_device();
     if (rc) return rc;
-    const bool exact = flags & HG_KV_EXACT;
+    const bool exact = (flags & HG_KV_FAST) == 0;
     const uint32_t qd = n_heads * hd, kvd = n_kv * hd, n = pos + 1, cap = n, S = std::max(64u, div_up(n, 256));
     std::vector<float> qkv(qd + 2 * kvd);
     memcpy(qkv.data(), q, qd * 4);

@@ -364,24 +364,26 @@ void pack_rows(uint32_t N, uint32_t K, PackedQ8 &out, Reader read_row) {
             for (int e = 0; e < QK; ++e) dst[chunk_pos(b * QK + e)] = (uint8_t)q[e];
         }
     });
-    // f16 scale storage when every scale round-trips through binary16 exactly
+    // normal binary16 values only (no f16 subnormals)
     bool f16_ok = true;
     for (float s : scales) {
         const _Float16 h = (_Float16)s;
         if ((float)h != s || (s != 0.0f && fabsf(s) < 6.103515625e-05f)) { f16_ok = false; break; }
     }
-    out.f32sc = !f16_ok;
-    if (f16_ok) {
-        out.sc.resize(scales.size() * 2);
-        _Float16 *h = reinterpret_cast<_Float16 *>(out.sc.data());
-        for (size_t i = 0; i < scales.size(); ++i) h[i] = (_Float16)scales[i];
-    } else {
-        out.sc.resize(scales.size() * 4);
-        memcpy(out.sc.data(), scales.data(), out.sc.size());
-    }
+    out.f16_exact = f16_ok;
+    out.sc32 = std::move(scales);
 }
 
 }  // namespace
+
+void PackedQ8::set_scale_storage(bool f32) {
+    f32sc = f32;
+    sc16.clear();
+    if (!f32) {
+        sc16.resize(sc32.size());
+        for (size_t i = 0; i < sc32.size(); ++i) sc16[i] = __builtin_bit_cast(uint16_t, (_Float16)sc32[i]);
+    }
+}
 
 void pack_q8_from_f32(const float *w, uint32_t N, uint32_t K, PackedQ8 &out) {
     pack_rows(N, K, out, [&](uint32_t r, float *buf) { memcpy(buf, w + (size_t)r * K, (size_t)K * 4); });

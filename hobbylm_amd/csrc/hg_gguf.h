@@ -61,10 +61,15 @@ int config_from_gguf(const Gguf &g, hg_config &c, std::string &err);
 // layout of hg_common.h (lane-major 128-byte chunks, scales per row).
 struct PackedQ8 {
     uint32_t N = 0, K = 0, nb = 0, nc = 0;
-    bool f32sc = false;
-    std::vector<uint8_t> qs;  // N * nc * 128
-    std::vector<uint8_t> sc;  // N * nc * 4 * (2 or 4)
+    bool f16_exact = false;    // every scale is a binary16 value exactly
+    bool f32sc = true;         // storage chosen by set_scale_storage
+    std::vector<uint8_t> qs;   // N * nc * 128
+    std::vector<float> sc32;   // N * nc * 4 scales (zero padded)
+    std::vector<uint16_t> sc16;
     uint64_t ref_bytes() const { return (uint64_t)N * K + (uint64_t)N * nb * 4; }  // Q8Tensor::bytes
+    void set_scale_storage(bool f32);
+    const void *sc_bytes() const { return f32sc ? (const void *)sc32.data() : (const void *)sc16.data(); }
+    size_t sc_size() const { return f32sc ? sc32.size() * 4 : sc16.size() * 2; }
 };
 
 // Requantize f32 rows (Q8Tensor::quantize) and pack them.

@@ -4,6 +4,7 @@
 
 namespace hg {
 
+hipError_t init_kernel_attributes();
 void launch_embed(hipStream_t st, const float *emb, uint32_t d, const StepParams *p, float *x);
 void launch_load_row(hipStream_t st, const float *inputs, uint32_t d, const StepParams *p, float *x);
 void launch_advance(hipStream_t st, StepParams *p);

@@ -58,84 +58,147 @@ __device__ inline void stage_act(const uint8_t *gq, const float *gd, uint32_t nc
     for (uint32_t i = tid; i < nc * 4; i += nthr) sd[i] = gd[i];
 }
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Storage vector of the four scales of one chunk: f32 (16 B) or f16 (8 B).
+template <bool SCF32> struct ScaleVec { typedef v2u T; };
+template <> struct ScaleVec<true> { typedef v4f T; };
+
+__device__ inline void unpack_scales(v4f s, float o[4]) { o[0] = s.x; o[1] = s.y; o[2] = s.z; o[3] = s.w; }
+__device__ inline void unpack_scales(v2u h, float o[4]) {
+    o[0] = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.x & 0xffffu));
+    o[1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.x >> 16));
+    o[2] = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.y & 0xffffu));
+    o[3] = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.y >> 16));
+}
+
 // Row dot of the Q8 matvec, lane j of the 8 lanes owning the row.
 //   ORDER_DECODE: qrow_dot_avx2 (quant.rs:44-67).  Lane j keeps accumulator lane j:
 //     acc_j = fma(sw[b]*dx[b], (float)sum_{m<4} w[32b+4j+m]*x[32b+4j+m], acc_j) over b,
 //     then ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) (the hsum of quant.rs:61-65) by xor 4/2/1.
 //   ORDER_PREFILL: Q8Tensor::matmul (quant.rs:171-184).  isum over the whole block (exact),
 //     acc += (sw[b]*dx[b]) * isum in block order, one accumulator.
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef unsigned int v2u __attribute__((ext_vector_type(2)));
-typedef float v4f __attribute__((ext_vector_type(4)));
+// begin() issues the first NCT chunks' weight and scale loads (branch free, the index
+// clamped into the row), so a kernel can start them before staging its activation; finish()
+// consumes them and streams the rest of the row NCT chunks at a time.
+template <int ORDER, bool SCF32, int NCT>
+struct Q8Row {
+    const uint8_t *w;
+    const void *s;
+    uint32_t nb, nc;
+    int j;
+    v4i wq[NCT];
+    typename ScaleVec<SCF32>::T sq[NCT];
 
-// The four scales of chunk c of a row (f16 or f32 storage).
-__device__ inline v4f load_scales4(const void *srow, uint32_t c, uint32_t f32) {
-    if (f32) return __builtin_nontemporal_load(reinterpret_cast<const v4f *>(srow) + c);
-    const v2u h = __builtin_nontemporal_load(reinterpret_cast<const v2u *>(srow) + c);
-    v4f r;
-    r.x = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.x & 0xffffu));
-    r.y = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.x >> 16));
-    r.z = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.y & 0xffffu));
-    r.w = (float)__builtin_bit_cast(_Float16, (unsigned short)(h.y >> 16));
-    return r;
-}
-
-template <int ORDER>
-__device__ inline float q8_row_dot(const uint8_t *__restrict__ wrow, const void *__restrict__ srow,
-                                   uint32_t sc_f32, const uint8_t *qx, const float *dx, uint32_t nb,
-                                   uint32_t nc, int j) {
-    float acc = 0.0f;
-    constexpr uint32_t U = 8;
-    for (uint32_t c0 = 0; c0 < nc; c0 += U) {
-        v4i w[U];
-        v4f sw[U];
+    __device__ inline void load(uint32_t c0) {
 #pragma unroll
-        for (uint32_t u = 0; u < U; ++u)
-            if (c0 + u < nc) {
-                w[u] = __builtin_nontemporal_load(
-                    reinterpret_cast<const v4i *>(wrow + (c0 + u) * CHUNK_BYTES + j * 16));
-                sw[u] = load_scales4(srow, c0 + u, sc_f32);
-            }
-#pragma unroll
-        for (uint32_t u = 0; u < U; ++u) {
-            const uint32_t c = c0 + u;
-            if (c >= nc) break;
-            const v4i x = *reinterpret_cast<const v4i *>(qx + c * CHUNK_BYTES + j * 16);
-            const v4f dxc = *reinterpret_cast<const v4f *>(dx + c * 4);
-            const int p[4] = {sdot4(w[u].x, x.x), sdot4(w[u].y, x.y), sdot4(w[u].z, x.z),
-                              sdot4(w[u].w, x.w)};
-            const float sv[4] = {sw[u].x, sw[u].y, sw[u].z, sw[u].w};
-            const float dv[4] = {dxc.x, dxc.y, dxc.z, dxc.w};
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint32_t b = c * 4 + t;
-                const float d = sv[t] * dv[t];
-                if (ORDER == ORDER_DECODE) {
-                    if (b < nb) acc = fmaf(d, (float)p[t], acc);
-                } else {
-                    int is = p[t];
-                    is += shfl_xor_i(is, 1);
-                    is += shfl_xor_i(is, 2);
-                    is += shfl_xor_i(is, 4);
-                    if (b < nb) acc = acc + d * (float)is;
-                }
-            }
+        for (int u = 0; u < NCT; ++u) {
+            const uint32_t c = min(c0 + (uint32_t)u, nc - 1);
+            wq[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(w + c * CHUNK_BYTES + j * 16));
+            sq[u] = __builtin_nontemporal_load(reinterpret_cast<const typename ScaleVec<SCF32>::T *>(s) + c);
         }
     }
-    if (ORDER == ORDER_DECODE) {
-        acc = acc + shfl_xor(acc, 4);
-        acc = acc + shfl_xor(acc, 2);
-        acc = acc + shfl_xor(acc, 1);
+    __device__ inline void begin(const uint8_t *w_, const void *s_, uint32_t nb_, uint32_t nc_, int j_) {
+        w = w_;
+        s = s_;
+        nb = nb_;
+        nc = nc_;
+        j = j_;
+        load(0);
     }
-    return acc;
-}
+    __device__ inline float finish(const uint8_t *qx, const float *dx) {
+        float acc = 0.0f;
+        uint32_t c0 = 0;
+        while (true) {
+#pragma unroll
+            for (int u = 0; u < NCT; ++u) {
+                const uint32_t c = c0 + u;
+                if (c < nc) {
+                    const v4i x = *reinterpret_cast<const v4i *>(qx + c * CHUNK_BYTES + j * 16);
+                    const v4f dxc = *reinterpret_cast<const v4f *>(dx + c * 4);
+                    const int p[4] = {sdot4(wq[u].x, x.x), sdot4(wq[u].y, x.y), sdot4(wq[u].z, x.z),
+                                      sdot4(wq[u].w, x.w)};
+                    float sv[4];
+                    unpack_scales(sq[u], sv);
+                    const float dv[4] = {dxc.x, dxc.y, dxc.z, dxc.w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const uint32_t b = c * 4 + t;
+                        const float d = sv[t] * dv[t];
+                        if (ORDER == ORDER_DECODE) {
+                            if (b < nb) acc = fmaf(d, (float)p[t], acc);
+                        } else {
+                            int is = p[t];
+                            is += shfl_xor_i(is, 1);
+                            is += shfl_xor_i(is, 2);
+                            is += shfl_xor_i(is, 4);
+                            if (b < nb) acc = acc + d * (float)is;
+                        }
+                    }
+                }
+            }
+            c0 += NCT;
+            if (c0 >= nc) break;
+            load(c0);
+        }
+        if (ORDER == ORDER_DECODE) {
+            acc = acc + shfl_xor(acc, 4);
+            acc = acc + shfl_xor(acc, 2);
+            acc = acc + shfl_xor(acc, 1);
+        }
+        return acc;
+    }
+};
 
 __device__ inline const uint8_t *row_qs(const Q8Mat &W, uint32_t r) {
     return W.qs + (size_t)r * W.nc * CHUNK_BYTES;
 }
+template <bool SCF32>
 __device__ inline const void *row_sc(const Q8Mat &W, uint32_t r) {
-    return W.sc_f32 ? (const void *)(reinterpret_cast<const float *>(W.sc) + (size_t)r * W.nc * 4)
-                    : (const void *)(reinterpret_cast<const _Float16 *>(W.sc) + (size_t)r * W.nc * 4);
+    return reinterpret_cast<const uint8_t *>(W.sc) + (size_t)r * W.nc * 4 * (SCF32 ? 4 : 2);
+}
+
+// s + a[0] + a[1] + ... + a[n-1], one rounded add at a time in index order (the reference's
+// sequential accumulations), run by a single lane over LDS.  Full batches of 32 are fetched
+// one batch ahead with 16-byte reads so the add chain never waits on LDS.  `a` is 16-byte
+// aligned.
+__device__ inline float seq_sum_lds(const float *a, uint32_t n, float s) {
+    constexpr uint32_t B = 32;
+    const uint32_t nfull = n / B * B;
+    v4f r0[B / 4], r1[B / 4];
+    const v4f *a4 = reinterpret_cast<const v4f *>(a);
+    if (nfull) {
+#pragma unroll
+        for (uint32_t u = 0; u < B / 4; ++u) r0[u] = a4[u];
+    }
+    for (uint32_t i0 = 0; i0 < nfull; i0 += 2 * B) {
+        const bool more1 = i0 + B < nfull;
+        if (more1)
+#pragma unroll
+            for (uint32_t u = 0; u < B / 4; ++u) r1[u] = a4[(i0 + B) / 4 + u];
+#pragma unroll
+        for (uint32_t u = 0; u < B / 4; ++u) {
+            s = s + r0[u].x;
+            s = s + r0[u].y;
+            s = s + r0[u].z;
+            s = s + r0[u].w;
+        }
+        if (!more1) break;
+        if (i0 + 2 * B < nfull)
+#pragma unroll
+            for (uint32_t u = 0; u < B / 4; ++u) r0[u] = a4[(i0 + 2 * B) / 4 + u];
+#pragma unroll
+        for (uint32_t u = 0; u < B / 4; ++u) {
+            s = s + r1[u].x;
+            s = s + r1[u].y;
+            s = s + r1[u].z;
+            s = s + r1[u].w;
+        }
+    }
+    for (uint32_t i = nfull; i < n; ++i) s = s + a[i];
+    return s;
 }
 
 // ------------------------------------------------------------------ embedding
@@ -159,33 +222,43 @@ __global__ void k_advance(StepParams *p) {
 // ------------------------------------------------------------------ RMSNorm + quantize
 // rmsnorm (ops.rs:85-96): ss = sum x^2; scale = 1/sqrt(ss/n + eps); h = x*scale*w; then
 // the activation quantization of the consuming matvec (quant.rs:111-123).
-// EXACT: ss accumulated sequentially as in the reference; otherwise a tree.
+// EXACT: the squares are formed in parallel and summed by one lane in index order (the
+// reference's `ss += v * v`); otherwise a tree.
+template <bool EXACT>
+__device__ inline float sum_squares(const float *xs, float *ps, uint32_t d, int tid, int nthr, float *red,
+                                    float *s_out) {
+    if (EXACT) {
+        for (uint32_t i = tid; i < d; i += nthr) ps[i] = xs[i] * xs[i];
+        __syncthreads();
+        if (tid == 0) *s_out = seq_sum_lds(ps, d, 0.0f);
+    } else {
+        float ss = 0.0f;
+        for (uint32_t i = tid; i < d; i += nthr) ss += xs[i] * xs[i];
+        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        if (tid == 0) {
+            float t = 0.0f;
+            for (int i = 0; i < nthr / 64; ++i) t += red[i];
+            *s_out = t;
+        }
+    }
+    __syncthreads();
+    return *s_out;
+}
+
 template <bool EXACT>
 __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float *__restrict__ x, const float *__restrict__ w,
                                                        float eps, uint32_t d, float *h_out, uint8_t *q_out,
                                                        float *d_out) {
-    extern __shared__ float xs[];
+    extern __shared__ __align__(16) float xs[];  // 2*d: x, then the squares
     __shared__ float red[4];
-    __shared__ float s_scale;
+    __shared__ float s_ss;
     const int tid = threadIdx.x;
     for (uint32_t i = tid; i < d; i += 256) xs[i] = x[i];
     __syncthreads();
-    if (EXACT) {
-        if (tid == 0) {
-            float ss = 0.0f;
-            for (uint32_t i = 0; i < d; ++i) ss = ss + xs[i] * xs[i];
-            s_scale = 1.0f / sqrtf(ss / (float)d + eps);
-        }
-    } else {
-        float ss = 0.0f;
-        for (uint32_t i = tid; i < d; i += 256) ss += xs[i] * xs[i];
-        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-        __syncthreads();
-        if (tid == 0) s_scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)d + eps);
-    }
-    __syncthreads();
-    const float scale = s_scale;
+    const float ss = sum_squares<EXACT>(xs, xs + d, d, tid, 256, red, &s_ss);
+    const float scale = 1.0f / sqrtf(ss / (float)d + eps);
     const uint32_t nb = d / QK, nc = div_up(nb, 4);
     const int j = tid & 7;
     for (uint32_t b0 = 0; b0 < nb; b0 += 32) {
@@ -223,12 +296,13 @@ __global__ __launch_bounds__(256) void k_quant_vec(const float *__restrict__ x, 
 
 // ------------------------------------------------------------------ Q8 matvec
 // Q8Tensor::matvec / matmul row loop (quant.rs:125-135, 168-185) over a pre-quantized
-// activation.  8 lanes per row; blockDim.x/8 rows per workgroup.
+// activation.  8 lanes per row; blockDim.x/8 rows per workgroup.  The weight stream of
+// each row is started before the activation is staged into LDS.
 //   EPI_STORE:  y[r] = v
 //   EPI_RESID:  y[r] = y[r] + v     (x[i] += attn[i], model.rs:169-171)
 //   EPI_LOGITS: y[r] = v, plus a per-workgroup (max, first index) over rows < valid for
 //               the greedy argmax (sample.rs:53-63 on logits masked per lib.rs:132-134).
-template <int ORDER, int EPI>
+template <int ORDER, int EPI, bool SCF32, int NCT>
 __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restrict__ gq,
                                                 const float *__restrict__ gd, float *y, uint32_t valid,
                                                 float *part_v, uint32_t *part_i) {
@@ -236,17 +310,17 @@ __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restri
     uint8_t *sq = smem;
     float *sd = reinterpret_cast<float *>(smem + W.nc * CHUNK_BYTES);
     const int tid = threadIdx.x, nthr = blockDim.x;
+    const uint32_t row = blockIdx.x * (nthr >> 3) + (tid >> 3);
+    const uint32_t lrow = min(row, W.N - 1);
+    const int j = tid & 7;
+    Q8Row<ORDER, SCF32, NCT> rd;
+    rd.begin(row_qs(W, lrow), row_sc<SCF32>(W, lrow), W.nb, W.nc, j);
     stage_act(gq, gd, W.nc, sq, sd, tid, nthr);
     __syncthreads();
-    const uint32_t row = blockIdx.x * (nthr >> 3) + (tid >> 3);
-    const int j = tid & 7;
-    float v = 0.0f;
-    if (row < W.N) {
-        v = q8_row_dot<ORDER>(row_qs(W, row), row_sc(W, row), W.sc_f32, sq, sd, W.nb, W.nc, j);
-        if (j == 0) {
-            if (EPI == EPI_RESID) y[row] = y[row] + v;
-            else y[row] = v;
-        }
+    const float v = rd.finish(sq, sd);
+    if (row < W.N && j == 0) {
+        if (EPI == EPI_RESID) y[row] = y[row] + v;
+        else y[row] = v;
     }
     if (EPI == EPI_LOGITS) {
         __shared__ float bv[32];
@@ -503,6 +577,10 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
 }
 
 // ------------------------------------------------------------------ attention (exact)
+// Reference-order decode attention (model.rs:218-233, ops.rs:7-36, 112-128) in three
+// launches: scores in parallel over the context, the softmax of each head with a
+// sequential sum, then P.V as one sequential chain per output element.
+
 // ops::dot (ops.rs:7-36) of two hd-vectors in the reference order: four 8-lane FMA
 // accumulators over 32-wide steps, 8-wide tail on accumulator 0, then
 // ((a0+a1)+(a2+a3)) reduced as ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)), then a scalar tail.
@@ -530,93 +608,198 @@ __device__ inline float dot_wide_serial(const float *a, const float *b, uint32_t
     return s;
 }
 
-// Reference-order attention of one query head (model.rs:218-233, ops.rs:112-128): scores
-// in parallel, softmax with glibc-exact exp and a sequential sum, o accumulated
-// sequentially over positions, then the quantization of o for attn_output.
+// Scores s[h][t] = dot(q_h, K_t) * (1/sqrt(hd)) for the rep query heads of kv head g over
+// split s of the context (grid n_kv x S), the QK-norm + RoPE of q and k, the cache append by
+// the split holding pos, and the split maximum of every head.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_exact(const float *__restrict__ qkv, const float *__restrict__ qn,
-                                                    const float *__restrict__ kn, float eps,
-                                                    const float *__restrict__ cs, const float *__restrict__ sn,
-                                                    const StepParams *p, float *kc, float *vc, uint32_t cap,
-                                                    uint32_t n_heads, uint32_t n_kv, float *scratch,
-                                                    float *o_out, uint8_t *q_out, float *d_out) {
-    constexpr uint32_t CH = 2048;
-    __shared__ __align__(16) float raw[3 * HD];
-    __shared__ __align__(16) float rot[2 * HD];
-    __shared__ float tmp[2 * HD];
-    __shared__ float buf[CH];
-    __shared__ float red[4];
-    __shared__ float s_m, s_sum;
-    __shared__ __align__(16) float ov[HD];
+__global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ qkv, const float *__restrict__ qn,
+                                                     const float *__restrict__ kn, float eps,
+                                                     const float *__restrict__ cs, const float *__restrict__ sn,
+                                                     const StepParams *p, float *kc, float *vc, uint32_t cap,
+                                                     uint32_t n_heads, uint32_t n_kv, uint32_t S, float *scores,
+                                                     float *pmax) {
+    constexpr int MAXREP = 8;
+    __shared__ __align__(16) float raw[(MAXREP + 2) * HD];
+    __shared__ __align__(16) float rot[(MAXREP + 1) * HD];
+    __shared__ float tmp[4 * HD];
+    __shared__ float red[4][MAXREP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t hq = blockIdx.x, rep = n_heads / n_kv, g = hq / rep;
+    const uint32_t g = blockIdx.x, s = blockIdx.y;
+    const uint32_t rep = n_heads / n_kv;
     const uint32_t pos = p->pos, n = pos + 1;
+    const uint32_t chunk = div_up(n, S);
+    const uint32_t t0 = s * chunk, t1 = min(n, t0 + chunk);
     const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
+    for (uint32_t i = tid; i < rep * HD; i += 256) raw[i] = qkv[g * rep * HD + i];
     for (uint32_t i = tid; i < HD; i += 256) {
-        raw[i] = qkv[hq * HD + i];
-        raw[HD + i] = qkv[qd + g * HD + i];
-        raw[2 * HD + i] = qkv[qd + kvd + g * HD + i];
+        raw[rep * HD + i] = qkv[qd + g * HD + i];
+        raw[(rep + 1) * HD + i] = qkv[qd + kvd + g * HD + i];
     }
     __syncthreads();
-    if (wave < 2) norm_rope_head(raw + wave * HD, rot + wave * HD, wave == 0 ? qn : kn, eps, HD, cs, sn, pos, tmp + wave * HD, lane);
+    for (uint32_t vi = wave; vi <= rep; vi += 4)
+        norm_rope_head(raw + vi * HD, rot + vi * HD, vi < rep ? qn : kn, eps, HD, cs, sn, pos, tmp + wave * HD, lane);
     __syncthreads();
-    const float *q = rot, *knew = rot + HD, *vnew = raw + 2 * HD;
+    const float *krot = rot + rep * HD;
     float *kcg = kc + (size_t)g * cap * HD;
     float *vcg = vc + (size_t)g * cap * HD;
-    if (hq % rep == 0)
+    if (t0 <= pos && pos < t1)
         for (uint32_t i = tid; i < HD; i += 256) {
-            kcg[(size_t)pos * HD + i] = knew[i];
-            vcg[(size_t)pos * HD + i] = vnew[i];
+            kcg[(size_t)pos * HD + i] = krot[i];
+            vcg[(size_t)pos * HD + i] = raw[(rep + 1) * HD + i];
         }
-    float *sc = scratch + (size_t)hq * cap;
     const float scale = 1.0f / sqrtf((float)HD);
-    float m = -__builtin_huge_valf();
-    for (uint32_t t = tid; t < n; t += 256) {
-        const float *kt = (t == pos) ? knew : kcg + (size_t)t * HD;
-        const float v = dot_wide_serial(q, kt, HD) * scale;
-        sc[t] = v;
-        m = fmaxf(m, v);
+    float mx[MAXREP];
+#pragma unroll
+    for (int r = 0; r < MAXREP; ++r) mx[r] = -__builtin_huge_valf();
+    for (uint32_t t = t0 + tid; t < t1; t += 256) {
+        float kt[HD];
+        const float *src = (t == pos) ? krot : kcg + (size_t)t * HD;
+#pragma unroll
+        for (int i = 0; i < HD; i += 4) *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(src + i);
+#pragma unroll
+        for (int r = 0; r < MAXREP; ++r) {
+            if (r < (int)rep) {
+                const float v = dot_wide_serial(rot + r * HD, kt, HD) * scale;
+                scores[(size_t)(g * rep + r) * cap + t] = v;
+                mx[r] = fmaxf(mx[r], v);
+            }
+        }
     }
-    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
-    if (lane == 0) red[wave] = m;
+#pragma unroll
+    for (int r = 0; r < MAXREP; ++r) {
+        if (r < (int)rep) {
+            float m = mx[r];
+            for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
+            if (lane == 0) red[wave][r] = m;
+        }
+    }
     __syncthreads();
-    if (tid == 0) s_m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    m = s_m;
-    for (uint32_t t = tid; t < n; t += 256) sc[t] = hg_expf(sc[t] - m);
-    __syncthreads();
-    // sum = e_0 + e_1 + ... in order (ops.rs:120-123), staged through LDS
+    if ((uint32_t)tid < rep)
+        pmax[(size_t)(g * rep + tid) * S + s] = fmaxf(fmaxf(red[0][tid], red[1][tid]), fmaxf(red[2][tid], red[3][tid]));
+}
+
+// Softmax of one head (ops.rs:112-128): m = max, e_t = exp(s_t - m) with the reference
+// expf, sum = e_0 + e_1 + ... sequentially, p_t = e_t * (1/sum), written over the scores.
+// Grid: n_heads workgroups of 256; the context is processed in LDS chunks.
+__global__ __launch_bounds__(256) void k_attn_softmax(float *scores, const float *__restrict__ pmax,
+                                                      const StepParams *p, uint32_t cap, uint32_t S) {
+    constexpr uint32_t CH = 4096;
+    __shared__ __align__(16) float buf[CH];
+    __shared__ float s_sum;
+    const int tid = threadIdx.x;
+    const uint32_t h = blockIdx.x, n = p->pos + 1;
+    float *sc = scores + (size_t)h * cap;
+    float m = -__builtin_huge_valf();
+    for (uint32_t s = 0; s < S; ++s) m = fmaxf(m, pmax[(size_t)h * S + s]);
     float sum = 0.0f;
     for (uint32_t c0 = 0; c0 < n; c0 += CH) {
         const uint32_t cl = min(CH, n - c0);
-        for (uint32_t i = tid; i < cl; i += 256) buf[i] = sc[c0 + i];
+        for (uint32_t i = tid; i < cl; i += 256) {
+            const float e = hg_expf(sc[c0 + i] - m);
+            buf[i] = e;
+            sc[c0 + i] = e;
+        }
         __syncthreads();
-        if (tid == 0)
-            for (uint32_t i = 0; i < cl; ++i) sum = sum + buf[i];
+        if (tid == 0) sum = seq_sum_lds(buf, cl, sum);
         __syncthreads();
     }
     if (tid == 0) s_sum = sum;
     __syncthreads();
     const float inv = 1.0f / s_sum;
     for (uint32_t t = tid; t < n; t += 256) sc[t] = sc[t] * inv;
+}
+
+// P.V of one head (model.rs:227-232): o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ...
+// One workgroup of 16 waves per head.  The first HD/64 waves run the sequential chains (lane =
+// output element); every other wave is a producer: producer w forms the rounded products
+// p_t * v_t[di] (the reference's separate multiply) of tiles w, w+NP, w+2NP, ... of PV_T
+// positions into a ring of PV_R LDS slots.  Slot readiness and consumption are LDS flags at
+// workgroup scope, so up to NP tiles are in flight while the chain does one LDS read and one
+// add per position.  Every wait is bounded: tile k only waits for tile k - PV_R to be consumed,
+// and the chain only for tile k to be produced.  Also writes o and its quantization.
+template <int HD> struct PvCfg {
+    static constexpr uint32_t T = 2048 / HD;  // positions per tile: an 8 KiB slot
+    static constexpr uint32_t R = 16;         // ring slots (128 KiB)
+};
+
+template <int HD>
+__global__ __launch_bounds__(1024) void k_attn_pv(const float *__restrict__ probs, const float *__restrict__ qkv,
+                                                  const StepParams *p, const float *__restrict__ vc, uint32_t cap,
+                                                  uint32_t n_heads, uint32_t n_kv, float *o_out, uint8_t *q_out,
+                                                  float *d_out) {
+    constexpr uint32_t T = PvCfg<HD>::T, R = PvCfg<HD>::R;
+    constexpr int NCW = HD > 64 ? HD / 64 : 1;   // chain waves
+    constexpr int NP = 16 - NCW;                 // producer waves
+    extern __shared__ __align__(16) float ring[];  // [R][T*HD]
+    __shared__ uint32_t ready[R];
+    __shared__ uint32_t done[NCW];
+    __shared__ __align__(16) float ov[HD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t h = blockIdx.x, rep = n_heads / n_kv, g = h / rep;
+    const uint32_t pos = p->pos, n = pos + 1;
+    const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
+    const float *pr = probs + (size_t)h * cap;
+    const float *vcg = vc + (size_t)g * cap * HD;
+    const float *vnew = qkv + qd + kvd + g * HD;  // row pos, appended this step
+    const uint32_t ntiles = div_up(n, T);
+    if (tid < (int)R) ready[tid] = 0;
+    if (tid < NCW) done[tid] = 0;
     __syncthreads();
-    // o[di] += p_t * v_t[di] over t in order (model.rs:227-232)
-    float o = 0.0f;
-    for (uint32_t c0 = 0; c0 < n; c0 += CH) {
-        const uint32_t cl = min(CH, n - c0);
-        for (uint32_t i = tid; i < cl; i += 256) buf[i] = sc[c0 + i];
-        __syncthreads();
-        if (tid < (int)HD)
-            for (uint32_t i = 0; i < cl; ++i) {
-                const uint32_t t = c0 + i;
-                const float vt = (t == pos) ? vnew[tid] : vcg[(size_t)t * HD + tid];
-                o = o + buf[i] * vt;
+    if (wave >= NCW) {
+        const int pw = wave - NCW;
+        constexpr uint32_t EPL = T * HD / 64;  // products per lane per tile
+        for (uint32_t k = pw; k < ntiles; k += NP) {
+            const uint32_t base = k * T;
+            float v[EPL];
+#pragma unroll
+            for (uint32_t u = 0; u < EPL; ++u) {
+                const uint32_t e = u * 64 + lane, tt = e / HD, di = e % HD, t = base + tt;
+                const uint32_t tc = min(t, n - 1);
+                v[u] = (tc == pos) ? vnew[di] : vcg[(size_t)tc * HD + di];
             }
-        __syncthreads();
-    }
-    if (tid < (int)HD) {
-        ov[tid] = o;
-        if (o_out) o_out[hq * HD + tid] = o;
+            float pv[EPL];
+#pragma unroll
+            for (uint32_t u = 0; u < EPL; ++u) {
+                const uint32_t e = u * 64 + lane, t = base + e / HD;
+                pv[u] = pr[min(t, n - 1)];
+            }
+            // the slot of tile k was last used by tile k - R
+            if (k >= R)
+                for (int c = 0; c < NCW; ++c)
+                    while (__hip_atomic_load(&done[c], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < k - R + 1)
+                        __builtin_amdgcn_s_sleep(1);
+            float *slot = ring + (size_t)(k % R) * T * HD;
+#pragma unroll
+            for (uint32_t u = 0; u < EPL; ++u) {
+                const uint32_t e = u * 64 + lane;
+                slot[e] = (base + e / HD < n) ? pv[u] * v[u] : 0.0f;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0) __hip_atomic_store(&ready[k % R], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    } else {
+        const uint32_t di = wave * 64 + lane;
+        float o = 0.0f;
+        for (uint32_t k = 0; k < ntiles; ++k) {
+            while (__hip_atomic_load(&ready[k % R], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != k + 1)
+                __builtin_amdgcn_s_sleep(1);
+            const float *slot = ring + (size_t)(k % R) * T * HD;
+            const uint32_t len = min(T, n - k * T);
+            if (di < HD) {
+                if (len == T) {
+#pragma unroll 16
+                    for (uint32_t tt = 0; tt < T; ++tt) o = o + slot[tt * HD + di];
+                } else {
+                    for (uint32_t tt = 0; tt < len; ++tt) o = o + slot[tt * HD + di];
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0) __hip_atomic_store(&done[wave], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        if (di < HD) {
+            ov[di] = o;
+            if (o_out) o_out[h * HD + di] = o;
+        }
     }
     __syncthreads();
     const uint32_t nbh = HD / QK;
@@ -626,11 +809,11 @@ __global__ __launch_bounds__(256) void k_attn_exact(const float *__restrict__ qk
         float v[4];
 #pragma unroll
         for (int mm = 0; mm < 4; ++mm) v[mm] = ov[bl * QK + j * 4 + mm];
-        quant_block_lane(v, j, hq * nbh + bl, q_out, d_out);
+        quant_block_lane(v, j, h * nbh + bl, q_out, d_out);
     }
-    if (hq == 0) {
+    if (h == 0) {
         const uint32_t nb = n_heads * HD / QK;
-        zero_pad(nb, div_up(nb, 4), q_out, d_out, tid, 256);
+        zero_pad(nb, div_up(nb, 4), q_out, d_out, tid, 1024);
     }
 }
 
@@ -648,35 +831,17 @@ __global__ __launch_bounds__(1024) void k_ffn_router(const float *__restrict__ x
                                                      uint8_t *q_out, float *d_out, uint32_t *topk_idx,
                                                      float *topk_w, uint32_t *order, uint32_t *rec_idx,
                                                      float *rec_w) {
-    extern __shared__ float hs[];  // d floats
+    extern __shared__ __align__(16) float hs[];  // 2*d floats: x / h, then the squares
     __shared__ float red[16];
-    __shared__ float s_scale;
+    __shared__ float s_ss;
     __shared__ float lg[256], scr[256], sel[256];
     __shared__ uint32_t tk[64];
     __shared__ float tw[64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     for (uint32_t i = tid; i < d; i += 1024) hs[i] = x[i];
     __syncthreads();
-    if (EXACT) {
-        if (tid == 0) {
-            float ss = 0.0f;
-            for (uint32_t i = 0; i < d; ++i) ss = ss + hs[i] * hs[i];
-            s_scale = 1.0f / sqrtf(ss / (float)d + eps);
-        }
-    } else {
-        float ss = 0.0f;
-        for (uint32_t i = tid; i < d; i += 1024) ss += hs[i] * hs[i];
-        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        if (tid == 0) {
-            float t = 0.0f;
-            for (int i = 0; i < 16; ++i) t += red[i];
-            s_scale = 1.0f / sqrtf(t / (float)d + eps);
-        }
-    }
-    __syncthreads();
-    const float scale = s_scale;
+    const float ss = sum_squares<EXACT>(hs, hs + d, d, tid, 1024, red, &s_ss);
+    const float scale = 1.0f / sqrtf(ss / (float)d + eps);
     for (uint32_t i = tid; i < d; i += 1024) hs[i] = hs[i] * scale * w[i];
     __syncthreads();
     {
@@ -753,15 +918,11 @@ __global__ __launch_bounds__(1024) void k_ffn_router(const float *__restrict__ x
             rec_w[r] = wr;
         }
         // slot order by ascending expert id (the prompt path's accumulation order)
-        uint32_t ord[64];
-        for (uint32_t r = 0; r < top_k; ++r) ord[r] = r;
-        for (uint32_t a = 1; a < top_k; ++a) {
-            const uint32_t v = ord[a];
-            uint32_t b = a;
-            while (b > 0 && tk[ord[b - 1]] > tk[v]) { ord[b] = ord[b - 1]; --b; }
-            ord[b] = v;
+        for (uint32_t r = 0; r < top_k; ++r) {
+            uint32_t rank = 0;
+            for (uint32_t q = 0; q < top_k; ++q) rank += tk[q] < tk[r];
+            order[rank] = r;
         }
-        for (uint32_t r = 0; r < top_k; ++r) order[r] = ord[r];
     }
 }
 
@@ -769,7 +930,7 @@ __global__ __launch_bounds__(1024) void k_ffn_router(const float *__restrict__ x
 // Gate and up rows of every active expert slot and a = silu(g)*u (model.rs:301-305,
 // 314-318; dense: 247-251).  blockIdx.y = slot: slots < top_k are routed experts
 // (topk_idx), the next one the shared expert (or the dense FFN).  8 rows per workgroup.
-template <int ORDER>
+template <int ORDER, bool SCF32, int NCT>
 __global__ __launch_bounds__(64) void k_ffn_gateup(Q8Mat Wg, Q8Mat Wu, Q8Mat Sg, Q8Mat Su,
                                                    const uint32_t *__restrict__ topk_idx, uint32_t top_k,
                                                    uint32_t f, const uint8_t *__restrict__ gq,
@@ -778,31 +939,31 @@ __global__ __launch_bounds__(64) void k_ffn_gateup(Q8Mat Wg, Q8Mat Wu, Q8Mat Sg,
     uint8_t *sq = smem;
     float *sd = reinterpret_cast<float *>(smem + Wg.nc * CHUNK_BYTES);
     const int tid = threadIdx.x;
-    stage_act(gq, gd, Wg.nc, sq, sd, tid, 64);
-    __syncthreads();
     const uint32_t slot = blockIdx.y;
     const uint32_t i = blockIdx.x * 8 + (tid >> 3);
+    const uint32_t li = min(i, f - 1);
     const int j = tid & 7;
-    if (i >= f) return;
-    float g, u;
-    if (slot < top_k) {
-        const uint32_t r = topk_idx[slot] * f + i;
-        g = q8_row_dot<ORDER>(row_qs(Wg, r), row_sc(Wg, r), Wg.sc_f32, sq, sd, Wg.nb, Wg.nc, j);
-        u = q8_row_dot<ORDER>(row_qs(Wu, r), row_sc(Wu, r), Wu.sc_f32, sq, sd, Wu.nb, Wu.nc, j);
-    } else {
-        g = q8_row_dot<ORDER>(row_qs(Sg, i), row_sc(Sg, i), Sg.sc_f32, sq, sd, Sg.nb, Sg.nc, j);
-        u = q8_row_dot<ORDER>(row_qs(Su, i), row_sc(Su, i), Su.sc_f32, sq, sd, Su.nb, Su.nc, j);
-    }
-    if (j == 0) a_out[(size_t)slot * f + i] = hg_silu(g) * u;
+    const bool routed = slot < top_k;
+    const Q8Mat &G = routed ? Wg : Sg;
+    const Q8Mat &U = routed ? Wu : Su;
+    const uint32_t r = routed ? topk_idx[slot] * f + li : li;
+    Q8Row<ORDER, SCF32, NCT> rg, ru;
+    rg.begin(row_qs(G, r), row_sc<SCF32>(G, r), G.nb, G.nc, j);
+    ru.begin(row_qs(U, r), row_sc<SCF32>(U, r), U.nb, U.nc, j);
+    stage_act(gq, gd, Wg.nc, sq, sd, tid, 64);
+    __syncthreads();
+    const float g = rg.finish(sq, sd);
+    const float u = ru.finish(sq, sd);
+    if (i < f && j == 0) a_out[(size_t)slot * f + i] = hg_silu(g) * u;
 }
 
 // Down rows of every slot and the fixed-order combination (model.rs:306-323; dense:
 // 253-254), then the residual add x += ffn (model.rs:173-176).  One wave per slot; each
-// wave first quantizes its slot's activation a[slot] (quant.rs:111-123) into LDS.
+// wave quantizes its slot's activation a[slot] (quant.rs:111-123) into LDS.
 //   decode:  out = ((0 + w_0 y_0) + w_1 y_1 ...) + y_shared    (rank order)
 //   prefill: the same sum in ascending expert-id order (model.rs:707-731)
 //   dense:   x += y
-template <int ORDER>
+template <int ORDER, bool SCF32, int NCT>
 __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uint32_t *__restrict__ topk_idx,
                                                    const float *__restrict__ topk_w,
                                                    const uint32_t *__restrict__ order, uint32_t top_k,
@@ -816,9 +977,16 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
     const uint32_t slot = wave;
     uint8_t *sq = smem + per * slot;
     float *sd = reinterpret_cast<float *>(sq + (size_t)nc * CHUNK_BYTES);
-    if (slot < n_slots) {
+    const uint32_t r = blockIdx.x * 8 + (lane >> 3);
+    const uint32_t lr = min(r, d - 1);
+    const int j = lane & 7;
+    const bool routed = slot < top_k;
+    const Q8Mat &D = routed ? Wd : Sd;
+    const uint32_t row = routed ? topk_idx[slot] * d + lr : lr;
+    Q8Row<ORDER, SCF32, NCT> rd;
+    rd.begin(row_qs(D, row), row_sc<SCF32>(D, row), nb, nc, j);
+    {
         const float *as = a + (size_t)slot * f;
-        const int j = lane & 7;
         for (uint32_t b0 = 0; b0 < nb; b0 += 8) {
             const uint32_t b = b0 + (lane >> 3);
             if (b < nb) {
@@ -831,18 +999,8 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
         zero_pad(nb, nc, sq, sd, lane, 64);
     }
     __syncthreads();
-    const uint32_t r = blockIdx.x * 8 + (lane >> 3);
-    const int j = lane & 7;
-    if (slot < n_slots && r < d) {
-        float y;
-        if (slot < top_k) {
-            const uint32_t row = topk_idx[slot] * d + r;
-            y = q8_row_dot<ORDER>(row_qs(Wd, row), row_sc(Wd, row), Wd.sc_f32, sq, sd, nb, nc, j);
-        } else {
-            y = q8_row_dot<ORDER>(row_qs(Sd, r), row_sc(Sd, r), Sd.sc_f32, sq, sd, nb, nc, j);
-        }
-        if (j == 0) ys[slot * 8 + (lane >> 3)] = y;
-    }
+    const float y = rd.finish(sq, sd);
+    if (j == 0) ys[slot * 8 + (lane >> 3)] = y;
     __syncthreads();
     if (tid < 8) {
         const uint32_t rr = blockIdx.x * 8 + tid;
@@ -865,6 +1023,31 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
 // ====================================================================== launchers
 #define LAUNCH(kern, grid, block, shm, st, ...) hipLaunchKernelGGL(kern, grid, block, shm, st, __VA_ARGS__)
 
+// Kernels whose LDS exceeds the 64 KiB default opt in to the larger gfx950 allocation.
+hipError_t init_kernel_attributes() {
+    hipError_t e = hipSuccess;
+#define PV_ATTR(HD)                                                                                         \
+    if (e == hipSuccess)                                                                                    \
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_pv<HD>),                             \
+                                hipFuncAttributeMaxDynamicSharedMemorySize,                                 \
+                                (int)(PvCfg<HD>::R * PvCfg<HD>::T * HD * sizeof(float)));
+    PV_ATTR(32) PV_ATTR(64) PV_ATTR(128)
+#undef PV_ATTR
+    return e;
+}
+
+// Chunks per load batch of a row of nc chunks.
+static int nct_of(uint32_t nc) { return nc >= 8 ? 8 : nc >= 4 ? 4 : nc >= 2 ? 2 : 1; }
+
+// Instantiate F<NCT> for the runtime batch size.
+#define DISPATCH_NCT(nc, F)                  \
+    switch (nct_of(nc)) {                    \
+    case 8: F(8); break;                     \
+    case 4: F(4); break;                     \
+    case 2: F(2); break;                     \
+    default: F(1); break;                    \
+    }
+
 void launch_embed(hipStream_t st, const float *emb, uint32_t d, const StepParams *p, float *x) {
     LAUNCH(k_embed, dim3(div_up(d, 256)), dim3(256), 0, st, emb, d, p, x);
 }
@@ -875,7 +1058,7 @@ void launch_advance(hipStream_t st, StepParams *p) { LAUNCH(k_advance, dim3(1), 
 
 void launch_rmsnorm_quant(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,
                           float *h, uint8_t *q, float *dq) {
-    const size_t shm = d * sizeof(float);
+    const size_t shm = 2 * d * sizeof(float);
     if (exact) LAUNCH(k_rmsnorm_quant<true>, dim3(1), dim3(256), shm, st, x, w, eps, d, h, q, dq);
     else LAUNCH(k_rmsnorm_quant<false>, dim3(1), dim3(256), shm, st, x, w, eps, d, h, q, dq);
 }
@@ -886,11 +1069,23 @@ void launch_quant_vec(hipStream_t st, const float *x, uint32_t n, uint8_t *q, fl
 
 uint32_t matvec_blocks(uint32_t N, uint32_t threads) { return div_up(N, threads / 8); }
 
-void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uint8_t *q, const float *dq, float *y,
-                   uint32_t threads, uint32_t valid, float *pv, uint32_t *pi) {
+template <int ORDER, int EPI, bool SCF32>
+static void mv_launch(hipStream_t st, const Q8Mat &W, const uint8_t *q, const float *dq, float *y, uint32_t threads,
+                      uint32_t valid, float *pv, uint32_t *pi) {
     const dim3 grid(matvec_blocks(W.N, threads)), block(threads);
     const size_t shm = (size_t)W.nc * CHUNK_BYTES + (size_t)W.nc * 4 * sizeof(float);
-#define MV(O, E) LAUNCH((k_matvec<O, E>), grid, block, shm, st, W, q, dq, y, valid, pv, pi)
+#define MVK(N) LAUNCH((k_matvec<ORDER, EPI, SCF32, N>), grid, block, shm, st, W, q, dq, y, valid, pv, pi)
+    DISPATCH_NCT(W.nc, MVK)
+#undef MVK
+}
+
+void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uint8_t *q, const float *dq, float *y,
+                   uint32_t threads, uint32_t valid, float *pv, uint32_t *pi) {
+#define MV(O, E)                                                                   \
+    do {                                                                           \
+        if (W.sc_f32) mv_launch<O, E, true>(st, W, q, dq, y, threads, valid, pv, pi);  \
+        else mv_launch<O, E, false>(st, W, q, dq, y, threads, valid, pv, pi);          \
+    } while (0)
     if (order == ORDER_DECODE) {
         if (epi == EPI_STORE) MV(ORDER_DECODE, EPI_STORE);
         else if (epi == EPI_RESID) MV(ORDER_DECODE, EPI_RESID);
@@ -915,38 +1110,48 @@ size_t attn_fast_shm(uint32_t hd, uint32_t rep, uint32_t cap, uint32_t S) {
     return floats * sizeof(float);
 }
 
+template <int HD>
+static void attn_exact_launch(hipStream_t st, const float *qkv, const float *qn, const float *kn, float eps,
+                              const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
+                              uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part,
+                              float *scratch, float *o_out, uint8_t *q_out, float *d_out) {
+    LAUNCH(k_attn_scores<HD>, dim3(n_kv, S), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
+           n_kv, S, scratch, part);
+    LAUNCH(k_attn_softmax, dim3(n_heads), dim3(256), 0, st, scratch, part, p, cap, S);
+    const size_t shm = (size_t)PvCfg<HD>::R * PvCfg<HD>::T * HD * sizeof(float);
+    LAUNCH(k_attn_pv<HD>, dim3(n_heads), dim3(1024), shm, st, scratch, qkv, p, vc, cap, n_heads, n_kv, o_out, q_out,
+           d_out);
+}
+
+template <int HD>
+static void attn_fast_launch(hipStream_t st, const float *qkv, const float *qn, const float *kn, float eps,
+                             const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
+                             uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *o_out,
+                             uint8_t *q_out, float *d_out) {
+    const size_t shm = attn_fast_shm(HD, n_heads / n_kv, cap, S);
+    LAUNCH(k_attn_fast<HD>, dim3(n_kv, S), dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
+           n_kv, S, part);
+    LAUNCH(k_attn_combine<HD>, dim3(1), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
+}
+
 bool launch_attn(hipStream_t st, bool exact, uint32_t hd, const float *qkv, const float *qn, const float *kn,
                  float eps, const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
                  uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,
                  float *o_out, uint8_t *q_out, float *d_out) {
-    const uint32_t rep = n_heads / n_kv;
-    if (exact) {
-        if (hd == 64)
-            LAUNCH(k_attn_exact<64>, dim3(n_heads), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
-                   n_kv, scratch, o_out, q_out, d_out);
-        else if (hd == 128)
-            LAUNCH(k_attn_exact<128>, dim3(n_heads), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap,
-                   n_heads, n_kv, scratch, o_out, q_out, d_out);
-        else if (hd == 32)
-            LAUNCH(k_attn_exact<32>, dim3(n_heads), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap,
-                   n_heads, n_kv, scratch, o_out, q_out, d_out);
-        else return false;
-        return true;
-    }
-    const size_t shm = attn_fast_shm(hd, rep, cap, S);
-    const dim3 grid(n_kv, S);
-    if (hd == 64) {
-        LAUNCH(k_attn_fast<64>, grid, dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part);
-        LAUNCH(k_attn_combine<64>, dim3(1), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
-    } else if (hd == 128) {
-        LAUNCH(k_attn_fast<128>, grid, dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part);
-        LAUNCH(k_attn_combine<128>, dim3(1), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
-    } else if (hd == 32) {
-        LAUNCH(k_attn_fast<32>, grid, dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part);
-        LAUNCH(k_attn_combine<32>, dim3(1), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
-    } else {
-        return false;
-    }
+#define ATTN(HD)                                                                                                    \
+    do {                                                                                                            \
+        if (exact)                                                                                                  \
+            attn_exact_launch<HD>(st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part, scratch,    \
+                                  o_out, q_out, d_out);                                                             \
+        else                                                                                                        \
+            attn_fast_launch<HD>(st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part, o_out,       \
+                                 q_out, d_out);                                                                     \
+    } while (0)
+    if (hd == 64) ATTN(64);
+    else if (hd == 128) ATTN(128);
+    else if (hd == 32) ATTN(32);
+    else return false;
+#undef ATTN
     return true;
 }
 
@@ -954,7 +1159,7 @@ void launch_ffn_router(hipStream_t st, bool exact, const float *x, const float *
                        const float *Wr, const float *bias, uint32_t E, uint32_t top_k, int gating_sigmoid,
                        int weights_norm, float weights_scale, uint8_t *q, float *dq, uint32_t *topk_idx,
                        float *topk_w, uint32_t *order, uint32_t *rec_idx, float *rec_w) {
-    const size_t shm = d * sizeof(float);
+    const size_t shm = 2 * d * sizeof(float);
     if (exact)
         LAUNCH(k_ffn_router<true>, dim3(1), dim3(1024), shm, st, x, w, eps, d, Wr, bias, E, top_k, gating_sigmoid,
                weights_norm, weights_scale, q, dq, topk_idx, topk_w, order, rec_idx, rec_w);
@@ -963,29 +1168,51 @@ void launch_ffn_router(hipStream_t st, bool exact, const float *x, const float *
                weights_norm, weights_scale, q, dq, topk_idx, topk_w, order, rec_idx, rec_w);
 }
 
+template <int ORDER, bool SCF32>
+static void gateup_launch(hipStream_t st, const Q8Mat &Wg, const Q8Mat &Wu, const Q8Mat &Sg, const Q8Mat &Su,
+                          const uint32_t *topk_idx, uint32_t top_k, uint32_t n_slots, uint32_t f, const uint8_t *q,
+                          const float *dq, float *a) {
+    const dim3 grid(div_up(f, 8), n_slots);
+    const size_t shm = (size_t)Wg.nc * CHUNK_BYTES + (size_t)Wg.nc * 4 * sizeof(float);
+#define GUK(N) LAUNCH((k_ffn_gateup<ORDER, SCF32, N>), grid, dim3(64), shm, st, Wg, Wu, Sg, Su, topk_idx, top_k, f, q, dq, a)
+    DISPATCH_NCT(Wg.nc, GUK)
+#undef GUK
+}
+
 void launch_ffn_gateup(hipStream_t st, int order, const Q8Mat &Wg, const Q8Mat &Wu, const Q8Mat &Sg,
                        const Q8Mat &Su, const uint32_t *topk_idx, uint32_t top_k, uint32_t n_slots, uint32_t f,
                        const uint8_t *q, const float *dq, float *a) {
-    const dim3 grid(div_up(f, 8), n_slots);
-    const size_t shm = (size_t)Wg.nc * CHUNK_BYTES + (size_t)Wg.nc * 4 * sizeof(float);
-    if (order == ORDER_DECODE)
-        LAUNCH(k_ffn_gateup<ORDER_DECODE>, grid, dim3(64), shm, st, Wg, Wu, Sg, Su, topk_idx, top_k, f, q, dq, a);
-    else
-        LAUNCH(k_ffn_gateup<ORDER_PREFILL>, grid, dim3(64), shm, st, Wg, Wu, Sg, Su, topk_idx, top_k, f, q, dq, a);
+    if (order == ORDER_DECODE) {
+        if (Wg.sc_f32) gateup_launch<ORDER_DECODE, true>(st, Wg, Wu, Sg, Su, topk_idx, top_k, n_slots, f, q, dq, a);
+        else gateup_launch<ORDER_DECODE, false>(st, Wg, Wu, Sg, Su, topk_idx, top_k, n_slots, f, q, dq, a);
+    } else {
+        if (Wg.sc_f32) gateup_launch<ORDER_PREFILL, true>(st, Wg, Wu, Sg, Su, topk_idx, top_k, n_slots, f, q, dq, a);
+        else gateup_launch<ORDER_PREFILL, false>(st, Wg, Wu, Sg, Su, topk_idx, top_k, n_slots, f, q, dq, a);
+    }
+}
+
+template <int ORDER, bool SCF32>
+static void down_launch(hipStream_t st, const Q8Mat &Wd, const Q8Mat &Sd, const uint32_t *topk_idx,
+                        const float *topk_w, const uint32_t *ord, uint32_t top_k, uint32_t n_slots, int dense,
+                        uint32_t d, uint32_t f, const float *a, float *x) {
+    const size_t per = (size_t)Sd.nc * CHUNK_BYTES + (size_t)Sd.nc * 4 * sizeof(float);
+    const size_t shm = per * n_slots + (size_t)n_slots * 8 * sizeof(float);
+    const dim3 grid(div_up(d, 8)), block(64 * n_slots);
+#define DNK(N) LAUNCH((k_ffn_down<ORDER, SCF32, N>), grid, block, shm, st, Wd, Sd, topk_idx, topk_w, ord, top_k, n_slots, dense, d, f, a, x)
+    DISPATCH_NCT(Sd.nc, DNK)
+#undef DNK
 }
 
 void launch_ffn_down(hipStream_t st, int order, const Q8Mat &Wd, const Q8Mat &Sd, const uint32_t *topk_idx,
                      const float *topk_w, const uint32_t *ord, uint32_t top_k, uint32_t n_slots, int dense,
                      uint32_t d, uint32_t f, const float *a, float *x) {
-    const size_t per = (size_t)Sd.nc * CHUNK_BYTES + (size_t)Sd.nc * 4 * sizeof(float);
-    const size_t shm = per * n_slots + (size_t)n_slots * 8 * sizeof(float);
-    const dim3 grid(div_up(d, 8)), block(64 * n_slots);
-    if (order == ORDER_DECODE)
-        LAUNCH(k_ffn_down<ORDER_DECODE>, grid, block, shm, st, Wd, Sd, topk_idx, topk_w, ord, top_k, n_slots, dense, d,
-               f, a, x);
-    else
-        LAUNCH(k_ffn_down<ORDER_PREFILL>, grid, block, shm, st, Wd, Sd, topk_idx, topk_w, ord, top_k, n_slots, dense, d,
-               f, a, x);
+    if (order == ORDER_DECODE) {
+        if (Sd.sc_f32) down_launch<ORDER_DECODE, true>(st, Wd, Sd, topk_idx, topk_w, ord, top_k, n_slots, dense, d, f, a, x);
+        else down_launch<ORDER_DECODE, false>(st, Wd, Sd, topk_idx, topk_w, ord, top_k, n_slots, dense, d, f, a, x);
+    } else {
+        if (Sd.sc_f32) down_launch<ORDER_PREFILL, true>(st, Wd, Sd, topk_idx, topk_w, ord, top_k, n_slots, dense, d, f, a, x);
+        else down_launch<ORDER_PREFILL, false>(st, Wd, Sd, topk_idx, topk_w, ord, top_k, n_slots, dense, d, f, a, x);
+    }
 }
 
 }  // namespace hg

@@ -14,12 +14,15 @@
  *     shares Arc<Engine>, hobby-chat/src-tauri/src/server.rs:15,28-30).  An hg_kv owns a
  *     HIP stream, its KV cache and its scratch, and must be used by one thread at a time
  *     (the reference's &mut KvCache).
- *   - Numerics: the Q8_0 matvec reproduces qrow_dot_avx2's lane order and FMAs
- *     (quant.rs:44-67) and every other operation of the step except two follows the
- *     reference's operation order; RMSNorm's sum of squares and attention's softmax sum
- *     and P.V sum are reduced as trees, unless the cache is created with HG_KV_EXACT, in
- *     which case they run in the reference's sequential order and the logits, routing and
- *     cache contents are bit-identical to hobby-rs's AVX2 path.
+ *   - Numerics: every operation of the step follows the reference's operation order: the
+ *     Q8_0 matvec reproduces qrow_dot_avx2's lane order and FMAs (quant.rs:44-67), ops::dot
+ *     its f32x8 accumulators, and RMSNorm's sum of squares and attention's softmax and P.V
+ *     sums run sequentially as in ops.rs / model.rs, with an expf equal to glibc's.  Logits,
+ *     expert routing and KV-cache contents are therefore bit-identical to hobby-rs's AVX2
+ *     path.  A cache created with HG_KV_FAST reassociates those three sums as trees; its
+ *     logits differ in the last bits, and because the sigmoid router selects experts by
+ *     gaps as small as 1e-4, such last-bit differences can flip a routing decision and
+ *     move the logits by percents: HG_KV_FAST is not a parity mode.
  */
 #ifndef HOBBY_GPU_H
 #define HOBBY_GPU_H
@@ -40,7 +43,9 @@ extern "C" {
 #define HG_ERR_NOMEM (-6)       /* device or host allocation failed */
 
 /* hg_kv_new flags */
-#define HG_KV_EXACT 1u /* reference-order (sequential) reductions: bit-identical to hobby-rs */
+#define HG_KV_FAST 1u /* tree reductions in RMSNorm and attention instead of the reference's
+                         sequential order: not bit-identical, and near-tied expert routing can
+                         then differ from hobby-rs (see the numerics note above) */
 
 typedef struct hg_model hg_model;
 typedef struct hg_kv hg_kv;
@@ -82,7 +87,7 @@ int hg_token_embedding(const hg_model *m, uint32_t id, float *out);
 /* ---- KV cache + decode step ---------------------------------------------------------- */
 
 /* KvCache::new (model.rs:67-74): a device-resident cache for max_ctx positions
- * (0 = context_length), layer-major, head-major within a layer. */
+ * (0 = context_length), layer-major, head-major within a layer.  flags: 0 or HG_KV_FAST. */
 int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out);
 void hg_kv_free(hg_kv *kv);
 /* KvCache.len (model.rs:63) */
@@ -147,7 +152,7 @@ int hg_q8_tensor_matvec_gather(const hg_q8_tensor *t, uint32_t rows_per_mat, con
  * projection: QK-norm (model.rs:753-763) and RoPE (ops.rs:139-166, theta, table of
  * rope_len positions) on q[n_heads*hd] and k[n_kv*hd], append of k and v at row pos of
  * the caches kc/vc ([pos+1][n_kv*hd] host arrays; rows < pos are inputs, row pos is
- * written), GQA attention over rows 0..pos, output out[n_heads*hd].  flags: HG_KV_EXACT. */
+ * written), GQA attention over rows 0..pos, output out[n_heads*hd].  flags: HG_KV_FAST. */
 int hg_attention_decode(const float *q, const float *k, const float *v, const float *q_norm,
                         const float *k_norm, float eps, float theta, uint32_t rope_len,
                         uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t pos, float *kc,

@@ -106,7 +106,7 @@ def _attn_case(orc, hg, ctx, exact, seed=0, nh=16, nkv=4, hd=64, theta=10000.0):
     kc_o, vc_o = kc.copy(), vc.copy()
     want, _, _ = orc.attention_decode(q, k, v, ones, ones, cos_t, sin_t, 1e-5, nh, nkv, hd, pos, kc_o, vc_o)
     kc_g, vc_g = kc.copy(), vc.copy()
-    got = hg.attention_decode(q, k, v, ones, ones, 1e-5, theta, ctx, nh, nkv, hd, pos, kc_g, vc_g, exact=exact)
+    got = hg.attention_decode(q, k, v, ones, ones, 1e-5, theta, ctx, nh, nkv, hd, pos, kc_g, vc_g, fast=not exact)
     assert _bits_equal(kc_g, kc_o) and _bits_equal(vc_g, vc_o)  # the append is bit-exact
     return got, want
 
