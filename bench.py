@@ -1,0 +1,219 @@
+#!/usr/bin/env python3
+"""Decode benchmark of the hobbylm sparse-MoE model on one MI355X.
+
+Workload: the 500M-shaped model (d1024, 24 layers, GQA 16q/4kv hd64, layer 0 dense FFN 4096,
+36 experts x 512 with top-6 + 1 shared, vocab 50257, tied embeddings), random-init Q8_0 GGUF
+from seed 1, batch 1.  A seeded 16-token prompt is prefilled, the model decodes greedily to
+position 2047 - steps, `warmup` of those steps run just before the timed window, and the
+timed window is the last `steps` greedy decode steps ending at position 2047 (context ~2k).
+Weights, the KV cache and the step's control block stay in HBM; the host collects the greedy
+tokens once at the end of the window.
+
+    python bench.py [--gpus 1] [--steps 256] [--warmup 16]
+
+Prints one JSON line.  Besides throughput it reports the per-kernel-class split of one step
+(HIP events on the cache's stream), the dominant kernel's roofline, the step's algorithmic
+HBM bandwidth, greedy-token parity with the committed oracle fixture, and a CPU baseline:
+the oracle (a C restatement of hobby-rs's AVX2 path) timed on this host's cores over a
+bounded sample of the same window, continuing from the GPU's KV cache.
+
+    python bench.py --window-stats <rocprofv3 dir>   per-kernel stats of the timed window
+"""
+import argparse
+import glob
+import json
+import os
+import sqlite3
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+CTX_END = 2048          # the timed window ends at position CTX_END - 1
+N_PROMPT = 16
+PEAK_HBM = 8.0e12       # MI355X HBM3E, bytes/s
+METRIC = "500M Q8_0 decode tok/s (bs1, ctx2k) + achieved HBM GB/s vs peak"
+
+
+def algorithmic_bytes(cfg, ctx):
+    """HBM bytes one decode step must read/write at context length ctx (positions 0..ctx-1).
+
+    Matrices at 34 B per 32 Q8_0 weights: QKV and attn_output every layer, the dense FFN in
+    the leading dense layers, top_k routed + the shared expert's gate/up/down in MoE layers,
+    the lm_head; the F32 router and bias, the norm gains, one F32 embedding row, the K/V row
+    appended per layer and the K/V rows read per layer."""
+    d, L, hd = cfg.d_model, cfg.n_layers, cfg.head_dim
+    qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    q8 = lambda n, k: n * k // 32 * 34
+    b = L * (q8(qd + 2 * kvd, d) + q8(d, qd))
+    b += cfg.n_dense * (2 * q8(cfg.dense_ffn, d) + q8(d, cfg.dense_ffn))
+    n_moe = L - cfg.n_dense
+    slots = cfg.top_k + (1 if cfg.n_shared else 0)
+    b += n_moe * slots * (2 * q8(cfg.expert_ffn, d) + q8(d, cfg.expert_ffn))
+    b += q8(cfg.vocab_size, d)
+    b += n_moe * (cfg.n_experts * d + cfg.n_experts) * 4            # router + bias
+    b += (2 * L + 1) * d * 4 + L * 2 * hd * 4                        # norm gains, QK-norm gains
+    b += d * 4                                                       # embedding row
+    b += L * 2 * kvd * 4                                             # KV append
+    b += L * 2 * kvd * 4 * ctx                                       # KV read
+    return b
+
+
+def attn_pv_bytes(cfg, ctx):
+    """Algorithmic bytes of one softmax+P.V launch (one layer, all heads): the scores and V
+    rows of every head's context (V of a kv group is shared by its query heads)."""
+    return cfg.n_heads * ctx * 4 + cfg.n_kv_heads * ctx * cfg.head_dim * 4
+
+
+def window_stats(prof_dir, steps):
+    """Per-kernel duration statistics over the dispatches of the last `steps` decode steps
+    of a rocprofv3 --kernel-trace run of this benchmark (one decode step ends with exactly one
+    k_argmax_final dispatch)."""
+    dbs = glob.glob(os.path.join(prof_dir, "**", "*.db"), recursive=True)
+    rows = sqlite3.connect(dbs[0]).execute("select name, start, end from kernels order by start").fetchall()
+    ends = [i for i, r in enumerate(rows) if "k_argmax_final" in r[0]]
+    lo = ends[-steps - 1] + 1 if len(ends) > steps else 0
+    agg = {}
+    for name, s, e in rows[lo:ends[-1] + 1]:
+        a = agg.setdefault(name, [0, 0.0])
+        a[0] += 1
+        a[1] += (e - s) / 1e3
+    tot = sum(v[1] for v in agg.values())
+    print(f"# rocprofv3 kernel stats over the last {steps} decode steps ({len(rows) - lo} dispatches)")
+    print(f"{'pct':>6} {'calls':>7} {'avg_us':>9} {'total_us':>11}  kernel")
+    for name, (c, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        print(f"{100 * t / tot:6.2f} {c:7d} {t / c:9.2f} {t:11.1f}  {name[:110]}")
+
+
+def cpu_baseline(path, gm, gkv, tokens, start, budget_s, max_steps):
+    """The oracle, continuing from the GPU's cache at position `start`, over the same tokens."""
+    import oracle
+    om = oracle.Model(path)
+    okv = om.new_cache()
+    c = gm.cfg
+    kvd = c.n_kv_heads * c.head_dim
+    K = np.empty((c.n_layers, start, kvd), np.float32)
+    V = np.empty_like(K)
+    for l in range(c.n_layers):
+        K[l], V[l] = gkv[l]
+    okv.load(K, V)
+    valid = min(c.vocab_size, 50257)
+    n = match = 0
+    t0 = time.perf_counter()
+    while n < max_steps and time.perf_counter() - t0 < budget_s:
+        lg = om.forward(int(tokens[n]), start + n, okv)
+        nxt = int(np.argmax(np.where(np.arange(c.vocab_size) < valid, lg, -np.inf)))
+        match += nxt == int(tokens[n + 1])
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": oracle.threads(), "kind": "port",
+            "sample": f"{n} greedy decode steps at positions {start}..{start + n - 1} (context ~2k) of the "
+                      f"same model, continuing from the GPU's KV cache; C restatement of hobby-rs's AVX2 "
+                      f"decode path, rows in parallel over {oracle.threads()} OpenMP threads",
+            "greedy_match": f"{match}/{n}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--window-stats", metavar="ROCPROF_DIR")
+    args = ap.parse_args()
+    if args.window_stats:
+        window_stats(args.window_stats, args.steps)
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this decode path does not shard (--gpus {args.gpus} requested)",
+              file=sys.stderr)
+        sys.exit(2)
+    steps, warmup = args.steps, args.warmup
+    start = CTX_END - steps
+    if start - warmup < N_PROMPT + 1:
+        sys.exit("--steps + --warmup leave no room for the prompt")
+
+    import torch
+    import hobbylm_amd as hg
+    from hobbylm_amd import gguf_synth as gs
+
+    path = gs.synth_path("500M", 1)
+    m = hg.Model(path)
+    cfg = m.cfg
+    kv = m.new_cache(max_ctx=CTX_END + 8)  # 8 spare rows for the profiling replay
+    prompt = gs.prompt_ids(1, N_PROMPT, 50257)
+    emb = np.stack([m.token_embedding(int(t)) for t in prompt])
+    _, first = m.prefill(emb, kv)
+    pre = m.decode_greedy(first, start - warmup - N_PROMPT, kv)
+    warm = m.decode_greedy(int(pre[-1]), warmup, kv)
+    assert kv.len == start
+    snap = [kv.read(l) for l in range(cfg.n_layers)] if not args.no_cpu else None
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ids = m.decode_greedy(int(warm[-1]), steps, kv)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tok_s = steps / dt
+
+    # parity of the whole greedy stream with the oracle's fixture
+    stream = [first] + [int(t) for t in pre] + [int(t) for t in warm] + [int(t) for t in ids]
+    fx = os.path.join(ROOT, "tests", "golden", "greedy_500M.json")
+    golden = None
+    if os.path.exists(fx):
+        g = json.load(open(fx))
+        n = min(len(g["tokens"]), len(stream))
+        golden = {"tokens_compared": n, "identical": g["tokens"][:n] == stream[:n]}
+
+    # per-kernel-class split of one step at the window's end (pos 2048, a spare row)
+    prof = m.profile_step(int(ids[-1]), kv, reps=10)
+    step_us = sum(v[0] for v in prof.values())
+    dom = max(prof, key=lambda k: prof[k][0])
+    mean_ctx = CTX_END - steps / 2.0
+    bytes_step = algorithmic_bytes(cfg, mean_ctx)
+    ach = bytes_step * tok_s
+    dom_us = prof[dom][0] / prof[dom][1]
+    if dom == "attn_softmax_pv":
+        dom_bytes = attn_pv_bytes(cfg, CTX_END + 1)
+        dom_note = "scores + V rows of all heads at context 2049 per launch (one layer)"
+    else:
+        dom_bytes = None
+        dom_note = "see DESIGN.md"
+    roof = None
+    if dom_bytes:
+        a = dom_bytes / (dom_us * 1e-6)
+        roof = {"bound": "hbm", "achieved": round(a / 1e9, 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                "frac": round(a / PEAK_HBM, 5), "traffic": None, "kernel": "k_attn_softmax_pv<64>",
+                "avg_launch_us": round(dom_us, 2), "bytes_per_launch": dom_bytes, "bytes_note": dom_note}
+
+    cpu = None
+    if not args.no_cpu:
+        all_tokens = [int(warm[-1])] + [int(t) for t in ids]
+        cpu = cpu_baseline(path, m, snap, all_tokens, start, args.cpu_seconds, steps)
+
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(dt * 1e3 / steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8xint8->f32 (Q8_0), f32 attention",
+        "data": "synthetic: random-init 500M-shaped Q8_0 GGUF (seed 1), seeded 16-token prompt",
+        "config": {"workload": f"hobbylm 500M-shaped sparse MoE, Q8_0, batch 1, greedy decode positions "
+                               f"{start}..{CTX_END - 1} after a 16-token prompt",
+                   "model": "hobbylm-500M-synthetic", "global_batch": 1, "seq_len": CTX_END,
+                   "parallelism": "none (1 GPU)", "kv_cache": "f32, layer-major, reference-order reductions"},
+        "step_bandwidth": {"algorithmic_bytes_per_token": bytes_step, "achieved_GBps": round(ach / 1e9, 2),
+                           "peak_GBps": PEAK_HBM / 1e9, "frac": round(ach / PEAK_HBM, 5)},
+        "roofline": roof,
+        "kernel_split_us": {k: round(v[0], 2) for k, v in sorted(prof.items(), key=lambda kv: -kv[1][0])},
+        "profiled_step_us": round(step_us, 1),
+        "parity": golden,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -68,6 +68,8 @@ SIGNATURES = {
     "hg_generate_greedy": (C.c_int, [_vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32,
                                      _u32p, C.POINTER(C.c_uint32)]),
     "hg_last_routing": (C.c_int, [_vp, _u32p, _f32p]),
+    "hg_profile_step": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, _f32p, _u32p]),
+    "hg_profile_class": (C.c_char_p, [C.c_uint32]),
     "hg_q8_tensor_quantize": (C.c_int, [_f32p, C.c_uint32, C.c_uint32, C.POINTER(_vp)]),
     "hg_q8_tensor_from_q8_0": (C.c_int, [_u8p, C.c_uint32, C.c_uint32, C.POINTER(_vp)]),
     "hg_q8_tensor_free": (None, [_vp]),
@@ -175,6 +177,15 @@ class Model:
         out = np.empty(max(n_steps, 1), np.uint32)
         _check(lib().hg_decode_greedy(self.h, cache.h, first_token, n_steps, out))
         return out[:n_steps]
+
+    def profile_step(self, token: int, cache: "KvCache", reps: int = 10) -> dict:
+        """Per-kernel-class microseconds of one decode step at pos = cache.len (HIP events on the
+        cache's stream); returns {class: (us_per_step, launches_per_step)}."""
+        n = 12
+        us = np.zeros(n, np.float32)
+        cnt = np.zeros(n, np.uint32)
+        _check(lib().hg_profile_step(self.h, cache.h, token, reps, us, cnt))
+        return {lib().hg_profile_class(c).decode(): (float(us[c]), int(cnt[c])) for c in range(n) if cnt[c]}
 
     def generate_greedy(self, prompt, max_new: int, cache: "KvCache", rep_penalty: float = 1.0,
                         eos: int = 50256) -> np.ndarray:

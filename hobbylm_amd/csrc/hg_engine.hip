@@ -154,6 +154,10 @@ struct hg_kv {
     float *h_logits = nullptr;
     hipGraphExec_t g_decode = nullptr, g_body = nullptr, g_tail = nullptr;
     bool use_graph = true;
+    // per-launch timing (hg_profile_step): an event before each launch group and its class
+    bool prof_on = false;
+    std::vector<hipEvent_t> prof_ev;
+    std::vector<int> prof_cls;
     ~hg_kv();
 };
 
@@ -331,6 +335,22 @@ int hg_token_embedding(const hg_model *m, uint32_t id, float *out) {
 // ======================================================================= step enqueue
 namespace {
 
+enum ProfClass { P_EMBED, P_NORM, P_QKV, P_ATTN_A, P_ATTN_B, P_OPROJ, P_ROUTER, P_GATEUP, P_DOWN, P_LMHEAD,
+                 P_ARGMAX, P_OTHER, P_COUNT };
+const char *const kProfNames[P_COUNT] = {"embed", "rmsnorm_quant", "qkv_matvec", "attn_scores", "attn_softmax_pv",
+                                         "o_proj_matvec", "ffn_norm_router", "expert_gate_up", "expert_down",
+                                         "lm_head_matvec", "argmax", "other"};
+
+// Start a launch group of class c (profiling only).
+void mark(hg_kv *kv, int c) {
+    if (!kv->prof_on) return;
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return;
+    (void)hipEventRecord(e, kv->st);
+    kv->prof_ev.push_back(e);
+    kv->prof_cls.push_back(c);
+}
+
 float *layer_k(const hg_kv *kv, uint32_t l) {
     const hg_config &c = kv->m->c;
     return kv->kc.as<float>() + (size_t)l * c.n_kv_heads * kv->cap * c.head_dim;
@@ -351,27 +371,39 @@ void enqueue_layers(hg_kv *kv, int order) {
     StepParams *p = kv->params.as<StepParams>();
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const Layer &L = *m->layers[l];
+        mark(kv, P_NORM);
         launch_rmsnorm_quant(st, kv->exact, x, L.attn_norm.as<float>(), c.rms_eps, d, nullptr, qa, da);
+        mark(kv, P_QKV);
         launch_matvec(st, order, EPI_STORE, L.qkv.m, qa, da, kv->qkv.as<float>(), 64, 0, nullptr, nullptr);
-        launch_attn(st, kv->exact, c.head_dim, kv->qkv.as<float>(), L.q_norm.as<float>(), L.k_norm.as<float>(),
-                    c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), p, layer_k(kv, l), layer_v(kv, l),
-                    kv->cap, c.n_heads, c.n_kv_heads, kv->S, kv->part.as<float>(), kv->scores.as<float>(), nullptr,
-                    qa, da);
+        for (int part = 0; part < 2; ++part) {
+            mark(kv, part == 0 ? P_ATTN_A : P_ATTN_B);
+            launch_attn(st, kv->exact, part, c.head_dim, kv->qkv.as<float>(), L.q_norm.as<float>(),
+                        L.k_norm.as<float>(), c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), p,
+                        layer_k(kv, l), layer_v(kv, l), kv->cap, c.n_heads, c.n_kv_heads, kv->S,
+                        kv->part.as<float>(), kv->scores.as<float>(), nullptr, qa, da);
+        }
+        mark(kv, P_OPROJ);
         launch_matvec(st, order, EPI_RESID, L.o.m, qa, da, x, 64, 0, nullptr, nullptr);
         if (L.moe) {
+            mark(kv, P_ROUTER);
             launch_ffn_router(st, kv->exact, x, L.ffn_norm.as<float>(), c.rms_eps, d, L.router.as<float>(),
                               L.bias.as<float>(), c.n_experts, c.top_k, c.gating_sigmoid, c.expert_weights_norm,
                               c.expert_weights_scale, qa, da, kv->topk_idx.as<uint32_t>(), kv->topk_w.as<float>(),
                               kv->order.as<uint32_t>(), kv->rec_idx.as<uint32_t>() + (size_t)l * c.top_k,
                               kv->rec_w.as<float>() + (size_t)l * c.top_k);
+            mark(kv, P_GATEUP);
             launch_ffn_gateup(st, order, L.gate_e.m, L.up_e.m, L.gate_sh.m, L.up_sh.m, kv->topk_idx.as<uint32_t>(),
                               c.top_k, m->n_slots, c.expert_ffn, qa, da, kv->a.as<float>());
+            mark(kv, P_DOWN);
             launch_ffn_down(st, order, L.down_e.m, L.down_sh.m, kv->topk_idx.as<uint32_t>(), kv->topk_w.as<float>(),
                             kv->order.as<uint32_t>(), c.top_k, m->n_slots, 0, d, c.expert_ffn, kv->a.as<float>(), x);
         } else {
+            mark(kv, P_NORM);
             launch_rmsnorm_quant(st, kv->exact, x, L.ffn_norm.as<float>(), c.rms_eps, d, nullptr, qa, da);
+            mark(kv, P_GATEUP);
             launch_ffn_gateup(st, order, L.gate.m, L.up.m, L.gate.m, L.up.m, nullptr, 0, 1, c.dense_ffn, qa, da,
                               kv->a.as<float>());
+            mark(kv, P_DOWN);
             launch_ffn_down(st, order, L.down.m, L.down.m, nullptr, nullptr, nullptr, 0, 1, 1, d, c.dense_ffn,
                             kv->a.as<float>(), x);
         }
@@ -383,15 +415,19 @@ void enqueue_tail(hg_kv *kv) {
     const hg_model *m = kv->m;
     const hg_config &c = m->c;
     const uint32_t valid = c.vocab_size < 50257 ? c.vocab_size : 50257;
+    mark(kv, P_NORM);
     launch_rmsnorm_quant(kv->st, kv->exact, kv->x.as<float>(), m->output_norm.as<float>(), c.rms_eps, c.d_model,
                          nullptr, kv->qa.as<uint8_t>(), kv->da.as<float>());
+    mark(kv, P_LMHEAD);
     launch_matvec(kv->st, ORDER_DECODE, EPI_LOGITS, m->output.m, kv->qa.as<uint8_t>(), kv->da.as<float>(),
                   kv->logits.as<float>(), kv->lm_threads, valid, kv->pv.as<float>(), kv->pi.as<uint32_t>());
+    mark(kv, P_ARGMAX);
     launch_argmax_final(kv->st, kv->pv.as<float>(), kv->pi.as<uint32_t>(), kv->n_part, kv->params.as<StepParams>(),
                         kv->out_ids.as<uint32_t>());
 }
 
 void enqueue_decode(hg_kv *kv) {
+    mark(kv, P_EMBED);
     launch_embed(kv->st, kv->m->token_embd.as<float>(), kv->m->c.d_model, kv->params.as<StepParams>(),
                  kv->x.as<float>());
     enqueue_layers(kv, ORDER_DECODE);
@@ -493,6 +529,8 @@ int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out) 
     const char *ge = getenv("HG_GRAPH");
     kv->use_graph = !(ge && ge[0] == '0');
     kv->S = std::max(64u, div_up(kv->cap, 256));  // splits of at most 256 positions (LDS bound)
+    if (kv->exact && pv_ring_slots(kv->cap) < 2)
+        return fail(HG_ERR_UNSUPPORTED, "a reference-order cache holds at most 32768 positions");
     HIP_TRY(hipStreamCreateWithFlags(&kv->st, hipStreamNonBlocking));
     const size_t kvsz = (size_t)c.n_layers * c.n_kv_heads * kv->cap * c.head_dim * 4;
     int rc;
@@ -659,6 +697,35 @@ int hg_generate_greedy(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uin
     return HG_OK;
 }
 
+int hg_profile_step(const hg_model *m, hg_kv *kv, uint32_t token, uint32_t reps, float *us, uint32_t *launches) {
+    if (!m || !kv || kv->m != m || !us || !launches) return fail(HG_ERR_ARG, "NULL argument");
+    if (kv->len >= kv->cap) return fail(HG_ERR_ARG, "the cache is full: no free position to replay a step at");
+    if (token >= m->c.vocab_size) return fail(HG_ERR_ARG, "token out of range");
+    for (int c = 0; c < P_COUNT; ++c) { us[c] = 0.0f; launches[c] = 0; }
+    int rc;
+    for (uint32_t r = 0; r < reps; ++r) {
+        if ((rc = set_params(kv, token, kv->len, 0, 1, kv->len))) return rc;
+        kv->prof_on = true;
+        enqueue_decode(kv);
+        mark(kv, P_OTHER);
+        kv->prof_on = false;
+        hipError_t e = hipStreamSynchronize(kv->st);
+        for (size_t i = 0; e == hipSuccess && i + 1 < kv->prof_ev.size(); ++i) {
+            float ms = 0.0f;
+            e = hipEventElapsedTime(&ms, kv->prof_ev[i], kv->prof_ev[i + 1]);
+            us[kv->prof_cls[i]] += ms * 1000.0f / reps;
+            if (r == 0) launches[kv->prof_cls[i]] += 1;
+        }
+        for (hipEvent_t ev : kv->prof_ev) (void)hipEventDestroy(ev);
+        kv->prof_ev.clear();
+        kv->prof_cls.clear();
+        if (e != hipSuccess) return fail(HG_ERR_DEVICE, std::string("profile: ") + hipGetErrorString(e));
+    }
+    return HG_OK;
+}
+
+const char *hg_profile_class(uint32_t c) { return c < P_COUNT ? kProfNames[c] : ""; }
+
 int hg_last_routing(const hg_kv *kv, uint32_t *idx, float *w) {
     if (!kv) return fail(HG_ERR_ARG, "NULL argument");
     const size_t n = (size_t)kv->m->c.n_layers * kv->m->c.top_k;
@@ -803,6 +870,8 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
     if (hd != 32 && hd != 64 && hd != 128) return fail(HG_ERR_UNSUPPORTED, "head_dim not in {32, 64, 128}");
     if (!n_kv || n_heads % n_kv || n_heads / n_kv > 8) return fail(HG_ERR_UNSUPPORTED, "unsupported head grouping");
     if (pos >= rope_len) return fail(HG_ERR_ARG, "pos beyond the RoPE table");
+    if (!(flags & HG_KV_FAST) && pv_ring_slots(pos + 1) < 2)
+        return fail(HG_ERR_UNSUPPORTED, "reference-order attention supports at most 32768 positions");
     int rc = check_device();
     if (rc) return rc;
     const bool exact = (flags & HG_KV_FAST) == 0;
@@ -830,10 +899,12 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
         (rc = dout.alloc((size_t)qd * 4)) || (rc = dq.alloc((size_t)div_up(qd / QK, 4) * CHUNK_BYTES)) ||
         (rc = dd.alloc((size_t)div_up(qd / QK, 4) * 16)))
         return rc;
-    if (!launch_attn(nullptr, exact, hd, dqkv.as<float>(), dqn.as<float>(), dkn.as<float>(), eps, dcs.as<float>(),
-                     dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap, n_heads, n_kv, S,
-                     dpart.as<float>(), dscr.as<float>(), dout.as<float>(), dq.as<uint8_t>(), dd.as<float>()))
-        return fail(HG_ERR_UNSUPPORTED, "head_dim not supported");
+    for (int which = 0; which < 2; ++which)
+        if (!launch_attn(nullptr, exact, which, hd, dqkv.as<float>(), dqn.as<float>(), dkn.as<float>(), eps,
+                         dcs.as<float>(), dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap,
+                         n_heads, n_kv, S, dpart.as<float>(), dscr.as<float>(), dout.as<float>(), dq.as<uint8_t>(),
+                         dd.as<float>()))
+            return fail(HG_ERR_UNSUPPORTED, "head_dim not supported");
     HIP_TRY(hipGetLastError());
     HIP_TRY(hipDeviceSynchronize());
     HIP_TRY(hipMemcpy(out, dout.p, (size_t)qd * 4, hipMemcpyDeviceToHost));

@@ -364,11 +364,10 @@ void pack_rows(uint32_t N, uint32_t K, PackedQ8 &out, Reader read_row) {
             for (int e = 0; e < QK; ++e) dst[chunk_pos(b * QK + e)] = (uint8_t)q[e];
         }
     });
-    // normal binary16 values only (no f16 subnormals)
     bool f16_ok = true;
     for (float s : scales) {
         const _Float16 h = (_Float16)s;
-        if ((float)h != s || (s != 0.0f && fabsf(s) < 6.103515625e-05f)) { f16_ok = false; break; }
+        if ((float)h != s) { f16_ok = false; break; }
     }
     out.f16_exact = f16_ok;
     out.sc32 = std::move(scales);

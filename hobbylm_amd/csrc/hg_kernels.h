@@ -5,6 +5,8 @@
 namespace hg {
 
 hipError_t init_kernel_attributes();
+// LDS ring slots of the reference-order P.V kernel for a cache of cap positions (>= 2 needed).
+__host__ __device__ uint32_t pv_ring_slots(uint32_t cap);
 void launch_embed(hipStream_t st, const float *emb, uint32_t d, const StepParams *p, float *x);
 void launch_load_row(hipStream_t st, const float *inputs, uint32_t d, const StepParams *p, float *x);
 void launch_advance(hipStream_t st, StepParams *p);
@@ -17,9 +19,10 @@ void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uin
 void launch_argmax_final(hipStream_t st, const float *pv, const uint32_t *pi, uint32_t n, StepParams *p,
                          uint32_t *out_ids);
 size_t attn_fast_shm(uint32_t hd, uint32_t rep, uint32_t cap, uint32_t S);
-bool launch_attn(hipStream_t st, bool exact, uint32_t hd, const float *qkv, const float *qn, const float *kn,
-                 float eps, const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
-                 uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,
+// which = 0: scores (reference order) or split partials (fast); which = 1: softmax + P.V or merge.
+bool launch_attn(hipStream_t st, bool exact, int which, uint32_t hd, const float *qkv, const float *qn,
+                 const float *kn, float eps, const float *cs, const float *sn, const StepParams *p, float *kc,
+                 float *vc, uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,
                  float *o_out, uint8_t *q_out, float *d_out);
 void launch_ffn_router(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,
                        const float *Wr, const float *bias, uint32_t E, uint32_t top_k, int gating_sigmoid,

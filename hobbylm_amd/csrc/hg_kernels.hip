@@ -678,101 +678,104 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
         pmax[(size_t)(g * rep + tid) * S + s] = fmaxf(fmaxf(red[0][tid], red[1][tid]), fmaxf(red[2][tid], red[3][tid]));
 }
 
-// Softmax of one head (ops.rs:112-128): m = max, e_t = exp(s_t - m) with the reference
-// expf, sum = e_0 + e_1 + ... sequentially, p_t = e_t * (1/sum), written over the scores.
-// Grid: n_heads workgroups of 256; the context is processed in LDS chunks.
-__global__ __launch_bounds__(256) void k_attn_softmax(float *scores, const float *__restrict__ pmax,
-                                                      const StepParams *p, uint32_t cap, uint32_t S) {
-    constexpr uint32_t CH = 4096;
-    __shared__ __align__(16) float buf[CH];
-    __shared__ float s_sum;
-    const int tid = threadIdx.x;
-    const uint32_t h = blockIdx.x, n = p->pos + 1;
-    float *sc = scores + (size_t)h * cap;
-    float m = -__builtin_huge_valf();
-    for (uint32_t s = 0; s < S; ++s) m = fmaxf(m, pmax[(size_t)h * S + s]);
-    float sum = 0.0f;
-    for (uint32_t c0 = 0; c0 < n; c0 += CH) {
-        const uint32_t cl = min(CH, n - c0);
-        for (uint32_t i = tid; i < cl; i += 256) {
-            const float e = hg_expf(sc[c0 + i] - m);
-            buf[i] = e;
-            sc[c0 + i] = e;
-        }
-        __syncthreads();
-        if (tid == 0) sum = seq_sum_lds(buf, cl, sum);
-        __syncthreads();
-    }
-    if (tid == 0) s_sum = sum;
-    __syncthreads();
-    const float inv = 1.0f / s_sum;
-    for (uint32_t t = tid; t < n; t += 256) sc[t] = sc[t] * inv;
-}
-
-// P.V of one head (model.rs:227-232): o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ...
-// One workgroup of 16 waves per head.  The first HD/64 waves run the sequential chains (lane =
-// output element); every other wave is a producer: producer w forms the rounded products
-// p_t * v_t[di] (the reference's separate multiply) of tiles w, w+NP, w+2NP, ... of PV_T
-// positions into a ring of PV_R LDS slots.  Slot readiness and consumption are LDS flags at
-// workgroup scope, so up to NP tiles are in flight while the chain does one LDS read and one
-// add per position.  Every wait is bounded: tile k only waits for tile k - PV_R to be consumed,
-// and the chain only for tile k to be produced.  Also writes o and its quantization.
+// Softmax and P.V of one query head (ops.rs:112-128, model.rs:227-232), one workgroup of 16
+// waves per head:
+//   e_t = exp(s_t - m) with the reference expf (all threads, into LDS);
+//   sum = e_0 + e_1 + ... sequentially (one lane), inv = 1/sum;
+//   o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ...  with p_t = e_t * inv, as one sequential
+//   chain per output element.
+// The first HD/64 waves run the chains (lane = output element).  Every other wave is a
+// producer: producer w forms the rounded products p_t * v_t[di] (the reference's separate
+// multiply) of tiles w, w+NP, ... of T positions into a ring of R LDS slots, so the chain is
+// one LDS read and one add per position while up to R-1 tiles are in flight.  Readiness and
+// release of slots are LDS flags at workgroup scope; every wait is bounded: tile k waits only
+// for tile k - R to be consumed, and the chain only for tile k to be produced.  The producers
+// issue their first V loads before the sum so the fetch overlaps it.  Also writes o and its
+// quantization for attn_output (quant.rs:111-123).
 template <int HD> struct PvCfg {
     static constexpr uint32_t T = 2048 / HD;  // positions per tile: an 8 KiB slot
-    static constexpr uint32_t R = 16;         // ring slots (128 KiB)
+    static constexpr uint32_t TPL = HD / 4;   // lanes per position (one float4 each)
+    static constexpr uint32_t PPI = 64 / TPL; // positions per wave instruction
+    static constexpr uint32_t NI = T / PPI;   // float4 per lane per tile
 };
+constexpr size_t PV_LDS_BUDGET = 156 * 1024;
+
+__host__ __device__ uint32_t pv_ring_slots(uint32_t cap) {
+    const size_t e_bytes = (size_t)div_up(cap, 4) * 16;
+    const size_t left = PV_LDS_BUDGET > e_bytes ? PV_LDS_BUDGET - e_bytes : 0;
+    const uint32_t r = (uint32_t)(left / 8192);
+    return r > 16 ? 16 : r;
+}
 
 template <int HD>
-__global__ __launch_bounds__(1024) void k_attn_pv(const float *__restrict__ probs, const float *__restrict__ qkv,
-                                                  const StepParams *p, const float *__restrict__ vc, uint32_t cap,
-                                                  uint32_t n_heads, uint32_t n_kv, float *o_out, uint8_t *q_out,
-                                                  float *d_out) {
-    constexpr uint32_t T = PvCfg<HD>::T, R = PvCfg<HD>::R;
+__global__ __launch_bounds__(1024) void k_attn_softmax_pv(const float *__restrict__ scores,
+                                                          const float *__restrict__ pmax,
+                                                          const float *__restrict__ qkv, const StepParams *p,
+                                                          const float *__restrict__ vc, uint32_t cap, uint32_t S,
+                                                          uint32_t n_heads, uint32_t n_kv, float *o_out,
+                                                          uint8_t *q_out, float *d_out) {
+    using C = PvCfg<HD>;
+    constexpr uint32_t T = C::T;
     constexpr int NCW = HD > 64 ? HD / 64 : 1;   // chain waves
     constexpr int NP = 16 - NCW;                 // producer waves
-    extern __shared__ __align__(16) float ring[];  // [R][T*HD]
-    __shared__ uint32_t ready[R];
+    extern __shared__ __align__(16) float lds[];
+    __shared__ uint32_t ready[16];
     __shared__ uint32_t done[NCW];
+    __shared__ float s_inv;
     __shared__ __align__(16) float ov[HD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t h = blockIdx.x, rep = n_heads / n_kv, g = h / rep;
     const uint32_t pos = p->pos, n = pos + 1;
+    const uint32_t R = pv_ring_slots(cap);
+    float *e = lds;                                     // [cap] e_t, then p_t
+    float *ring = lds + (size_t)div_up(cap, 4) * 4;     // [R][T*HD]
+    const float *sc = scores + (size_t)h * cap;
+    float m = -__builtin_huge_valf();
+    for (uint32_t s = 0; s < S; ++s) m = fmaxf(m, pmax[(size_t)h * S + s]);
+    for (uint32_t t = tid; t < n; t += 1024) e[t] = hg_expf(sc[t] - m);
+    if (tid < 16) ready[tid] = 0;
+    if (tid < NCW) done[tid] = 0;
     const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
-    const float *pr = probs + (size_t)h * cap;
     const float *vcg = vc + (size_t)g * cap * HD;
     const float *vnew = qkv + qd + kvd + g * HD;  // row pos, appended this step
     const uint32_t ntiles = div_up(n, T);
-    if (tid < (int)R) ready[tid] = 0;
-    if (tid < NCW) done[tid] = 0;
+    const uint32_t sub = lane / C::TPL, d4 = (lane % C::TPL) * 4;  // producer lane -> (position, dims)
+    const int pw = wave - NCW;
+    // producers: start the V fetch of their first tile before the sum
+    v4f vr[C::NI];
+    auto fetch = [&](uint32_t k) {
+#pragma unroll
+        for (uint32_t i = 0; i < C::NI; ++i) {
+            const uint32_t t = min(k * T + i * C::PPI + sub, n - 1);
+            vr[i] = (t == pos) ? *reinterpret_cast<const v4f *>(vnew + d4)
+                               : *reinterpret_cast<const v4f *>(vcg + (size_t)t * HD + d4);
+        }
+    };
+    if (pw >= 0 && (uint32_t)pw < ntiles) fetch(pw);
     __syncthreads();
-    if (wave >= NCW) {
-        const int pw = wave - NCW;
-        constexpr uint32_t EPL = T * HD / 64;  // products per lane per tile
+    if (tid == 0) s_inv = 1.0f / seq_sum_lds(e, n, 0.0f);
+    __syncthreads();
+    const float inv = s_inv;
+    for (uint32_t t = tid; t < n; t += 1024) e[t] = e[t] * inv;
+    __syncthreads();
+    if (pw >= 0) {
         for (uint32_t k = pw; k < ntiles; k += NP) {
-            const uint32_t base = k * T;
-            float v[EPL];
-#pragma unroll
-            for (uint32_t u = 0; u < EPL; ++u) {
-                const uint32_t e = u * 64 + lane, tt = e / HD, di = e % HD, t = base + tt;
-                const uint32_t tc = min(t, n - 1);
-                v[u] = (tc == pos) ? vnew[di] : vcg[(size_t)tc * HD + di];
-            }
-            float pv[EPL];
-#pragma unroll
-            for (uint32_t u = 0; u < EPL; ++u) {
-                const uint32_t e = u * 64 + lane, t = base + e / HD;
-                pv[u] = pr[min(t, n - 1)];
-            }
-            // the slot of tile k was last used by tile k - R
+            if (k != (uint32_t)pw) fetch(k);
             if (k >= R)
                 for (int c = 0; c < NCW; ++c)
                     while (__hip_atomic_load(&done[c], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < k - R + 1)
                         __builtin_amdgcn_s_sleep(1);
             float *slot = ring + (size_t)(k % R) * T * HD;
 #pragma unroll
-            for (uint32_t u = 0; u < EPL; ++u) {
-                const uint32_t e = u * 64 + lane;
-                slot[e] = (base + e / HD < n) ? pv[u] * v[u] : 0.0f;
+            for (uint32_t i = 0; i < C::NI; ++i) {
+                const uint32_t tt = i * C::PPI + sub, t = k * T + tt;
+                const float pt = (t < n) ? e[t] : 0.0f;
+                v4f r;
+                r.x = pt * vr[i].x;
+                r.y = pt * vr[i].y;
+                r.z = pt * vr[i].z;
+                r.w = pt * vr[i].w;
+                *reinterpret_cast<v4f *>(slot + tt * HD + d4) = r;
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             if (lane == 0) __hip_atomic_store(&ready[k % R], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -838,6 +841,22 @@ __global__ __launch_bounds__(1024) void k_ffn_router(const float *__restrict__ x
     __shared__ uint32_t tk[64];
     __shared__ float tw[64];
     const int tid = threadIdx.x;
+    // router rows of this lane group, fetched before the RMSNorm so the load overlaps it:
+    // lane l32 of group grp holds W_r[e][32 i + l32] for e = grp, grp + 32 and i < d/32
+    constexpr uint32_t RMAX = 2, IMAX = 32;
+    const int grp = tid >> 5, l32 = tid & 31;
+    const uint32_t main = d - d % 32;
+    const bool pre = main / 32 <= IMAX && E <= 32 * RMAX && main == d;
+    float wr[RMAX][IMAX];
+    if (pre) {
+#pragma unroll
+        for (uint32_t rr = 0; rr < RMAX; ++rr)
+#pragma unroll
+            for (uint32_t i = 0; i < IMAX; ++i) {
+                const uint32_t e = min(grp + 32 * rr, E - 1), k = min(32 * i + l32, d - 1);
+                wr[rr][i] = Wr[(size_t)e * d + k];
+            }
+    }
     for (uint32_t i = tid; i < d; i += 1024) hs[i] = x[i];
     __syncthreads();
     const float ss = sum_squares<EXACT>(hs, hs + d, d, tid, 1024, red, &s_ss);
@@ -858,24 +877,41 @@ __global__ __launch_bounds__(1024) void k_ffn_router(const float *__restrict__ x
         }
         zero_pad(nb, nc, q_out, d_out, tid, 1024);
     }
-    // router logits, 32 lanes per expert
-    const int grp = tid >> 5, l32 = tid & 31;
-    const uint32_t main = d - d % 32;
-    for (uint32_t e = grp; e < E; e += 32) {
-        const float *row = Wr + (size_t)e * d;
-        float acc = 0.0f;
-        uint32_t i = 0;
-        for (; i < main; i += 32) acc = fmaf(row[i + l32], hs[i + l32], acc);
-        for (; i + 8 <= d; i += 8)
-            if (l32 < 8) acc = fmaf(row[i + l32], hs[i + l32], acc);
-        acc = acc + shfl_xor(acc, 8);
-        acc = acc + shfl_xor(acc, 16);
-        acc = acc + shfl_xor(acc, 4);
-        acc = acc + shfl_xor(acc, 2);
-        acc = acc + shfl_xor(acc, 1);
-        if (l32 == 0) {
-            for (; i < d; ++i) acc = acc + row[i] * hs[i];
-            lg[e] = acc;
+    // router logits, 32 lanes per expert row (ops::dot order)
+    if (pre) {
+#pragma unroll
+        for (uint32_t rr = 0; rr < RMAX; ++rr) {
+            const uint32_t e = grp + 32 * rr;
+            if (e < E) {
+                float acc = 0.0f;
+#pragma unroll
+                for (uint32_t i = 0; i < IMAX; ++i)
+                    if (32 * i < d) acc = fmaf(wr[rr][i], hs[32 * i + l32], acc);
+                acc = acc + shfl_xor(acc, 8);
+                acc = acc + shfl_xor(acc, 16);
+                acc = acc + shfl_xor(acc, 4);
+                acc = acc + shfl_xor(acc, 2);
+                acc = acc + shfl_xor(acc, 1);
+                if (l32 == 0) lg[e] = acc;
+            }
+        }
+    } else {
+        for (uint32_t e = grp; e < E; e += 32) {
+            const float *row = Wr + (size_t)e * d;
+            float acc = 0.0f;
+            uint32_t i = 0;
+            for (; i < main; i += 32) acc = fmaf(row[i + l32], hs[i + l32], acc);
+            for (; i + 8 <= d; i += 8)
+                if (l32 < 8) acc = fmaf(row[i + l32], hs[i + l32], acc);
+            acc = acc + shfl_xor(acc, 8);
+            acc = acc + shfl_xor(acc, 16);
+            acc = acc + shfl_xor(acc, 4);
+            acc = acc + shfl_xor(acc, 2);
+            acc = acc + shfl_xor(acc, 1);
+            if (l32 == 0) {
+                for (; i < d; ++i) acc = acc + row[i] * hs[i];
+                lg[e] = acc;
+            }
         }
     }
     __syncthreads();
@@ -1028,9 +1064,8 @@ hipError_t init_kernel_attributes() {
     hipError_t e = hipSuccess;
 #define PV_ATTR(HD)                                                                                         \
     if (e == hipSuccess)                                                                                    \
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_pv<HD>),                             \
-                                hipFuncAttributeMaxDynamicSharedMemorySize,                                 \
-                                (int)(PvCfg<HD>::R * PvCfg<HD>::T * HD * sizeof(float)));
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_softmax_pv<HD>),                     \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_LDS_BUDGET);
     PV_ATTR(32) PV_ATTR(64) PV_ATTR(128)
 #undef PV_ATTR
     return e;
@@ -1111,41 +1146,46 @@ size_t attn_fast_shm(uint32_t hd, uint32_t rep, uint32_t cap, uint32_t S) {
 }
 
 template <int HD>
-static void attn_exact_launch(hipStream_t st, const float *qkv, const float *qn, const float *kn, float eps,
-                              const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
+static void attn_exact_launch(hipStream_t st, int which, const float *qkv, const float *qn, const float *kn,
+                              float eps, const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
                               uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part,
                               float *scratch, float *o_out, uint8_t *q_out, float *d_out) {
-    LAUNCH(k_attn_scores<HD>, dim3(n_kv, S), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
-           n_kv, S, scratch, part);
-    LAUNCH(k_attn_softmax, dim3(n_heads), dim3(256), 0, st, scratch, part, p, cap, S);
-    const size_t shm = (size_t)PvCfg<HD>::R * PvCfg<HD>::T * HD * sizeof(float);
-    LAUNCH(k_attn_pv<HD>, dim3(n_heads), dim3(1024), shm, st, scratch, qkv, p, vc, cap, n_heads, n_kv, o_out, q_out,
-           d_out);
+    if (which == 0) {
+        LAUNCH(k_attn_scores<HD>, dim3(n_kv, S), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
+               n_kv, S, scratch, part);
+        return;
+    }
+    const size_t shm = (size_t)div_up(cap, 4) * 16 + (size_t)pv_ring_slots(cap) * 8192;
+    LAUNCH(k_attn_softmax_pv<HD>, dim3(n_heads), dim3(1024), shm, st, scratch, part, qkv, p, vc, cap, S, n_heads,
+           n_kv, o_out, q_out, d_out);
 }
 
 template <int HD>
-static void attn_fast_launch(hipStream_t st, const float *qkv, const float *qn, const float *kn, float eps,
+static void attn_fast_launch(hipStream_t st, int which, const float *qkv, const float *qn, const float *kn, float eps,
                              const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
                              uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *o_out,
                              uint8_t *q_out, float *d_out) {
-    const size_t shm = attn_fast_shm(HD, n_heads / n_kv, cap, S);
-    LAUNCH(k_attn_fast<HD>, dim3(n_kv, S), dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
-           n_kv, S, part);
+    if (which == 0) {
+        const size_t shm = attn_fast_shm(HD, n_heads / n_kv, cap, S);
+        LAUNCH(k_attn_fast<HD>, dim3(n_kv, S), dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
+               n_kv, S, part);
+        return;
+    }
     LAUNCH(k_attn_combine<HD>, dim3(1), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
 }
 
-bool launch_attn(hipStream_t st, bool exact, uint32_t hd, const float *qkv, const float *qn, const float *kn,
-                 float eps, const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
-                 uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,
+bool launch_attn(hipStream_t st, bool exact, int which, uint32_t hd, const float *qkv, const float *qn,
+                 const float *kn, float eps, const float *cs, const float *sn, const StepParams *p, float *kc,
+                 float *vc, uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,
                  float *o_out, uint8_t *q_out, float *d_out) {
 #define ATTN(HD)                                                                                                    \
     do {                                                                                                            \
         if (exact)                                                                                                  \
-            attn_exact_launch<HD>(st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part, scratch,    \
-                                  o_out, q_out, d_out);                                                             \
+            attn_exact_launch<HD>(st, which, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part,      \
+                                  scratch, o_out, q_out, d_out);                                                    \
         else                                                                                                        \
-            attn_fast_launch<HD>(st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part, o_out,       \
-                                 q_out, d_out);                                                                     \
+            attn_fast_launch<HD>(st, which, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part,       \
+                                 o_out, q_out, d_out);                                                              \
     } while (0)
     if (hd == 64) ATTN(64);
     else if (hd == 128) ATTN(128);

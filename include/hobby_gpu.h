@@ -129,6 +129,19 @@ int hg_generate_greedy(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uin
  * idx[L*top_k] (UINT32_MAX for dense layers) and the scaled weights w[L*top_k]. */
 int hg_last_routing(const hg_kv *kv, uint32_t *idx, float *w);
 
+/* ---- instrumentation (no counterpart in the reference) -------------------------------- */
+
+#define HG_PROF_CLASSES 12
+/* Time one decode step per kernel class, for measurement tools: the step at pos = len is
+ * replayed `reps` times with HIP events recorded on the cache's own stream between launch
+ * groups (launched one by one, not as a graph); the cache length does not advance, and the
+ * row written at len is overwritten by the next real step.  us[c] = mean microseconds per
+ * step in class c, launches[c] = kernel launch groups per step; arrays of HG_PROF_CLASSES. */
+int hg_profile_step(const hg_model *m, hg_kv *kv, uint32_t token, uint32_t reps, float *us,
+                    uint32_t *launches);
+/* Name of profile class c ("" when out of range). */
+const char *hg_profile_class(uint32_t c);
+
 /* ---- operator level (hobby-rs/src/quant.rs, model.rs:199-233) ------------------------ */
 
 /* Q8Tensor::quantize(w, out, in) (quant.rs:78-102) from f32 weights [out][in]. */
