@@ -82,6 +82,16 @@ def window_stats(prof_dir, steps):
         a[0] += 1
         a[1] += (e - s) / 1e3
     tot = sum(v[1] for v in agg.values())
+    whole = {}
+    for name, s, e in rows:
+        a = whole.setdefault(name, [0, 0.0])
+        a[0] += 1
+        a[1] += (e - s) / 1e3
+    print(f"# rocprofv3 kernel stats over the whole run ({len(rows)} dispatches)")
+    print(f"{'calls':>7} {'avg_us':>9} {'total_us':>12}  kernel")
+    for name, (c, t) in sorted(whole.items(), key=lambda kv: -kv[1][1])[:20]:
+        print(f"{c:7d} {t / c:9.2f} {t:12.1f}  {name[:110]}")
+    print()
     print(f"# rocprofv3 kernel stats over the last {steps} decode steps ({len(rows) - lo} dispatches)")
     print(f"{'pct':>6} {'calls':>7} {'avg_us':>9} {'total_us':>11}  kernel")
     for name, (c, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):

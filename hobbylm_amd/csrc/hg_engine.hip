@@ -146,7 +146,7 @@ struct hg_kv {
     uint32_t S = 0;         // attention context splits
     uint32_t lm_threads = 256, n_part = 0;
     DevBuf kc, vc;          // [L][n_kv][cap][hd]
-    DevBuf x, qkv, part, scores, a, logits, pv, pi, qa, da, topk_idx, topk_w, order, rec_idx, rec_w, params,
+    DevBuf x, qkv, o, part, scores, a, logits, pv, pi, qa, da, topk_idx, topk_w, order, rec_idx, rec_w, params,
         out_ids, inputs;
     uint32_t inputs_rows = 0;
     StepParams *h_params = nullptr;
@@ -154,10 +154,7 @@ struct hg_kv {
     float *h_logits = nullptr;
     hipGraphExec_t g_decode = nullptr, g_body = nullptr, g_tail = nullptr;
     bool use_graph = true;
-    // per-launch timing (hg_profile_step): an event before each launch group and its class
-    bool prof_on = false;
-    std::vector<hipEvent_t> prof_ev;
-    std::vector<int> prof_cls;
+    LaunchTimer *timer = nullptr;  // hg_profile_step: per-dispatch timing
     ~hg_kv();
 };
 
@@ -341,14 +338,9 @@ const char *const kProfNames[P_COUNT] = {"embed", "rmsnorm_quant", "qkv_matvec",
                                          "o_proj_matvec", "ffn_norm_router", "expert_gate_up", "expert_down",
                                          "lm_head_matvec", "argmax", "other"};
 
-// Start a launch group of class c (profiling only).
+// Tag the following launches with class c (profiling only).
 void mark(hg_kv *kv, int c) {
-    if (!kv->prof_on) return;
-    hipEvent_t e = nullptr;
-    if (hipEventCreate(&e) != hipSuccess) return;
-    (void)hipEventRecord(e, kv->st);
-    kv->prof_ev.push_back(e);
-    kv->prof_cls.push_back(c);
+    if (kv->timer) kv->timer->cls = c;
 }
 
 float *layer_k(const hg_kv *kv, uint32_t l) {
@@ -380,10 +372,15 @@ void enqueue_layers(hg_kv *kv, int order) {
             launch_attn(st, kv->exact, part, c.head_dim, kv->qkv.as<float>(), L.q_norm.as<float>(),
                         L.k_norm.as<float>(), c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), p,
                         layer_k(kv, l), layer_v(kv, l), kv->cap, c.n_heads, c.n_kv_heads, kv->S,
-                        kv->part.as<float>(), kv->scores.as<float>(), nullptr, qa, da);
+                        kv->part.as<float>(), kv->scores.as<float>(), kv->o.as<float>(),
+                        kv->exact ? nullptr : qa, da);
         }
         mark(kv, P_OPROJ);
-        launch_matvec(st, order, EPI_RESID, L.o.m, qa, da, x, 64, 0, nullptr, nullptr);
+        if (kv->exact)  // attn_output quantizes o itself
+            launch_matvec(st, order, EPI_RESID, L.o.m, reinterpret_cast<const uint8_t *>(kv->o.as<float>()), nullptr,
+                          x, 64, 0, nullptr, nullptr);
+        else
+            launch_matvec(st, order, EPI_RESID, L.o.m, qa, da, x, 64, 0, nullptr, nullptr);
         if (L.moe) {
             mark(kv, P_ROUTER);
             launch_ffn_router(st, kv->exact, x, L.ffn_norm.as<float>(), c.rms_eps, d, L.router.as<float>(),
@@ -541,6 +538,7 @@ int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out) 
     const uint32_t ffw = std::max(c.dense_ffn, c.expert_ffn) * std::max(m->n_slots, 1u);
     kv->n_part = matvec_blocks(c.vocab_size, kv->lm_threads);
     if ((rc = kv->x.alloc(c.d_model * 4)) || (rc = kv->qkv.alloc((size_t)(qd + 2 * kvd) * 4)) ||
+        (rc = kv->o.alloc((size_t)qd * 4)) ||
         (rc = kv->part.alloc((size_t)c.n_heads * kv->S * (c.head_dim + 2) * 4)) ||
         (rc = kv->scores.alloc(kv->exact ? (size_t)c.n_heads * kv->cap * 4 : 4)) ||
         (rc = kv->a.alloc((size_t)ffw * 4)) || (rc = kv->logits.alloc((size_t)c.vocab_size * 4)) ||
@@ -705,20 +703,23 @@ int hg_profile_step(const hg_model *m, hg_kv *kv, uint32_t token, uint32_t reps,
     int rc;
     for (uint32_t r = 0; r < reps; ++r) {
         if ((rc = set_params(kv, token, kv->len, 0, 1, kv->len))) return rc;
-        kv->prof_on = true;
+        LaunchTimer timer;
+        kv->timer = &timer;
+        set_launch_timer(&timer);
         enqueue_decode(kv);
-        mark(kv, P_OTHER);
-        kv->prof_on = false;
+        set_launch_timer(nullptr);
+        kv->timer = nullptr;
         hipError_t e = hipStreamSynchronize(kv->st);
-        for (size_t i = 0; e == hipSuccess && i + 1 < kv->prof_ev.size(); ++i) {
+        for (size_t i = 0; e == hipSuccess && i < timer.ev.size(); ++i) {
             float ms = 0.0f;
-            e = hipEventElapsedTime(&ms, kv->prof_ev[i], kv->prof_ev[i + 1]);
-            us[kv->prof_cls[i]] += ms * 1000.0f / reps;
-            if (r == 0) launches[kv->prof_cls[i]] += 1;
+            e = hipEventElapsedTime(&ms, timer.ev[i].first, timer.ev[i].second);
+            us[timer.tags[i]] += ms * 1000.0f / reps;
+            if (r == 0) launches[timer.tags[i]] += 1;
         }
-        for (hipEvent_t ev : kv->prof_ev) (void)hipEventDestroy(ev);
-        kv->prof_ev.clear();
-        kv->prof_cls.clear();
+        for (auto &pr : timer.ev) {
+            (void)hipEventDestroy(pr.first);
+            (void)hipEventDestroy(pr.second);
+        }
         if (e != hipSuccess) return fail(HG_ERR_DEVICE, std::string("profile: ") + hipGetErrorString(e));
     }
     return HG_OK;

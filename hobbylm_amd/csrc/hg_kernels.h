@@ -2,7 +2,18 @@
 #pragma once
 #include "hg_common.h"
 
+#include <vector>
+
 namespace hg {
+
+// Kernel-execution timing of every launch issued while installed (profiling only).
+struct LaunchTimer {
+    int cls = 0;                                           // class tag of the next launches
+    std::vector<int> tags;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
+    void add(hipEvent_t a, hipEvent_t b) { ev.emplace_back(a, b); tags.push_back(cls); }
+};
+void set_launch_timer(LaunchTimer *t);
 
 hipError_t init_kernel_attributes();
 // LDS ring slots of the reference-order P.V kernel for a cache of cap positions (>= 2 needed).
@@ -14,12 +25,14 @@ void launch_rmsnorm_quant(hipStream_t st, bool exact, const float *x, const floa
                           float *h, uint8_t *q, float *dq);
 void launch_quant_vec(hipStream_t st, const float *x, uint32_t n, uint8_t *q, float *dq);
 uint32_t matvec_blocks(uint32_t N, uint32_t threads);
+// dq == nullptr: q points to an f32 activation that each workgroup quantizes in its prologue.
 void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uint8_t *q, const float *dq, float *y,
                    uint32_t threads, uint32_t valid, float *pv, uint32_t *pi);
 void launch_argmax_final(hipStream_t st, const float *pv, const uint32_t *pi, uint32_t n, StepParams *p,
                          uint32_t *out_ids);
 size_t attn_fast_shm(uint32_t hd, uint32_t rep, uint32_t cap, uint32_t S);
 // which = 0: scores (reference order) or split partials (fast); which = 1: softmax + P.V or merge.
+// Reference order with q_out == nullptr leaves the quantization of o to its consumer.
 bool launch_attn(hipStream_t st, bool exact, int which, uint32_t hd, const float *qkv, const float *qn,
                  const float *kn, float eps, const float *cs, const float *sn, const StepParams *p, float *kc,
                  float *vc, uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,

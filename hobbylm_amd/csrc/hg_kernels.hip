@@ -6,6 +6,8 @@
 // reassociated.  The build uses -ffp-contract=off; each fmaf() stands where the reference
 // issues an FMA.  Wavefronts are 64 wide; a Q8 row is owned by 8 adjacent lanes (see
 // hg_common.h for the device row layout).
+#include <hip/hip_ext.h>
+
 #include "hg_common.h"
 #include "hg_expf.h"
 #include "hg_kernels.h"
@@ -302,7 +304,22 @@ __global__ __launch_bounds__(256) void k_quant_vec(const float *__restrict__ x, 
 //   EPI_RESID:  y[r] = y[r] + v     (x[i] += attn[i], model.rs:169-171)
 //   EPI_LOGITS: y[r] = v, plus a per-workgroup (max, first index) over rows < valid for
 //               the greedy argmax (sample.rs:53-63 on logits masked per lib.rs:132-134).
-template <int ORDER, int EPI, bool SCF32, int NCT>
+// Quantize an f32 activation x[K] into the LDS chunk layout (quant.rs:111-123), all threads.
+__device__ inline void quant_to_lds(const float *__restrict__ x, uint32_t nb, uint32_t nc, uint8_t *sq, float *sd,
+                                    int tid, int nthr) {
+    const int j = tid & 7;
+    for (uint32_t b0 = 0; b0 < nb; b0 += nthr / 8) {
+        const uint32_t b = b0 + tid / 8;
+        if (b < nb) {
+            const v4f xv = *reinterpret_cast<const v4f *>(x + b * QK + j * 4);
+            const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+            quant_block_lane(v, j, b, sq, sd);
+        }
+    }
+    zero_pad(nb, nc, sq, sd, tid, nthr);
+}
+
+template <int ORDER, int EPI, bool SCF32, int NCT, bool AF32 = false>
 __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restrict__ gq,
                                                 const float *__restrict__ gd, float *y, uint32_t valid,
                                                 float *part_v, uint32_t *part_i) {
@@ -315,7 +332,8 @@ __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restri
     const int j = tid & 7;
     Q8Row<ORDER, SCF32, NCT> rd;
     rd.begin(row_qs(W, lrow), row_sc<SCF32>(W, lrow), W.nb, W.nc, j);
-    stage_act(gq, gd, W.nc, sq, sd, tid, nthr);
+    if (AF32) quant_to_lds(reinterpret_cast<const float *>(gq), W.nb, W.nc, sq, sd, tid, nthr);
+    else stage_act(gq, gd, W.nc, sq, sd, tid, nthr);
     __syncthreads();
     const float v = rd.finish(sq, sd);
     if (row < W.N && j == 0) {
@@ -630,6 +648,16 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     const uint32_t chunk = div_up(n, S);
     const uint32_t t0 = s * chunk, t1 = min(n, t0 + chunk);
     const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
+    float *kcg = kc + (size_t)g * cap * HD;
+    float *vcg = vc + (size_t)g * cap * HD;
+    // one position per thread (a split holds at most 256); its K row is fetched first
+    const uint32_t t = t0 + tid;
+    const bool mine = t < t1;
+    float kt[HD];
+    if (mine && t != pos)
+#pragma unroll
+        for (int i = 0; i < HD; i += 4)
+            *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kcg + (size_t)t * HD + i);
     for (uint32_t i = tid; i < rep * HD; i += 256) raw[i] = qkv[g * rep * HD + i];
     for (uint32_t i = tid; i < HD; i += 256) {
         raw[rep * HD + i] = qkv[qd + g * HD + i];
@@ -640,108 +668,91 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
         norm_rope_head(raw + vi * HD, rot + vi * HD, vi < rep ? qn : kn, eps, HD, cs, sn, pos, tmp + wave * HD, lane);
     __syncthreads();
     const float *krot = rot + rep * HD;
-    float *kcg = kc + (size_t)g * cap * HD;
-    float *vcg = vc + (size_t)g * cap * HD;
     if (t0 <= pos && pos < t1)
         for (uint32_t i = tid; i < HD; i += 256) {
             kcg[(size_t)pos * HD + i] = krot[i];
             vcg[(size_t)pos * HD + i] = raw[(rep + 1) * HD + i];
         }
+    if (mine && t == pos)
+#pragma unroll
+        for (int i = 0; i < HD; ++i) kt[i] = krot[i];
     const float scale = 1.0f / sqrtf((float)HD);
-    float mx[MAXREP];
-#pragma unroll
-    for (int r = 0; r < MAXREP; ++r) mx[r] = -__builtin_huge_valf();
-    for (uint32_t t = t0 + tid; t < t1; t += 256) {
-        float kt[HD];
-        const float *src = (t == pos) ? krot : kcg + (size_t)t * HD;
-#pragma unroll
-        for (int i = 0; i < HD; i += 4) *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(src + i);
-#pragma unroll
-        for (int r = 0; r < MAXREP; ++r) {
-            if (r < (int)rep) {
-                const float v = dot_wide_serial(rot + r * HD, kt, HD) * scale;
-                scores[(size_t)(g * rep + r) * cap + t] = v;
-                mx[r] = fmaxf(mx[r], v);
-            }
+#pragma unroll 1
+    for (uint32_t r = 0; r < rep; ++r) {
+        float v = -__builtin_huge_valf();
+        if (mine) {
+            v = dot_wide_serial(rot + r * HD, kt, HD) * scale;
+            scores[(size_t)(g * rep + r) * cap + t] = v;
         }
-    }
-#pragma unroll
-    for (int r = 0; r < MAXREP; ++r) {
-        if (r < (int)rep) {
-            float m = mx[r];
-            for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
-            if (lane == 0) red[wave][r] = m;
-        }
+        for (int k = 32; k >= 1; k >>= 1) v = fmaxf(v, shfl_xor(v, k));
+        if (lane == 0) red[wave][r] = v;
     }
     __syncthreads();
     if ((uint32_t)tid < rep)
         pmax[(size_t)(g * rep + tid) * S + s] = fmaxf(fmaxf(red[0][tid], red[1][tid]), fmaxf(red[2][tid], red[3][tid]));
 }
 
-// Softmax and P.V of one query head (ops.rs:112-128, model.rs:227-232), one workgroup of 16
-// waves per head:
+// Softmax and P.V of one query head (ops.rs:112-128, model.rs:227-232):
 //   e_t = exp(s_t - m) with the reference expf (all threads, into LDS);
-//   sum = e_0 + e_1 + ... sequentially (one lane), inv = 1/sum;
-//   o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ...  with p_t = e_t * inv, as one sequential
-//   chain per output element.
-// The first HD/64 waves run the chains (lane = output element).  Every other wave is a
-// producer: producer w forms the rounded products p_t * v_t[di] (the reference's separate
-// multiply) of tiles w, w+NP, ... of T positions into a ring of R LDS slots, so the chain is
-// one LDS read and one add per position while up to R-1 tiles are in flight.  Readiness and
-// release of slots are LDS flags at workgroup scope; every wait is bounded: tile k waits only
-// for tile k - R to be consumed, and the chain only for tile k to be produced.  The producers
-// issue their first V loads before the sum so the fetch overlaps it.  Also writes o and its
+//   sum = e_0 + e_1 + ... sequentially (one lane), inv = 1/sum, p_t = e_t * inv;
+//   o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ...  one sequential chain per output element.
+// Grid: (n_heads, HD/16); workgroup (h, q) owns the 16 output elements [16q, 16q+16) of head h
+// (the softmax is recomputed identically by the HD/16 workgroups of a head).  Wave 0 lanes
+// 0..15 run the chains; waves 1..7 are producers: producer w forms the rounded products
+// p_t * v_t[di] (the reference's separate multiply) of tiles w-1, w-1+NP, ... of T positions
+// into a ring of R LDS slots, stored [element][position] so the chain reads four positions per
+// 16-byte LDS load.  Readiness and release of slots are LDS flags at workgroup scope; every wait
+// is bounded: tile k waits only for tile k - R to be consumed, the chain only for tile k to be
+// produced.  Producers start their first V fetch before the sum.  Also writes o and its
 // quantization for attn_output (quant.rs:111-123).
-template <int HD> struct PvCfg {
-    static constexpr uint32_t T = 2048 / HD;  // positions per tile: an 8 KiB slot
-    static constexpr uint32_t TPL = HD / 4;   // lanes per position (one float4 each)
-    static constexpr uint32_t PPI = 64 / TPL; // positions per wave instruction
-    static constexpr uint32_t NI = T / PPI;   // float4 per lane per tile
+struct PvCfg {
+    static constexpr uint32_t D = 16;          // output elements per workgroup
+    static constexpr uint32_t T = 128;         // positions per tile
+    static constexpr uint32_t TP = T + 4;      // padded row of a slot
+    static constexpr uint32_t SLOT = D * TP;   // floats per slot
+    static constexpr uint32_t NW = 8;          // waves per workgroup
+    static constexpr uint32_t NP = NW - 1;     // producer waves
+    static constexpr uint32_t LPP = D / 4;     // producer lanes per position (one float4 each)
+    static constexpr uint32_t PPI = 64 / LPP;  // positions per producer instruction
+    static constexpr uint32_t NI = T / PPI;    // float4 per producer lane per tile
+    static constexpr uint32_t RMAX = 16;
 };
 constexpr size_t PV_LDS_BUDGET = 156 * 1024;
 
 __host__ __device__ uint32_t pv_ring_slots(uint32_t cap) {
     const size_t e_bytes = (size_t)div_up(cap, 4) * 16;
     const size_t left = PV_LDS_BUDGET > e_bytes ? PV_LDS_BUDGET - e_bytes : 0;
-    const uint32_t r = (uint32_t)(left / 8192);
-    return r > 16 ? 16 : r;
+    const uint32_t r = (uint32_t)(left / (PvCfg::SLOT * 4));
+    return r > PvCfg::RMAX ? PvCfg::RMAX : r;
 }
 
 template <int HD>
-__global__ __launch_bounds__(1024) void k_attn_softmax_pv(const float *__restrict__ scores,
-                                                          const float *__restrict__ pmax,
-                                                          const float *__restrict__ qkv, const StepParams *p,
-                                                          const float *__restrict__ vc, uint32_t cap, uint32_t S,
-                                                          uint32_t n_heads, uint32_t n_kv, float *o_out,
-                                                          uint8_t *q_out, float *d_out) {
-    using C = PvCfg<HD>;
-    constexpr uint32_t T = C::T;
-    constexpr int NCW = HD > 64 ? HD / 64 : 1;   // chain waves
-    constexpr int NP = 16 - NCW;                 // producer waves
+__global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict__ scores,
+                                                         const float *__restrict__ pmax,
+                                                         const float *__restrict__ qkv, const StepParams *p,
+                                                         const float *__restrict__ vc, uint32_t cap, uint32_t S,
+                                                         uint32_t n_heads, uint32_t n_kv, float *o_out,
+                                                         uint8_t *q_out, float *d_out) {
+    using C = PvCfg;
+    constexpr uint32_t T = C::T, TP = C::TP, D = C::D;
     extern __shared__ __align__(16) float lds[];
-    __shared__ uint32_t ready[16];
-    __shared__ uint32_t done[NCW];
+    __shared__ uint32_t ready[C::RMAX];
+    __shared__ uint32_t done;
     __shared__ float s_inv;
-    __shared__ __align__(16) float ov[HD];
+    __shared__ __align__(16) float ov[D];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t h = blockIdx.x, rep = n_heads / n_kv, g = h / rep;
+    const uint32_t h = blockIdx.x, q = blockIdx.y, rep = n_heads / n_kv, g = h / rep;
     const uint32_t pos = p->pos, n = pos + 1;
     const uint32_t R = pv_ring_slots(cap);
     float *e = lds;                                     // [cap] e_t, then p_t
-    float *ring = lds + (size_t)div_up(cap, 4) * 4;     // [R][T*HD]
+    float *ring = lds + (size_t)div_up(cap, 4) * 4;     // [R][D][TP]
     const float *sc = scores + (size_t)h * cap;
-    float m = -__builtin_huge_valf();
-    for (uint32_t s = 0; s < S; ++s) m = fmaxf(m, pmax[(size_t)h * S + s]);
-    for (uint32_t t = tid; t < n; t += 1024) e[t] = hg_expf(sc[t] - m);
-    if (tid < 16) ready[tid] = 0;
-    if (tid < NCW) done[tid] = 0;
     const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
-    const float *vcg = vc + (size_t)g * cap * HD;
-    const float *vnew = qkv + qd + kvd + g * HD;  // row pos, appended this step
+    const float *vcg = vc + (size_t)g * cap * HD + q * D;
+    const float *vnew = qkv + qd + kvd + g * HD + q * D;  // row pos, appended this step
     const uint32_t ntiles = div_up(n, T);
-    const uint32_t sub = lane / C::TPL, d4 = (lane % C::TPL) * 4;  // producer lane -> (position, dims)
-    const int pw = wave - NCW;
-    // producers: start the V fetch of their first tile before the sum
+    const uint32_t sub = lane / C::LPP, d4 = (lane % C::LPP) * 4;  // producer lane -> (position, elements)
+    const int pw = wave - 1;
     v4f vr[C::NI];
     auto fetch = [&](uint32_t k) {
 #pragma unroll
@@ -751,73 +762,89 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_pv(const float *__restric
                                : *reinterpret_cast<const v4f *>(vcg + (size_t)t * HD + d4);
         }
     };
-    if (pw >= 0 && (uint32_t)pw < ntiles) fetch(pw);
+    if (pw >= 0 && (uint32_t)pw < ntiles) fetch(pw);   // V does not depend on the softmax
+    float m = -__builtin_huge_valf();
+    for (uint32_t s = 0; s < S; ++s) m = fmaxf(m, pmax[(size_t)h * S + s]);
+    for (uint32_t t = tid; t < n; t += 512) e[t] = hg_expf(sc[t] - m);
+    if (tid < (int)C::RMAX) ready[tid] = 0;
+    if (tid == 0) done = 0;
     __syncthreads();
     if (tid == 0) s_inv = 1.0f / seq_sum_lds(e, n, 0.0f);
     __syncthreads();
     const float inv = s_inv;
-    for (uint32_t t = tid; t < n; t += 1024) e[t] = e[t] * inv;
+    for (uint32_t t = tid; t < n; t += 512) e[t] = e[t] * inv;
     __syncthreads();
     if (pw >= 0) {
-        for (uint32_t k = pw; k < ntiles; k += NP) {
+        for (uint32_t k = pw; k < ntiles; k += C::NP) {
             if (k != (uint32_t)pw) fetch(k);
             if (k >= R)
-                for (int c = 0; c < NCW; ++c)
-                    while (__hip_atomic_load(&done[c], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < k - R + 1)
-                        __builtin_amdgcn_s_sleep(1);
-            float *slot = ring + (size_t)(k % R) * T * HD;
+                while (__hip_atomic_load(&done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < k - R + 1)
+                    __builtin_amdgcn_s_sleep(1);
+            float *slot = ring + (size_t)(k % R) * C::SLOT;
 #pragma unroll
             for (uint32_t i = 0; i < C::NI; ++i) {
                 const uint32_t tt = i * C::PPI + sub, t = k * T + tt;
                 const float pt = (t < n) ? e[t] : 0.0f;
-                v4f r;
-                r.x = pt * vr[i].x;
-                r.y = pt * vr[i].y;
-                r.z = pt * vr[i].z;
-                r.w = pt * vr[i].w;
-                *reinterpret_cast<v4f *>(slot + tt * HD + d4) = r;
+                slot[(d4 + 0) * TP + tt] = pt * vr[i].x;
+                slot[(d4 + 1) * TP + tt] = pt * vr[i].y;
+                slot[(d4 + 2) * TP + tt] = pt * vr[i].z;
+                slot[(d4 + 3) * TP + tt] = pt * vr[i].w;
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             if (lane == 0) __hip_atomic_store(&ready[k % R], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     } else {
-        const uint32_t di = wave * 64 + lane;
         float o = 0.0f;
+        const uint32_t di = lane;
         for (uint32_t k = 0; k < ntiles; ++k) {
             while (__hip_atomic_load(&ready[k % R], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != k + 1)
                 __builtin_amdgcn_s_sleep(1);
-            const float *slot = ring + (size_t)(k % R) * T * HD;
-            const uint32_t len = min(T, n - k * T);
-            if (di < HD) {
+            if (di < D) {
+                const v4f *row = reinterpret_cast<const v4f *>(ring + (size_t)(k % R) * C::SLOT + di * TP);
+                const uint32_t len = min(T, n - k * T);
                 if (len == T) {
-#pragma unroll 16
-                    for (uint32_t tt = 0; tt < T; ++tt) o = o + slot[tt * HD + di];
+#pragma unroll 8
+                    for (uint32_t u = 0; u < T / 4; ++u) {
+                        const v4f r = row[u];
+                        o = o + r.x;
+                        o = o + r.y;
+                        o = o + r.z;
+                        o = o + r.w;
+                    }
                 } else {
-                    for (uint32_t tt = 0; tt < len; ++tt) o = o + slot[tt * HD + di];
+                    const float *rs = reinterpret_cast<const float *>(row);
+                    for (uint32_t tt = 0; tt < len; ++tt) o = o + rs[tt];
                 }
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane == 0) __hip_atomic_store(&done[wave], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) __hip_atomic_store(&done, k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        if (di < HD) {
+        if (di < D) {
             ov[di] = o;
-            if (o_out) o_out[h * HD + di] = o;
+            if (o_out) o_out[h * HD + q * D + di] = o;
         }
     }
     __syncthreads();
-    const uint32_t nbh = HD / QK;
-    if ((uint32_t)tid < nbh * 8) {
-        const uint32_t bl = tid >> 3;
-        const int j = tid & 7;
-        float v[4];
+    // quantization of this workgroup's half block (16 of the 32 elements of a block): the 32
+    // elements of block b of the head are the output of workgroups 2b/D.. -- handled below by
+    // writing o and letting the last workgroup of the head quantize.
+}
+
+// Quantize the attention output o (f32, [n_heads*HD]) for attn_output (quant.rs:111-123).
+__global__ __launch_bounds__(256) void k_quant_o(const float *__restrict__ o, uint32_t n, uint8_t *q_out,
+                                                 float *d_out) {
+    const int tid = threadIdx.x, j = tid & 7;
+    const uint32_t nb = n / QK, nc = div_up(nb, 4);
+    for (uint32_t b0 = 0; b0 < nb; b0 += 32) {
+        const uint32_t b = b0 + (tid >> 3);
+        if (b < nb) {
+            float v[4];
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm) v[mm] = ov[bl * QK + j * 4 + mm];
-        quant_block_lane(v, j, h * nbh + bl, q_out, d_out);
+            for (int m = 0; m < 4; ++m) v[m] = o[b * QK + j * 4 + m];
+            quant_block_lane(v, j, b, q_out, d_out);
+        }
     }
-    if (h == 0) {
-        const uint32_t nb = n_heads * HD / QK;
-        zero_pad(nb, div_up(nb, 4), q_out, d_out, tid, 1024);
-    }
+    zero_pad(nb, nc, q_out, d_out, tid, 256);
 }
 
 // ------------------------------------------------------------------ MoE router
@@ -1057,7 +1084,23 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
 }
 
 // ====================================================================== launchers
-#define LAUNCH(kern, grid, block, shm, st, ...) hipLaunchKernelGGL(kern, grid, block, shm, st, __VA_ARGS__)
+// While a LaunchTimer is installed on this thread, every launch carries a start/stop event
+// pair recorded by its own dispatch (hipExtLaunchKernelGGL): the kernel's execution time.
+thread_local LaunchTimer *g_timer = nullptr;
+void set_launch_timer(LaunchTimer *t) { g_timer = t; }
+
+#define LAUNCH(kern, grid, block, shm, st, ...)                                                              \
+    do {                                                                                                     \
+        if (g_timer) {                                                                                       \
+            hipEvent_t a_ = nullptr, b_ = nullptr;                                                           \
+            (void)hipEventCreate(&a_);                                                                       \
+            (void)hipEventCreate(&b_);                                                                       \
+            hipExtLaunchKernelGGL(kern, grid, block, shm, st, a_, b_, 0, __VA_ARGS__);                       \
+            g_timer->add(a_, b_);                                                                            \
+        } else {                                                                                             \
+            hipLaunchKernelGGL(kern, grid, block, shm, st, __VA_ARGS__);                                     \
+        }                                                                                                    \
+    } while (0)
 
 // Kernels whose LDS exceeds the 64 KiB default opt in to the larger gfx950 allocation.
 hipError_t init_kernel_attributes() {
@@ -1109,6 +1152,12 @@ static void mv_launch(hipStream_t st, const Q8Mat &W, const uint8_t *q, const fl
                       uint32_t valid, float *pv, uint32_t *pi) {
     const dim3 grid(matvec_blocks(W.N, threads)), block(threads);
     const size_t shm = (size_t)W.nc * CHUNK_BYTES + (size_t)W.nc * 4 * sizeof(float);
+    if (dq == nullptr) {  // q holds an f32 activation, quantized by each workgroup
+#define MVKF(N) LAUNCH((k_matvec<ORDER, EPI, SCF32, N, true>), grid, block, shm, st, W, q, dq, y, valid, pv, pi)
+        DISPATCH_NCT(W.nc, MVKF)
+#undef MVKF
+        return;
+    }
 #define MVK(N) LAUNCH((k_matvec<ORDER, EPI, SCF32, N>), grid, block, shm, st, W, q, dq, y, valid, pv, pi)
     DISPATCH_NCT(W.nc, MVK)
 #undef MVK
@@ -1150,14 +1199,16 @@ static void attn_exact_launch(hipStream_t st, int which, const float *qkv, const
                               float eps, const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
                               uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part,
                               float *scratch, float *o_out, uint8_t *q_out, float *d_out) {
+    const bool fuse_quant = q_out == nullptr;  // the consumer quantizes o itself
     if (which == 0) {
         LAUNCH(k_attn_scores<HD>, dim3(n_kv, S), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
                n_kv, S, scratch, part);
         return;
     }
-    const size_t shm = (size_t)div_up(cap, 4) * 16 + (size_t)pv_ring_slots(cap) * 8192;
-    LAUNCH(k_attn_softmax_pv<HD>, dim3(n_heads), dim3(1024), shm, st, scratch, part, qkv, p, vc, cap, S, n_heads,
-           n_kv, o_out, q_out, d_out);
+    const size_t shm = (size_t)div_up(cap, 4) * 16 + (size_t)pv_ring_slots(cap) * PvCfg::SLOT * 4;
+    LAUNCH(k_attn_softmax_pv<HD>, dim3(n_heads, HD / PvCfg::D), dim3(PvCfg::NW * 64), shm, st, scratch, part, qkv, p,
+           vc, cap, S, n_heads, n_kv, o_out, q_out, d_out);
+    if (!fuse_quant) LAUNCH(k_quant_o, dim3(1), dim3(256), 0, st, o_out, n_heads * HD, q_out, d_out);
 }
 
 template <int HD>

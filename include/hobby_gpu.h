@@ -133,10 +133,11 @@ int hg_last_routing(const hg_kv *kv, uint32_t *idx, float *w);
 
 #define HG_PROF_CLASSES 12
 /* Time one decode step per kernel class, for measurement tools: the step at pos = len is
- * replayed `reps` times with HIP events recorded on the cache's own stream between launch
- * groups (launched one by one, not as a graph); the cache length does not advance, and the
- * row written at len is overwritten by the next real step.  us[c] = mean microseconds per
- * step in class c, launches[c] = kernel launch groups per step; arrays of HG_PROF_CLASSES. */
+ * replayed `reps` times on the cache's own stream, every kernel launched with a start/stop
+ * HIP event pair recorded by its own dispatch (hipExtLaunchKernelGGL), i.e. kernel execution
+ * time; the cache length does not advance, and the row written at len is overwritten by the
+ * next real step.  us[c] = mean microseconds per step spent in class c, launches[c] = kernel
+ * launches per step; arrays of HG_PROF_CLASSES. */
 int hg_profile_step(const hg_model *m, hg_kv *kv, uint32_t token, uint32_t reps, float *us,
                     uint32_t *launches);
 /* Name of profile class c ("" when out of range). */
