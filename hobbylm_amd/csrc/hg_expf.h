@@ -23,7 +23,7 @@
 
 namespace hg {
 
-HG_HD inline double hg_exp2_tab(uint32_t i) {
+HG_HD inline uint64_t hg_exp2_bits(uint32_t i) {
     // 2^(i/32) with i<<47 subtracted from its bit pattern; indexed by k mod 32
     constexpr uint64_t T[32] = {
         0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
@@ -35,22 +35,20 @@ HG_HD inline double hg_exp2_tab(uint32_t i) {
         0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
         0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
     };
-    return __builtin_bit_cast(double, T[i & 31]);
+    return T[i & 31];
 }
 
 #ifndef HG_EXPF_VARIANT
 #define HG_EXPF_VARIANT 2  // 0: no fusion, 1: fused polynomial, 2: fused polynomial + range reduction
 #endif
 
-HG_HD inline float hg_expf(float x) {
+// expf with the table read through `lookup(i)` (i < 32 -> hg_exp2_bits(i)).  The main path
+// runs for every input and the special cases are selected afterwards, so a lookup that
+// exchanges values between lanes is reached by every lane of a uniform call.
+template <class Lookup>
+HG_HD inline float hg_expf_l(float x, const Lookup &lookup) {
     const uint32_t ix = __builtin_bit_cast(uint32_t, x);
     const uint32_t abstop = (ix >> 20) & 0x7ff;
-    if (abstop >= 0x42b) {                       // |x| >= 88 or x is NaN
-        if (ix == 0xff800000u) return 0.0f;      // -inf
-        if (abstop >= 0x7f8) return x + x;       // +inf or NaN
-        if (x > 0x1.62e42ep6f) return __builtin_huge_valf();   // overflow
-        if (x < -0x1.9fe368p6f) return 0.0f;                   // underflow
-    }
     const double InvLn2N = 0x1.71547652b82fep+0 * 32;
     const double SHIFT = 0x1.8p+52;
     const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -69,7 +67,7 @@ HG_HD inline float hg_expf(float x) {
     kd -= SHIFT;
     const double r = z0 - kd;
 #endif
-    uint64_t t = __builtin_bit_cast(uint64_t, hg_exp2_tab((uint32_t)(ki % 32)));
+    uint64_t t = lookup((uint32_t)(ki % 32));
     t += ki << 47;
     const double s = __builtin_bit_cast(double, t);
 #if HG_EXPF_VARIANT >= 1
@@ -84,11 +82,28 @@ HG_HD inline float hg_expf(float x) {
     y = z * r2 + y;
 #endif
     y = y * s;
-    return (float)y;
+    float res = (float)y;
+    if (abstop >= 0x42b) {                                       // |x| >= 88 or x is NaN
+        if (ix == 0xff800000u) res = 0.0f;                       // -inf
+        else if (abstop >= 0x7f8) res = x + x;                   // +inf or NaN
+        else if (x > 0x1.62e42ep6f) res = __builtin_huge_valf(); // overflow
+        else if (x < -0x1.9fe368p6f) res = 0.0f;                 // underflow
+    }
+    return res;
 }
 
+struct Exp2Const {
+    HG_HD uint64_t operator()(uint32_t i) const { return hg_exp2_bits(i); }
+};
+
+HG_HD inline float hg_expf(float x) { return hg_expf_l(x, Exp2Const{}); }
+
 // 1/(1+exp(-x)) and x*sigmoid(x) as ops.rs:75-82 write them, with the reference expf.
-HG_HD inline float hg_sigmoid(float x) { return 1.0f / (1.0f + hg_expf(-x)); }
-HG_HD inline float hg_silu(float x) { return x * hg_sigmoid(x); }
+template <class Lookup>
+HG_HD inline float hg_sigmoid_l(float x, const Lookup &lookup) { return 1.0f / (1.0f + hg_expf_l(-x, lookup)); }
+template <class Lookup>
+HG_HD inline float hg_silu_l(float x, const Lookup &lookup) { return x * hg_sigmoid_l(x, lookup); }
+HG_HD inline float hg_sigmoid(float x) { return hg_sigmoid_l(x, Exp2Const{}); }
+HG_HD inline float hg_silu(float x) { return hg_silu_l(x, Exp2Const{}); }
 
 }  // namespace hg

@@ -20,6 +20,22 @@ __device__ inline int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
 
 __device__ inline int sdot4(int a, int b) { return __builtin_amdgcn_sdot4(a, b, 0, false); }
 
+// The 32-entry exp table held by the lanes of a wave (lane l: entry l mod 32) and read by
+// lane shuffles, so an exp costs no dependent memory load.  load() is issued at kernel
+// start; the lookup must be reached by every lane of the wave (hg_expf_l guarantees that
+// within one call, the caller that the call itself is uniform).
+struct WaveExpTab {
+    int lo, hi;
+    __device__ static WaveExpTab load(int lane) {
+        const uint64_t b = hg_exp2_bits((uint32_t)lane & 31);
+        return {(int)(uint32_t)b, (int)(uint32_t)(b >> 32)};
+    }
+    __device__ uint64_t operator()(uint32_t i) const {
+        const uint32_t l = (uint32_t)__shfl(lo, (int)i, 64), h = (uint32_t)__shfl(hi, (int)i, 64);
+        return ((uint64_t)h << 32) | l;
+    }
+};
+
 // One 32-block of activation quantization (quant.rs:114-122), lanes j = 0..7 of 8 adjacent
 // threads each holding v[0..3] = x[32b + 4j + 0..3].  d = amax/127, id = 1/d (0 if d == 0),
 // q = clamp(round_half_away(x*id), +-127).  Writes q into the lane-major chunk layout.
@@ -253,29 +269,57 @@ template <bool EXACT>
 __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float *__restrict__ x, const float *__restrict__ w,
                                                        float eps, uint32_t d, float *h_out, uint8_t *q_out,
                                                        float *d_out) {
-    extern __shared__ __align__(16) float xs[];  // 2*d: x, then the squares
+    extern __shared__ __align__(16) float ps[];  // d squares
     __shared__ float red[4];
     __shared__ float s_ss;
-    const int tid = threadIdx.x;
-    for (uint32_t i = tid; i < d; i += 256) xs[i] = x[i];
-    __syncthreads();
-    const float ss = sum_squares<EXACT>(xs, xs + d, d, tid, 256, red, &s_ss);
-    const float scale = 1.0f / sqrtf(ss / (float)d + eps);
-    const uint32_t nb = d / QK, nc = div_up(nb, 4);
-    const int j = tid & 7;
-    for (uint32_t b0 = 0; b0 < nb; b0 += 32) {
-        const uint32_t b = b0 + (tid >> 3);
-        if (b < nb) {
-            float v[4];
+    const int tid = threadIdx.x, j = tid & 7;
+    const uint32_t nb = d / QK, nc = div_up(nb, 4), ng = d / 4;
+    // thread tid owns the float4 groups g = tid + 256 u: elements 4g..4g+3, i.e. lane j of
+    // quantization block g / 8.  x and the gain of the first RQ groups are fetched up front.
+    constexpr uint32_t RQ = 4;
+    v4f xv[RQ], wv[RQ];
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const uint32_t i = b * QK + j * 4 + m;
-                v[m] = xs[i] * scale * w[i];
-                if (h_out) h_out[i] = v[m];
-            }
-            quant_block_lane(v, j, b, q_out, d_out);
-        }
+    for (uint32_t u = 0; u < RQ; ++u) {
+        const uint32_t g = min(tid + 256 * u, ng - 1);
+        xv[u] = reinterpret_cast<const v4f *>(x)[g];
+        wv[u] = reinterpret_cast<const v4f *>(w)[g];
     }
+    float ss = 0.0f;
+    auto squares = [&](const v4f a, uint32_t g) {
+        if (EXACT) {
+            reinterpret_cast<v4f *>(ps)[g] = a * a;
+        } else {
+            ss += a.x * a.x;
+            ss += a.y * a.y;
+            ss += a.z * a.z;
+            ss += a.w * a.w;
+        }
+    };
+#pragma unroll
+    for (uint32_t u = 0; u < RQ; ++u)
+        if (tid + 256 * u < ng) squares(xv[u], tid + 256 * u);
+    for (uint32_t g = tid + 256 * RQ; g < ng; g += 256) squares(reinterpret_cast<const v4f *>(x)[g], g);
+    if (EXACT) {
+        __syncthreads();
+        if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
+    } else {
+        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        if (tid == 0) s_ss = (red[0] + red[1]) + (red[2] + red[3]);
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf(s_ss / (float)d + eps);
+    auto emit = [&](const v4f a, const v4f gw, uint32_t g) {
+        const float v[4] = {a.x * scale * gw.x, a.y * scale * gw.y, a.z * scale * gw.z, a.w * scale * gw.w};
+        if (h_out) reinterpret_cast<v4f *>(h_out)[g] = v4f{v[0], v[1], v[2], v[3]};
+        quant_block_lane(v, j, g / 8, q_out, d_out);
+    };
+#pragma unroll
+    for (uint32_t u = 0; u < RQ; ++u)   // a block's 8 groups are all < ng or all >= ng
+        if (tid + 256 * u < ng) emit(xv[u], wv[u], tid + 256 * u);
+    for (uint32_t g = tid + 256 * RQ; g < ng; g += 256)
+        emit(reinterpret_cast<const v4f *>(x)[g], reinterpret_cast<const v4f *>(w)[g], g);
     zero_pad(nb, nc, q_out, d_out, tid, 256);
 }
 
@@ -399,30 +443,87 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float *__restrict__
 }
 
 // ------------------------------------------------------------------ QK-norm + RoPE
+// Per-lane constants of norm_rope_head for one step, fetched at kernel start: the q and k
+// norm gains of elements lane + 64k and the RoPE cos/sin row at pos for pairs lane + 64k.
+template <int HD>
+struct HeadConst {
+    static constexpr int NW = (HD + 63) / 64, NR = (HD / 2 + 63) / 64;
+    float qn[NW], kn[NW], c[NR], s[NR];
+    __device__ inline void load(const float *__restrict__ qnw, const float *__restrict__ knw,
+                                const float *__restrict__ cs, const float *__restrict__ sn, uint32_t pos,
+                                int lane) {
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            const uint32_t i = min((uint32_t)(lane + 64 * k), (uint32_t)HD - 1);
+            qn[k] = qnw[i];
+            kn[k] = knw[i];
+        }
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            const uint32_t i = min((uint32_t)(lane + 64 * k), (uint32_t)HD / 2 - 1);
+            c[k] = cs[(size_t)pos * (HD / 2) + i];
+            s[k] = sn[(size_t)pos * (HD / 2) + i];
+        }
+    }
+};
+
 // norm_head (model.rs:753-763) then Rope::apply (ops.rs:155-166) of one head vector held in
-// LDS `u` (hd floats); result in `o`.  The sum of squares is sequential (as the reference);
+// LDS `u` (HD floats); result in `o`.  The sum of squares is sequential (as the reference);
 // called by one wave, lane 0 doing the sum.
-__device__ inline void norm_rope_head(const float *u, float *o, const float *__restrict__ w, float eps, uint32_t hd,
-                                      const float *__restrict__ cs, const float *__restrict__ sn, uint32_t pos,
+template <int HD>
+__device__ inline void norm_rope_head(const float *u, float *o, const HeadConst<HD> &hc, bool is_q, float eps,
                                       float *tmp, int lane) {
     float scale = 0.0f;
     if (lane == 0) {
         float ss = 0.0f;
-        for (uint32_t i = 0; i < hd; ++i) ss = ss + u[i] * u[i];
-        scale = 1.0f / sqrtf(ss / (float)hd + eps);
+        for (uint32_t i = 0; i < HD; ++i) ss = ss + u[i] * u[i];
+        scale = 1.0f / sqrtf(ss / (float)HD + eps);
     }
     scale = __shfl(scale, 0, 64);
-    for (uint32_t i = lane; i < hd; i += 64) tmp[i] = u[i] * scale * w[i];
+#pragma unroll
+    for (int k = 0; k < HeadConst<HD>::NW; ++k) {
+        const uint32_t i = lane + 64 * k;
+        if (i < HD) tmp[i] = u[i] * scale * (is_q ? hc.qn[k] : hc.kn[k]);
+    }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    const uint32_t half = hd / 2;
-    for (uint32_t i = lane; i < half; i += 64) {
-        const float c = cs[(size_t)pos * half + i], s = sn[(size_t)pos * half + i];
-        const float x1 = tmp[i], x2 = tmp[half + i];
-        o[i] = x1 * c - x2 * s;
-        o[half + i] = x2 * c + x1 * s;
+    constexpr uint32_t half = HD / 2;
+#pragma unroll
+    for (int k = 0; k < HeadConst<HD>::NR; ++k) {
+        const uint32_t i = lane + 64 * k;
+        if (i < half) {
+            const float c = hc.c[k], s = hc.s[k];
+            const float x1 = tmp[i], x2 = tmp[half + i];
+            o[i] = x1 * c - x2 * s;
+            o[half + i] = x2 * c + x1 * s;
+        }
     }
 }
+
+// The group's q heads, k and v as the QKV matvec produced them ((rep + 2) * HD floats),
+// fetched into registers (issue first, store to LDS `raw` later).
+template <int HD, int MAXREP>
+struct GroupRaw {
+    static constexpr uint32_t N = ((MAXREP + 2) * HD + 255) / 256;
+    float v[N];
+    __device__ inline void load(const float *__restrict__ qkv, uint32_t g, uint32_t rep, uint32_t qd, uint32_t kvd,
+                                int tid) {
+        const uint32_t nraw = (rep + 2) * HD;
+#pragma unroll
+        for (uint32_t u = 0; u < N; ++u) {
+            const uint32_t i = min(tid + 256 * u, nraw - 1);
+            const uint32_t src = i < rep * HD         ? g * rep * HD + i
+                                 : i < (rep + 1) * HD ? qd + g * HD + (i - rep * HD)
+                                                      : qd + kvd + g * HD + (i - (rep + 1) * HD);
+            v[u] = qkv[src];
+        }
+    }
+    __device__ inline void store(float *raw, uint32_t rep, int tid) const {
+#pragma unroll
+        for (uint32_t u = 0; u < N; ++u)
+            if (tid + 256 * u < (rep + 2) * HD) raw[tid + 256 * u] = v[u];
+    }
+};
 
 // ------------------------------------------------------------------ attention (fast)
 // Longest split of a cache of `cap` positions cut in S parts, rounded to whole float4s.
@@ -458,14 +559,14 @@ __global__ __launch_bounds__(256) void k_attn_fast(const float *__restrict__ qkv
     const uint32_t maxchunk = attn_maxchunk(cap, S);
     float *red = sc + rep * maxchunk;        // TOK * rep * HD partial P.V sums
     float *stat = red + TOK * rep * HD;      // 2*rep (max, sum)
-    for (uint32_t i = tid; i < rep * HD; i += 256) raw[i] = qkv[g * rep * HD + i];
-    for (uint32_t i = tid; i < HD; i += 256) {
-        raw[rep * HD + i] = qkv[qd + g * HD + i];
-        raw[(rep + 1) * HD + i] = qkv[qd + kvd + g * HD + i];
-    }
+    GroupRaw<HD, MAXREP> gr;
+    gr.load(qkv, g, rep, qd, kvd, tid);
+    HeadConst<HD> hc;
+    hc.load(qn, kn, cs, sn, pos, lane);
+    gr.store(raw, rep, tid);
     __syncthreads();
     for (uint32_t vi = wave; vi <= rep; vi += 4)
-        norm_rope_head(raw + vi * HD, rot + vi * HD, vi < rep ? qn : kn, eps, HD, cs, sn, pos, tmp + wave * HD, lane);
+        norm_rope_head<HD>(raw + vi * HD, rot + vi * HD, hc, vi < rep, eps, tmp + wave * HD, lane);
     __syncthreads();
     const float *krot = rot + rep * HD;
     const float *vnew = raw + (rep + 1) * HD;
@@ -650,22 +751,26 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
     float *kcg = kc + (size_t)g * cap * HD;
     float *vcg = vc + (size_t)g * cap * HD;
-    // one position per thread (a split holds at most 256); its K row is fetched first
+    // loads in issue order: the group's q, k, v, the norm gains and RoPE row, then this
+    // thread's K row (one position per thread; a split holds at most 256), so the waits for
+    // the first ones leave the K row in flight.  Rows >= n are clamped (not used).
+    GroupRaw<HD, MAXREP> gr;
+    gr.load(qkv, g, rep, qd, kvd, tid);
+    HeadConst<HD> hc;
+    hc.load(qn, kn, cs, sn, pos, lane);
     const uint32_t t = t0 + tid;
     const bool mine = t < t1;
     float kt[HD];
-    if (mine && t != pos)
+    {
+        const uint32_t tr = min(t, n - 1);
 #pragma unroll
         for (int i = 0; i < HD; i += 4)
-            *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kcg + (size_t)t * HD + i);
-    for (uint32_t i = tid; i < rep * HD; i += 256) raw[i] = qkv[g * rep * HD + i];
-    for (uint32_t i = tid; i < HD; i += 256) {
-        raw[rep * HD + i] = qkv[qd + g * HD + i];
-        raw[(rep + 1) * HD + i] = qkv[qd + kvd + g * HD + i];
+            *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kcg + (size_t)tr * HD + i);
     }
+    gr.store(raw, rep, tid);
     __syncthreads();
     for (uint32_t vi = wave; vi <= rep; vi += 4)
-        norm_rope_head(raw + vi * HD, rot + vi * HD, vi < rep ? qn : kn, eps, HD, cs, sn, pos, tmp + wave * HD, lane);
+        norm_rope_head<HD>(raw + vi * HD, rot + vi * HD, hc, vi < rep, eps, tmp + wave * HD, lane);
     __syncthreads();
     const float *krot = rot + rep * HD;
     if (t0 <= pos && pos < t1)
@@ -693,8 +798,8 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
 }
 
 // Softmax and P.V of one query head (ops.rs:112-128, model.rs:227-232):
-//   e_t = exp(s_t - m) with the reference expf (all threads, into LDS);
-//   sum = e_0 + e_1 + ... sequentially (one lane), inv = 1/sum, p_t = e_t * inv;
+//   m = max_t s_t (order-free), e_t = exp(s_t - m) with the reference expf (all threads,
+//   into LDS); sum = e_0 + e_1 + ... sequentially (one lane), inv = 1/sum, p_t = e_t * inv;
 //   o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ...  one sequential chain per output element.
 // Grid: (n_heads, HD/16); workgroup (h, q) owns the 16 output elements [16q, 16q+16) of head h
 // (the softmax is recomputed identically by the HD/16 workgroups of a head).  Wave 0 lanes
@@ -758,22 +863,43 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
 #pragma unroll
         for (uint32_t i = 0; i < C::NI; ++i) {
             const uint32_t t = min(k * T + i * C::PPI + sub, n - 1);
-            vr[i] = (t == pos) ? *reinterpret_cast<const v4f *>(vnew + d4)
-                               : *reinterpret_cast<const v4f *>(vcg + (size_t)t * HD + d4);
+            const float *src = (t == pos) ? vnew + d4 : vcg + (size_t)t * HD + d4;
+            vr[i] = *reinterpret_cast<const v4f *>(src);
         }
     };
-    if (pw >= 0 && (uint32_t)pw < ntiles) fetch(pw);   // V does not depend on the softmax
-    float m = -__builtin_huge_valf();
-    for (uint32_t s = 0; s < S; ++s) m = fmaxf(m, pmax[(size_t)h * S + s]);
-    for (uint32_t t = tid; t < n; t += 512) e[t] = hg_expf(sc[t] - m);
+    // loads in issue order: the split maxima (one per lane), this thread's first scores, the
+    // exp table, then the producers' first V tile, so waiting for the first ones leaves V in
+    // flight
+    constexpr uint32_t EB = 8;
+    float m = pmax[(size_t)h * S + min((uint32_t)lane, S - 1)];
+    float sv[EB];
+#pragma unroll
+    for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(u * 512 + tid, n - 1)];
+    const WaveExpTab tab = WaveExpTab::load(lane);
+    // V does not depend on the softmax.  Every wave fetches (wave 0 and idle producers a
+    // clamped tile they do not use): a load under a branch would make the waits for the
+    // scores after the join also wait for V.
+    fetch(pw < 0 ? 0u : (uint32_t)pw);
+    for (uint32_t s = lane + 64; s < S; s += 64) m = fmaxf(m, pmax[(size_t)h * S + s]);
+    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));   // max is order-free
+    for (uint32_t t0 = 0; t0 < n; t0 += EB * 512) {
+        if (t0)
+#pragma unroll
+            for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(t0 + u * 512 + tid, n - 1)];
+#pragma unroll
+        for (uint32_t u = 0; u < EB; ++u)
+            if (t0 + u * 512 < n) {                      // uniform: every lane calls the exp
+                const uint32_t t = t0 + u * 512 + tid;
+                const float ev = hg_expf_l(sv[u] - m, tab);
+                if (t < n) e[t] = ev;
+            }
+    }
     if (tid < (int)C::RMAX) ready[tid] = 0;
     if (tid == 0) done = 0;
     __syncthreads();
     if (tid == 0) s_inv = 1.0f / seq_sum_lds(e, n, 0.0f);
     __syncthreads();
-    const float inv = s_inv;
-    for (uint32_t t = tid; t < n; t += 512) e[t] = e[t] * inv;
-    __syncthreads();
+    const float inv = s_inv;   // p_t = e_t * inv, formed by the producers
     if (pw >= 0) {
         for (uint32_t k = pw; k < ntiles; k += C::NP) {
             if (k != (uint32_t)pw) fetch(k);
@@ -784,7 +910,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
 #pragma unroll
             for (uint32_t i = 0; i < C::NI; ++i) {
                 const uint32_t tt = i * C::PPI + sub, t = k * T + tt;
-                const float pt = (t < n) ? e[t] : 0.0f;
+                const float pt = (t < n) ? e[t] * inv : 0.0f;
                 slot[(d4 + 0) * TP + tt] = pt * vr[i].x;
                 slot[(d4 + 1) * TP + tt] = pt * vr[i].y;
                 slot[(d4 + 2) * TP + tt] = pt * vr[i].z;
@@ -849,51 +975,107 @@ __global__ __launch_bounds__(256) void k_quant_o(const float *__restrict__ o, ui
 
 // ------------------------------------------------------------------ MoE router
 // ffn_norm RMSNorm + quantization of h, then the F32 router of Model::ffn (model.rs:270-293):
-// logits = W_r h with ops::dot's order (32 lanes per expert row: lane 8a+l is accumulator a,
-// lane l), sigmoid (or softmax) gate, sel = score + bias, descending rank (equal keys:
-// lower expert first), top-k in rank order, optional renormalisation, x weights_scale.
-// One workgroup of 1024 threads.
-template <bool EXACT>
-__global__ __launch_bounds__(1024) void k_ffn_router(const float *__restrict__ x, const float *__restrict__ w,
+// logits = W_r h in ops::dot's order, sigmoid (or softmax) gate, sel = score + bias,
+// descending rank (equal keys: lower expert first), top-k in rank order, optional
+// renormalisation, x weights_scale.  One workgroup of ROUTER_THREADS(E) threads.
+// ops::dot (ops.rs:7-36) keeps 32 accumulator chains c = 8a + l (a: the four f32x8
+// accumulators, l: the lane) over 32-wide steps; here 16 lanes own an expert row, lane l16
+// running chains l16 and l16 + 16, so (acc0 + acc1) + (acc2 + acc3) is a xor-8 exchange and
+// the 8-lane hsum the xor 4/2/1 butterfly.  With d % 32 == 0 and d <= 1024 each lane's 2*d/32
+// router weights are fetched before the RMSNorm chain, so that load overlaps it.
+constexpr uint32_t ROUTER_IMAX = 32;   // 32-wide steps held in registers (d <= 1024)
+
+__host__ __device__ inline uint32_t router_threads(uint32_t E) {
+    const uint32_t t = (E * 16 + 63) / 64 * 64;
+    return t < 256 ? 256 : (t > 1024 ? 1024 : t);
+}
+
+template <bool EXACT, int MAXT>
+__global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x, const float *__restrict__ w,
                                                      float eps, uint32_t d, const float *__restrict__ Wr,
                                                      const float *__restrict__ bias, uint32_t E, uint32_t top_k,
                                                      int gating_sigmoid, int weights_norm, float weights_scale,
                                                      uint8_t *q_out, float *d_out, uint32_t *topk_idx,
                                                      float *topk_w, uint32_t *order, uint32_t *rec_idx,
                                                      float *rec_w) {
-    extern __shared__ __align__(16) float hs[];  // 2*d floats: x / h, then the squares
+    extern __shared__ __align__(16) float hs[];  // 2*d floats: h, then the squares
     __shared__ float red[16];
     __shared__ float s_ss;
     __shared__ float lg[256], scr[256], sel[256];
     __shared__ uint32_t tk[64];
     __shared__ float tw[64];
-    const int tid = threadIdx.x;
-    // router rows of this lane group, fetched before the RMSNorm so the load overlaps it:
-    // lane l32 of group grp holds W_r[e][32 i + l32] for e = grp, grp + 32 and i < d/32
-    constexpr uint32_t RMAX = 2, IMAX = 32;
-    const int grp = tid >> 5, l32 = tid & 31;
+    const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63;
+    const uint32_t e16 = (uint32_t)tid >> 4, l16 = (uint32_t)tid & 15;
     const uint32_t main = d - d % 32;
-    const bool pre = main / 32 <= IMAX && E <= 32 * RMAX && main == d;
-    float wr[RMAX][IMAX];
-    if (pre) {
+    const bool pre = d % 32 == 0 && d / 32 <= ROUTER_IMAX && E * 16 <= (uint32_t)nthr;
+    // loads in issue order: x and the norm gain (needed first), the exp table, the bias, then
+    // the router rows: lane l16 of row e16 holds W_r[e][32 i + l16] and W_r[e][32 i + 16 + l16]
+    constexpr uint32_t XB = 4;
+    float xv[XB], wv[XB];
 #pragma unroll
-        for (uint32_t rr = 0; rr < RMAX; ++rr)
-#pragma unroll
-            for (uint32_t i = 0; i < IMAX; ++i) {
-                const uint32_t e = min(grp + 32 * rr, E - 1), k = min(32 * i + l32, d - 1);
-                wr[rr][i] = Wr[(size_t)e * d + k];
-            }
+    for (uint32_t u = 0; u < XB; ++u) {
+        const uint32_t i = min(tid + u * nthr, d - 1);
+        xv[u] = x[i];
+        wv[u] = w[i];
     }
-    for (uint32_t i = tid; i < d; i += 1024) hs[i] = x[i];
-    __syncthreads();
-    const float ss = sum_squares<EXACT>(hs, hs + d, d, tid, 1024, red, &s_ss);
-    const float scale = 1.0f / sqrtf(ss / (float)d + eps);
-    for (uint32_t i = tid; i < d; i += 1024) hs[i] = hs[i] * scale * w[i];
-    __syncthreads();
+    const WaveExpTab tab = WaveExpTab::load(lane);
+    const float bv = (uint32_t)tid < E ? bias[tid] : 0.0f;
+    // unconditional (addresses clamped, unused without `pre`): a load under a branch makes
+    // the compiler's wait for x after the join count as if the weights were not in flight
+    float wr1[ROUTER_IMAX], wr2[ROUTER_IMAX];
     {
+        const uint32_t e = min(e16, E - 1);
+#pragma unroll
+        for (uint32_t i = 0; i < ROUTER_IMAX; ++i) {
+            const uint32_t k = min(32 * i, d - 32) + l16;   // block start clamped, k + 16 < d
+            wr1[i] = Wr[(size_t)e * d + k];
+            wr2[i] = Wr[(size_t)e * d + k + 16];
+        }
+    }
+    float scale;
+    {
+        float *ps = hs + d;
+        float ss = 0.0f;
+#pragma unroll
+        for (uint32_t u = 0; u < XB; ++u) {
+            const uint32_t i = tid + u * nthr;
+            if (i < d) {
+                if (EXACT) ps[i] = xv[u] * xv[u];
+                else ss += xv[u] * xv[u];
+            }
+        }
+        for (uint32_t i = tid + XB * nthr; i < d; i += nthr) {   // d > XB * nthr only
+            const float v = x[i];
+            if (EXACT) ps[i] = v * v;
+            else ss += v * v;
+        }
+        if (EXACT) {
+            __syncthreads();
+            if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
+        } else {
+            for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+            if (lane == 0) red[tid >> 6] = ss;
+            __syncthreads();
+            if (tid == 0) {
+                float t = 0.0f;
+                for (int i = 0; i < nthr / 64; ++i) t += red[i];
+                s_ss = t;
+            }
+        }
+        __syncthreads();
+        scale = 1.0f / sqrtf(s_ss / (float)d + eps);
+#pragma unroll
+        for (uint32_t u = 0; u < XB; ++u) {
+            const uint32_t i = tid + u * nthr;
+            if (i < d) hs[i] = xv[u] * scale * wv[u];
+        }
+        for (uint32_t i = tid + XB * nthr; i < d; i += nthr) hs[i] = x[i] * scale * w[i];
+    }
+    __syncthreads();
+    {   // quantization of h for the expert matvecs (quant.rs:111-123)
         const uint32_t nb = d / QK, nc = div_up(nb, 4);
         const int j = tid & 7;
-        for (uint32_t b0 = 0; b0 < nb; b0 += 128) {
+        for (uint32_t b0 = 0; b0 < nb; b0 += nthr / 8) {
             const uint32_t b = b0 + (tid >> 3);
             if (b < nb) {
                 float v[4];
@@ -902,90 +1084,104 @@ __global__ __launch_bounds__(1024) void k_ffn_router(const float *__restrict__ x
                 quant_block_lane(v, j, b, q_out, d_out);
             }
         }
-        zero_pad(nb, nc, q_out, d_out, tid, 1024);
+        zero_pad(nb, nc, q_out, d_out, tid, nthr);
     }
-    // router logits, 32 lanes per expert row (ops::dot order)
-    if (pre) {
+    // router logits
+    for (uint32_t e0 = 0; e0 < E; e0 += nthr / 16) {
+        const uint32_t e = e0 + e16;
+        float a1 = 0.0f, a2 = 0.0f;
+        if (e < E) {
+            if (pre) {
 #pragma unroll
-        for (uint32_t rr = 0; rr < RMAX; ++rr) {
-            const uint32_t e = grp + 32 * rr;
-            if (e < E) {
-                float acc = 0.0f;
-#pragma unroll
-                for (uint32_t i = 0; i < IMAX; ++i)
-                    if (32 * i < d) acc = fmaf(wr[rr][i], hs[32 * i + l32], acc);
-                acc = acc + shfl_xor(acc, 8);
-                acc = acc + shfl_xor(acc, 16);
-                acc = acc + shfl_xor(acc, 4);
-                acc = acc + shfl_xor(acc, 2);
-                acc = acc + shfl_xor(acc, 1);
-                if (l32 == 0) lg[e] = acc;
+                for (uint32_t i = 0; i < ROUTER_IMAX; ++i)
+                    if (32 * i < d) {
+                        a1 = fmaf(wr1[i], hs[32 * i + l16], a1);
+                        a2 = fmaf(wr2[i], hs[32 * i + 16 + l16], a2);
+                    }
+            } else {
+                const float *row = Wr + (size_t)e * d;
+                uint32_t i = 0;
+                for (; i < main; i += 32) {
+                    a1 = fmaf(row[i + l16], hs[i + l16], a1);
+                    a2 = fmaf(row[i + 16 + l16], hs[i + 16 + l16], a2);
+                }
+                for (; i + 8 <= d; i += 8)      // 8-wide tail into accumulator 0
+                    if (l16 < 8) a1 = fmaf(row[i + l16], hs[i + l16], a1);
             }
         }
-    } else {
-        for (uint32_t e = grp; e < E; e += 32) {
-            const float *row = Wr + (size_t)e * d;
-            float acc = 0.0f;
-            uint32_t i = 0;
-            for (; i < main; i += 32) acc = fmaf(row[i + l32], hs[i + l32], acc);
-            for (; i + 8 <= d; i += 8)
-                if (l32 < 8) acc = fmaf(row[i + l32], hs[i + l32], acc);
-            acc = acc + shfl_xor(acc, 8);
-            acc = acc + shfl_xor(acc, 16);
-            acc = acc + shfl_xor(acc, 4);
-            acc = acc + shfl_xor(acc, 2);
-            acc = acc + shfl_xor(acc, 1);
-            if (l32 == 0) {
-                for (; i < d; ++i) acc = acc + row[i] * hs[i];
-                lg[e] = acc;
-            }
+        float v = (a1 + shfl_xor(a1, 8)) + (a2 + shfl_xor(a2, 8));
+        v = v + shfl_xor(v, 4);
+        v = v + shfl_xor(v, 2);
+        v = v + shfl_xor(v, 1);
+        if (e < E && l16 == 0) {
+            const uint32_t t0 = pre ? d : d - d % 8;
+            for (uint32_t i = t0; i < d; ++i) v = v + Wr[(size_t)e * d + i] * hs[i];
+            lg[e] = v;
         }
     }
+    if ((uint32_t)tid < E) sel[tid] = bv;   // bias, combined below
     __syncthreads();
+    if (tid >= 64) return;
+    // gate, selection and weights in wave 0 (lane: experts lane, lane + 64, ...)
+    const uint32_t KE = div_up(E, 64);
     if (gating_sigmoid) {
-        if ((uint32_t)tid < E) scr[tid] = hg_sigmoid(lg[tid]);
-    } else if (tid == 0) {
+        for (uint32_t k = 0; k < KE; ++k) {
+            const uint32_t e = lane + 64 * k;
+            const float sg = hg_sigmoid_l(lg[min(e, E - 1)], tab);
+            if (e < E) scr[e] = sg;
+        }
+    } else {   // softmax (ops.rs:112-128): max, exp, sequential sum, scale by 1/sum
         float mx = -__builtin_huge_valf();
-        for (uint32_t e = 0; e < E; ++e)
-            if (lg[e] > mx) mx = lg[e];
+        for (uint32_t k = 0; k < KE; ++k)
+            if (lane + 64 * k < E) mx = fmaxf(mx, lg[lane + 64 * k]);
+        for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, shfl_xor(mx, m));
+        for (uint32_t k = 0; k < KE; ++k) {
+            const uint32_t e = lane + 64 * k;
+            const float ex = hg_expf_l(lg[min(e, E - 1)] - mx, tab);
+            if (e < E) scr[e] = ex;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float sum = 0.0f;
-        for (uint32_t e = 0; e < E; ++e) {
-            scr[e] = hg_expf(lg[e] - mx);
-            sum = sum + scr[e];
-        }
+        for (uint32_t e = 0; e < E; ++e) sum = sum + scr[e];
         const float inv = 1.0f / sum;
-        for (uint32_t e = 0; e < E; ++e) scr[e] = scr[e] * inv;
+        __builtin_amdgcn_wave_barrier();
+        for (uint32_t k = 0; k < KE; ++k)
+            if (lane + 64 * k < E) scr[lane + 64 * k] = scr[lane + 64 * k] * inv;
     }
-    __syncthreads();
-    if ((uint32_t)tid < E) sel[tid] = scr[tid] + bias[tid];
-    __syncthreads();
-    if ((uint32_t)tid < E) {
-        const float me = sel[tid];
-        uint32_t rank = 0;
-        for (uint32_t e = 0; e < E; ++e) rank += (sel[e] > me) || (sel[e] == me && e < (uint32_t)tid);
-        if (rank < top_k) { tk[rank] = tid; tw[rank] = scr[tid]; }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        if (weights_norm) {
-            float s = 0.0f;
-            for (uint32_t r = 0; r < top_k; ++r) s = s + tw[r];
-            s = s + 1e-9f;
-            for (uint32_t r = 0; r < top_k; ++r) tw[r] = tw[r] / s;
-        }
-        for (uint32_t r = 0; r < top_k; ++r) {
-            const float wr = tw[r] * weights_scale;
-            topk_idx[r] = tk[r];
-            topk_w[r] = wr;
-            rec_idx[r] = tk[r];
-            rec_w[r] = wr;
-        }
-        // slot order by ascending expert id (the prompt path's accumulation order)
-        for (uint32_t r = 0; r < top_k; ++r) {
+    for (uint32_t k = 0; k < KE; ++k)
+        if (lane + 64 * k < E) sel[lane + 64 * k] = scr[lane + 64 * k] + sel[lane + 64 * k];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (uint32_t k = 0; k < KE; ++k) {
+        const uint32_t me_e = lane + 64 * k;
+        if (me_e < E) {
+            const float me = sel[me_e];
             uint32_t rank = 0;
-            for (uint32_t q = 0; q < top_k; ++q) rank += tk[q] < tk[r];
-            order[rank] = r;
+            for (uint32_t e = 0; e < E; ++e) rank += (sel[e] > me) || (sel[e] == me && e < me_e);
+            if (rank < top_k) { tk[rank] = me_e; tw[rank] = scr[me_e]; }
         }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float s = 0.0f;   // every lane forms the same sequential sum (f32 iterator sum + 1e-9)
+    if (weights_norm) {
+        for (uint32_t r = 0; r < top_k; ++r) s = s + tw[r];
+        s = s + 1e-9f;
+    }
+    if ((uint32_t)lane < top_k) {
+        const uint32_t r = lane, ei = tk[r];
+        const float wr = (weights_norm ? tw[r] / s : tw[r]) * weights_scale;
+        topk_idx[r] = ei;
+        topk_w[r] = wr;
+        rec_idx[r] = ei;
+        rec_w[r] = wr;
+        uint32_t rk = 0;   // slot order by ascending expert id (the prompt path's accumulation order)
+        for (uint32_t q = 0; q < top_k; ++q) rk += tk[q] < ei;
+        order[rk] = r;
     }
 }
 
@@ -1013,11 +1209,13 @@ __global__ __launch_bounds__(64) void k_ffn_gateup(Q8Mat Wg, Q8Mat Wu, Q8Mat Sg,
     Q8Row<ORDER, SCF32, NCT> rg, ru;
     rg.begin(row_qs(G, r), row_sc<SCF32>(G, r), G.nb, G.nc, j);
     ru.begin(row_qs(U, r), row_sc<SCF32>(U, r), U.nb, U.nc, j);
+    const WaveExpTab tab = WaveExpTab::load(tid);
     stage_act(gq, gd, Wg.nc, sq, sd, tid, 64);
     __syncthreads();
     const float g = rg.finish(sq, sd);
     const float u = ru.finish(sq, sd);
-    if (i < f && j == 0) a_out[(size_t)slot * f + i] = hg_silu(g) * u;
+    const float a = hg_silu_l(g, tab) * u;   // every lane: the table lookup is a lane exchange
+    if (i < f && j == 0) a_out[(size_t)slot * f + i] = a;
 }
 
 // Down rows of every slot and the fixed-order combination (model.rs:306-323; dense:
@@ -1043,27 +1241,45 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
     const uint32_t r = blockIdx.x * 8 + (lane >> 3);
     const uint32_t lr = min(r, d - 1);
     const int j = lane & 7;
+    __shared__ float wsl[64];   // combine weights topk_w[0..top_k)
     const bool routed = slot < top_k;
     const Q8Mat &D = routed ? Wd : Sd;
+    // loads in issue order: the slot's activation (lane j of blocks b = 8u + lane/8) and the
+    // combine weights, then the down row, whose index waits for the router's pick
+    const float *as = a + (size_t)slot * f;
+    constexpr uint32_t AB = 4;
+    v4f av[AB];
+#pragma unroll
+    for (uint32_t u = 0; u < AB; ++u) {
+        const uint32_t b = min(u * 8 + (lane >> 3), nb - 1);
+        av[u] = *reinterpret_cast<const v4f *>(as + b * QK + j * 4);
+    }
+    const float wsel = (!dense && top_k) ? topk_w[min((uint32_t)lane, top_k - 1)] : 0.0f;
     const uint32_t row = routed ? topk_idx[slot] * d + lr : lr;
     Q8Row<ORDER, SCF32, NCT> rd;
     rd.begin(row_qs(D, row), row_sc<SCF32>(D, row), nb, nc, j);
-    {
-        const float *as = a + (size_t)slot * f;
-        for (uint32_t b0 = 0; b0 < nb; b0 += 8) {
-            const uint32_t b = b0 + (lane >> 3);
-            if (b < nb) {
-                float v[4];
 #pragma unroll
-                for (int m = 0; m < 4; ++m) v[m] = as[b * QK + j * 4 + m];
-                quant_block_lane(v, j, b, sq, sd);
-            }
+    for (uint32_t u = 0; u < AB; ++u) {   // a block's 8 lanes are all in or all out
+        const uint32_t b = u * 8 + (lane >> 3);
+        if (b < nb) {
+            const float v[4] = {av[u].x, av[u].y, av[u].z, av[u].w};
+            quant_block_lane(v, j, b, sq, sd);
         }
-        zero_pad(nb, nc, sq, sd, lane, 64);
     }
+    for (uint32_t b0 = AB * 8; b0 < nb; b0 += 8) {
+        const uint32_t b = b0 + (lane >> 3);
+        if (b < nb) {
+            float v[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) v[m] = as[b * QK + j * 4 + m];
+            quant_block_lane(v, j, b, sq, sd);
+        }
+    }
+    zero_pad(nb, nc, sq, sd, lane, 64);
     __syncthreads();
     const float y = rd.finish(sq, sd);
     if (j == 0) ys[slot * 8 + (lane >> 3)] = y;
+    if (wave == 0 && (uint32_t)lane < top_k) wsl[lane] = wsel;
     __syncthreads();
     if (tid < 8) {
         const uint32_t rr = blockIdx.x * 8 + tid;
@@ -1074,7 +1290,7 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
                 float acc = 0.0f;
                 for (uint32_t q = 0; q < top_k; ++q) {
                     const uint32_t s = (ORDER == ORDER_PREFILL) ? order[q] : q;
-                    acc = acc + topk_w[s] * ys[s * 8 + tid];
+                    acc = acc + wsl[s] * ys[s * 8 + tid];
                 }
                 if (n_slots > top_k) acc = acc + ys[top_k * 8 + tid];
                 x[rr] = x[rr] + acc;
@@ -1251,12 +1467,18 @@ void launch_ffn_router(hipStream_t st, bool exact, const float *x, const float *
                        int weights_norm, float weights_scale, uint8_t *q, float *dq, uint32_t *topk_idx,
                        float *topk_w, uint32_t *order, uint32_t *rec_idx, float *rec_w) {
     const size_t shm = 2 * d * sizeof(float);
-    if (exact)
-        LAUNCH(k_ffn_router<true>, dim3(1), dim3(1024), shm, st, x, w, eps, d, Wr, bias, E, top_k, gating_sigmoid,
-               weights_norm, weights_scale, q, dq, topk_idx, topk_w, order, rec_idx, rec_w);
-    else
-        LAUNCH(k_ffn_router<false>, dim3(1), dim3(1024), shm, st, x, w, eps, d, Wr, bias, E, top_k, gating_sigmoid,
-               weights_norm, weights_scale, q, dq, topk_idx, topk_w, order, rec_idx, rec_w);
+    const uint32_t nt = router_threads(E);
+    // up to 640 threads (E <= 40) the kernel may hold 168 VGPRs: no spills with the prefetch
+#define RTK(EX, MT) LAUNCH((k_ffn_router<EX, MT>), dim3(1), dim3(nt), shm, st, x, w, eps, d, Wr, bias, E, top_k, \
+                           gating_sigmoid, weights_norm, weights_scale, q, dq, topk_idx, topk_w, order, rec_idx, rec_w)
+    if (nt <= 640) {
+        if (exact) RTK(true, 640);
+        else RTK(false, 640);
+    } else {
+        if (exact) RTK(true, 1024);
+        else RTK(false, 1024);
+    }
+#undef RTK
 }
 
 template <int ORDER, bool SCF32>
