@@ -192,12 +192,12 @@ def main():
         dom_note = "scores + V rows of all heads at context 2049 per launch (one layer)"
     else:
         dom_bytes = None
-        dom_note = "see DESIGN.md"
+        dom_note = "no algorithmic byte count for this kernel class"
     roof = None
     if dom_bytes:
         a = dom_bytes / (dom_us * 1e-6)
         roof = {"bound": "hbm", "achieved": round(a / 1e9, 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                "frac": round(a / PEAK_HBM, 5), "traffic": None, "kernel": "k_attn_softmax_pv<64>",
+                "frac": round(a / PEAK_HBM, 5), "traffic": None, "kernel": "k_attn_softmax_pv_res<64>",
                 "avg_launch_us": round(dom_us, 2), "bytes_per_launch": dom_bytes, "bytes_note": dom_note}
 
     cpu = None

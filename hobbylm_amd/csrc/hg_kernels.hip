@@ -178,44 +178,45 @@ __device__ inline const void *row_sc(const Q8Mat &W, uint32_t r) {
     return reinterpret_cast<const uint8_t *>(W.sc) + (size_t)r * W.nc * 4 * (SCF32 ? 4 : 2);
 }
 
-// s + a[0] + a[1] + ... + a[n-1], one rounded add at a time in index order (the reference's
-// sequential accumulations), run by a single lane over LDS.  Full batches of 32 are fetched
-// one batch ahead with 16-byte reads so the add chain never waits on LDS.  `a` is 16-byte
-// aligned.
+// s + a[0] + a[1] + ... + a[n-1] in index order (binary32), by one lane over LDS `a`
+// (16-byte aligned).  Batches of 32 values (eight 16-byte reads) alternate between two
+// register sets; each batch's reads are issued before the previous batch's adds and the
+// instruction order is pinned, so the reads stay ahead of the dependent adds.
 __device__ inline float seq_sum_lds(const float *a, uint32_t n, float s) {
     constexpr uint32_t B = 32;
-    const uint32_t nfull = n / B * B;
-    v4f r0[B / 4], r1[B / 4];
+    const uint32_t nb = n / B;
     const v4f *a4 = reinterpret_cast<const v4f *>(a);
-    if (nfull) {
+    if (nb) {
+        v4f ra[B / 4], rb[B / 4];
+        auto ld = [&](v4f(&r)[B / 4], uint32_t b) {
 #pragma unroll
-        for (uint32_t u = 0; u < B / 4; ++u) r0[u] = a4[u];
-    }
-    for (uint32_t i0 = 0; i0 < nfull; i0 += 2 * B) {
-        const bool more1 = i0 + B < nfull;
-        if (more1)
+            for (uint32_t u = 0; u < B / 4; ++u) r[u] = a4[b * (B / 4) + u];
+        };
+        auto add = [&](const v4f(&r)[B / 4]) {
 #pragma unroll
-            for (uint32_t u = 0; u < B / 4; ++u) r1[u] = a4[(i0 + B) / 4 + u];
-#pragma unroll
-        for (uint32_t u = 0; u < B / 4; ++u) {
-            s = s + r0[u].x;
-            s = s + r0[u].y;
-            s = s + r0[u].z;
-            s = s + r0[u].w;
+            for (uint32_t u = 0; u < B / 4; ++u) {
+                s = s + r[u].x;
+                s = s + r[u].y;
+                s = s + r[u].z;
+                s = s + r[u].w;
+            }
+        };
+        ld(ra, 0);
+        ld(rb, min(1u, nb - 1));
+        uint32_t b = 0;
+        for (; b + 2 <= nb; b += 2) {
+            __builtin_amdgcn_sched_barrier(0);
+            add(ra);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(ra, min(b + 2, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            add(rb);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(rb, min(b + 3, nb - 1));
         }
-        if (!more1) break;
-        if (i0 + 2 * B < nfull)
-#pragma unroll
-            for (uint32_t u = 0; u < B / 4; ++u) r0[u] = a4[(i0 + 2 * B) / 4 + u];
-#pragma unroll
-        for (uint32_t u = 0; u < B / 4; ++u) {
-            s = s + r1[u].x;
-            s = s + r1[u].y;
-            s = s + r1[u].z;
-            s = s + r1[u].w;
-        }
+        if (b < nb) add(ra);
     }
-    for (uint32_t i = nfull; i < n; ++i) s = s + a[i];
+    for (uint32_t i = nb * B; i < n; ++i) s = s + a[i];
     return s;
 }
 
@@ -803,8 +804,9 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
 //   o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ...  one sequential chain per output element.
 // Grid: (n_heads, HD/16); workgroup (h, q) owns the 16 output elements [16q, 16q+16) of head h
 // (the softmax is recomputed identically by the HD/16 workgroups of a head).  Wave 0 lanes
-// 0..15 run the chains; waves 1..7 are producers: producer w forms the rounded products
-// p_t * v_t[di] (the reference's separate multiply) of tiles w-1, w-1+NP, ... of T positions
+// 0..15 run the chains; waves 1-3 and 5-7 are producers (wave 4, on the chain's SIMD, idles):
+// producer i forms the rounded products p_t * v_t[di] (the reference's separate multiply) of
+// tiles i, i+NP, ... of T positions
 // into a ring of R LDS slots, stored [element][position] so the chain reads four positions per
 // 16-byte LDS load.  Readiness and release of slots are LDS flags at workgroup scope; every wait
 // is bounded: tile k waits only for tile k - R to be consumed, the chain only for tile k to be
@@ -816,7 +818,7 @@ struct PvCfg {
     static constexpr uint32_t TP = T + 4;      // padded row of a slot
     static constexpr uint32_t SLOT = D * TP;   // floats per slot
     static constexpr uint32_t NW = 8;          // waves per workgroup
-    static constexpr uint32_t NP = NW - 1;     // producer waves
+    static constexpr uint32_t NP = NW - 2;     // producer waves (not wave 0 or wave 4)
     static constexpr uint32_t LPP = D / 4;     // producer lanes per position (one float4 each)
     static constexpr uint32_t PPI = 64 / LPP;  // positions per producer instruction
     static constexpr uint32_t NI = T / PPI;    // float4 per producer lane per tile
@@ -844,7 +846,6 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
     __shared__ uint32_t ready[C::RMAX];
     __shared__ uint32_t done;
     __shared__ float s_inv;
-    __shared__ __align__(16) float ov[D];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t h = blockIdx.x, q = blockIdx.y, rep = n_heads / n_kv, g = h / rep;
     const uint32_t pos = p->pos, n = pos + 1;
@@ -857,7 +858,9 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
     const float *vnew = qkv + qd + kvd + g * HD + q * D;  // row pos, appended this step
     const uint32_t ntiles = div_up(n, T);
     const uint32_t sub = lane / C::LPP, d4 = (lane % C::LPP) * 4;  // producer lane -> (position, elements)
-    const int pw = wave - 1;
+    // waves run on SIMD wave % 4: wave 4 shares SIMD 0 with the chain wave and stays idle so
+    // the chain's dependent adds never wait behind a producer's VALU issue
+    const int pw = wave == 4 ? -1 : (wave < 4 ? wave - 1 : wave - 2);
     v4f vr[C::NI];
     auto fetch = [&](uint32_t k) {
 #pragma unroll
@@ -910,50 +913,245 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
 #pragma unroll
             for (uint32_t i = 0; i < C::NI; ++i) {
                 const uint32_t tt = i * C::PPI + sub, t = k * T + tt;
-                const float pt = (t < n) ? e[t] * inv : 0.0f;
-                slot[(d4 + 0) * TP + tt] = pt * vr[i].x;
-                slot[(d4 + 1) * TP + tt] = pt * vr[i].y;
-                slot[(d4 + 2) * TP + tt] = pt * vr[i].z;
-                slot[(d4 + 3) * TP + tt] = pt * vr[i].w;
+                // positions past the context hold -0, the exact identity of the chain's adds
+                const bool in = t < n;
+                const float pt = in ? e[t] * inv : 0.0f;
+                slot[(d4 + 0) * TP + tt] = in ? pt * vr[i].x : -0.0f;
+                slot[(d4 + 1) * TP + tt] = in ? pt * vr[i].y : -0.0f;
+                slot[(d4 + 2) * TP + tt] = in ? pt * vr[i].z : -0.0f;
+                slot[(d4 + 3) * TP + tt] = in ? pt * vr[i].w : -0.0f;
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             if (lane == 0) __hip_atomic_store(&ready[k % R], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-    } else {
+    } else if (wave == 0 && lane < (int)D) {
+        // Chain lanes 0..15: o += product, position order, 32 positions (eight 16-byte LDS
+        // reads) per chunk, the next chunk's reads issued before the current chunk's adds; the
+        // instruction order is pinned so the reads stay ahead of the dependent adds.
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's unused V prefetch is done
         float o = 0.0f;
         const uint32_t di = lane;
-        for (uint32_t k = 0; k < ntiles; ++k) {
+        auto ready_wait = [&](uint32_t k) {
             while (__hip_atomic_load(&ready[k % R], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != k + 1)
                 __builtin_amdgcn_s_sleep(1);
-            if (di < D) {
-                const v4f *row = reinterpret_cast<const v4f *>(ring + (size_t)(k % R) * C::SLOT + di * TP);
-                const uint32_t len = min(T, n - k * T);
-                if (len == T) {
-#pragma unroll 8
-                    for (uint32_t u = 0; u < T / 4; ++u) {
-                        const v4f r = row[u];
-                        o = o + r.x;
-                        o = o + r.y;
-                        o = o + r.z;
-                        o = o + r.w;
-                    }
-                } else {
-                    const float *rs = reinterpret_cast<const float *>(row);
-                    for (uint32_t tt = 0; tt < len; ++tt) o = o + rs[tt];
-                }
+        };
+        auto rowp = [&](uint32_t k) {
+            return reinterpret_cast<const v4f *>(ring + (size_t)(k % R) * C::SLOT + di * TP);
+        };
+        v4f ca[8], cb[8];
+        auto ld = [&](v4f(&c)[8], const v4f *p) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) c[u] = p[u];
+        };
+        auto add = [&](const v4f(&c)[8]) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                o = o + c[u].x;
+                o = o + c[u].y;
+                o = o + c[u].z;
+                o = o + c[u].w;
             }
+        };
+        static_assert(T == 128, "four chunks of 32 positions per tile");
+        ready_wait(0);
+        ld(ca, rowp(0));
+        for (uint32_t k = 0; k < ntiles; ++k) {
+            const v4f *row = rowp(k);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(cb, row + 8);
+            __builtin_amdgcn_sched_barrier(0);
+            add(ca);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(ca, row + 16);
+            __builtin_amdgcn_sched_barrier(0);
+            add(cb);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(cb, row + 24);
+            __builtin_amdgcn_sched_barrier(0);
+            add(ca);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k + 1 < ntiles) {
+                ready_wait(k + 1);
+                ld(ca, rowp(k + 1));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            add(cb);
+            __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             if (lane == 0) __hip_atomic_store(&done, k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        if (di < D) {
-            ov[di] = o;
-            if (o_out) o_out[h * HD + q * D + di] = o;
+        if (o_out) o_out[h * HD + q * D + di] = o;
+    }
+}
+
+// Softmax and P.V of one query head, as k_attn_softmax_pv, for caches whose V slice and
+// products fit in LDS (pv_res_fits): no ring.  Workgroup (h, q), 512 threads:
+//   while lane 0 sums e_t sequentially, waves 1..7 fetch the 16-element V slice of all
+//   positions and write it transposed into LDS P[d][t]; after inv is known, they replace
+//   P[d][t] by the
+//   rounded product p_t * V[d][t] (p_t = e_t * inv; -0 past the context, the exact identity
+//   of the chain's adds) in groups of G positions, each group flagged when written;
+//   wave 0 lanes 0..15 run the 16 sequential chains over P, waiting only for each group's flag.
+struct PvResCfg {
+    static constexpr uint32_t D = 16;     // output elements per workgroup
+    static constexpr uint32_t G = 64;     // positions per product group (two chain chunks)
+    static constexpr uint32_t VB = 21;    // V float4 per staging thread: 448 * VB >= 4 * cap
+    static constexpr uint32_t NG = 64;    // product groups: one bit each of the ready mask
+};
+
+__host__ __device__ inline uint32_t pv_res_rows(uint32_t cap) { return div_up(cap, 32) * 32; }
+__host__ __device__ inline size_t pv_res_lds(uint32_t cap) {
+    const uint32_t rc = pv_res_rows(cap);
+    return ((size_t)rc + (size_t)PvResCfg::D * (rc + 4)) * 4;
+}
+__host__ __device__ bool pv_res_fits(uint32_t cap) {
+    return cap >= 1 && pv_res_lds(cap) <= PV_LDS_BUDGET && 4 * cap <= 448 * PvResCfg::VB &&
+           div_up(pv_res_rows(cap), PvResCfg::G) <= PvResCfg::NG;
+}
+
+template <int HD>
+__global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__restrict__ scores,
+                                                             const float *__restrict__ pmax,
+                                                             const float *__restrict__ qkv, const StepParams *p,
+                                                             const float *__restrict__ vc, uint32_t cap, uint32_t S,
+                                                             uint32_t n_heads, uint32_t n_kv, float *o_out) {
+    using C = PvResCfg;
+    constexpr uint32_t D = C::D, G = C::G, EB = 8;
+    extern __shared__ __align__(16) float lds[];
+    __shared__ uint64_t ready;   // bit gi: product group gi written
+    __shared__ float s_inv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t h = blockIdx.x, q = blockIdx.y, rep = n_heads / n_kv, g = h / rep;
+    const uint32_t pos = p->pos, n = pos + 1;
+    const uint32_t rc = pv_res_rows(cap), TPC = rc + 4;   // row stride 4 mod 32 banks
+    float *e = lds;                                         // [rc]  e_t
+    float *P = lds + rc;                                    // [D][TPC]  V, then the products
+    const float *sc = scores + (size_t)h * cap;
+    const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
+    const float *vcg = vc + (size_t)g * cap * HD + q * D;
+    const float *vnew = qkv + qd + kvd + g * HD + q * D;   // row pos, appended this step
+    const uint32_t npad = div_up(n, 32) * 32, ngroups = div_up(npad, G);
+    // loads in issue order: the split maxima, this thread's first scores, the exp table
+    float m = pmax[(size_t)h * S + min((uint32_t)lane, S - 1)];
+    float sv[EB];
+#pragma unroll
+    for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(u * 512 + tid, n - 1)];
+    const WaveExpTab tab = WaveExpTab::load(lane);
+    for (uint32_t s = lane + 64; s < S; s += 64) m = fmaxf(m, pmax[(size_t)h * S + s]);
+    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));   // max is order-free
+    for (uint32_t t0 = 0; t0 < n; t0 += EB * 512) {
+        if (t0)
+#pragma unroll
+            for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(t0 + u * 512 + tid, n - 1)];
+#pragma unroll
+        for (uint32_t u = 0; u < EB; ++u)
+            if (t0 + u * 512 < n) {                      // uniform: every lane calls the exp
+                const uint32_t t = t0 + u * 512 + tid;
+                const float ev = hg_expf_l(sv[u] - m, tab);
+                if (t < n) e[t] = ev;
+            }
+    }
+    if (tid == 0) ready = 0;
+    __syncthreads();
+    if (tid == 0) {
+        s_inv = 1.0f / seq_sum_lds(e, n, 0.0f);
+    } else if (wave > 0) {
+        // V items j = vt + 448 r of staging thread vt (position j / 4, elements 4 (j % 4) .. +3),
+        // fetched while lane 0 sums (their issue would otherwise hold up the exps)
+        const uint32_t vt = tid - 64;
+        v4f vv[C::VB];
+#pragma unroll
+        for (uint32_t r = 0; r < C::VB; ++r) {
+            const uint32_t j = min(vt + 448 * r, 4 * n - 1), t = j >> 2, dq = j & 3;
+            const float *src = (t == pos) ? vnew + 4 * dq : vcg + (size_t)t * HD + 4 * dq;
+            vv[r] = *reinterpret_cast<const v4f *>(src);
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < C::VB; ++r) {
+            const uint32_t j = vt + 448 * r;
+            if (j < 4 * n) {
+                const uint32_t t = j >> 2, d0 = 4 * (j & 3);
+                P[(d0 + 0) * TPC + t] = vv[r].x;
+                P[(d0 + 1) * TPC + t] = vv[r].y;
+                P[(d0 + 2) * TPC + t] = vv[r].z;
+                P[(d0 + 3) * TPC + t] = vv[r].w;
+            }
         }
     }
     __syncthreads();
-    // quantization of this workgroup's half block (16 of the 32 elements of a block): the 32
-    // elements of block b of the head are the output of workgroups 2b/D.. -- handled below by
-    // writing o and letting the last workgroup of the head quantize.
+    const float inv = s_inv;
+    if (wave > 0) {
+        // group gi by wave 1 + gi % 7; lane l: positions G gi + 4 (l / 4) .. + 3 of rows
+        // 4 (l % 4) .. + 3
+        static_assert(C::G == 64 && D == 16, "16 position quads x 4 row quads per group");
+        const uint32_t pq = lane >> 2, d0 = 4 * (lane & 3);
+        for (uint32_t gi = wave - 1; gi < ngroups; gi += 7) {
+            const uint32_t t0 = gi * G + 4 * pq;
+            if (t0 < npad) {   // npad is a multiple of 4: the four positions are all in or all out
+                const v4f ev = *reinterpret_cast<const v4f *>(e + t0);
+                const bool in[4] = {t0 < n, t0 + 1 < n, t0 + 2 < n, t0 + 3 < n};
+                const float pt[4] = {in[0] ? ev.x * inv : 0.0f, in[1] ? ev.y * inv : 0.0f,
+                                     in[2] ? ev.z * inv : 0.0f, in[3] ? ev.w * inv : 0.0f};
+                v4f x[4];   // all four rows read before any is written back
+#pragma unroll
+                for (uint32_t c = 0; c < 4; ++c) x[c] = *reinterpret_cast<const v4f *>(P + (d0 + c) * TPC + t0);
+#pragma unroll
+                for (uint32_t c = 0; c < 4; ++c)
+                    *reinterpret_cast<v4f *>(P + (d0 + c) * TPC + t0) =
+                        v4f{in[0] ? pt[0] * x[c].x : -0.0f, in[1] ? pt[1] * x[c].y : -0.0f,
+                            in[2] ? pt[2] * x[c].z : -0.0f, in[3] ? pt[3] * x[c].w : -0.0f};
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0)
+                __hip_atomic_fetch_or(&ready, 1ull << gi, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    } else if (lane < (int)D) {
+        // chains: 32 positions (eight 16-byte reads) per chunk, the next chunk's reads issued
+        // before the current chunk's adds (unconditional, index clamped), order pinned
+        float o = 0.0f;
+        const v4f *row = reinterpret_cast<const v4f *>(P + lane * TPC);
+        const uint32_t nch = npad / 32;
+        uint64_t known = 0;   // ready bits seen so far
+        auto ready_wait = [&](uint32_t gi) {
+            while (!((known >> gi) & 1)) {
+                known = __hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (!((known >> gi) & 1)) __builtin_amdgcn_s_sleep(1);
+            }
+        };
+        v4f ca[8], cb[8];
+        auto ld = [&](v4f(&c)[8], uint32_t ch) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) c[u] = row[ch * 8 + u];
+        };
+        auto add = [&](const v4f(&c)[8]) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                o = o + c[u].x;
+                o = o + c[u].y;
+                o = o + c[u].z;
+                o = o + c[u].w;
+            }
+        };
+        static_assert(G == 64, "a group is the chunk pair c, c + 1 (c even)");
+        ready_wait(0);
+        ld(ca, 0);
+        for (uint32_t c = 0; c < nch; c += 2) {
+            const uint32_t c1 = min(c + 1, nch - 1), c2 = min(c + 2, nch - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(cb, c1);
+            __builtin_amdgcn_sched_barrier(0);
+            add(ca);
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + 1 >= nch) break;
+            if (c2 != c1) ready_wait(c2 / 2);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(ca, c2);
+            __builtin_amdgcn_sched_barrier(0);
+            add(cb);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        o_out[h * HD + q * D + lane] = o;
+    }
 }
 
 // Quantize the attention output o (f32, [n_heads*HD]) for attn_output (quant.rs:111-123).
@@ -1327,6 +1525,12 @@ hipError_t init_kernel_attributes() {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_LDS_BUDGET);
     PV_ATTR(32) PV_ATTR(64) PV_ATTR(128)
 #undef PV_ATTR
+#define PVR_ATTR(HD)                                                                                        \
+    if (e == hipSuccess)                                                                                    \
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_softmax_pv_res<HD>),                 \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_LDS_BUDGET);
+    PVR_ATTR(32) PVR_ATTR(64) PVR_ATTR(128)
+#undef PVR_ATTR
     return e;
 }
 
@@ -1421,9 +1625,14 @@ static void attn_exact_launch(hipStream_t st, int which, const float *qkv, const
                n_kv, S, scratch, part);
         return;
     }
-    const size_t shm = (size_t)div_up(cap, 4) * 16 + (size_t)pv_ring_slots(cap) * PvCfg::SLOT * 4;
-    LAUNCH(k_attn_softmax_pv<HD>, dim3(n_heads, HD / PvCfg::D), dim3(PvCfg::NW * 64), shm, st, scratch, part, qkv, p,
-           vc, cap, S, n_heads, n_kv, o_out, q_out, d_out);
+    if (pv_res_fits(cap)) {
+        LAUNCH(k_attn_softmax_pv_res<HD>, dim3(n_heads, HD / PvResCfg::D), dim3(512), pv_res_lds(cap), st, scratch,
+               part, qkv, p, vc, cap, S, n_heads, n_kv, o_out);
+    } else {
+        const size_t shm = (size_t)div_up(cap, 4) * 16 + (size_t)pv_ring_slots(cap) * PvCfg::SLOT * 4;
+        LAUNCH(k_attn_softmax_pv<HD>, dim3(n_heads, HD / PvCfg::D), dim3(PvCfg::NW * 64), shm, st, scratch, part, qkv,
+               p, vc, cap, S, n_heads, n_kv, o_out, q_out, d_out);
+    }
     if (!fuse_quant) LAUNCH(k_quant_o, dim3(1), dim3(256), 0, st, o_out, n_heads * HD, q_out, d_out);
 }
 
