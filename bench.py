@@ -36,6 +36,7 @@ CTX_END = 2048          # the timed window ends at position CTX_END - 1
 N_PROMPT = 16
 PEAK_HBM = 8.0e12       # MI355X HBM3E, bytes/s
 METRIC = "500M Q8_0 decode tok/s (bs1, ctx2k) + achieved HBM GB/s vs peak"
+DOM_KERNEL = "k_attn_softmax_pv_res<64>"
 
 
 def algorithmic_bytes(cfg, ctx):
@@ -126,6 +127,123 @@ def cpu_baseline(path, gm, gkv, tokens, start, budget_s, max_steps):
             "greedy_match": f"{match}/{n}"}
 
 
+def op_matvec():
+    """Operator-level Q8 matvec (quant.rs:106-136): seeded W ~ N(0, 0.02) quantized by the ggml
+    Q8_0 algorithm, x ~ N(0, 1).  Hot: the same weights every call.  Cold: calls rotate through
+    replicas totalling >= 320 MB, past the 256 MB last-level cache.  Bytes = N K 34/32 + 4K + 4N."""
+    import hobbylm_amd as hg
+    from hobbylm_amd import gguf_synth as gs
+    rng = np.random.default_rng(2)
+    rows = []
+    for n, k, gather in [(1024, 1024, None), (3072, 1024, None), (512, 1024, None), (1024, 512, None),
+                         (512, 1024, 36)]:
+        nm = n * (gather or 1)
+        w = (rng.standard_normal((nm, k)) * 0.02).astype(np.float32)
+        t = hg.Q8Tensor.from_q8_0(gs.quantize_q8_0(w), nm, k)
+        x = rng.standard_normal(k).astype(np.float32)
+        if gather:
+            ids = np.sort(rng.choice(gather, 6, replace=False)).astype(np.uint32)
+            nbytes = 6 * n * k * 34 // 32 + 4 * k + 4 * 6 * n
+            mat_bytes = nm * k * 34 // 32
+            copies = max(1, -(-320 * 2**20 // mat_bytes))
+            hot = t.time_matvec(x, reps=200, rows_per_mat=n, ids=ids)
+            cold = t.time_matvec(x, reps=200, copies=copies, rows_per_mat=n, ids=ids)
+            shape = f"gather 6 of [{gather}x{n}, {k}]"
+        else:
+            nbytes = n * k * 34 // 32 + 4 * k + 4 * n
+            copies = max(1, -(-320 * 2**20 // (n * k * 34 // 32)))
+            hot = t.time_matvec(x, reps=200)
+            cold = t.time_matvec(x, reps=200, copies=copies)
+            shape = f"{n}x{k}"
+        for kind, us in (("hot", hot), ("cold", cold)):
+            gbs = nbytes / (us * 1e-6) / 1e9
+            rows.append({"shape": shape, "cache": kind, "us": round(us, 3), "bytes": nbytes,
+                         "GBps": round(gbs, 1), "frac": round(gbs * 1e9 / PEAK_HBM, 4)})
+        t.close()
+    print(json.dumps({"metric": "Q8_0 matvec kernel time (bs1)", "unit": "us", "higher_is_better": False,
+                      "reps": 200, "data": "synthetic: seeded N(0,0.02) weights, ggml Q8_0", "rows": rows}))
+
+
+def op_attention():
+    """One decode-attention layer (model.rs:199-233): 16 q / 4 kv heads of 64, seeded q, k, v
+    and fp32 cache, append at pos = ctx - 1.  Bytes ~ 2 ctx 256 4 + 2 KB + 8 KB."""
+    import hobbylm_amd as hg
+    rows = []
+    for ctx in (512, 2048, 8192):
+        nbytes = 2 * ctx * 256 * 4 + 2048 + 8192
+        for fast in (False, True):
+            s_us, p_us = hg.attention_time(16, 4, 64, ctx, reps=50, fast=fast)
+            us = s_us + p_us
+            gbs = nbytes / (us * 1e-6) / 1e9
+            rows.append({"ctx": ctx, "mode": "fast" if fast else "reference-order", "us": round(us, 2),
+                         "us_split": [round(s_us, 2), round(p_us, 2)], "bytes": nbytes, "GBps": round(gbs, 1),
+                         "frac": round(gbs * 1e9 / PEAK_HBM, 4)})
+    print(json.dumps({"metric": "decode attention layer kernel time (16q/4kv, hd64, fp32 cache)", "unit": "us",
+                      "higher_is_better": False, "reps": 50, "data": "synthetic seeded", "rows": rows}))
+
+
+COPY_BYTES = 256 * 2**20
+
+
+def pmc_calib():
+    """For rocprofv3 --pmc runs: 4 device copies of COPY_BYTES (the calibration of the byte
+    counters), then prefill + 16 decode steps at positions 2032..2047 of the bench model."""
+    import torch
+    import hobbylm_amd as hg
+    from hobbylm_amd import gguf_synth as gs
+    a = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(4):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    m = hg.Model(gs.synth_path("500M", 1))
+    kv = m.new_cache(max_ctx=CTX_END + 8)
+    prompt = gs.prompt_ids(1, N_PROMPT, 50257)
+    emb = np.stack([m.token_embedding(int(t)) for t in prompt])
+    _, first = m.prefill(emb, kv)
+    pre = m.decode_greedy(first, CTX_END - 16 - N_PROMPT, kv)
+    m.decode_greedy(int(pre[-1]), 16, kv)
+    torch.cuda.synchronize()
+    print("pmc-calib done", flush=True)
+
+
+def _counter_rows(d):
+    """(kernel name, counter name, value) of every dispatch in a rocprofv3 --pmc output dir."""
+    import csv
+    out = []
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            out.append((r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"])))
+    return out
+
+
+def pmc_stats(fetch_dir, write_dir):
+    """Per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) of the decode kernels, scaled so that the
+    calibration copy (COPY_BYTES read, COPY_BYTES written) reads exactly its size."""
+    res = {}
+    factors = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = [r for r in _counter_rows(d) if r[1] == counter]
+        copy = [v for k, c, v in rows if "copy" in k.lower() or "elementwise" in k.lower()]
+        copy = [v for v in copy if v * 1024 > COPY_BYTES / 4]   # the 256 MiB copies only
+        if not copy:
+            raise SystemExit(f"no calibration copy found in {d}")
+        f = COPY_BYTES / (float(np.median(copy)) * 1024)
+        factors[counter] = f
+        agg = {}
+        for k, c, v in rows:
+            if k.startswith("void hg::") or k.startswith("hg::"):
+                name = k.split("(")[0].replace("void ", "").replace("hg::", "")
+                agg.setdefault(name, []).append(v * 1024 * f)
+        for name, vals in agg.items():
+            res.setdefault(name, {})[counter.lower() + "_bytes"] = float(np.mean(vals))
+            res[name]["dispatches"] = len(vals)
+    for name, r in res.items():
+        r["hbm_bytes_per_dispatch"] = round(r.get("fetch_size_bytes", 0.0) + r.get("write_size_bytes", 0.0))
+    return {"calibration": {"copy_bytes": COPY_BYTES, "factor_fetch": factors.get("FETCH_SIZE"),
+                            "factor_write": factors.get("WRITE_SIZE")}, "kernels": res}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -133,10 +251,28 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--repeats", type=int, default=3, help="timed windows; the median is reported")
     ap.add_argument("--window-stats", metavar="ROCPROF_DIR")
+    ap.add_argument("--op", choices=["matvec", "attention"], help="operator-level measurement instead")
+    ap.add_argument("--pmc-calib", action="store_true",
+                    help="a copy of known size, then a short decode window (for rocprofv3 --pmc runs)")
+    ap.add_argument("--pmc-stats", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="HBM traffic per dispatch from two rocprofv3 --pmc runs of --pmc-calib")
     args = ap.parse_args()
     if args.window_stats:
         window_stats(args.window_stats, args.steps)
+        return
+    if args.pmc_stats:
+        print(json.dumps(pmc_stats(*args.pmc_stats)))
+        return
+    if args.op == "matvec":
+        op_matvec()
+        return
+    if args.op == "attention":
+        op_attention()
+        return
+    if args.pmc_calib:
+        pmc_calib()
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this decode path does not shard (--gpus {args.gpus} requested)",
@@ -163,11 +299,20 @@ def main():
     assert kv.len == start
     snap = [kv.read(l) for l in range(cfg.n_layers)] if not args.no_cpu else None
 
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ids = m.decode_greedy(int(warm[-1]), steps, kv)
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
+    times = []
+    for r in range(max(1, args.repeats)):
+        if r:
+            kv.truncate(start)   # the same window again: identical tokens, rows rewritten
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ids_r = m.decode_greedy(int(warm[-1]), steps, kv)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        if r == 0:
+            ids = ids_r
+        elif list(ids_r) != list(ids):
+            sys.exit("repeated window produced different tokens")
+    dt = float(np.median(times))
     tok_s = steps / dt
 
     # parity of the whole greedy stream with the oracle's fixture
@@ -196,9 +341,19 @@ def main():
     roof = None
     if dom_bytes:
         a = dom_bytes / (dom_us * 1e-6)
+        traffic, tnote = None, None
+        tf = os.path.join(ROOT, "profiles", "traffic_decode_500M_ctx2k.json")
+        if os.path.exists(tf):
+            tj = json.load(open(tf))
+            k = tj.get("kernels", {}).get(DOM_KERNEL)
+            if k:
+                traffic = k["hbm_bytes_per_dispatch"]
+                tnote = f"rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, copy-calibrated ({os.path.relpath(tf, ROOT)})"
         roof = {"bound": "hbm", "achieved": round(a / 1e9, 2), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                "frac": round(a / PEAK_HBM, 5), "traffic": None, "kernel": "k_attn_softmax_pv_res<64>",
+                "frac": round(a / PEAK_HBM, 5), "traffic": traffic, "kernel": DOM_KERNEL,
                 "avg_launch_us": round(dom_us, 2), "bytes_per_launch": dom_bytes, "bytes_note": dom_note}
+        if tnote:
+            roof["traffic_note"] = tnote
 
     cpu = None
     if not args.no_cpu:
@@ -208,6 +363,7 @@ def main():
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps,
         "warmup": warmup, "ms_per_step": round(dt * 1e3 / steps, 4), "higher_is_better": True,
+        "repeats_ms_per_step": [round(t * 1e3 / steps, 4) for t in times],
         "scaling": "weak", "vs_baseline": None, "dtype": "int8xint8->f32 (Q8_0), f32 attention",
         "data": "synthetic: random-init 500M-shaped Q8_0 GGUF (seed 1), seeded 16-token prompt",
         "config": {"workload": f"hobbylm 500M-shaped sparse MoE, Q8_0, batch 1, greedy decode positions "

@@ -60,6 +60,7 @@ SIGNATURES = {
     "hg_kv_new": (C.c_int, [_vp, C.c_uint32, C.c_uint32, C.POINTER(_vp)]),
     "hg_kv_free": (None, [_vp]),
     "hg_kv_len": (C.c_uint32, [_vp]),
+    "hg_kv_truncate": (C.c_int, [_vp, C.c_uint32]),
     "hg_kv_read": (C.c_int, [_vp, C.c_uint32, _f32p, _f32p]),
     "hg_forward": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, _vp, C.POINTER(C.c_uint32)]),
     "hg_forward_x": (C.c_int, [_vp, _vp, _f32p, C.c_uint32, _vp, C.POINTER(C.c_uint32)]),
@@ -80,6 +81,9 @@ SIGNATURES = {
     "hg_attention_decode": (C.c_int, [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_float, C.c_float, C.c_uint32,
                                       C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _f32p, _f32p, _f32p,
                                       C.c_uint32]),
+    "hg_q8_tensor_time_matvec": (C.c_int, [_vp, _f32p, C.c_uint32, C.c_uint32, C.c_uint32, _vp, C.c_uint32, _f32p]),
+    "hg_attention_time": (C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                    _f32p]),
 }
 
 _lib = None
@@ -221,6 +225,10 @@ class KvCache:
     def len(self) -> int:
         return int(lib().hg_kv_len(self.h))
 
+    def truncate(self, length: int):
+        """cache.len = length (model.rs:63): decode continues from `length`."""
+        _check(lib().hg_kv_truncate(self.h, length))
+
     def read(self, layer: int):
         c = self.model.cfg
         kvd = c.n_kv_heads * c.head_dim
@@ -284,6 +292,20 @@ class Q8Tensor:
         _check(lib().hg_q8_tensor_matvec(self.h, np.ascontiguousarray(x, np.float32), y))
         return y
 
+    def time_matvec(self, x: np.ndarray, reps: int = 100, copies: int = 1, rows_per_mat: int = 0,
+                    ids=None) -> float:
+        """Mean kernel microseconds of a device-resident matvec (or gather over `ids`), rotating
+        through `copies` replicas of the weights (measurement only)."""
+        us = np.zeros(1, np.float32)
+        if ids is None:
+            _check(lib().hg_q8_tensor_time_matvec(self.h, np.ascontiguousarray(x, np.float32), reps, copies, 0,
+                                                  None, 0, us))
+        else:
+            idv = np.ascontiguousarray(ids, np.uint32)
+            _check(lib().hg_q8_tensor_time_matvec(self.h, np.ascontiguousarray(x, np.float32), reps, copies,
+                                                  rows_per_mat, idv.ctypes.data_as(_vp), len(idv), us))
+        return float(us[0])
+
     def matmul(self, x: np.ndarray) -> np.ndarray:
         tn = x.shape[0]
         y = np.empty((tn, self.out), np.float32)
@@ -296,6 +318,14 @@ class Q8Tensor:
         _check(lib().hg_q8_tensor_matvec_gather(self.h, rows_per_mat, ids, ids.size,
                                                 np.ascontiguousarray(x, np.float32), y.reshape(-1)))
         return y
+
+
+def attention_time(n_heads: int, n_kv: int, hd: int, ctx: int, reps: int = 50, fast: bool = False):
+    """Mean kernel microseconds (scores, softmax + P.V) of one decode-attention layer at
+    context ctx on seeded device-resident data (measurement only)."""
+    us = np.zeros(2, np.float32)
+    _check(lib().hg_attention_time(n_heads, n_kv, hd, ctx, reps, HG_KV_FAST if fast else 0, us))
+    return float(us[0]), float(us[1])
 
 
 def attention_decode(q, k, v, q_norm, k_norm, eps, theta, rope_len, n_heads, n_kv, hd, pos, kcache, vcache,

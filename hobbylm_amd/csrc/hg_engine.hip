@@ -844,23 +844,94 @@ int hg_q8_tensor_matvec_gather(const hg_q8_tensor *t, uint32_t rows_per_mat, con
     const uint32_t n_mat = W.N / rows_per_mat;
     for (uint32_t i = 0; i < n_ids; ++i)
         if (ids[i] >= n_mat) return fail(HG_ERR_ARG, "expert id " + std::to_string(ids[i]) + " out of range");
+    if (n_ids == 0) return HG_OK;
     return with_act(t, x, 1, [&](DevBuf &qa, DevBuf &da) -> int {
-        DevBuf dy;
-        int rc = dy.alloc((size_t)rows_per_mat * n_ids * 4);
-        if (rc) return rc;
-        const size_t sc_elem = W.sc_f32 ? 4 : 2;
-        for (uint32_t i = 0; i < n_ids; ++i) {
-            Q8Mat v = W;
-            v.N = rows_per_mat;
-            v.qs = W.qs + (size_t)ids[i] * rows_per_mat * W.nc * CHUNK_BYTES;
-            v.sc = static_cast<const uint8_t *>(W.sc) + (size_t)ids[i] * rows_per_mat * W.nc * 4 * sc_elem;
-            launch_matvec(t->st, ORDER_DECODE, EPI_STORE, v, qa.as<uint8_t>(), da.as<float>(),
-                          dy.as<float>() + (size_t)i * rows_per_mat, 64, 0, nullptr, nullptr);
-        }
+        DevBuf dy, did;
+        int rc;
+        if ((rc = dy.alloc((size_t)rows_per_mat * n_ids * 4)) || (rc = did.upload(ids, (size_t)n_ids * 4))) return rc;
+        launch_matvec_gather(t->st, W, rows_per_mat, did.as<uint32_t>(), n_ids, qa.as<uint8_t>(), da.as<float>(),
+                             dy.as<float>());
         HIP_TRY(hipGetLastError());
         HIP_TRY(hipMemcpyAsync(y, dy.p, (size_t)rows_per_mat * n_ids * 4, hipMemcpyDeviceToHost, t->st));
         HIP_TRY(hipStreamSynchronize(t->st));
         return HG_OK;
+    });
+}
+
+namespace {
+// Mean kernel microseconds of the launches a timer recorded (after the stream is drained).
+int timer_mean_us(LaunchTimer &timer, float *us) {
+    double tot = 0.0;
+    hipError_t e = hipSuccess;
+    for (size_t i = 0; e == hipSuccess && i < timer.ev.size(); ++i) {
+        float ms = 0.0f;
+        e = hipEventElapsedTime(&ms, timer.ev[i].first, timer.ev[i].second);
+        tot += ms;
+    }
+    for (auto &pr : timer.ev) {
+        (void)hipEventDestroy(pr.first);
+        (void)hipEventDestroy(pr.second);
+    }
+    if (e != hipSuccess) return fail(HG_ERR_DEVICE, std::string("timing: ") + hipGetErrorString(e));
+    *us = timer.ev.empty() ? 0.0f : (float)(tot * 1000.0 / timer.ev.size());
+    return HG_OK;
+}
+}  // namespace
+
+int hg_q8_tensor_time_matvec(const hg_q8_tensor *t, const float *x, uint32_t reps, uint32_t copies,
+                             uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids, float *us) {
+    if (!t || !x || !us || !reps || !copies) return fail(HG_ERR_ARG, "NULL argument or zero count");
+    const Q8Mat &W = t->w.m;
+    const bool gather = ids != nullptr;
+    if (gather) {
+        if (rows_per_mat == 0 || W.N % rows_per_mat || n_ids == 0) return fail(HG_ERR_ARG, "bad gather shape");
+        for (uint32_t i = 0; i < n_ids; ++i)
+            if (ids[i] >= W.N / rows_per_mat) return fail(HG_ERR_ARG, "expert id out of range");
+    }
+    const size_t qs_bytes = (size_t)W.N * W.nc * CHUNK_BYTES, sc_bytes = (size_t)W.N * W.nc * 4 * (W.sc_f32 ? 4 : 2);
+    return with_act(t, x, 1, [&](DevBuf &qa, DevBuf &da) -> int {
+        DevBuf dy, did, rep;
+        int rc;
+        const uint32_t rows = gather ? rows_per_mat * n_ids : W.N;
+        if ((rc = dy.alloc((size_t)rows * 4))) return rc;
+        if (gather && (rc = did.upload(ids, (size_t)n_ids * 4))) return rc;
+        if (copies > 1) {   // replicas of the weights, each (qs, scales) 256-byte aligned
+            const size_t one = (qs_bytes + 255) / 256 * 256 + (sc_bytes + 255) / 256 * 256;
+            if ((rc = rep.alloc(one * copies))) return rc;
+            for (uint32_t c = 0; c < copies; ++c) {
+                uint8_t *b = rep.as<uint8_t>() + one * c;
+                HIP_TRY(hipMemcpyAsync(b, W.qs, qs_bytes, hipMemcpyDeviceToDevice, t->st));
+                HIP_TRY(hipMemcpyAsync(b + (qs_bytes + 255) / 256 * 256, W.sc, sc_bytes, hipMemcpyDeviceToDevice, t->st));
+            }
+        }
+        const size_t one = (qs_bytes + 255) / 256 * 256 + (sc_bytes + 255) / 256 * 256;
+        auto view = [&](uint32_t c) {
+            Q8Mat v = W;
+            if (copies > 1) {
+                uint8_t *b = rep.as<uint8_t>() + one * c;
+                v.qs = b;
+                v.sc = b + (qs_bytes + 255) / 256 * 256;
+            }
+            return v;
+        };
+        auto call = [&](uint32_t r) {
+            const Q8Mat v = view(r % copies);
+            if (gather)
+                launch_matvec_gather(t->st, v, rows_per_mat, did.as<uint32_t>(), n_ids, qa.as<uint8_t>(), da.as<float>(),
+                                     dy.as<float>());
+            else
+                launch_matvec(t->st, ORDER_DECODE, EPI_STORE, v, qa.as<uint8_t>(), da.as<float>(), dy.as<float>(), 64, 0,
+                              nullptr, nullptr);
+        };
+        for (uint32_t r = 0; r < 3; ++r) call(r);   // warm-up
+        HIP_TRY(hipStreamSynchronize(t->st));
+        LaunchTimer timer;
+        set_launch_timer(&timer);
+        for (uint32_t r = 0; r < reps; ++r) call(r);
+        set_launch_timer(nullptr);
+        HIP_TRY(hipGetLastError());
+        HIP_TRY(hipStreamSynchronize(t->st));
+        return timer_mean_us(timer, us);
     });
 }
 
@@ -915,6 +986,94 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
         memcpy(kc + ((size_t)pos * n_kv + g) * hd, &kh[((size_t)g * cap + pos) * hd], hd * 4);
         memcpy(vc + ((size_t)pos * n_kv + g) * hd, &vh[((size_t)g * cap + pos) * hd], hd * 4);
     }
+    return HG_OK;
+}
+
+int hg_attention_time(uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t ctx, uint32_t reps, uint32_t flags,
+                      float *us) {
+    if (!us || !reps || !ctx) return fail(HG_ERR_ARG, "NULL argument or zero count");
+    if (hd != 32 && hd != 64 && hd != 128) return fail(HG_ERR_UNSUPPORTED, "head_dim not in {32, 64, 128}");
+    if (!n_kv || n_heads % n_kv || n_heads / n_kv > 8) return fail(HG_ERR_UNSUPPORTED, "unsupported head grouping");
+    const bool exact = (flags & HG_KV_FAST) == 0;
+    if (exact && !pv_res_fits(ctx) && pv_ring_slots(ctx) < 2)
+        return fail(HG_ERR_UNSUPPORTED, "reference-order attention supports at most 32768 positions");
+    int rc = check_device();
+    if (rc) return rc;
+    const uint32_t qd = n_heads * hd, kvd = n_kv * hd, cap = ctx, S = std::max(64u, div_up(ctx, 256)), pos = ctx - 1;
+    // seeded N(0,1)-like data: q, k, v and the cache rows 0 .. pos-1; unit QK-norm gains
+    uint64_t st = 0x9e3779b97f4a7c15ull;
+    auto rnd = [&]() {
+        st ^= st << 13; st ^= st >> 7; st ^= st << 17;
+        return (float)((double)(st >> 11) * 0x1p-53 * 2.0 - 1.0) * 1.7320508f;
+    };
+    std::vector<float> qkv(qd + 2 * kvd), kh((size_t)n_kv * cap * hd), vh(kh.size()), ones(hd, 1.0f), cs, sn;
+    for (float &v : qkv) v = rnd();
+    for (float &v : kh) v = rnd();
+    for (float &v : vh) v = rnd();
+    rope_table(hd, ctx, 10000.0f, cs, sn);
+    StepParams hp{};
+    hp.pos = pos;
+    DevBuf dqkv, dqn, dcs, dsn, dk, dv, dp, dpart, dscr, dout, dq, dd;
+    const size_t part_floats = exact ? (size_t)n_heads * S : (size_t)n_heads * S * (hd + 2);
+    // the fast path's merge also writes the quantized o (the exact path leaves it to attn_output)
+    if ((rc = dq.alloc((size_t)div_up(qd / QK, 4) * CHUNK_BYTES)) || (rc = dd.alloc((size_t)div_up(qd / QK, 4) * 16)))
+        return rc;
+    uint8_t *q_out = exact ? nullptr : dq.as<uint8_t>();
+    float *d_out = exact ? nullptr : dd.as<float>();
+    if ((rc = dqkv.upload(qkv.data(), qkv.size() * 4)) || (rc = dqn.upload(ones.data(), hd * 4)) ||
+        (rc = dcs.upload(cs.data(), cs.size() * 4)) || (rc = dsn.upload(sn.data(), sn.size() * 4)) ||
+        (rc = dk.upload(kh.data(), kh.size() * 4)) || (rc = dv.upload(vh.data(), vh.size() * 4)) ||
+        (rc = dp.upload(&hp, sizeof hp)) || (rc = dpart.alloc(std::max(part_floats, (size_t)n_heads * S * (hd + 2)) * 4)) ||
+        (rc = dscr.alloc((size_t)n_heads * cap * 4)) || (rc = dout.alloc((size_t)qd * 4)))
+        return rc;
+    HIP_TRY(hipDeviceSynchronize());
+    hipStream_t s0 = nullptr;
+    HIP_TRY(hipStreamCreateWithFlags(&s0, hipStreamNonBlocking));
+    auto layer = [&]() {
+        for (int which = 0; which < 2; ++which)
+            launch_attn(s0, exact, which, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f,
+                        dcs.as<float>(), dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap,
+                        n_heads, n_kv, S, dpart.as<float>(), dscr.as<float>(), dout.as<float>(), q_out, d_out);
+    };
+    for (int r = 0; r < 3; ++r) layer();
+    hipError_t e = hipStreamSynchronize(s0);
+    LaunchTimer timer;
+    if (e == hipSuccess) {
+        set_launch_timer(&timer);
+        for (uint32_t r = 0; r < reps; ++r) {
+            timer.cls = 0;
+            launch_attn(s0, exact, 0, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f, dcs.as<float>(),
+                        dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap, n_heads, n_kv, S,
+                        dpart.as<float>(), dscr.as<float>(), dout.as<float>(), q_out, d_out);
+            timer.cls = 1;
+            launch_attn(s0, exact, 1, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f, dcs.as<float>(),
+                        dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap, n_heads, n_kv, S,
+                        dpart.as<float>(), dscr.as<float>(), dout.as<float>(), q_out, d_out);
+        }
+        set_launch_timer(nullptr);
+        e = hipStreamSynchronize(s0);
+    }
+    double t[2] = {0.0, 0.0};
+    for (size_t i = 0; e == hipSuccess && i < timer.ev.size(); ++i) {
+        float ms = 0.0f;
+        e = hipEventElapsedTime(&ms, timer.ev[i].first, timer.ev[i].second);
+        t[timer.tags[i] ? 1 : 0] += ms;
+    }
+    for (auto &pr : timer.ev) {
+        (void)hipEventDestroy(pr.first);
+        (void)hipEventDestroy(pr.second);
+    }
+    (void)hipStreamDestroy(s0);
+    if (e != hipSuccess) return fail(HG_ERR_DEVICE, std::string("attention timing: ") + hipGetErrorString(e));
+    us[0] = (float)(t[0] * 1000.0 / reps);
+    us[1] = (float)(t[1] * 1000.0 / reps);
+    return HG_OK;
+}
+
+int hg_kv_truncate(hg_kv *kv, uint32_t len) {
+    if (!kv) return fail(HG_ERR_ARG, "NULL argument");
+    if (len > kv->len) return fail(HG_ERR_ARG, "truncate can only shorten the cache");
+    kv->len = len;
     return HG_OK;
 }
 

@@ -18,6 +18,8 @@ void set_launch_timer(LaunchTimer *t);
 hipError_t init_kernel_attributes();
 // LDS ring slots of the reference-order P.V kernel for a cache of cap positions (>= 2 needed).
 __host__ __device__ uint32_t pv_ring_slots(uint32_t cap);
+// Whether the V slice and products of a cache of cap positions fit the LDS-resident P.V kernel.
+__host__ __device__ bool pv_res_fits(uint32_t cap);
 void launch_embed(hipStream_t st, const float *emb, uint32_t d, const StepParams *p, float *x);
 void launch_load_row(hipStream_t st, const float *inputs, uint32_t d, const StepParams *p, float *x);
 void launch_advance(hipStream_t st, StepParams *p);
@@ -28,6 +30,9 @@ uint32_t matvec_blocks(uint32_t N, uint32_t threads);
 // dq == nullptr: q points to an f32 activation that each workgroup quantizes in its prologue.
 void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uint8_t *q, const float *dq, float *y,
                    uint32_t threads, uint32_t valid, float *pv, uint32_t *pi);
+// The matvecs of matrices ids[0..n_ids) of a stack of rows_per_mat-row matrices, one launch.
+void launch_matvec_gather(hipStream_t st, const Q8Mat &W, uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids,
+                          const uint8_t *q, const float *dq, float *y);
 void launch_argmax_final(hipStream_t st, const float *pv, const uint32_t *pi, uint32_t n, StepParams *p,
                          uint32_t *out_ids);
 size_t attn_fast_shm(uint32_t hd, uint32_t rep, uint32_t cap, uint32_t S);

@@ -408,6 +408,28 @@ __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restri
     }
 }
 
+// Q8Tensor::matvec of the matrices ids[0..n) of a stack of equal matrices (rows_per_mat rows
+// each; the expert matvecs of model.rs:301-318 at the operator level), one launch:
+// blockIdx.y = position in ids, y[blockIdx.y * rows_per_mat + r].  Same row order as k_matvec.
+template <bool SCF32, int NCT>
+__global__ __launch_bounds__(256) void k_matvec_gather(Q8Mat W, uint32_t rows_per_mat, const uint32_t *__restrict__ ids,
+                                                       const uint8_t *__restrict__ gq, const float *__restrict__ gd,
+                                                       float *y) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint8_t *sq = smem;
+    float *sd = reinterpret_cast<float *>(smem + W.nc * CHUNK_BYTES);
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const uint32_t r = blockIdx.x * (nthr >> 3) + (tid >> 3), lr = min(r, rows_per_mat - 1);
+    const uint32_t row = ids[blockIdx.y] * rows_per_mat + lr;
+    const int j = tid & 7;
+    Q8Row<ORDER_DECODE, SCF32, NCT> rd;
+    rd.begin(row_qs(W, row), row_sc<SCF32>(W, row), W.nb, W.nc, j);
+    stage_act(gq, gd, W.nc, sq, sd, tid, nthr);
+    __syncthreads();
+    const float v = rd.finish(sq, sd);
+    if (r < rows_per_mat && j == 0) y[(size_t)blockIdx.y * rows_per_mat + r] = v;
+}
+
 // Final greedy argmax over the per-workgroup partials; writes out_ids[step] and, in
 // feedback mode, chains the next step (token = next, pos += 1).
 __global__ __launch_bounds__(1024) void k_argmax_final(const float *__restrict__ pv, const uint32_t *__restrict__ pi,
@@ -1600,6 +1622,19 @@ void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uin
         else MV(ORDER_PREFILL, EPI_LOGITS);
     }
 #undef MV
+}
+
+void launch_matvec_gather(hipStream_t st, const Q8Mat &W, uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids,
+                          const uint8_t *q, const float *dq, float *y) {
+    const dim3 grid(div_up(rows_per_mat, 32), n_ids);
+    const size_t shm = (size_t)W.nc * CHUNK_BYTES + (size_t)W.nc * 4 * sizeof(float);
+#define MGK(N)                                                                                               \
+    do {                                                                                                     \
+        if (W.sc_f32) LAUNCH((k_matvec_gather<true, N>), grid, dim3(256), shm, st, W, rows_per_mat, ids, q, dq, y);   \
+        else LAUNCH((k_matvec_gather<false, N>), grid, dim3(256), shm, st, W, rows_per_mat, ids, q, dq, y);           \
+    } while (0)
+    DISPATCH_NCT(W.nc, MGK)
+#undef MGK
 }
 
 void launch_argmax_final(hipStream_t st, const float *pv, const uint32_t *pi, uint32_t n, StepParams *p,

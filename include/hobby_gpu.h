@@ -92,6 +92,9 @@ int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out);
 void hg_kv_free(hg_kv *kv);
 /* KvCache.len (model.rs:63) */
 uint32_t hg_kv_len(const hg_kv *kv);
+/* `cache.len = len` on the reference's pub field (model.rs:63): keep rows [0, len) and
+ * decode on from len (len <= hg_kv_len; later rows are overwritten). */
+int hg_kv_truncate(hg_kv *kv, uint32_t len);
 /* Cache rows [0, len) of one layer in the reference layout KvCache.k[layer] /
  * KvCache.v[layer] ([len][n_kv_heads*head_dim], model.rs:60-64, 210-211). */
 int hg_kv_read(const hg_kv *kv, uint32_t layer, float *k, float *v);
@@ -171,6 +174,22 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
                         const float *k_norm, float eps, float theta, uint32_t rope_len,
                         uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t pos, float *kc,
                         float *vc, float *out, uint32_t flags);
+
+/* ---- measurement (no counterpart in the reference) ------------------------------------ */
+
+/* Kernel time of t's matvec on device-resident data: x[in] is quantized once on the device,
+ * then `reps` matvecs (ids != NULL: the gather of hg_q8_tensor_matvec_gather, one launch)
+ * run back to back, each timed by events its own dispatch records.  copies > 1 replicates
+ * the weights that many times and rotates through the replicas (cold caches when
+ * copies * bytes exceeds the last-level cache).  us = mean microseconds per call. */
+int hg_q8_tensor_time_matvec(const hg_q8_tensor *t, const float *x, uint32_t reps, uint32_t copies,
+                             uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids, float *us);
+/* Kernel time of one decode-attention layer (the two kernels of hg_attention_decode) at
+ * context ctx on seeded device-resident q, k, v and cache (unit QK-norm gains, theta
+ * 10000), run `reps` times: us[0] = scores (or split partials with HG_KV_FAST), us[1] =
+ * softmax + P.V (or merge), mean microseconds per layer. */
+int hg_attention_time(uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t ctx, uint32_t reps,
+                      uint32_t flags, float *us);
 
 #ifdef __cplusplus
 }
