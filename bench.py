@@ -187,7 +187,9 @@ COPY_BYTES = 256 * 2**20
 
 def pmc_calib():
     """For rocprofv3 --pmc runs: 4 device copies of COPY_BYTES (the calibration of the byte
-    counters), then prefill + 16 decode steps at positions 2032..2047 of the bench model."""
+    counters); the attention layer of the timed window (16 q / 4 kv heads, context 2049,
+    reference order) 10 times; then prefill + 16 decode steps of the bench model (the other
+    kernels' shapes do not depend on the context)."""
     import torch
     import hobbylm_amd as hg
     from hobbylm_amd import gguf_synth as gs
@@ -196,25 +198,26 @@ def pmc_calib():
     for _ in range(4):
         b.copy_(a)
     torch.cuda.synchronize()
+    hg.attention_time(16, 4, 64, CTX_END + 1, reps=10)
     m = hg.Model(gs.synth_path("500M", 1))
-    kv = m.new_cache(max_ctx=CTX_END + 8)
+    kv = m.new_cache(max_ctx=64)
     prompt = gs.prompt_ids(1, N_PROMPT, 50257)
     emb = np.stack([m.token_embedding(int(t)) for t in prompt])
     _, first = m.prefill(emb, kv)
-    pre = m.decode_greedy(first, CTX_END - 16 - N_PROMPT, kv)
-    m.decode_greedy(int(pre[-1]), 16, kv)
+    m.decode_greedy(first, 16, kv)
     torch.cuda.synchronize()
     print("pmc-calib done", flush=True)
 
 
 def _counter_rows(d):
-    """(kernel name, counter name, value) of every dispatch in a rocprofv3 --pmc output dir."""
+    """(kernel name, counter name, value) of every dispatch in a rocprofv3 --pmc output dir,
+    in dispatch order."""
     import csv
     out = []
     for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
         for r in csv.DictReader(open(f)):
-            out.append((r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"])))
-    return out
+            out.append((int(r["Dispatch_Id"]), r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"])))
+    return [r[1:] for r in sorted(out)]
 
 
 def pmc_stats(fetch_dir, write_dir):
@@ -235,9 +238,15 @@ def pmc_stats(fetch_dir, write_dir):
             if k.startswith("void hg::") or k.startswith("hg::"):
                 name = k.split("(")[0].replace("void ", "").replace("hg::", "")
                 agg.setdefault(name, []).append(v * 1024 * f)
+        # the first 13 attention dispatches are the context-2049 layer of --pmc-calib
+        for name in ("k_attn_scores<64>", DOM_KERNEL):
+            if name in agg:
+                agg[name + " @ctx2049"] = agg[name][:13]
+                agg[name] = agg[name][13:]
         for name, vals in agg.items():
-            res.setdefault(name, {})[counter.lower() + "_bytes"] = float(np.mean(vals))
-            res[name]["dispatches"] = len(vals)
+            if vals:
+                res.setdefault(name, {})[counter.lower() + "_bytes"] = float(np.mean(vals))
+                res[name]["dispatches"] = len(vals)
     for name, r in res.items():
         r["hbm_bytes_per_dispatch"] = round(r.get("fetch_size_bytes", 0.0) + r.get("write_size_bytes", 0.0))
     return {"calibration": {"copy_bytes": COPY_BYTES, "factor_fetch": factors.get("FETCH_SIZE"),
@@ -345,7 +354,7 @@ def main():
         tf = os.path.join(ROOT, "profiles", "traffic_decode_500M_ctx2k.json")
         if os.path.exists(tf):
             tj = json.load(open(tf))
-            k = tj.get("kernels", {}).get(DOM_KERNEL)
+            k = tj.get("kernels", {}).get(DOM_KERNEL + " @ctx2049")
             if k:
                 traffic = k["hbm_bytes_per_dispatch"]
                 tnote = f"rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, copy-calibrated ({os.path.relpath(tf, ROOT)})"

@@ -834,6 +834,23 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
 // is bounded: tile k waits only for tile k - R to be consumed, the chain only for tile k to be
 // produced.  Producers start their first V fetch before the sum.  Also writes o and its
 // quantization for attn_output (quant.rs:111-123).
+// Workgroup -> (head h, output quarter q) of the softmax + P.V kernels (1-D grid of
+// n_heads * nq).  Workgroups are dealt to the 8 XCDs round-robin by linear id, each XCD with its
+// own L2; the rep query heads of a kv group read the same V slice, so the rep workgroups of one
+// (kv group, quarter) key are given ids that are equal mod 8, keeping the shared V in one L2.
+__device__ inline void pv_head_quarter(uint32_t L, uint32_t n_heads, uint32_t n_kv, uint32_t nq, uint32_t *h,
+                                       uint32_t *q) {
+    const uint32_t rep = n_heads / n_kv, nkeys = n_kv * nq;
+    if (nkeys % 8 == 0) {
+        const uint32_t slot = L / 8, key = L % 8 + 8 * (slot / rep), r = slot % rep;
+        *h = (key / nq) * rep + r;
+        *q = key % nq;
+    } else {
+        *h = L % n_heads;
+        *q = L / n_heads;
+    }
+}
+
 struct PvCfg {
     static constexpr uint32_t D = 16;          // output elements per workgroup
     static constexpr uint32_t T = 128;         // positions per tile
@@ -869,7 +886,9 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
     __shared__ uint32_t done;
     __shared__ float s_inv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t h = blockIdx.x, q = blockIdx.y, rep = n_heads / n_kv, g = h / rep;
+    uint32_t h, q;
+    pv_head_quarter(blockIdx.x, n_heads, n_kv, HD / D, &h, &q);
+    const uint32_t rep = n_heads / n_kv, g = h / rep;
     const uint32_t pos = p->pos, n = pos + 1;
     const uint32_t R = pv_ring_slots(cap);
     float *e = lds;                                     // [cap] e_t, then p_t
@@ -1043,7 +1062,9 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     __shared__ uint64_t ready;   // bit gi: product group gi written
     __shared__ float s_inv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t h = blockIdx.x, q = blockIdx.y, rep = n_heads / n_kv, g = h / rep;
+    uint32_t h, q;
+    pv_head_quarter(blockIdx.x, n_heads, n_kv, HD / D, &h, &q);
+    const uint32_t rep = n_heads / n_kv, g = h / rep;
     const uint32_t pos = p->pos, n = pos + 1;
     const uint32_t rc = pv_res_rows(cap), TPC = rc + 4;   // row stride 4 mod 32 banks
     float *e = lds;                                         // [rc]  e_t
@@ -1661,11 +1682,11 @@ static void attn_exact_launch(hipStream_t st, int which, const float *qkv, const
         return;
     }
     if (pv_res_fits(cap)) {
-        LAUNCH(k_attn_softmax_pv_res<HD>, dim3(n_heads, HD / PvResCfg::D), dim3(512), pv_res_lds(cap), st, scratch,
+        LAUNCH(k_attn_softmax_pv_res<HD>, dim3(n_heads * (HD / PvResCfg::D)), dim3(512), pv_res_lds(cap), st, scratch,
                part, qkv, p, vc, cap, S, n_heads, n_kv, o_out);
     } else {
         const size_t shm = (size_t)div_up(cap, 4) * 16 + (size_t)pv_ring_slots(cap) * PvCfg::SLOT * 4;
-        LAUNCH(k_attn_softmax_pv<HD>, dim3(n_heads, HD / PvCfg::D), dim3(PvCfg::NW * 64), shm, st, scratch, part, qkv,
+        LAUNCH(k_attn_softmax_pv<HD>, dim3(n_heads * (HD / PvCfg::D)), dim3(PvCfg::NW * 64), shm, st, scratch, part, qkv,
                p, vc, cap, S, n_heads, n_kv, o_out, q_out, d_out);
     }
     if (!fuse_quant) LAUNCH(k_quant_o, dim3(1), dim3(256), 0, st, o_out, n_heads * HD, q_out, d_out);
