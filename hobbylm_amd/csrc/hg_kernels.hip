@@ -680,42 +680,63 @@ __global__ __launch_bounds__(256) void k_attn_fast(const float *__restrict__ qkv
     }
 }
 
-// Merge the split partials of every head into o = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M),
-// write o (optional) and its quantization for the attn_output matvec (quant.rs:111-123).
+// Merge of the split partials of one head per workgroup (flash-decoding combine, tree
+// order): M = max_s M_s, f_s = exp(M_s - M), o = sum_s f_s P_s / sum_s f_s L_s; then the
+// quantization of the head's o blocks for attn_output (quant.rs:111-123).
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part, uint32_t n_heads, uint32_t S,
                                                       float *o_out, uint8_t *q_out, float *d_out) {
-    const int tid = threadIdx.x;
-    const uint32_t total4 = n_heads * HD / 4;
-    const uint32_t nb = n_heads * HD / QK, nc = div_up(nb, 4);
-    for (uint32_t base = 0; base < total4; base += 256) {
-        const uint32_t t = base + tid;
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-        if (t < total4) {
-            const uint32_t h = (t * 4) / HD, di = (t * 4) % HD;
-            const float *ph = part + (size_t)h * S * (HD + 2);
-            float M = -__builtin_huge_valf();
-            for (uint32_t s = 0; s < S; ++s) M = fmaxf(M, ph[(size_t)s * (HD + 2)]);
-            float L = 0.0f;
-            for (uint32_t s = 0; s < S; ++s) {
-                const float *pr = ph + (size_t)s * (HD + 2);
-                if (pr[1] == 0.0f) continue;
-                const float f = __expf(pr[0] - M);
-                L += pr[1] * f;
-#pragma unroll
-                for (int m = 0; m < 4; ++m) v[m] += pr[2 + di + m] * f;
-            }
-            const float inv = 1.0f / L;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) v[m] *= inv;
-            if (o_out)
-#pragma unroll
-                for (int m = 0; m < 4; ++m) o_out[t * 4 + m] = v[m];
-        }
-        const uint32_t b = t / 8;
-        if (b < nb) quant_block_lane(v, t & 7, b, q_out, d_out);
+    constexpr uint32_t NG = 256 / HD;   // split groups
+    __shared__ float fs[1024];
+    __shared__ float red[4];
+    __shared__ float acc_s[NG][HD];
+    __shared__ float s_m, s_inv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t h = blockIdx.x;
+    const float *ph = part + (size_t)h * S * (HD + 2);
+    float m = -__builtin_huge_valf();
+    for (uint32_t s = tid; s < S; s += 256) m = fmaxf(m, ph[(size_t)s * (HD + 2)]);
+    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    if (tid == 0) s_m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    const float M = s_m;
+    float l = 0.0f;
+    for (uint32_t s = tid; s < S; s += 256) {
+        const float *pr = ph + (size_t)s * (HD + 2);
+        const float f = (pr[1] == 0.0f) ? 0.0f : __expf(pr[0] - M);
+        fs[s] = f;
+        l += pr[1] * f;
     }
-    zero_pad(nb, nc, q_out, d_out, tid, 256);
+    for (int k = 32; k >= 1; k >>= 1) l += shfl_xor(l, k);
+    __syncthreads();
+    if (lane == 0) red[wave] = l;
+    __syncthreads();
+    if (tid == 0) s_inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
+    const uint32_t d = tid % HD, sg = tid / HD;
+    float a = 0.0f;
+    if (sg < NG)
+        for (uint32_t s = sg; s < S; s += NG) a += ph[(size_t)s * (HD + 2) + 2 + d] * fs[s];
+    if (sg < NG) acc_s[sg][d] = a;
+    __syncthreads();
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t nbh = HD / QK;   // blocks of this head
+    const uint32_t t = (uint32_t)tid;   // thread t < HD / 4: elements 4t .. 4t+3 of the head
+    if (t < HD / 4) {
+#pragma unroll
+        for (int m4 = 0; m4 < 4; ++m4) {
+            float o = 0.0f;
+            for (uint32_t g = 0; g < NG; ++g) o += acc_s[g][4 * t + m4];
+            v[m4] = o * s_inv;
+            if (o_out) o_out[h * HD + 4 * t + m4] = v[m4];
+        }
+    }
+    if (t < nbh * 8) quant_block_lane(v, t & 7, h * nbh + t / 8, q_out, d_out);
+    if (h == 0) {
+        const uint32_t nb = n_heads * HD / QK;
+        zero_pad(nb, div_up(nb, 4), q_out, d_out, tid, 256);
+    }
 }
 
 // ------------------------------------------------------------------ attention (exact)
@@ -1703,7 +1724,7 @@ static void attn_fast_launch(hipStream_t st, int which, const float *qkv, const 
                n_kv, S, part);
         return;
     }
-    LAUNCH(k_attn_combine<HD>, dim3(1), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
+    LAUNCH(k_attn_combine<HD>, dim3(n_heads), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
 }
 
 bool launch_attn(hipStream_t st, bool exact, int which, uint32_t hd, const float *qkv, const float *qn,
