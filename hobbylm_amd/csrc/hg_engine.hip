@@ -123,7 +123,7 @@ struct DevQ8 {
 
 struct Layer {
     bool moe = false;
-    DevBuf attn_norm, q_norm, k_norm, ffn_norm, router, bias;
+    DevBuf attn_norm, q_norm, k_norm, ffn_norm, router, router_p, bias;
     DevQ8 qkv, o, gate, up, down, gate_e, up_e, down_e, gate_sh, up_sh, down_sh;
 };
 
@@ -271,6 +271,11 @@ int hg_model_load(const char *path, int quant, hg_model **out) {
             if (rw.size() != (size_t)c.n_experts * d)
                 return fail(HG_ERR_FORMAT, "tensor `" + p + "ffn_gate_inp.weight` has wrong size");
             if ((rc = L->router.upload(rw.data(), rw.size() * 4))) return rc;
+            if (d % 32) return fail(HG_ERR_FORMAT, "d_model must be a multiple of 32");
+            std::vector<float> rp(rw.size());   // the router kernel's 16-byte-per-step row layout
+            for (size_t e = 0; e < c.n_experts; ++e)
+                for (uint32_t k = 0; k < d; ++k) rp[e * d + router_perm(k)] = rw[e * d + k];
+            if ((rc = L->router_p.upload(rp.data(), rp.size() * 4))) return rc;
             if ((rc = load_norm(g, p + "exp_probs_b.bias", c.n_experts, L->bias))) return rc;
             if ((rc = load_q8(g, p + "ffn_gate_exps.weight", c.n_experts * f, d, L->gate_e, m.get()))) return rc;
             if ((rc = load_q8(g, p + "ffn_up_exps.weight", c.n_experts * f, d, L->up_e, m.get()))) return rc;
@@ -334,7 +339,7 @@ namespace {
 
 enum ProfClass { P_EMBED, P_NORM, P_QKV, P_ATTN_A, P_ATTN_B, P_OPROJ, P_ROUTER, P_GATEUP, P_DOWN, P_LMHEAD,
                  P_ARGMAX, P_OTHER, P_COUNT };
-const char *const kProfNames[P_COUNT] = {"embed", "rmsnorm_quant", "qkv_matvec", "attn_scores", "attn_softmax_pv",
+const char *const kProfNames[P_COUNT] = {"embed", "rmsnorm_quant", "attn_norm_qkv_matvec", "attn_scores", "attn_softmax_pv",
                                          "o_proj_matvec", "ffn_norm_router", "expert_gate_up", "expert_down",
                                          "lm_head_matvec", "argmax", "other"};
 
@@ -363,10 +368,9 @@ void enqueue_layers(hg_kv *kv, int order) {
     StepParams *p = kv->params.as<StepParams>();
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const Layer &L = *m->layers[l];
-        mark(kv, P_NORM);
-        launch_rmsnorm_quant(st, kv->exact, x, L.attn_norm.as<float>(), c.rms_eps, d, nullptr, qa, da);
-        mark(kv, P_QKV);
-        launch_matvec(st, order, EPI_STORE, L.qkv.m, qa, da, kv->qkv.as<float>(), 64, 0, nullptr, nullptr);
+        mark(kv, P_QKV);   // attn_norm + attn_qkv (model.rs:164-165, 194)
+        launch_norm_matvec(st, kv->exact, order, L.qkv.m, x, L.attn_norm.as<float>(), c.rms_eps, kv->qkv.as<float>(),
+                           256);
         for (int part = 0; part < 2; ++part) {
             mark(kv, part == 0 ? P_ATTN_A : P_ATTN_B);
             launch_attn(st, kv->exact, part, c.head_dim, kv->qkv.as<float>(), L.q_norm.as<float>(),
@@ -384,7 +388,7 @@ void enqueue_layers(hg_kv *kv, int order) {
         if (L.moe) {
             mark(kv, P_ROUTER);
             launch_ffn_router(st, kv->exact, x, L.ffn_norm.as<float>(), c.rms_eps, d, L.router.as<float>(),
-                              L.bias.as<float>(), c.n_experts, c.top_k, c.gating_sigmoid, c.expert_weights_norm,
+                              L.router_p.as<float>(), L.bias.as<float>(), c.n_experts, c.top_k, c.gating_sigmoid, c.expert_weights_norm,
                               c.expert_weights_scale, qa, da, kv->topk_idx.as<uint32_t>(), kv->topk_w.as<float>(),
                               kv->order.as<uint32_t>(), kv->rec_idx.as<uint32_t>() + (size_t)l * c.top_k,
                               kv->rec_w.as<float>() + (size_t)l * c.top_k);

@@ -30,6 +30,9 @@ uint32_t matvec_blocks(uint32_t N, uint32_t threads);
 // dq == nullptr: q points to an f32 activation that each workgroup quantizes in its prologue.
 void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uint8_t *q, const float *dq, float *y,
                    uint32_t threads, uint32_t valid, float *pv, uint32_t *pi);
+// y = W * quant(rmsnorm(x, w)) with the norm formed by every workgroup (no activation buffer).
+void launch_norm_matvec(hipStream_t st, bool exact, int order, const Q8Mat &W, const float *x, const float *w,
+                        float eps, float *y, uint32_t threads);
 // The matvecs of matrices ids[0..n_ids) of a stack of rows_per_mat-row matrices, one launch.
 void launch_matvec_gather(hipStream_t st, const Q8Mat &W, uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids,
                           const uint8_t *q, const float *dq, float *y);
@@ -42,10 +45,16 @@ bool launch_attn(hipStream_t st, bool exact, int which, uint32_t hd, const float
                  const float *kn, float eps, const float *cs, const float *sn, const StepParams *p, float *kc,
                  float *vc, uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,
                  float *o_out, uint8_t *q_out, float *d_out);
+// Router row permutation the kernel expects in Wp (d a multiple of 32): element k of a row is
+// stored at 32 (k / 32) + 4 (k % 8) + (k % 32) / 8, so the chains k % 32 = l, 8 + l, 16 + l,
+// 24 + l of a 32-wide step are the four consecutive floats 4 l .. 4 l + 3.
+__host__ __device__ inline uint32_t router_perm(uint32_t k) {
+    return (k / 32) * 32 + 4 * (k % 8) + (k % 32) / 8;
+}
 void launch_ffn_router(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,
-                       const float *Wr, const float *bias, uint32_t E, uint32_t top_k, int gating_sigmoid,
-                       int weights_norm, float weights_scale, uint8_t *q, float *dq, uint32_t *topk_idx,
-                       float *topk_w, uint32_t *order, uint32_t *rec_idx, float *rec_w);
+                       const float *Wr, const float *Wp, const float *bias, uint32_t E, uint32_t top_k,
+                       int gating_sigmoid, int weights_norm, float weights_scale, uint8_t *q, float *dq,
+                       uint32_t *topk_idx, float *topk_w, uint32_t *order, uint32_t *rec_idx, float *rec_w);
 void launch_ffn_gateup(hipStream_t st, int order, const Q8Mat &Wg, const Q8Mat &Wu, const Q8Mat &Sg,
                        const Q8Mat &Su, const uint32_t *topk_idx, uint32_t top_k, uint32_t n_slots, uint32_t f,
                        const uint8_t *q, const float *dq, float *a);

@@ -36,14 +36,33 @@ struct WaveExpTab {
     }
 };
 
+// Lane moves within rows of 16 lanes (DPP): no LDS round trip.  quad_perm [1,0,3,2] and
+// [2,3,0,1] exchange with lane^1 and lane^2; row_ror:12 reads lane+4 and row_ror:4 lane-4
+// (mod 16), so lane^4 is the one or the other by bit 2 of the lane.
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v),
+                                                                 CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ inline uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xf, 0xf, false);
+}
+// max over the 8 aligned lanes of a quantization block (lane j = lane & 7); every lane of the
+// group must be active.
+__device__ inline float max8_lanes(float m, int j) {
+    m = fmaxf(m, dpp_f<0xB1>(m));
+    m = fmaxf(m, dpp_f<0x4E>(m));
+    const float up = dpp_f<0x12C>(m), dn = dpp_f<0x124>(m);
+    return fmaxf(m, (j & 4) ? dn : up);
+}
+
 // One 32-block of activation quantization (quant.rs:114-122), lanes j = 0..7 of 8 adjacent
 // threads each holding v[0..3] = x[32b + 4j + 0..3].  d = amax/127, id = 1/d (0 if d == 0),
 // q = clamp(round_half_away(x*id), +-127).  Writes q into the lane-major chunk layout.
 __device__ inline void quant_block_lane(const float v[4], int j, uint32_t b, uint8_t *q, float *d) {
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = fmaxf(amax, shfl_xor(amax, 1));
-    amax = fmaxf(amax, shfl_xor(amax, 2));
-    amax = fmaxf(amax, shfl_xor(amax, 4));
+    amax = max8_lanes(amax, j);
     const float dd = amax / 127.0f;
     const float id = dd > 0.0f ? 1.0f / dd : 0.0f;
     uint32_t packed = 0;
@@ -375,14 +394,63 @@ __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restri
     const uint32_t row = blockIdx.x * (nthr >> 3) + (tid >> 3);
     const uint32_t lrow = min(row, W.N - 1);
     const int j = tid & 7;
+    // the activation's loads are issued before the weight stream (the memory counter retires
+    // in order, so the wait for the activation then leaves the weights in flight); the first
+    // XQ rounds are held in registers, larger activations finish with a loop
+    constexpr uint32_t XQ = 4;
+    const uint32_t bstep = (uint32_t)nthr / 8, nb = W.nb, nc = W.nc;
+    v4f xv[XQ];
+    v4i qv[XQ];
+    float dv = 0.0f;
+    const float *xf = reinterpret_cast<const float *>(gq);
+#pragma unroll
+    for (uint32_t u = 0; u < XQ; ++u) {
+        if (AF32) {
+            const uint32_t b = min(u * bstep + (uint32_t)(tid >> 3), nb - 1);
+            xv[u] = *reinterpret_cast<const v4f *>(xf + b * QK + j * 4);
+        } else {
+            const uint32_t i = min(u * (uint32_t)nthr + (uint32_t)tid, nc * 8 - 1);
+            qv[u] = reinterpret_cast<const v4i *>(gq)[i];
+        }
+    }
+    if (!AF32) dv = gd[min((uint32_t)tid, nc * 4 - 1)];
+    const float yold = (EPI == EPI_RESID) ? y[min(row, W.N - 1)] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
     Q8Row<ORDER, SCF32, NCT> rd;
-    rd.begin(row_qs(W, lrow), row_sc<SCF32>(W, lrow), W.nb, W.nc, j);
-    if (AF32) quant_to_lds(reinterpret_cast<const float *>(gq), W.nb, W.nc, sq, sd, tid, nthr);
-    else stage_act(gq, gd, W.nc, sq, sd, tid, nthr);
+    rd.begin(row_qs(W, lrow), row_sc<SCF32>(W, lrow), nb, nc, j);
+    __builtin_amdgcn_sched_barrier(0);
+    if (AF32) {
+#pragma unroll
+        for (uint32_t u = 0; u < XQ; ++u) {   // a block's 8 lanes are all in or all out
+            const uint32_t b = u * bstep + (uint32_t)(tid >> 3);
+            if (b < nb) {
+                const float v4[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+                quant_block_lane(v4, j, b, sq, sd);
+            }
+        }
+        for (uint32_t b0 = XQ * bstep; b0 < nb; b0 += bstep) {
+            const uint32_t b = b0 + (uint32_t)(tid >> 3);
+            if (b < nb) {
+                const v4f x4 = *reinterpret_cast<const v4f *>(xf + b * QK + j * 4);
+                const float v4[4] = {x4.x, x4.y, x4.z, x4.w};
+                quant_block_lane(v4, j, b, sq, sd);
+            }
+        }
+        zero_pad(nb, nc, sq, sd, tid, nthr);
+    } else {
+#pragma unroll
+        for (uint32_t u = 0; u < XQ; ++u) {
+            const uint32_t i = u * (uint32_t)nthr + (uint32_t)tid;
+            if (i < nc * 8) reinterpret_cast<v4i *>(sq)[i] = qv[u];
+        }
+        for (uint32_t i = XQ * (uint32_t)nthr + (uint32_t)tid; i < nc * 8; i += nthr)
+            reinterpret_cast<v4i *>(sq)[i] = reinterpret_cast<const v4i *>(gq)[i];
+        for (uint32_t i = (uint32_t)tid; i < nc * 4; i += nthr) sd[i] = i == (uint32_t)tid ? dv : gd[i];
+    }
     __syncthreads();
     const float v = rd.finish(sq, sd);
     if (row < W.N && j == 0) {
-        if (EPI == EPI_RESID) y[row] = y[row] + v;
+        if (EPI == EPI_RESID) y[row] = yold + v;
         else y[row] = v;
     }
     if (EPI == EPI_LOGITS) {
@@ -406,6 +474,84 @@ __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restri
             part_i[blockIdx.x] = mi;
         }
     }
+}
+
+// rmsnorm (ops.rs:98-109) of x with gain w, its activation quantization (quant.rs:111-123)
+// and the Q8 matvec (quant.rs:125-135) in one launch: the attn_norm + attn_qkv pair of
+// model.rs:164-165 and 194.  Every workgroup forms the norm of the whole vector itself, in
+// the reference's order, while its weight rows are in flight, and quantizes straight into
+// LDS, so the normed activation never round-trips through memory.  y[r] = v (EPI_STORE).
+template <bool EXACT, int ORDER, bool SCF32, int NCT>
+__global__ __launch_bounds__(256) void k_norm_matvec(Q8Mat W, const float *__restrict__ x,
+                                                     const float *__restrict__ w, float eps, float *y) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint8_t *sq = smem;
+    float *sd = reinterpret_cast<float *>(smem + W.nc * CHUNK_BYTES);
+    float *ps = sd + W.nc * 4;   // the d squares
+    __shared__ float red[4];
+    __shared__ float s_ss;
+    const int tid = threadIdx.x, nthr = blockDim.x, j = tid & 7;
+    const uint32_t d = W.K, ng = d / 4;
+    // x and the gain first, alone in the memory pipeline (the chain waits for them); the
+    // weight stream of this thread's row is issued once the squares are formed and arrives
+    // during the chain
+    constexpr uint32_t RQ = 4;
+    v4f xv[RQ], wv[RQ];
+#pragma unroll
+    for (uint32_t u = 0; u < RQ; ++u) {
+        const uint32_t g = min(tid + nthr * u, ng - 1);
+        xv[u] = reinterpret_cast<const v4f *>(x)[g];
+        wv[u] = reinterpret_cast<const v4f *>(w)[g];
+    }
+    const uint32_t row = blockIdx.x * (nthr >> 3) + (tid >> 3);
+    const uint32_t lrow = min(row, W.N - 1);
+    Q8Row<ORDER, SCF32, NCT> rd;
+    float ss = 0.0f;
+    auto squares = [&](const v4f a, uint32_t g) {
+        if (EXACT) {
+            reinterpret_cast<v4f *>(ps)[g] = a * a;
+        } else {
+            ss += a.x * a.x;
+            ss += a.y * a.y;
+            ss += a.z * a.z;
+            ss += a.w * a.w;
+        }
+    };
+#pragma unroll
+    for (uint32_t u = 0; u < RQ; ++u)
+        if (tid + nthr * u < ng) squares(xv[u], tid + nthr * u);
+    for (uint32_t g = tid + nthr * RQ; g < ng; g += nthr) squares(reinterpret_cast<const v4f *>(x)[g], g);
+    __builtin_amdgcn_sched_barrier(0);
+    rd.begin(row_qs(W, lrow), row_sc<SCF32>(W, lrow), W.nb, W.nc, j);
+    __builtin_amdgcn_sched_barrier(0);
+    if (EXACT) {
+        __syncthreads();
+        if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
+    } else {
+        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        if (tid == 0) {
+            float t = 0.0f;
+            for (int i = 0; i < nthr / 64; ++i) t += red[i];
+            s_ss = t;
+        }
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf(s_ss / (float)d + eps);
+    auto emit = [&](const v4f a, const v4f gw, uint32_t g) {
+        const float v[4] = {a.x * scale * gw.x, a.y * scale * gw.y, a.z * scale * gw.z, a.w * scale * gw.w};
+        quant_block_lane(v, j, g / 8, sq, sd);
+    };
+#pragma unroll
+    for (uint32_t u = 0; u < RQ; ++u)   // a block's 8 groups are all < ng or all >= ng
+        if (tid + nthr * u < ng) emit(xv[u], wv[u], tid + nthr * u);
+    for (uint32_t g = tid + nthr * RQ; g < ng; g += nthr)
+        emit(reinterpret_cast<const v4f *>(x)[g], reinterpret_cast<const v4f *>(w)[g], g);
+    zero_pad(W.nb, W.nc, sq, sd, tid, nthr);
+    __syncthreads();
+    const float v = rd.finish(sq, sd);
+    if (row < W.N && j == 0) y[row] = v;
 }
 
 // Q8Tensor::matvec of the matrices ids[0..n) of a stack of equal matrices (rows_per_mat rows
@@ -1239,39 +1385,55 @@ __global__ __launch_bounds__(256) void k_quant_o(const float *__restrict__ o, ui
 // ffn_norm RMSNorm + quantization of h, then the F32 router of Model::ffn (model.rs:270-293):
 // logits = W_r h in ops::dot's order, sigmoid (or softmax) gate, sel = score + bias,
 // descending rank (equal keys: lower expert first), top-k in rank order, optional
-// renormalisation, x weights_scale.  One workgroup of ROUTER_THREADS(E) threads.
+// renormalisation, x weights_scale.  One workgroup of router_threads(E) threads.
 // ops::dot (ops.rs:7-36) keeps 32 accumulator chains c = 8a + l (a: the four f32x8
-// accumulators, l: the lane) over 32-wide steps; here 16 lanes own an expert row, lane l16
-// running chains l16 and l16 + 16, so (acc0 + acc1) + (acc2 + acc3) is a xor-8 exchange and
-// the 8-lane hsum the xor 4/2/1 butterfly.  With d % 32 == 0 and d <= 1024 each lane's 2*d/32
-// router weights are fetched before the RMSNorm chain, so that load overlaps it.
+// accumulators, l: the lane) over 32-wide steps; here 8 lanes own an expert row and lane l
+// runs the four chains l, 8 + l, 16 + l, 24 + l, so (acc0 + acc1) + (acc2 + acc3) is formed in
+// the lane and the 8-lane hsum is the xor 4/2/1 butterfly.  With d % 32 == 0 and d <= 1024 the
+// router rows come pre-permuted (Wp[e][32 i + 4 l + a] = W_r[e][32 i + 8 a + l]), so a lane's
+// four weights of a step are one 16-byte load, and all of them are fetched before the RMSNorm
+// chain; h is kept in LDS both in order (for the quantization) and permuted the same way.
+// d must be a multiple of 32 (the Q8_0 rows of the same layer already require it); Wr is the
+// row-major router, Wp its permuted copy.
 constexpr uint32_t ROUTER_IMAX = 32;   // 32-wide steps held in registers (d <= 1024)
+constexpr uint32_t ROUTER_MAXE = 64;   // experts ranked by the register path (wave 0's lanes)
 
+// Wave 0 runs the RMSNorm chain and the final selection; waves 1.. own the expert rows (8
+// lanes each), so their row fetch (all of it through this one CU's memory pipeline) is issued
+// during the chain instead of before it.
 __host__ __device__ inline uint32_t router_threads(uint32_t E) {
-    const uint32_t t = (E * 16 + 63) / 64 * 64;
+    const uint32_t t = 64 + (E * 8 + 63) / 64 * 64;
     return t < 256 ? 256 : (t > 1024 ? 1024 : t);
 }
 
-template <bool EXACT, int MAXT>
+// NST: d / 32 when the rows are prefetched (compile-time, so the steps unroll without guards
+// and their LDS reads issue back to back), 0 for the generic path.
+template <bool EXACT, int MAXT, int NST>
 __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x, const float *__restrict__ w,
                                                      float eps, uint32_t d, const float *__restrict__ Wr,
+                                                     const float *__restrict__ Wp,
                                                      const float *__restrict__ bias, uint32_t E, uint32_t top_k,
                                                      int gating_sigmoid, int weights_norm, float weights_scale,
                                                      uint8_t *q_out, float *d_out, uint32_t *topk_idx,
                                                      float *topk_w, uint32_t *order, uint32_t *rec_idx,
                                                      float *rec_w) {
-    extern __shared__ __align__(16) float hs[];  // 2*d floats: h, then the squares
+    extern __shared__ __align__(16) float hs[];  // 3*d floats: h, h permuted, the squares
+    float *hp = hs + d, *ps = hs + 2 * d;
     __shared__ float red[16];
     __shared__ float s_ss;
-    __shared__ float lg[256], scr[256], sel[256];
-    __shared__ uint32_t tk[64];
-    __shared__ float tw[64];
+    __shared__ __align__(16) float lg[256], scr[256], sel[256];
+    __shared__ __align__(16) uint32_t tk[64];
+    __shared__ __align__(16) float tw[64];
     const int tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63;
-    const uint32_t e16 = (uint32_t)tid >> 4, l16 = (uint32_t)tid & 15;
+    const bool rows = tid >= 64;   // waves 1..: the expert rows
+    const uint32_t e8 = rows ? (uint32_t)(tid - 64) >> 3 : 0u, l8 = (uint32_t)tid & 7;
+    const uint32_t nrt = (uint32_t)nthr - 64;   // row threads
     const uint32_t main = d - d % 32;
-    const bool pre = d % 32 == 0 && d / 32 <= ROUTER_IMAX && E * 16 <= (uint32_t)nthr;
+    constexpr bool pre = NST > 0;
+    static_assert(NST <= (int)ROUTER_IMAX, "prefetched steps");
     // loads in issue order: x and the norm gain (needed first), the exp table, the bias, then
-    // the router rows: lane l16 of row e16 holds W_r[e][32 i + l16] and W_r[e][32 i + 16 + l16]
+    // the permuted router rows (unconditional, addresses clamped: a load under a branch makes
+    // the compiler's wait for x at the join count as if the weights were not in flight)
     constexpr uint32_t XB = 4;
     float xv[XB], wv[XB];
 #pragma unroll
@@ -1282,21 +1444,16 @@ __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x
     }
     const WaveExpTab tab = WaveExpTab::load(lane);
     const float bv = (uint32_t)tid < E ? bias[tid] : 0.0f;
-    // unconditional (addresses clamped, unused without `pre`): a load under a branch makes
-    // the compiler's wait for x after the join count as if the weights were not in flight
-    float wr1[ROUTER_IMAX], wr2[ROUTER_IMAX];
-    {
-        const uint32_t e = min(e16, E - 1);
+    const float bv8 = bias[min(e8, E - 1)];   // the bias of this thread's expert row
+    v4f wr[NST > 0 ? NST : 1];   // issued once the squares are formed
+    auto fetch_rows = [&] {
+        const uint32_t e = min(e8, E - 1);
+        const float *rowp = Wp + (size_t)e * d;
 #pragma unroll
-        for (uint32_t i = 0; i < ROUTER_IMAX; ++i) {
-            const uint32_t k = min(32 * i, d - 32) + l16;   // block start clamped, k + 16 < d
-            wr1[i] = Wr[(size_t)e * d + k];
-            wr2[i] = Wr[(size_t)e * d + k + 16];
-        }
-    }
+        for (int i = 0; i < NST; ++i) wr[i] = *reinterpret_cast<const v4f *>(rowp + 32 * i + 4 * l8);
+    };
     float scale;
     {
-        float *ps = hs + d;
         float ss = 0.0f;
 #pragma unroll
         for (uint32_t u = 0; u < XB; ++u) {
@@ -1313,11 +1470,13 @@ __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x
         }
         if (EXACT) {
             __syncthreads();
+            if (rows) fetch_rows();   // arrives during the chain
             if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
         } else {
             for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
             if (lane == 0) red[tid >> 6] = ss;
             __syncthreads();
+            if (rows) fetch_rows();
             if (tid == 0) {
                 float t = 0.0f;
                 for (int i = 0; i < nthr / 64; ++i) t += red[i];
@@ -1326,65 +1485,140 @@ __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x
         }
         __syncthreads();
         scale = 1.0f / sqrtf(s_ss / (float)d + eps);
+        auto put = [&](uint32_t i, float v) {
+            hs[i] = v;
+            if (pre) hp[router_perm(i)] = v;
+        };
 #pragma unroll
         for (uint32_t u = 0; u < XB; ++u) {
             const uint32_t i = tid + u * nthr;
-            if (i < d) hs[i] = xv[u] * scale * wv[u];
+            if (i < d) put(i, xv[u] * scale * wv[u]);
         }
-        for (uint32_t i = tid + XB * nthr; i < d; i += nthr) hs[i] = x[i] * scale * w[i];
+        for (uint32_t i = tid + XB * nthr; i < d; i += nthr) put(i, x[i] * scale * w[i]);
     }
     __syncthreads();
-    {   // quantization of h for the expert matvecs (quant.rs:111-123)
-        const uint32_t nb = d / QK, nc = div_up(nb, 4);
-        const int j = tid & 7;
-        for (uint32_t b0 = 0; b0 < nb; b0 += nthr / 8) {
-            const uint32_t b = b0 + (tid >> 3);
-            if (b < nb) {
-                float v[4];
-#pragma unroll
-                for (int m = 0; m < 4; ++m) v[m] = hs[b * QK + j * 4 + m];
-                quant_block_lane(v, j, b, q_out, d_out);
-            }
-        }
-        zero_pad(nb, nc, q_out, d_out, tid, nthr);
-    }
-    // router logits
-    for (uint32_t e0 = 0; e0 < E; e0 += nthr / 16) {
-        const uint32_t e = e0 + e16;
-        float a1 = 0.0f, a2 = 0.0f;
+    // router logits: lane l8 of expert e8 runs chains l8 + 8 a, a = 0..3; after the butterfly
+    // every lane of the 8 holds the logit (each add pairs the same two operands in every lane)
+    float myv = 0.0f;
+    for (uint32_t e0 = 0; rows && e0 < E; e0 += nrt / 8) {   // (uniform per wave)
+        const uint32_t e = e0 + e8;
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (e < E) {
             if (pre) {
 #pragma unroll
-                for (uint32_t i = 0; i < ROUTER_IMAX; ++i)
-                    if (32 * i < d) {
-                        a1 = fmaf(wr1[i], hs[32 * i + l16], a1);
-                        a2 = fmaf(wr2[i], hs[32 * i + 16 + l16], a2);
-                    }
+                for (int i = 0; i < NST; ++i) {
+                    const v4f hv = *reinterpret_cast<const v4f *>(hp + 32 * i + 4 * l8);
+                    a[0] = fmaf(wr[i].x, hv.x, a[0]);
+                    a[1] = fmaf(wr[i].y, hv.y, a[1]);
+                    a[2] = fmaf(wr[i].z, hv.z, a[2]);
+                    a[3] = fmaf(wr[i].w, hv.w, a[3]);
+                }
             } else {
                 const float *row = Wr + (size_t)e * d;
                 uint32_t i = 0;
                 for (; i < main; i += 32) {
-                    a1 = fmaf(row[i + l16], hs[i + l16], a1);
-                    a2 = fmaf(row[i + 16 + l16], hs[i + 16 + l16], a2);
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; ++c) a[c] = fmaf(row[i + 8 * c + l8], hs[i + 8 * c + l8], a[c]);
                 }
                 for (; i + 8 <= d; i += 8)      // 8-wide tail into accumulator 0
-                    if (l16 < 8) a1 = fmaf(row[i + l16], hs[i + l16], a1);
+                    a[0] = fmaf(row[i + l8], hs[i + l8], a[0]);
             }
         }
-        float v = (a1 + shfl_xor(a1, 8)) + (a2 + shfl_xor(a2, 8));
-        v = v + shfl_xor(v, 4);
-        v = v + shfl_xor(v, 2);
-        v = v + shfl_xor(v, 1);
-        if (e < E && l16 == 0) {
-            const uint32_t t0 = pre ? d : d - d % 8;
-            for (uint32_t i = t0; i < d; ++i) v = v + Wr[(size_t)e * d + i] * hs[i];
-            lg[e] = v;
+        float v = (a[0] + a[1]) + (a[2] + a[3]);
+        {   // both moves in every lane, then the select (a move under a branch would read
+            // lanes the branch switched off)
+            const float dn = dpp_f<0x124>(v), up = dpp_f<0x12C>(v);
+            v = v + ((l8 & 4) ? dn : up);   // lane ^ 4
         }
+        v = v + dpp_f<0x4E>(v);   // lane ^ 2
+        v = v + dpp_f<0xB1>(v);   // lane ^ 1
+        if (e0 == 0) myv = v;     // (d is a multiple of 32: no scalar tail)
+        if (e < E && l8 == 0) lg[e] = v;
+    }
+    // quantization of h for the expert matvecs (quant.rs:111-123), by waves 1.. after the last
+    // barrier (a barrier after global stores waits for them to complete)
+    auto quantize_h = [&] {
+        const uint32_t nb = d / QK, nc = div_up(nb, 4);
+        const int j = tid & 7, qt = tid - 64, nq = nthr - 64;
+        for (uint32_t b0 = 0; b0 < nb; b0 += nq / 8) {
+            const uint32_t b = b0 + (qt >> 3);
+            if (b < nb) {
+                const v4f hv = *reinterpret_cast<const v4f *>(hs + b * QK + j * 4);
+                const float v[4] = {hv.x, hv.y, hv.z, hv.w};
+                quant_block_lane(v, j, b, q_out, d_out);
+            }
+        }
+        zero_pad(nb, nc, q_out, d_out, qt, nq);
+    };
+    auto rlf = [](float v, uint32_t l) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), (int)l));
+    };
+    auto rlu = [](uint32_t v, uint32_t l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l); };
+    if (gating_sigmoid && E * 8 <= nrt && E <= ROUTER_MAXE && top_k <= 64) {
+        // every row's 8 lanes form its gate and key; the rank of expert e is
+        // #{e' : key_e' > key_e or (key_e' == key_e and e' < e)}, one unsigned 64-bit compare
+        // (high word the key's order-preserving bits with -0 made +0, as the float compare has
+        // -0 == +0; low word ~e), lane l8 counting the experts l8, l8 + 8, ...
+        __shared__ uint64_t K[ROUTER_MAXE];
+        const float g = hg_sigmoid_l(myv, tab);   // (wave 0: unused)
+        const float key = (g + bv8) + 0.0f;
+        const uint32_t mb = __builtin_bit_cast(uint32_t, key);
+        const uint64_t mk = ((uint64_t)((mb & 0x80000000u) ? ~mb : (mb | 0x80000000u)) << 32) | (uint32_t)~e8;
+        if (rows && l8 == 0 && e8 < E) K[e8] = mk;
+        __syncthreads();
+        if (rows) {
+            uint64_t kk[ROUTER_MAXE / 8];
+#pragma unroll
+            for (uint32_t q = 0; q < ROUTER_MAXE / 8; ++q) kk[q] = K[min(l8 + 8 * q, E - 1)];
+            uint32_t cnt = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < ROUTER_MAXE / 8; ++q) cnt += (l8 + 8 * q < E) && (kk[q] > mk);
+            {
+                const uint32_t dn = dpp_u<0x124>(cnt), up = dpp_u<0x12C>(cnt);
+                cnt += (l8 & 4) ? dn : up;
+            }
+            cnt += dpp_u<0x4E>(cnt);
+            cnt += dpp_u<0xB1>(cnt);
+            if (l8 == 0 && e8 < E && cnt < top_k) { tk[cnt] = e8; tw[cnt] = g; }
+        }
+        __syncthreads();
+        if (tid >= 64) {
+            quantize_h();
+            return;
+        }
+        const uint32_t rl = min((uint32_t)lane, top_k - 1);
+        const uint32_t ei = tk[rl];
+        const float twl = tw[rl];
+        float s = 0.0f;   // every lane forms the same sequential sum (f32 iterator sum + 1e-9)
+        if (weights_norm) {
+            for (uint32_t r = 0; r < top_k; ++r) s = s + rlf(twl, r);
+            s = s + 1e-9f;
+        }
+        uint32_t rk = 0;   // slot order by ascending expert id (the prompt path's accumulation order)
+        for (uint32_t q = 0; q < top_k; ++q) rk += rlu(ei, q) < ei;
+        if ((uint32_t)lane < top_k) {
+            const uint32_t r = lane;
+            const float wr_ = (weights_norm ? twl / s : twl) * weights_scale;
+            topk_idx[r] = ei;
+            topk_w[r] = wr_;
+            rec_idx[r] = ei;
+            rec_w[r] = wr_;
+            order[rk] = r;
+        }
+        return;
     }
     if ((uint32_t)tid < E) sel[tid] = bv;   // bias, combined below
     __syncthreads();
-    if (tid >= 64) return;
-    // gate, selection and weights in wave 0 (lane: experts lane, lane + 64, ...)
+    if (tid >= 64) {
+        quantize_h();
+        return;
+    }
+    auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // general path: lane owns experts lane, lane + 64, ...
     const uint32_t KE = div_up(E, 64);
     if (gating_sigmoid) {
         for (uint32_t k = 0; k < KE; ++k) {
@@ -1402,21 +1636,17 @@ __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x
             const float ex = hg_expf_l(lg[min(e, E - 1)] - mx, tab);
             if (e < E) scr[e] = ex;
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        wave_sync();
         float sum = 0.0f;
         for (uint32_t e = 0; e < E; ++e) sum = sum + scr[e];
         const float inv = 1.0f / sum;
-        __builtin_amdgcn_wave_barrier();
+        wave_sync();
         for (uint32_t k = 0; k < KE; ++k)
             if (lane + 64 * k < E) scr[lane + 64 * k] = scr[lane + 64 * k] * inv;
     }
     for (uint32_t k = 0; k < KE; ++k)
         if (lane + 64 * k < E) sel[lane + 64 * k] = scr[lane + 64 * k] + sel[lane + 64 * k];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_sync();
     for (uint32_t k = 0; k < KE; ++k) {
         const uint32_t me_e = lane + 64 * k;
         if (me_e < E) {
@@ -1426,9 +1656,7 @@ __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x
             if (rank < top_k) { tk[rank] = me_e; tw[rank] = scr[me_e]; }
         }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_sync();
     float s = 0.0f;   // every lane forms the same sequential sum (f32 iterator sum + 1e-9)
     if (weights_norm) {
         for (uint32_t r = 0; r < top_k; ++r) s = s + tw[r];
@@ -1436,11 +1664,11 @@ __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x
     }
     if ((uint32_t)lane < top_k) {
         const uint32_t r = lane, ei = tk[r];
-        const float wr = (weights_norm ? tw[r] / s : tw[r]) * weights_scale;
+        const float wr_ = (weights_norm ? tw[r] / s : tw[r]) * weights_scale;
         topk_idx[r] = ei;
-        topk_w[r] = wr;
+        topk_w[r] = wr_;
         rec_idx[r] = ei;
-        rec_w[r] = wr;
+        rec_w[r] = wr_;
         uint32_t rk = 0;   // slot order by ascending expert id (the prompt path's accumulation order)
         for (uint32_t q = 0; q < top_k; ++q) rk += tk[q] < ei;
         order[rk] = r;
@@ -1467,12 +1695,27 @@ __global__ __launch_bounds__(64) void k_ffn_gateup(Q8Mat Wg, Q8Mat Wu, Q8Mat Sg,
     const bool routed = slot < top_k;
     const Q8Mat &G = routed ? Wg : Sg;
     const Q8Mat &U = routed ? Wu : Su;
-    const uint32_t r = routed ? topk_idx[slot] * f + li : li;
+    // loads in issue order: the router's pick, the activation (first 2 x 64 chunks in
+    // registers) and the exp table, then the rows the pick selects
+    const uint32_t e = routed ? topk_idx[slot] : 0u;
+    const uint32_t nc = Wg.nc;
+    v4i qv[2];
+#pragma unroll
+    for (uint32_t u = 0; u < 2; ++u) qv[u] = reinterpret_cast<const v4i *>(gq)[min(u * 64 + (uint32_t)tid, nc * 8 - 1)];
+    const float dv = gd[min((uint32_t)tid, nc * 4 - 1)];
+    const WaveExpTab tab = WaveExpTab::load(tid);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t r = routed ? e * f + li : li;
     Q8Row<ORDER, SCF32, NCT> rg, ru;
     rg.begin(row_qs(G, r), row_sc<SCF32>(G, r), G.nb, G.nc, j);
     ru.begin(row_qs(U, r), row_sc<SCF32>(U, r), U.nb, U.nc, j);
-    const WaveExpTab tab = WaveExpTab::load(tid);
-    stage_act(gq, gd, Wg.nc, sq, sd, tid, 64);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t u = 0; u < 2; ++u)
+        if (u * 64 + (uint32_t)tid < nc * 8) reinterpret_cast<v4i *>(sq)[u * 64 + tid] = qv[u];
+    for (uint32_t q = 128 + (uint32_t)tid; q < nc * 8; q += 64)
+        reinterpret_cast<v4i *>(sq)[q] = reinterpret_cast<const v4i *>(gq)[q];
+    for (uint32_t q = (uint32_t)tid; q < nc * 4; q += 64) sd[q] = q == (uint32_t)tid ? dv : gd[q];
     __syncthreads();
     const float g = rg.finish(sq, sd);
     const float u = ru.finish(sq, sd);
@@ -1517,6 +1760,7 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
         av[u] = *reinterpret_cast<const v4f *>(as + b * QK + j * 4);
     }
     const float wsel = (!dense && top_k) ? topk_w[min((uint32_t)lane, top_k - 1)] : 0.0f;
+    const float xold = x[min(blockIdx.x * 8 + (uint32_t)(tid & 7), d - 1)];   // the residual, used by tid < 8
     const uint32_t row = routed ? topk_idx[slot] * d + lr : lr;
     Q8Row<ORDER, SCF32, NCT> rd;
     rd.begin(row_qs(D, row), row_sc<SCF32>(D, row), nb, nc, j);
@@ -1547,7 +1791,7 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
         const uint32_t rr = blockIdx.x * 8 + tid;
         if (rr < d) {
             if (dense) {
-                x[rr] = x[rr] + ys[tid];
+                x[rr] = xold + ys[tid];
             } else {
                 float acc = 0.0f;
                 for (uint32_t q = 0; q < top_k; ++q) {
@@ -1555,7 +1799,7 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
                     acc = acc + wsl[s] * ys[s * 8 + tid];
                 }
                 if (n_slots > top_k) acc = acc + ys[top_k * 8 + tid];
-                x[rr] = x[rr] + acc;
+                x[rr] = xold + acc;
             }
         }
     }
@@ -1666,6 +1910,32 @@ void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uin
 #undef MV
 }
 
+void launch_norm_matvec(hipStream_t st, bool exact, int order, const Q8Mat &W, const float *x, const float *w,
+                        float eps, float *y, uint32_t threads) {
+    const dim3 grid(matvec_blocks(W.N, threads)), block(threads);
+    const size_t shm = (size_t)W.nc * CHUNK_BYTES + (size_t)W.nc * 4 * sizeof(float) + (size_t)W.K * sizeof(float);
+#define NMV(E, O, S, N) LAUNCH((k_norm_matvec<E, O, S, N>), grid, block, shm, st, W, x, w, eps, y)
+#define NMV_S(E, O, N)                  \
+    do {                                \
+        if (W.sc_f32) NMV(E, O, true, N);  \
+        else NMV(E, O, false, N);          \
+    } while (0)
+#define NMV_E(N)                                                                     \
+    do {                                                                             \
+        if (order == ORDER_DECODE) {                                                 \
+            if (exact) NMV_S(true, ORDER_DECODE, N);                                 \
+            else NMV_S(false, ORDER_DECODE, N);                                      \
+        } else {                                                                     \
+            if (exact) NMV_S(true, ORDER_PREFILL, N);                                \
+            else NMV_S(false, ORDER_PREFILL, N);                                     \
+        }                                                                            \
+    } while (0)
+    DISPATCH_NCT(W.nc, NMV_E)
+#undef NMV_E
+#undef NMV_S
+#undef NMV
+}
+
 void launch_matvec_gather(hipStream_t st, const Q8Mat &W, uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids,
                           const uint8_t *q, const float *dq, float *y) {
     const dim3 grid(div_up(rows_per_mat, 32), n_ids);
@@ -1749,21 +2019,33 @@ bool launch_attn(hipStream_t st, bool exact, int which, uint32_t hd, const float
 }
 
 void launch_ffn_router(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,
-                       const float *Wr, const float *bias, uint32_t E, uint32_t top_k, int gating_sigmoid,
-                       int weights_norm, float weights_scale, uint8_t *q, float *dq, uint32_t *topk_idx,
-                       float *topk_w, uint32_t *order, uint32_t *rec_idx, float *rec_w) {
-    const size_t shm = 2 * d * sizeof(float);
+                       const float *Wr, const float *Wp, const float *bias, uint32_t E, uint32_t top_k,
+                       int gating_sigmoid, int weights_norm, float weights_scale, uint8_t *q, float *dq,
+                       uint32_t *topk_idx, float *topk_w, uint32_t *order, uint32_t *rec_idx, float *rec_w) {
+    const size_t shm = 3 * d * sizeof(float);
     const uint32_t nt = router_threads(E);
-    // up to 640 threads (E <= 40) the kernel may hold 168 VGPRs: no spills with the prefetch
-#define RTK(EX, MT) LAUNCH((k_ffn_router<EX, MT>), dim3(1), dim3(nt), shm, st, x, w, eps, d, Wr, bias, E, top_k, \
-                           gating_sigmoid, weights_norm, weights_scale, q, dq, topk_idx, topk_w, order, rec_idx, rec_w)
-    if (nt <= 640) {
-        if (exact) RTK(true, 640);
-        else RTK(false, 640);
+    // up to 512 threads (E <= 64) the kernel may hold 256 VGPRs (the prefetched weights)
+#define RTK(EX, MT, NS) LAUNCH((k_ffn_router<EX, MT, NS>), dim3(1), dim3(nt), shm, st, x, w, eps, d, Wr, Wp, bias, E, \
+                               top_k, gating_sigmoid, weights_norm, weights_scale, q, dq, topk_idx, topk_w, order,  \
+                               rec_idx, rec_w)
+#define RTK_E(MT, NS)               \
+    do {                            \
+        if (exact) RTK(true, MT, NS);  \
+        else RTK(false, MT, NS);       \
+    } while (0)
+    if (nt <= 512) {
+        switch (d) {
+        case 1024: RTK_E(512, 32); break;
+        case 768: RTK_E(512, 24); break;
+        case 512: RTK_E(512, 16); break;
+        case 256: RTK_E(512, 8); break;
+        case 128: RTK_E(512, 4); break;
+        default: RTK_E(512, 0); break;
+        }
     } else {
-        if (exact) RTK(true, 1024);
-        else RTK(false, 1024);
+        RTK_E(1024, 0);
     }
+#undef RTK_E
 #undef RTK
 }
 
