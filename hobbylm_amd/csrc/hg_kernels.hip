@@ -145,45 +145,72 @@ struct Q8Row {
         j = j_;
         load(0);
     }
+    // One chunk c (batch slot u) against the activation chunk x and its scales.
+    __device__ inline void chunk(int u, uint32_t c, const v4i x, const v4f dxc, bool guard, float &acc) const {
+        const int p[4] = {sdot4(wq[u].x, x.x), sdot4(wq[u].y, x.y), sdot4(wq[u].z, x.z), sdot4(wq[u].w, x.w)};
+        float sv[4];
+        unpack_scales(sq[u], sv);
+        const float dv[4] = {dxc.x, dxc.y, dxc.z, dxc.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t b = c * 4 + t;
+            const float d = sv[t] * dv[t];
+            if (ORDER == ORDER_DECODE) {
+                if (!guard || b < nb) acc = fmaf(d, (float)p[t], acc);
+            } else {   // the block's integer sum over the 8 lanes (exact in any order)
+                int is = p[t];
+                is += (int)dpp_u<0xB1>((uint32_t)is);
+                is += (int)dpp_u<0x4E>((uint32_t)is);
+                {
+                    const int dn = (int)dpp_u<0x124>((uint32_t)is), up = (int)dpp_u<0x12C>((uint32_t)is);
+                    is += (j & 4) ? dn : up;
+                }
+                if (!guard || b < nb) acc = acc + d * (float)is;
+            }
+        }
+    }
+    // Every lane of the row's 8 must be active.
     __device__ inline float finish(const uint8_t *qx, const float *dx) {
         float acc = 0.0f;
-        uint32_t c0 = 0;
-        while (true) {
+        if (nc == (uint32_t)NCT && nb == 4 * (uint32_t)NCT) {
+            // one batch and no padding blocks: straight-line code
+            v4i xa[NCT];
+            v4f xs[NCT];
 #pragma unroll
             for (int u = 0; u < NCT; ++u) {
-                const uint32_t c = c0 + u;
-                if (c < nc) {
-                    const v4i x = *reinterpret_cast<const v4i *>(qx + c * CHUNK_BYTES + j * 16);
-                    const v4f dxc = *reinterpret_cast<const v4f *>(dx + c * 4);
-                    const int p[4] = {sdot4(wq[u].x, x.x), sdot4(wq[u].y, x.y), sdot4(wq[u].z, x.z),
-                                      sdot4(wq[u].w, x.w)};
-                    float sv[4];
-                    unpack_scales(sq[u], sv);
-                    const float dv[4] = {dxc.x, dxc.y, dxc.z, dxc.w};
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const uint32_t b = c * 4 + t;
-                        const float d = sv[t] * dv[t];
-                        if (ORDER == ORDER_DECODE) {
-                            if (b < nb) acc = fmaf(d, (float)p[t], acc);
-                        } else {
-                            int is = p[t];
-                            is += shfl_xor_i(is, 1);
-                            is += shfl_xor_i(is, 2);
-                            is += shfl_xor_i(is, 4);
-                            if (b < nb) acc = acc + d * (float)is;
-                        }
-                    }
-                }
+                xa[u] = *reinterpret_cast<const v4i *>(qx + u * CHUNK_BYTES + j * 16);
+                xs[u] = *reinterpret_cast<const v4f *>(dx + u * 4);
             }
-            c0 += NCT;
-            if (c0 >= nc) break;
-            load(c0);
+#pragma unroll
+            for (int u = 0; u < NCT; ++u) chunk(u, (uint32_t)u, xa[u], xs[u], false, acc);
+        } else {
+            uint32_t c0 = 0;
+            while (true) {
+                // the batch's activation chunks and scales, read from LDS together (addresses
+                // clamped into the row) before any of them is used
+                v4i xa[NCT];
+                v4f xs[NCT];
+#pragma unroll
+                for (int u = 0; u < NCT; ++u) {
+                    const uint32_t c = min(c0 + (uint32_t)u, nc - 1);
+                    xa[u] = *reinterpret_cast<const v4i *>(qx + c * CHUNK_BYTES + j * 16);
+                    xs[u] = *reinterpret_cast<const v4f *>(dx + c * 4);
+                }
+#pragma unroll
+                for (int u = 0; u < NCT; ++u)
+                    if (c0 + u < nc) chunk(u, c0 + u, xa[u], xs[u], true, acc);
+                c0 += NCT;
+                if (c0 >= nc) break;
+                load(c0);
+            }
         }
-        if (ORDER == ORDER_DECODE) {
-            acc = acc + shfl_xor(acc, 4);
-            acc = acc + shfl_xor(acc, 2);
-            acc = acc + shfl_xor(acc, 1);
+        if (ORDER == ORDER_DECODE) {   // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) in lane 0 (quant.rs:61-65)
+            {
+                const float dn = dpp_f<0x124>(acc), up = dpp_f<0x12C>(acc);
+                acc = acc + ((j & 4) ? dn : up);
+            }
+            acc = acc + dpp_f<0x4E>(acc);
+            acc = acc + dpp_f<0xB1>(acc);
         }
         return acc;
     }
@@ -493,8 +520,8 @@ __global__ __launch_bounds__(256) void k_norm_matvec(Q8Mat W, const float *__res
     const int tid = threadIdx.x, nthr = blockDim.x, j = tid & 7;
     const uint32_t d = W.K, ng = d / 4;
     // x and the gain first, alone in the memory pipeline (the chain waits for them); the
-    // weight stream of this thread's row is issued once the squares are formed and arrives
-    // during the chain
+    // weight stream of this thread's row is issued after the barrier that starts the chain and
+    // arrives during it
     constexpr uint32_t RQ = 4;
     v4f xv[RQ], wv[RQ];
 #pragma unroll
@@ -521,13 +548,14 @@ __global__ __launch_bounds__(256) void k_norm_matvec(Q8Mat W, const float *__res
     for (uint32_t u = 0; u < RQ; ++u)
         if (tid + nthr * u < ng) squares(xv[u], tid + nthr * u);
     for (uint32_t g = tid + nthr * RQ; g < ng; g += nthr) squares(reinterpret_cast<const v4f *>(x)[g], g);
-    __builtin_amdgcn_sched_barrier(0);
-    rd.begin(row_qs(W, lrow), row_sc<SCF32>(W, lrow), W.nb, W.nc, j);
-    __builtin_amdgcn_sched_barrier(0);
     if (EXACT) {
         __syncthreads();
+        // the weight stream is issued here, so that issuing it does not hold the barrier back
+        rd.begin(row_qs(W, lrow), row_sc<SCF32>(W, lrow), W.nb, W.nc, j);
+        __builtin_amdgcn_sched_barrier(0);
         if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
     } else {
+        rd.begin(row_qs(W, lrow), row_sc<SCF32>(W, lrow), W.nb, W.nc, j);
         for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
