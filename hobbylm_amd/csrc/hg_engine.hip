@@ -368,9 +368,10 @@ void enqueue_layers(hg_kv *kv, int order) {
     StepParams *p = kv->params.as<StepParams>();
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const Layer &L = *m->layers[l];
-        mark(kv, P_QKV);   // attn_norm + attn_qkv (model.rs:164-165, 194)
-        launch_norm_matvec(st, kv->exact, order, L.qkv.m, x, L.attn_norm.as<float>(), c.rms_eps, kv->qkv.as<float>(),
-                           256);
+        mark(kv, P_QKV);   // attn_norm + attn_qkv + QK-norm + RoPE + append (model.rs:164-165, 194-211)
+        launch_qkv_head(st, kv->exact, order, c.head_dim, L.qkv.m, x, L.attn_norm.as<float>(), c.rms_eps,
+                        L.q_norm.as<float>(), L.k_norm.as<float>(), m->rope_cos.as<float>(), m->rope_sin.as<float>(), p,
+                        c.n_heads, c.n_kv_heads, layer_k(kv, l), layer_v(kv, l), kv->cap, kv->qkv.as<float>());
         for (int part = 0; part < 2; ++part) {
             mark(kv, part == 0 ? P_ATTN_A : P_ATTN_B);
             launch_attn(st, kv->exact, part, c.head_dim, kv->qkv.as<float>(), L.q_norm.as<float>(),
@@ -975,6 +976,9 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
         (rc = dout.alloc((size_t)qd * 4)) || (rc = dq.alloc((size_t)div_up(qd / QK, 4) * CHUNK_BYTES)) ||
         (rc = dd.alloc((size_t)div_up(qd / QK, 4) * 16)))
         return rc;
+    if (!launch_qk_rope_append(nullptr, hd, dqkv.as<float>(), dqn.as<float>(), dkn.as<float>(), eps, dcs.as<float>(),
+                               dsn.as<float>(), dp.as<StepParams>(), n_heads, n_kv, dk.as<float>(), dv.as<float>(), cap))
+        return fail(HG_ERR_UNSUPPORTED, "head_dim not supported");
     for (int which = 0; which < 2; ++which)
         if (!launch_attn(nullptr, exact, which, hd, dqkv.as<float>(), dqn.as<float>(), dkn.as<float>(), eps,
                          dcs.as<float>(), dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap,
@@ -1039,6 +1043,9 @@ int hg_attention_time(uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t ctx
                         dcs.as<float>(), dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap,
                         n_heads, n_kv, S, dpart.as<float>(), dscr.as<float>(), dout.as<float>(), q_out, d_out);
     };
+    // q, k normed and rotated and the row pos appended once (the QKV step's work, not timed)
+    launch_qk_rope_append(s0, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f, dcs.as<float>(),
+                          dsn.as<float>(), dp.as<StepParams>(), n_heads, n_kv, dk.as<float>(), dv.as<float>(), cap);
     for (int r = 0; r < 3; ++r) layer();
     hipError_t e = hipStreamSynchronize(s0);
     LaunchTimer timer;

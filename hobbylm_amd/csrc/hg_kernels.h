@@ -30,9 +30,16 @@ uint32_t matvec_blocks(uint32_t N, uint32_t threads);
 // dq == nullptr: q points to an f32 activation that each workgroup quantizes in its prologue.
 void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uint8_t *q, const float *dq, float *y,
                    uint32_t threads, uint32_t valid, float *pv, uint32_t *pi);
-// y = W * quant(rmsnorm(x, w)) with the norm formed by every workgroup (no activation buffer).
-void launch_norm_matvec(hipStream_t st, bool exact, int order, const Q8Mat &W, const float *x, const float *w,
-                        float eps, float *y, uint32_t threads);
+// out = the q | k | v rows of W times quant(rmsnorm(x, w)), with q and k normed (qn, kn) and
+// rotated at p->pos, and k, v appended to the caches at row p->pos; one workgroup per head.
+bool launch_qkv_head(hipStream_t st, bool exact, int order, uint32_t hd, const Q8Mat &W, const float *x,
+                     const float *w, float eps, const float *qn, const float *kn, const float *cs, const float *sn,
+                     const StepParams *p, uint32_t n_heads, uint32_t n_kv, float *kc, float *vc, uint32_t cap,
+                     float *out);
+// The same head steps for a q | k | v vector computed elsewhere (rewritten in place).
+bool launch_qk_rope_append(hipStream_t st, uint32_t hd, float *qkv, const float *qn, const float *kn, float eps,
+                           const float *cs, const float *sn, const StepParams *p, uint32_t n_heads, uint32_t n_kv,
+                           float *kc, float *vc, uint32_t cap);
 // The matvecs of matrices ids[0..n_ids) of a stack of rows_per_mat-row matrices, one launch.
 void launch_matvec_gather(hipStream_t st, const Q8Mat &W, uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids,
                           const uint8_t *q, const float *dq, float *y);
@@ -40,6 +47,8 @@ void launch_argmax_final(hipStream_t st, const float *pv, const uint32_t *pi, ui
                          uint32_t *out_ids);
 size_t attn_fast_shm(uint32_t hd, uint32_t rep, uint32_t cap, uint32_t S);
 // which = 0: scores (reference order) or split partials (fast); which = 1: softmax + P.V or merge.
+// qkv holds q and k normed and rotated, and the caches row pos already (launch_qkv_head or
+// launch_qk_rope_append); qn, kn, eps, cs, sn are not read.
 // Reference order with q_out == nullptr leaves the quantization of o to its consumer.
 bool launch_attn(hipStream_t st, bool exact, int which, uint32_t hd, const float *qkv, const float *qn,
                  const float *kn, float eps, const float *cs, const float *sn, const StepParams *p, float *kc,

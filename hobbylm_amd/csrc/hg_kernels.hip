@@ -60,7 +60,11 @@ __device__ inline float max8_lanes(float m, int j) {
 // One 32-block of activation quantization (quant.rs:114-122), lanes j = 0..7 of 8 adjacent
 // threads each holding v[0..3] = x[32b + 4j + 0..3].  d = amax/127, id = 1/d (0 if d == 0),
 // q = clamp(round_half_away(x*id), +-127).  Writes q into the lane-major chunk layout.
-__device__ inline void quant_block_lane(const float v[4], int j, uint32_t b, uint8_t *q, float *d) {
+// `store` = false computes without writing: callers run the lane exchanges with every lane
+// active and keep the loads that feed them unconditional (a load used only under a branch is
+// moved into it by the compiler, behind later loads).
+__device__ inline void quant_block_lane(const float v[4], int j, uint32_t b, uint8_t *q, float *d,
+                                        bool store = true) {
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     amax = max8_lanes(amax, j);
     const float dd = amax / 127.0f;
@@ -73,8 +77,10 @@ __device__ inline void quant_block_lane(const float v[4], int j, uint32_t b, uin
         r = fminf(fmaxf(r, -127.0f), 127.0f);
         packed |= (uint32_t)(uint8_t)(int8_t)(int)r << (8 * m);
     }
-    *reinterpret_cast<uint32_t *>(q + (b / 4) * CHUNK_BYTES + j * 16 + (b % 4) * 4) = packed;
-    if (j == 0) d[b] = dd;
+    if (store) {
+        *reinterpret_cast<uint32_t *>(q + (b / 4) * CHUNK_BYTES + j * 16 + (b % 4) * 4) = packed;
+        if (j == 0) d[b] = dd;
+    }
 }
 
 // Zero the padding blocks of a partial last chunk so padded lanes contribute 0.
@@ -395,21 +401,6 @@ __global__ __launch_bounds__(256) void k_quant_vec(const float *__restrict__ x, 
 //   EPI_RESID:  y[r] = y[r] + v     (x[i] += attn[i], model.rs:169-171)
 //   EPI_LOGITS: y[r] = v, plus a per-workgroup (max, first index) over rows < valid for
 //               the greedy argmax (sample.rs:53-63 on logits masked per lib.rs:132-134).
-// Quantize an f32 activation x[K] into the LDS chunk layout (quant.rs:111-123), all threads.
-__device__ inline void quant_to_lds(const float *__restrict__ x, uint32_t nb, uint32_t nc, uint8_t *sq, float *sd,
-                                    int tid, int nthr) {
-    const int j = tid & 7;
-    for (uint32_t b0 = 0; b0 < nb; b0 += nthr / 8) {
-        const uint32_t b = b0 + tid / 8;
-        if (b < nb) {
-            const v4f xv = *reinterpret_cast<const v4f *>(x + b * QK + j * 4);
-            const float v[4] = {xv.x, xv.y, xv.z, xv.w};
-            quant_block_lane(v, j, b, sq, sd);
-        }
-    }
-    zero_pad(nb, nc, sq, sd, tid, nthr);
-}
-
 template <int ORDER, int EPI, bool SCF32, int NCT, bool AF32 = false>
 __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restrict__ gq,
                                                 const float *__restrict__ gd, float *y, uint32_t valid,
@@ -450,10 +441,8 @@ __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restri
 #pragma unroll
         for (uint32_t u = 0; u < XQ; ++u) {   // a block's 8 lanes are all in or all out
             const uint32_t b = u * bstep + (uint32_t)(tid >> 3);
-            if (b < nb) {
-                const float v4[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
-                quant_block_lane(v4, j, b, sq, sd);
-            }
+            const float v4[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+            quant_block_lane(v4, j, min(b, nb - 1), sq, sd, b < nb);
         }
         for (uint32_t b0 = XQ * bstep; b0 < nb; b0 += bstep) {
             const uint32_t b = b0 + (uint32_t)(tid >> 3);
@@ -466,13 +455,12 @@ __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restri
         zero_pad(nb, nc, sq, sd, tid, nthr);
     } else {
 #pragma unroll
-        for (uint32_t u = 0; u < XQ; ++u) {
-            const uint32_t i = u * (uint32_t)nthr + (uint32_t)tid;
-            if (i < nc * 8) reinterpret_cast<v4i *>(sq)[i] = qv[u];
-        }
+        for (uint32_t u = 0; u < XQ; ++u)   // (clamped slots rewrite the value they already hold)
+            reinterpret_cast<v4i *>(sq)[min(u * (uint32_t)nthr + (uint32_t)tid, nc * 8 - 1)] = qv[u];
         for (uint32_t i = XQ * (uint32_t)nthr + (uint32_t)tid; i < nc * 8; i += nthr)
             reinterpret_cast<v4i *>(sq)[i] = reinterpret_cast<const v4i *>(gq)[i];
-        for (uint32_t i = (uint32_t)tid; i < nc * 4; i += nthr) sd[i] = i == (uint32_t)tid ? dv : gd[i];
+        sd[min((uint32_t)tid, nc * 4 - 1)] = dv;
+        for (uint32_t i = (uint32_t)tid + nthr; i < nc * 4; i += nthr) sd[i] = gd[i];
     }
     __syncthreads();
     const float v = rd.finish(sq, sd);
@@ -501,85 +489,6 @@ __global__ __launch_bounds__(256) void k_matvec(Q8Mat W, const uint8_t *__restri
             part_i[blockIdx.x] = mi;
         }
     }
-}
-
-// rmsnorm (ops.rs:98-109) of x with gain w, its activation quantization (quant.rs:111-123)
-// and the Q8 matvec (quant.rs:125-135) in one launch: the attn_norm + attn_qkv pair of
-// model.rs:164-165 and 194.  Every workgroup forms the norm of the whole vector itself, in
-// the reference's order, while its weight rows are in flight, and quantizes straight into
-// LDS, so the normed activation never round-trips through memory.  y[r] = v (EPI_STORE).
-template <bool EXACT, int ORDER, bool SCF32, int NCT>
-__global__ __launch_bounds__(256) void k_norm_matvec(Q8Mat W, const float *__restrict__ x,
-                                                     const float *__restrict__ w, float eps, float *y) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    uint8_t *sq = smem;
-    float *sd = reinterpret_cast<float *>(smem + W.nc * CHUNK_BYTES);
-    float *ps = sd + W.nc * 4;   // the d squares
-    __shared__ float red[4];
-    __shared__ float s_ss;
-    const int tid = threadIdx.x, nthr = blockDim.x, j = tid & 7;
-    const uint32_t d = W.K, ng = d / 4;
-    // x and the gain first, alone in the memory pipeline (the chain waits for them); the
-    // weight stream of this thread's row is issued after the barrier that starts the chain and
-    // arrives during it
-    constexpr uint32_t RQ = 4;
-    v4f xv[RQ], wv[RQ];
-#pragma unroll
-    for (uint32_t u = 0; u < RQ; ++u) {
-        const uint32_t g = min(tid + nthr * u, ng - 1);
-        xv[u] = reinterpret_cast<const v4f *>(x)[g];
-        wv[u] = reinterpret_cast<const v4f *>(w)[g];
-    }
-    const uint32_t row = blockIdx.x * (nthr >> 3) + (tid >> 3);
-    const uint32_t lrow = min(row, W.N - 1);
-    Q8Row<ORDER, SCF32, NCT> rd;
-    float ss = 0.0f;
-    auto squares = [&](const v4f a, uint32_t g) {
-        if (EXACT) {
-            reinterpret_cast<v4f *>(ps)[g] = a * a;
-        } else {
-            ss += a.x * a.x;
-            ss += a.y * a.y;
-            ss += a.z * a.z;
-            ss += a.w * a.w;
-        }
-    };
-#pragma unroll
-    for (uint32_t u = 0; u < RQ; ++u)
-        if (tid + nthr * u < ng) squares(xv[u], tid + nthr * u);
-    for (uint32_t g = tid + nthr * RQ; g < ng; g += nthr) squares(reinterpret_cast<const v4f *>(x)[g], g);
-    if (EXACT) {
-        __syncthreads();
-        // the weight stream is issued here, so that issuing it does not hold the barrier back
-        rd.begin(row_qs(W, lrow), row_sc<SCF32>(W, lrow), W.nb, W.nc, j);
-        __builtin_amdgcn_sched_barrier(0);
-        if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
-    } else {
-        rd.begin(row_qs(W, lrow), row_sc<SCF32>(W, lrow), W.nb, W.nc, j);
-        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-        __syncthreads();
-        if (tid == 0) {
-            float t = 0.0f;
-            for (int i = 0; i < nthr / 64; ++i) t += red[i];
-            s_ss = t;
-        }
-    }
-    __syncthreads();
-    const float scale = 1.0f / sqrtf(s_ss / (float)d + eps);
-    auto emit = [&](const v4f a, const v4f gw, uint32_t g) {
-        const float v[4] = {a.x * scale * gw.x, a.y * scale * gw.y, a.z * scale * gw.z, a.w * scale * gw.w};
-        quant_block_lane(v, j, g / 8, sq, sd);
-    };
-#pragma unroll
-    for (uint32_t u = 0; u < RQ; ++u)   // a block's 8 groups are all < ng or all >= ng
-        if (tid + nthr * u < ng) emit(xv[u], wv[u], tid + nthr * u);
-    for (uint32_t g = tid + nthr * RQ; g < ng; g += nthr)
-        emit(reinterpret_cast<const v4f *>(x)[g], reinterpret_cast<const v4f *>(w)[g], g);
-    zero_pad(W.nb, W.nc, sq, sd, tid, nthr);
-    __syncthreads();
-    const float v = rd.finish(sq, sd);
-    if (row < W.N && j == 0) y[row] = v;
 }
 
 // Q8Tensor::matvec of the matrices ids[0..n) of a stack of equal matrices (rows_per_mat rows
@@ -671,9 +580,18 @@ template <int HD>
 __device__ inline void norm_rope_head(const float *u, float *o, const HeadConst<HD> &hc, bool is_q, float eps,
                                       float *tmp, int lane) {
     float scale = 0.0f;
-    if (lane == 0) {
+    if (lane == 0) {   // ss += x * x in index order; the reads are issued together first
+        v4f r[HD / 4];
+#pragma unroll
+        for (int i = 0; i < HD / 4; ++i) r[i] = reinterpret_cast<const v4f *>(u)[i];
         float ss = 0.0f;
-        for (uint32_t i = 0; i < HD; ++i) ss = ss + u[i] * u[i];
+#pragma unroll
+        for (int i = 0; i < HD / 4; ++i) {
+            ss = ss + r[i].x * r[i].x;
+            ss = ss + r[i].y * r[i].y;
+            ss = ss + r[i].z * r[i].z;
+            ss = ss + r[i].w * r[i].w;
+        }
         scale = 1.0f / sqrtf(ss / (float)HD + eps);
     }
     scale = __shfl(scale, 0, 64);
@@ -722,16 +640,171 @@ struct GroupRaw {
     }
 };
 
+// ------------------------------------------------------------------ attention front
+// attn_norm + attn_qkv + QK-norm + RoPE + cache append for one head (model.rs:164-165,
+// 194-211): rmsnorm (ops.rs:98-109) of x with gain w and its activation quantization
+// (quant.rs:111-123), the head's HD rows of the Q8 matvec (quant.rs:125-135), then for a q or
+// k head norm_head (model.rs:753-763) and Rope::apply (ops.rs:155-166), and for k and v the
+// append of row pos to the caches.  Workgroup hh: q head hh (hh < n_heads), k head
+// hh - n_heads, or v head hh - n_heads - n_kv (the rows of W are q | k | v, so rows
+// hh*HD .. hh*HD + HD - 1).  Every workgroup forms the norm of the whole x itself, in the
+// reference's order; a separate chain wave (HD <= 64) runs it while the row waves fetch their
+// weights.  Writes q, k (normed and rotated) and v into out (the q | k | v layout).
+template <int HD> struct QkvCfg {
+    static constexpr int CW = HD <= 64 ? 64 : 0;   // threads of the chain wave
+    static constexpr int NT = CW + 8 * HD;         // + 8 lanes per row
+};
+template <bool EXACT, int ORDER, bool SCF32, int NCT, int HD>
+__global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const float *__restrict__ x,
+                                                            const float *__restrict__ w, float eps,
+                                                            const float *__restrict__ qn, const float *__restrict__ kn,
+                                                            const float *__restrict__ cs, const float *__restrict__ sn,
+                                                            const StepParams *p, uint32_t n_heads, uint32_t n_kv,
+                                                            float *kc, float *vc, uint32_t cap, float *out) {
+    constexpr int CW = QkvCfg<HD>::CW, NT = QkvCfg<HD>::NT;
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint8_t *sq = smem;
+    float *sd = reinterpret_cast<float *>(smem + W.nc * CHUNK_BYTES);
+    float *ps = sd + W.nc * 4;   // the d squares
+    __shared__ __align__(16) float hv[HD], ho[HD], tmp[HD];
+    __shared__ float red[NT / 64];
+    __shared__ float s_ss;
+    const int tid = threadIdx.x, lane = tid & 63, j = tid & 7;
+    const bool rowt = tid >= CW;
+    const uint32_t hh = blockIdx.x, d = W.K, ng = d / 4;
+    const uint32_t kind = hh < n_heads ? 0u : (hh < n_heads + n_kv ? 1u : 2u);   // q, k, v
+    // x and the gain first, alone in the memory pipeline (the chain waits for them)
+    constexpr uint32_t RQ = (1024 / 4 + NT - 1) / NT;
+    v4f xv[RQ], wv[RQ];
+#pragma unroll
+    for (uint32_t u = 0; u < RQ; ++u) {
+        const uint32_t g = min(tid + NT * u, ng - 1);
+        xv[u] = reinterpret_cast<const v4f *>(x)[g];
+        wv[u] = reinterpret_cast<const v4f *>(w)[g];
+    }
+    const uint32_t pos = p->pos;
+    HeadConst<HD> hc;   // gains and RoPE row, used by wave 0 at the end
+    if (tid < 64) hc.load(qn, kn, cs, sn, pos, lane);
+    const uint32_t row = hh * HD + (rowt ? (uint32_t)(tid - CW) >> 3 : 0u);
+    Q8Row<ORDER, SCF32, NCT> rd;
+    float ss = 0.0f;
+    auto squares = [&](const v4f a, uint32_t g) {
+        if (EXACT) {
+            reinterpret_cast<v4f *>(ps)[g] = a * a;
+        } else {
+            ss += a.x * a.x;
+            ss += a.y * a.y;
+            ss += a.z * a.z;
+            ss += a.w * a.w;
+        }
+    };
+#pragma unroll
+    for (uint32_t u = 0; u < RQ; ++u)
+        if (tid + NT * u < ng) squares(xv[u], tid + NT * u);
+    for (uint32_t g = tid + NT * RQ; g < ng; g += NT) squares(reinterpret_cast<const v4f *>(x)[g], g);
+    if (EXACT) {
+        __syncthreads();
+        // the row waves issue their weights now (arriving during the chain)
+        if (rowt) rd.begin(row_qs(W, row), row_sc<SCF32>(W, row), W.nb, W.nc, j);
+        __builtin_amdgcn_sched_barrier(0);
+        if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
+    } else {
+        if (rowt) rd.begin(row_qs(W, row), row_sc<SCF32>(W, row), W.nb, W.nc, j);
+        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+        if (lane == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        if (tid == 0) {
+            float t = 0.0f;
+            for (int i = 0; i < NT / 64; ++i) t += red[i];
+            s_ss = t;
+        }
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf(s_ss / (float)d + eps);
+    auto emit = [&](const v4f a, const v4f gw, uint32_t g, bool store) {
+        const float v[4] = {a.x * scale * gw.x, a.y * scale * gw.y, a.z * scale * gw.z, a.w * scale * gw.w};
+        quant_block_lane(v, j, g / 8, sq, sd, store);
+    };
+#pragma unroll
+    for (uint32_t u = 0; u < RQ; ++u) {   // a block's 8 groups are all < ng or all >= ng
+        const uint32_t g = tid + NT * u;
+        emit(xv[u], wv[u], min(g, ng - 1), g < ng);
+    }
+    for (uint32_t g = tid + NT * RQ; g < ng; g += NT)
+        emit(reinterpret_cast<const v4f *>(x)[g], reinterpret_cast<const v4f *>(w)[g], g, true);
+    zero_pad(W.nb, W.nc, sq, sd, tid, NT);
+    __syncthreads();
+    if (rowt) {
+        const float v = rd.finish(sq, sd);
+        if (j == 0) hv[(tid - CW) >> 3] = v;
+    }
+    __syncthreads();
+    if (tid >= 64) return;
+    float *dst = out + (size_t)hh * HD;   // q | k | v regions are contiguous in head order
+    if (kind == 2) {
+        const uint32_t g = hh - n_heads - n_kv;
+        float *vcr = vc + ((size_t)g * cap + pos) * HD;
+        for (uint32_t i = lane; i < HD; i += 64) {
+            dst[i] = hv[i];
+            vcr[i] = hv[i];
+        }
+        return;
+    }
+    norm_rope_head<HD>(hv, ho, hc, kind == 0, eps, tmp, lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (uint32_t i = lane; i < HD; i += 64) dst[i] = ho[i];
+    if (kind == 1) {
+        float *kcr = kc + ((size_t)(hh - n_heads) * cap + pos) * HD;
+        for (uint32_t i = lane; i < HD; i += 64) kcr[i] = ho[i];
+    }
+}
+
+// QK-norm + RoPE of q and k and the cache append of k and v for a q | k | v vector as the QKV
+// matvec produced it (the same steps as k_qkv_head's end, for callers that hold the raw
+// vector): workgroup hh as in k_qkv_head, 64 threads; qkv is rewritten in place.
+template <int HD>
+__global__ __launch_bounds__(64) void k_qk_rope_append(float *qkv, const float *__restrict__ qn,
+                                                       const float *__restrict__ kn, float eps,
+                                                       const float *__restrict__ cs, const float *__restrict__ sn,
+                                                       const StepParams *p, uint32_t n_heads, uint32_t n_kv, float *kc,
+                                                       float *vc, uint32_t cap) {
+    __shared__ __align__(16) float u[HD], o[HD], tmp[HD];
+    const int lane = threadIdx.x;
+    const uint32_t hh = blockIdx.x, pos = p->pos;
+    float *src = qkv + (size_t)hh * HD;
+    HeadConst<HD> hc;
+    hc.load(qn, kn, cs, sn, pos, lane);
+    for (uint32_t i = lane; i < HD; i += 64) u[i] = src[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (hh >= n_heads + n_kv) {
+        float *vcr = vc + ((size_t)(hh - n_heads - n_kv) * cap + pos) * HD;
+        for (uint32_t i = lane; i < HD; i += 64) vcr[i] = u[i];
+        return;
+    }
+    norm_rope_head<HD>(u, o, hc, hh < n_heads, eps, tmp, lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (uint32_t i = lane; i < HD; i += 64) src[i] = o[i];
+    if (hh >= n_heads) {
+        float *kcr = kc + ((size_t)(hh - n_heads) * cap + pos) * HD;
+        for (uint32_t i = lane; i < HD; i += 64) kcr[i] = o[i];
+    }
+}
+
 // ------------------------------------------------------------------ attention (fast)
 // Longest split of a cache of `cap` positions cut in S parts, rounded to whole float4s.
 __host__ __device__ inline uint32_t attn_maxchunk(uint32_t cap, uint32_t S) { return div_up(div_up(cap, S), 4) * 4; }
 
 // Decode attention of model.rs:212-233, split over the context (flash-decoding): workgroup
 // (g, s) handles kv head g and positions [t0, t1) of split s for the rep = n_heads/n_kv query
-// heads of the group, and writes an unnormalised partial (max, sum, o[hd]) per head.  Every
-// workgroup redoes the QK-norm + RoPE of its q heads and of k (reference order, exact);
-// the split holding `pos` appends k and v to the cache (model.rs:210-211).  Softmax and
-// P.V are reduced as trees across lanes and splits.
+// heads of the group, and writes an unnormalised partial (max, sum, o[hd]) per head.  q and k
+// arrive normed and rotated, and k, v already appended (model.rs:197-211), from the QKV step.
+// Softmax and P.V are reduced as trees across lanes and splits.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_fast(const float *__restrict__ qkv, const float *__restrict__ qn,
                                                    const float *__restrict__ kn, float eps,
@@ -749,32 +822,23 @@ __global__ __launch_bounds__(256) void k_attn_fast(const float *__restrict__ qkv
     const uint32_t chunk = div_up(n, S);
     const uint32_t t0 = s * chunk, t1 = min(n, t0 + chunk);
     const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
-    float *raw = sm;                         // (rep+2)*HD : q heads, k, v as produced
-    float *rot = raw + (rep + 2) * HD;       // (rep+1)*HD : normalised + rotated q heads, k
-    float *tmp = rot + (rep + 1) * HD;       // 4*HD scratch (one per wave)
+    float *raw = sm;                         // (rep+2)*HD : q heads, k, v of this step
+    float *rot = raw + (rep + 2) * HD;       // (rep+1)*HD : (unused)
+    float *tmp = rot + (rep + 1) * HD;       // 4*HD : (unused)
     float *sc = tmp + 4 * HD;                // rep * chunk scores
     const uint32_t maxchunk = attn_maxchunk(cap, S);
     float *red = sc + rep * maxchunk;        // TOK * rep * HD partial P.V sums
     float *stat = red + TOK * rep * HD;      // 2*rep (max, sum)
+    // q and k are normed and rotated, and k, v appended to the caches, by the QKV step
     GroupRaw<HD, MAXREP> gr;
     gr.load(qkv, g, rep, qd, kvd, tid);
-    HeadConst<HD> hc;
-    hc.load(qn, kn, cs, sn, pos, lane);
     gr.store(raw, rep, tid);
     __syncthreads();
-    for (uint32_t vi = wave; vi <= rep; vi += 4)
-        norm_rope_head<HD>(raw + vi * HD, rot + vi * HD, hc, vi < rep, eps, tmp + wave * HD, lane);
-    __syncthreads();
-    const float *krot = rot + rep * HD;
+    const float *qrot = raw;
+    const float *krot = raw + rep * HD;
     const float *vnew = raw + (rep + 1) * HD;
-    float *kcg = kc + (size_t)g * cap * HD;
-    float *vcg = vc + (size_t)g * cap * HD;
-    if (t0 <= pos && pos < t1) {
-        for (uint32_t i = tid; i < HD; i += 256) {
-            kcg[(size_t)pos * HD + i] = krot[i];
-            vcg[(size_t)pos * HD + i] = vnew[i];
-        }
-    }
+    const float *kcg = kc + (size_t)g * cap * HD;
+    const float *vcg = vc + (size_t)g * cap * HD;
     float *pout = part + (size_t)(g * rep) * S * (HD + 2);
     if (t0 >= t1) {
         for (uint32_t r = 0; r < rep; ++r) {
@@ -795,7 +859,7 @@ __global__ __launch_bounds__(256) void k_attn_fast(const float *__restrict__ qkv
 #pragma unroll
         for (int r = 0; r < MAXREP; ++r) {
             if (r < (int)rep) {
-                const float4 q4 = *reinterpret_cast<const float4 *>(rot + r * HD + tl * 4);
+                const float4 q4 = *reinterpret_cast<const float4 *>(qrot + r * HD + tl * 4);
                 acc[r] = q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
             }
         }
@@ -945,74 +1009,63 @@ __device__ inline float dot_wide_serial(const float *a, const float *b, uint32_t
     return s;
 }
 
-// Scores s[h][t] = dot(q_h, K_t) * (1/sqrt(hd)) for the rep query heads of kv head g over
-// split s of the context (grid n_kv x S), the QK-norm + RoPE of q and k, the cache append by
-// the split holding pos, and the split maximum of every head.
+// Scores s[h][t] = dot(q_h, K_t) * (1/sqrt(hd)) (model.rs:213-218, ops::dot's order) for the
+// rep query heads of kv head g over split s of the cache (grid n_kv x S; split s covers
+// positions [s c, s c + c) with c = ceil(cap / S), a layout independent of the step, so the K
+// rows are fetched before the step's position is known), and the split maximum of every head.
+// q (normed, rotated) comes from the QKV step's output, K (with this step's row appended) from
+// the cache.  Wave w handles heads w, w + 4, ...; lane l the positions l, l + 64, ... of the split.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ qkv, const float *__restrict__ qn,
-                                                     const float *__restrict__ kn, float eps,
-                                                     const float *__restrict__ cs, const float *__restrict__ sn,
-                                                     const StepParams *p, float *kc, float *vc, uint32_t cap,
-                                                     uint32_t n_heads, uint32_t n_kv, uint32_t S, float *scores,
-                                                     float *pmax) {
+__global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ qkv, const StepParams *p,
+                                                     const float *__restrict__ kc, uint32_t cap, uint32_t n_heads,
+                                                     uint32_t n_kv, uint32_t S, float *scores, float *pmax) {
     constexpr int MAXREP = 8;
-    __shared__ __align__(16) float raw[(MAXREP + 2) * HD];
-    __shared__ __align__(16) float rot[(MAXREP + 1) * HD];
-    __shared__ float tmp[4 * HD];
-    __shared__ float red[4][MAXREP];
+    __shared__ __align__(16) float qs[MAXREP * HD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t g = blockIdx.x, s = blockIdx.y;
     const uint32_t rep = n_heads / n_kv;
-    const uint32_t pos = p->pos, n = pos + 1;
-    const uint32_t chunk = div_up(n, S);
-    const uint32_t t0 = s * chunk, t1 = min(n, t0 + chunk);
-    const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
-    float *kcg = kc + (size_t)g * cap * HD;
-    float *vcg = vc + (size_t)g * cap * HD;
-    // loads in issue order: the group's q, k, v, the norm gains and RoPE row, then this
-    // thread's K row (one position per thread; a split holds at most 256), so the waits for
-    // the first ones leave the K row in flight.  Rows >= n are clamped (not used).
-    GroupRaw<HD, MAXREP> gr;
-    gr.load(qkv, g, rep, qd, kvd, tid);
-    HeadConst<HD> hc;
-    hc.load(qn, kn, cs, sn, pos, lane);
-    const uint32_t t = t0 + tid;
-    const bool mine = t < t1;
+    const uint32_t chunk = div_up(cap, S), t0 = s * chunk, t1 = min(cap, t0 + chunk);
+    const float *kcg = kc + (size_t)g * cap * HD;
+    // loads in issue order: the group's q heads, this lane's first K row, the position
+    for (uint32_t i = tid; i < rep * HD; i += 256) qs[i] = qkv[(size_t)g * rep * HD + i];
     float kt[HD];
     {
-        const uint32_t tr = min(t, n - 1);
+        const uint32_t tr = min(t0 + (uint32_t)lane, cap - 1);
 #pragma unroll
         for (int i = 0; i < HD; i += 4)
             *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kcg + (size_t)tr * HD + i);
     }
-    gr.store(raw, rep, tid);
+    const uint32_t n = p->pos + 1;
     __syncthreads();
-    for (uint32_t vi = wave; vi <= rep; vi += 4)
-        norm_rope_head<HD>(raw + vi * HD, rot + vi * HD, hc, vi < rep, eps, tmp + wave * HD, lane);
-    __syncthreads();
-    const float *krot = rot + rep * HD;
-    if (t0 <= pos && pos < t1)
-        for (uint32_t i = tid; i < HD; i += 256) {
-            kcg[(size_t)pos * HD + i] = krot[i];
-            vcg[(size_t)pos * HD + i] = raw[(rep + 1) * HD + i];
-        }
-    if (mine && t == pos)
-#pragma unroll
-        for (int i = 0; i < HD; ++i) kt[i] = krot[i];
     const float scale = 1.0f / sqrtf((float)HD);
-#pragma unroll 1
-    for (uint32_t r = 0; r < rep; ++r) {
-        float v = -__builtin_huge_valf();
-        if (mine) {
-            v = dot_wide_serial(rot + r * HD, kt, HD) * scale;
-            scores[(size_t)(g * rep + r) * cap + t] = v;
+    float mx[MAXREP / 4];
+#pragma unroll
+    for (int k = 0; k < MAXREP / 4; ++k) mx[k] = -__builtin_huge_valf();
+    for (uint32_t tb = t0; tb < t1; tb += 64) {
+        const uint32_t t = tb + lane;
+        if (tb != t0) {   // splits longer than 64 positions: the next K row
+            const uint32_t tr = min(t, cap - 1);
+#pragma unroll
+            for (int i = 0; i < HD; i += 4)
+                *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kcg + (size_t)tr * HD + i);
         }
-        for (int k = 32; k >= 1; k >>= 1) v = fmaxf(v, shfl_xor(v, k));
-        if (lane == 0) red[wave][r] = v;
+#pragma unroll
+        for (int k = 0; k < MAXREP / 4; ++k) {
+            const uint32_t r = wave + 4 * k;
+            if (r < rep && t < t1 && t < n) {
+                const float v = dot_wide_serial(qs + r * HD, kt, HD) * scale;
+                scores[(size_t)(g * rep + r) * cap + t] = v;
+                mx[k] = fmaxf(mx[k], v);
+            }
+        }
     }
-    __syncthreads();
-    if ((uint32_t)tid < rep)
-        pmax[(size_t)(g * rep + tid) * S + s] = fmaxf(fmaxf(red[0][tid], red[1][tid]), fmaxf(red[2][tid], red[3][tid]));
+#pragma unroll
+    for (int k = 0; k < MAXREP / 4; ++k) {
+        const uint32_t r = wave + 4 * k;
+        float m = mx[k];
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, shfl_xor(m, o));
+        if (r < rep && lane == 0) pmax[(size_t)(g * rep + r) * S + s] = m;
+    }
 }
 
 // Softmax and P.V of one query head (ops.rs:112-128, model.rs:227-232):
@@ -1739,11 +1792,12 @@ __global__ __launch_bounds__(64) void k_ffn_gateup(Q8Mat Wg, Q8Mat Wu, Q8Mat Sg,
     ru.begin(row_qs(U, r), row_sc<SCF32>(U, r), U.nb, U.nc, j);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (uint32_t u = 0; u < 2; ++u)
-        if (u * 64 + (uint32_t)tid < nc * 8) reinterpret_cast<v4i *>(sq)[u * 64 + tid] = qv[u];
+    for (uint32_t u = 0; u < 2; ++u)   // (clamped slots rewrite the value they already hold)
+        reinterpret_cast<v4i *>(sq)[min(u * 64 + (uint32_t)tid, nc * 8 - 1)] = qv[u];
     for (uint32_t q = 128 + (uint32_t)tid; q < nc * 8; q += 64)
         reinterpret_cast<v4i *>(sq)[q] = reinterpret_cast<const v4i *>(gq)[q];
-    for (uint32_t q = (uint32_t)tid; q < nc * 4; q += 64) sd[q] = q == (uint32_t)tid ? dv : gd[q];
+    sd[min((uint32_t)tid, nc * 4 - 1)] = dv;
+    for (uint32_t q = (uint32_t)tid + 64; q < nc * 4; q += 64) sd[q] = gd[q];
     __syncthreads();
     const float g = rg.finish(sq, sd);
     const float u = ru.finish(sq, sd);
@@ -1795,10 +1849,8 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
 #pragma unroll
     for (uint32_t u = 0; u < AB; ++u) {   // a block's 8 lanes are all in or all out
         const uint32_t b = u * 8 + (lane >> 3);
-        if (b < nb) {
-            const float v[4] = {av[u].x, av[u].y, av[u].z, av[u].w};
-            quant_block_lane(v, j, b, sq, sd);
-        }
+        const float v[4] = {av[u].x, av[u].y, av[u].z, av[u].w};
+        quant_block_lane(v, j, min(b, nb - 1), sq, sd, b < nb);
     }
     for (uint32_t b0 = AB * 8; b0 < nb; b0 += 8) {
         const uint32_t b = b0 + (lane >> 3);
@@ -1938,30 +1990,61 @@ void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uin
 #undef MV
 }
 
-void launch_norm_matvec(hipStream_t st, bool exact, int order, const Q8Mat &W, const float *x, const float *w,
-                        float eps, float *y, uint32_t threads) {
-    const dim3 grid(matvec_blocks(W.N, threads)), block(threads);
+bool launch_qkv_head(hipStream_t st, bool exact, int order, uint32_t hd, const Q8Mat &W, const float *x,
+                     const float *w, float eps, const float *qn, const float *kn, const float *cs, const float *sn,
+                     const StepParams *p, uint32_t n_heads, uint32_t n_kv, float *kc, float *vc, uint32_t cap,
+                     float *out) {
+    const dim3 grid(n_heads + 2 * n_kv);
     const size_t shm = (size_t)W.nc * CHUNK_BYTES + (size_t)W.nc * 4 * sizeof(float) + (size_t)W.K * sizeof(float);
-#define NMV(E, O, S, N) LAUNCH((k_norm_matvec<E, O, S, N>), grid, block, shm, st, W, x, w, eps, y)
-#define NMV_S(E, O, N)                  \
-    do {                                \
-        if (W.sc_f32) NMV(E, O, true, N);  \
-        else NMV(E, O, false, N);          \
+#define QKH(E, O, S, N, HD)                                                                                     \
+    LAUNCH((k_qkv_head<E, O, S, N, HD>), grid, dim3(QkvCfg<HD>::NT), shm, st, W, x, w, eps, qn, kn, cs, sn, p, \
+           n_heads, n_kv, kc, vc, cap, out)
+#define QKH_S(E, O, N, HD)                  \
+    do {                                    \
+        if (W.sc_f32) QKH(E, O, true, N, HD);  \
+        else QKH(E, O, false, N, HD);          \
     } while (0)
-#define NMV_E(N)                                                                     \
-    do {                                                                             \
-        if (order == ORDER_DECODE) {                                                 \
-            if (exact) NMV_S(true, ORDER_DECODE, N);                                 \
-            else NMV_S(false, ORDER_DECODE, N);                                      \
-        } else {                                                                     \
-            if (exact) NMV_S(true, ORDER_PREFILL, N);                                \
-            else NMV_S(false, ORDER_PREFILL, N);                                     \
-        }                                                                            \
+#define QKH_O(N, HD)                                      \
+    do {                                                  \
+        if (order == ORDER_DECODE) {                      \
+            if (exact) QKH_S(true, ORDER_DECODE, N, HD);  \
+            else QKH_S(false, ORDER_DECODE, N, HD);       \
+        } else {                                          \
+            if (exact) QKH_S(true, ORDER_PREFILL, N, HD); \
+            else QKH_S(false, ORDER_PREFILL, N, HD);      \
+        }                                                 \
     } while (0)
-    DISPATCH_NCT(W.nc, NMV_E)
-#undef NMV_E
-#undef NMV_S
-#undef NMV
+#define QKH_N(HD)                    \
+    switch (nct_of(W.nc)) {          \
+    case 8: QKH_O(8, HD); break;     \
+    case 4: QKH_O(4, HD); break;     \
+    case 2: QKH_O(2, HD); break;     \
+    default: QKH_O(1, HD); break;    \
+    }
+    switch (hd) {
+    case 32: QKH_N(32); break;
+    case 64: QKH_N(64); break;
+    case 128: QKH_N(128); break;
+    default: return false;
+    }
+#undef QKH_N
+#undef QKH_O
+#undef QKH_S
+#undef QKH
+    return true;
+}
+
+bool launch_qk_rope_append(hipStream_t st, uint32_t hd, float *qkv, const float *qn, const float *kn, float eps,
+                           const float *cs, const float *sn, const StepParams *p, uint32_t n_heads, uint32_t n_kv,
+                           float *kc, float *vc, uint32_t cap) {
+    const dim3 grid(n_heads + 2 * n_kv);
+    switch (hd) {
+    case 32: LAUNCH(k_qk_rope_append<32>, grid, dim3(64), 0, st, qkv, qn, kn, eps, cs, sn, p, n_heads, n_kv, kc, vc, cap); break;
+    case 64: LAUNCH(k_qk_rope_append<64>, grid, dim3(64), 0, st, qkv, qn, kn, eps, cs, sn, p, n_heads, n_kv, kc, vc, cap); break;
+    case 128: LAUNCH(k_qk_rope_append<128>, grid, dim3(64), 0, st, qkv, qn, kn, eps, cs, sn, p, n_heads, n_kv, kc, vc, cap); break;
+    default: return false;
+    }
+    return true;
 }
 
 void launch_matvec_gather(hipStream_t st, const Q8Mat &W, uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids,
@@ -1996,8 +2079,8 @@ static void attn_exact_launch(hipStream_t st, int which, const float *qkv, const
                               float *scratch, float *o_out, uint8_t *q_out, float *d_out) {
     const bool fuse_quant = q_out == nullptr;  // the consumer quantizes o itself
     if (which == 0) {
-        LAUNCH(k_attn_scores<HD>, dim3(n_kv, S), dim3(256), 0, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
-               n_kv, S, scratch, part);
+        LAUNCH(k_attn_scores<HD>, dim3(n_kv, S), dim3(256), 0, st, qkv, p, kc, cap, n_heads, n_kv, S, scratch,
+               part);
         return;
     }
     if (pv_res_fits(cap)) {
