@@ -1014,58 +1014,57 @@ __device__ inline float dot_wide_serial(const float *a, const float *b, uint32_t
 // positions [s c, s c + c) with c = ceil(cap / S), a layout independent of the step, so the K
 // rows are fetched before the step's position is known), and the split maximum of every head.
 // q (normed, rotated) comes from the QKV step's output, K (with this step's row appended) from
-// the cache.  Wave w handles heads w, w + 4, ...; lane l the positions l, l + 64, ... of the split.
+// the cache.  Lane l of the workgroup's 256 threads takes head l % R and position
+// t0 + l / R (+ 256 / R, ...), R = rep rounded up to a power of two: the R lanes of a position
+// read the same K row (one memory request per row).
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ qkv, const StepParams *p,
                                                      const float *__restrict__ kc, uint32_t cap, uint32_t n_heads,
                                                      uint32_t n_kv, uint32_t S, float *scores, float *pmax) {
     constexpr int MAXREP = 8;
     __shared__ __align__(16) float qs[MAXREP * HD];
+    __shared__ float wm[4][MAXREP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t g = blockIdx.x, s = blockIdx.y;
     const uint32_t rep = n_heads / n_kv;
+    const uint32_t R = rep <= 1 ? 1u : rep <= 2 ? 2u : rep <= 4 ? 4u : 8u;   // lanes per position
+    const uint32_t r = (uint32_t)tid % R, pp = 256 / R;                      // head, positions per pass
     const uint32_t chunk = div_up(cap, S), t0 = s * chunk, t1 = min(cap, t0 + chunk);
     const float *kcg = kc + (size_t)g * cap * HD;
-    // loads in issue order: the group's q heads, this lane's first K row, the position
-    for (uint32_t i = tid; i < rep * HD; i += 256) qs[i] = qkv[(size_t)g * rep * HD + i];
+    // loads in issue order: this lane's first K row, the group's q heads, the position
     float kt[HD];
     {
-        const uint32_t tr = min(t0 + (uint32_t)lane, cap - 1);
+        const uint32_t tr = min(t0 + (uint32_t)tid / R, cap - 1);
 #pragma unroll
         for (int i = 0; i < HD; i += 4)
             *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kcg + (size_t)tr * HD + i);
     }
+    for (uint32_t i = tid; i < rep * HD; i += 256) qs[i] = qkv[(size_t)g * rep * HD + i];
     const uint32_t n = p->pos + 1;
     __syncthreads();
     const float scale = 1.0f / sqrtf((float)HD);
-    float mx[MAXREP / 4];
-#pragma unroll
-    for (int k = 0; k < MAXREP / 4; ++k) mx[k] = -__builtin_huge_valf();
-    for (uint32_t tb = t0; tb < t1; tb += 64) {
-        const uint32_t t = tb + lane;
-        if (tb != t0) {   // splits longer than 64 positions: the next K row
+    float mx = -__builtin_huge_valf();
+    const float *qr = qs + min(r, rep - 1) * HD;
+    for (uint32_t tb = t0; tb < t1; tb += pp) {
+        const uint32_t t = tb + (uint32_t)tid / R;
+        if (tb != t0) {   // splits longer than 256 / R positions: the next K row
             const uint32_t tr = min(t, cap - 1);
 #pragma unroll
             for (int i = 0; i < HD; i += 4)
                 *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kcg + (size_t)tr * HD + i);
         }
-#pragma unroll
-        for (int k = 0; k < MAXREP / 4; ++k) {
-            const uint32_t r = wave + 4 * k;
-            if (r < rep && t < t1 && t < n) {
-                const float v = dot_wide_serial(qs + r * HD, kt, HD) * scale;
-                scores[(size_t)(g * rep + r) * cap + t] = v;
-                mx[k] = fmaxf(mx[k], v);
-            }
+        if (r < rep && t < t1 && t < n) {
+            const float v = dot_wide_serial(qr, kt, HD) * scale;
+            scores[(size_t)(g * rep + r) * cap + t] = v;
+            mx = fmaxf(mx, v);
         }
     }
-#pragma unroll
-    for (int k = 0; k < MAXREP / 4; ++k) {
-        const uint32_t r = wave + 4 * k;
-        float m = mx[k];
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, shfl_xor(m, o));
-        if (r < rep && lane == 0) pmax[(size_t)(g * rep + r) * S + s] = m;
-    }
+    // split maximum of each head: over the lanes of equal r (xor of the position bits), then waves
+    for (uint32_t o = R; o < 64; o <<= 1) mx = fmaxf(mx, shfl_xor(mx, (int)o));
+    if ((uint32_t)lane < R) wm[wave][lane] = mx;
+    __syncthreads();
+    if ((uint32_t)tid < rep)
+        pmax[(size_t)(g * rep + tid) * S + s] = fmaxf(fmaxf(wm[0][tid], wm[1][tid]), fmaxf(wm[2][tid], wm[3][tid]));
 }
 
 // Softmax and P.V of one query head (ops.rs:112-128, model.rs:227-232):
