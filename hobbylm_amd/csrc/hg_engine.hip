@@ -386,8 +386,18 @@ void enqueue_layers(hg_kv *kv, int order) {
                           x, 64, 0, nullptr, nullptr);
         else
             launch_matvec(st, order, EPI_RESID, L.o.m, qa, da, x, 64, 0, nullptr, nullptr);
-        if (L.moe) {
-            mark(kv, P_ROUTER);
+        if (L.moe) mark(kv, P_ROUTER);   // ffn_norm + router (+ gate/up when fused)
+        if (L.moe && launch_ffn_front(st, kv->exact, order, x, L.ffn_norm.as<float>(), c.rms_eps, d,
+                                      L.router_p.as<float>(), L.bias.as<float>(), c.n_experts, c.top_k,
+                                      c.gating_sigmoid, c.expert_weights_norm, c.expert_weights_scale, L.gate_e.m,
+                                      L.up_e.m, L.gate_sh.m, L.up_sh.m, m->n_slots, c.expert_ffn,
+                                      kv->topk_idx.as<uint32_t>(), kv->topk_w.as<float>(), kv->order.as<uint32_t>(),
+                                      kv->rec_idx.as<uint32_t>() + (size_t)l * c.top_k,
+                                      kv->rec_w.as<float>() + (size_t)l * c.top_k, kv->a.as<float>())) {
+            mark(kv, P_DOWN);
+            launch_ffn_down(st, order, L.down_e.m, L.down_sh.m, kv->topk_idx.as<uint32_t>(), kv->topk_w.as<float>(),
+                            kv->order.as<uint32_t>(), c.top_k, m->n_slots, 0, d, c.expert_ffn, kv->a.as<float>(), x);
+        } else if (L.moe) {
             launch_ffn_router(st, kv->exact, x, L.ffn_norm.as<float>(), c.rms_eps, d, L.router.as<float>(),
                               L.router_p.as<float>(), L.bias.as<float>(), c.n_experts, c.top_k, c.gating_sigmoid, c.expert_weights_norm,
                               c.expert_weights_scale, qa, da, kv->topk_idx.as<uint32_t>(), kv->topk_w.as<float>(),

@@ -64,6 +64,14 @@ void launch_ffn_router(hipStream_t st, bool exact, const float *x, const float *
                        const float *Wr, const float *Wp, const float *bias, uint32_t E, uint32_t top_k,
                        int gating_sigmoid, int weights_norm, float weights_scale, uint8_t *q, float *dq,
                        uint32_t *topk_idx, float *topk_w, uint32_t *order, uint32_t *rec_idx, float *rec_w);
+// ffn_norm + router + gate/up of every slot in one launch (E == 0: the dense FFN, slot 0);
+// false when the shapes are outside what it handles (the caller then uses the router and
+// gate/up launches).
+bool launch_ffn_front(hipStream_t st, bool exact, int order, const float *x, const float *w, float eps, uint32_t d,
+                      const float *Wp, const float *bias, uint32_t E, uint32_t top_k, int gating_sigmoid,
+                      int weights_norm, float weights_scale, const Q8Mat &Wg, const Q8Mat &Wu, const Q8Mat &Sg,
+                      const Q8Mat &Su, uint32_t n_slots, uint32_t f, uint32_t *topk_idx, float *topk_w,
+                      uint32_t *ord, uint32_t *rec_idx, float *rec_w, float *a);
 void launch_ffn_gateup(hipStream_t st, int order, const Q8Mat &Wg, const Q8Mat &Wu, const Q8Mat &Sg,
                        const Q8Mat &Su, const uint32_t *topk_idx, uint32_t top_k, uint32_t n_slots, uint32_t f,
                        const uint8_t *q, const float *dq, float *a);

@@ -1306,7 +1306,8 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     using C = PvResCfg;
     constexpr uint32_t D = C::D, G = C::G, EB = 8;
     extern __shared__ __align__(16) float lds[];
-    __shared__ uint64_t ready;   // bit gi: product group gi written
+    __shared__ uint64_t ready;           // bit gi: product group gi written
+    __shared__ uint32_t gcount[64];      // products of group gi written so far (of 4 G)
     __shared__ float s_inv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t h, q;
@@ -1342,58 +1343,58 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
             }
     }
     if (tid == 0) ready = 0;
+    if (tid < 64) gcount[tid] = 0;
     __syncthreads();
+    // V items j = vt + 448 r of thread vt = tid - 64 of waves 1..7 (position j / 4, elements
+    // 4 (j % 4) .. + 3), fetched into registers while lane 0 sums (no LDS traffic beside the
+    // chain's reads), turned into the rounded products p_t v_t[di] once inv is known and written
+    // transposed, P[di][t]; positions n .. npad - 1 get -0, the exact identity of an add.  A wave's
+    // 64 items of a round are consecutive, so they fall in at most two groups of 4 G items; the
+    // write that completes a group sets its ready bit.
+    v4f vv[C::VB];
+    const uint32_t vt = tid - 64;
     if (tid == 0) {
         s_inv = 1.0f / seq_sum_lds(e, n, 0.0f);
     } else if (wave > 0) {
-        // V items j = vt + 448 r of staging thread vt (position j / 4, elements 4 (j % 4) .. +3),
-        // fetched while lane 0 sums (their issue would otherwise hold up the exps)
-        const uint32_t vt = tid - 64;
-        v4f vv[C::VB];
 #pragma unroll
         for (uint32_t r = 0; r < C::VB; ++r) {
             const uint32_t j = min(vt + 448 * r, 4 * n - 1), t = j >> 2, dq = j & 3;
             const float *src = (t == pos) ? vnew + 4 * dq : vcg + (size_t)t * HD + 4 * dq;
             vv[r] = *reinterpret_cast<const v4f *>(src);
         }
-#pragma unroll
-        for (uint32_t r = 0; r < C::VB; ++r) {
-            const uint32_t j = vt + 448 * r;
-            if (j < 4 * n) {
-                const uint32_t t = j >> 2, d0 = 4 * (j & 3);
-                P[(d0 + 0) * TPC + t] = vv[r].x;
-                P[(d0 + 1) * TPC + t] = vv[r].y;
-                P[(d0 + 2) * TPC + t] = vv[r].z;
-                P[(d0 + 3) * TPC + t] = vv[r].w;
-            }
-        }
     }
     __syncthreads();
     const float inv = s_inv;
     if (wave > 0) {
-        // group gi by wave 1 + gi % 7; lane l: positions G gi + 4 (l / 4) .. + 3 of rows
-        // 4 (l % 4) .. + 3
-        static_assert(C::G == 64 && D == 16, "16 position quads x 4 row quads per group");
-        const uint32_t pq = lane >> 2, d0 = 4 * (lane & 3);
-        for (uint32_t gi = wave - 1; gi < ngroups; gi += 7) {
-            const uint32_t t0 = gi * G + 4 * pq;
-            if (t0 < npad) {   // npad is a multiple of 4: the four positions are all in or all out
-                const v4f ev = *reinterpret_cast<const v4f *>(e + t0);
-                const bool in[4] = {t0 < n, t0 + 1 < n, t0 + 2 < n, t0 + 3 < n};
-                const float pt[4] = {in[0] ? ev.x * inv : 0.0f, in[1] ? ev.y * inv : 0.0f,
-                                     in[2] ? ev.z * inv : 0.0f, in[3] ? ev.w * inv : 0.0f};
-                v4f x[4];   // all four rows read before any is written back
+        static_assert(C::G == 64 && D == 16, "a group is 64 positions x 4 element quads");
+        const uint32_t nitems = 4 * npad;
 #pragma unroll
-                for (uint32_t c = 0; c < 4; ++c) x[c] = *reinterpret_cast<const v4f *>(P + (d0 + c) * TPC + t0);
-#pragma unroll
-                for (uint32_t c = 0; c < 4; ++c)
-                    *reinterpret_cast<v4f *>(P + (d0 + c) * TPC + t0) =
-                        v4f{in[0] ? pt[0] * x[c].x : -0.0f, in[1] ? pt[1] * x[c].y : -0.0f,
-                            in[2] ? pt[2] * x[c].z : -0.0f, in[3] ? pt[3] * x[c].w : -0.0f};
+        for (uint32_t r = 0; r < C::VB; ++r) {
+            const uint32_t jw = 448 * r + 64 * (uint32_t)(wave - 1);   // the wave's first item
+            if (jw >= nitems) break;                                    // (uniform)
+            const uint32_t j = jw + (uint32_t)lane;
+            if (j < nitems) {
+                const uint32_t t = j >> 2, d0 = 4 * (j & 3);
+                const bool in = t < n;
+                const float pt = in ? e[t] * inv : 0.0f;
+                P[(d0 + 0) * TPC + t] = in ? pt * vv[r].x : -0.0f;
+                P[(d0 + 1) * TPC + t] = in ? pt * vv[r].y : -0.0f;
+                P[(d0 + 2) * TPC + t] = in ? pt * vv[r].z : -0.0f;
+                P[(d0 + 3) * TPC + t] = in ? pt * vv[r].w : -0.0f;
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane == 0)
-                __hip_atomic_fetch_or(&ready, 1ull << gi, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) {
+                const uint32_t je = min(jw + 64, nitems);   // items [jw, je) written by this wave
+                const uint32_t g0 = jw / (4 * G), g1 = (je - 1) / (4 * G);
+                for (uint32_t gi = g0; gi <= g1; ++gi) {
+                    const uint32_t lo = max(jw, gi * 4 * G), hi = min(je, (gi + 1) * 4 * G);
+                    const uint32_t full = min((gi + 1) * 4 * G, nitems) - gi * 4 * G;
+                    const uint32_t before =
+                        __hip_atomic_fetch_add(&gcount[gi], hi - lo, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    if (before + (hi - lo) == full)
+                        __hip_atomic_fetch_or(&ready, 1ull << gi, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+            }
         }
     } else if (lane < (int)D) {
         // chains: 32 positions (eight 16-byte reads) per chunk, the next chunk's reads issued
@@ -1753,6 +1754,195 @@ __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x
         for (uint32_t q = 0; q < top_k; ++q) rk += tk[q] < ei;
         order[rk] = r;
     }
+}
+
+// ffn_norm RMSNorm, the F32 router and the gate/up rows of one expert slot in one launch (the
+// router of k_ffn_router and the rows of k_ffn_gateup; model.rs:170-172, 270-305, 314-318).
+// Workgroup (bx, slot) owns rows 16 bx .. 16 bx + 15 of the slot's expert: the routed pick
+// `slot` (slot < top_k) or the shared expert; with E == 0 slot 0 is the dense FFN
+// (model.rs:247-251).  Every workgroup forms the norm, the router logits and the ranking itself
+// (the same deterministic arithmetic, so every workgroup picks the same experts) and quantizes h
+// into its LDS, so the expert rows are fetched without a kernel boundary and without a round
+// trip through memory; workgroup (0, 0) also writes the picks for the down projection.
+// Threads: wave 0 runs the chain; threads 64 + 8 e .. 64 + 8 e + 7 own router row e (prefetched
+// during the chain in the 16-byte-step layout of k_ffn_router); waves 0-1 own the 16 rows.  Few
+// rows per workgroup spread the expert rows, which cannot be fetched before the ranking, over
+// many CUs (one CU issues about 64 bytes a clock).
+constexpr uint32_t FF_NT = 512, FF_ROWS = 16;   // gate/up rows per workgroup: waves 0-1
+constexpr uint32_t FF_MAXE = (FF_NT - 64) / 8;   // 56 experts
+template <bool EXACT, int ORDER, bool SCF32, int NCT, int NST>
+__global__ __launch_bounds__(512) void k_ffn_front(const float *__restrict__ x, const float *__restrict__ w, float eps,
+                                                   uint32_t d, const float *__restrict__ Wp,
+                                                   const float *__restrict__ bias, uint32_t E, uint32_t top_k,
+                                                   int weights_norm, float weights_scale, Q8Mat Wg, Q8Mat Wu,
+                                                   Q8Mat Sg, Q8Mat Su, uint32_t f, uint32_t *topk_idx,
+                                                   float *topk_w, uint32_t *order, uint32_t *rec_idx,
+                                                   float *rec_w, float *a_out) {
+    static_assert(NST >= 1 && NST <= 32, "router steps held in registers");
+    extern __shared__ __align__(16) float hs[];   // h, h permuted, squares (3 d), then sq / sd
+    float *hp = hs + d, *ps = hs + 2 * d;
+    uint8_t *sq = reinterpret_cast<uint8_t *>(hs + 3 * d);
+    float *sd = reinterpret_cast<float *>(sq + Wg.nc * CHUNK_BYTES);
+    __shared__ float red[FF_NT / 64];
+    __shared__ float s_ss;
+    __shared__ uint64_t K[64];
+    __shared__ __align__(16) uint32_t tk[64];
+    __shared__ __align__(16) float tw[64];
+    const int tid = threadIdx.x, lane = tid & 63, j = tid & 7;
+    const bool rows = tid >= 64;
+    const uint32_t e8 = rows ? (uint32_t)(tid - 64) >> 3 : 0u, l8 = (uint32_t)tid & 7;
+    const bool router = E > 0;
+    const uint32_t slot = blockIdx.y, row = blockIdx.x * FF_ROWS + ((uint32_t)tid >> 3);
+    const uint32_t lrow = min(row, f - 1);
+    // loads in issue order: x and the norm gain (needed first), the exp table, the bias of this
+    // thread's router row
+    constexpr uint32_t XB = 2;   // d <= 1024 in registers
+    float xv[XB], wv[XB];
+#pragma unroll
+    for (uint32_t u = 0; u < XB; ++u) {
+        const uint32_t i = min(tid + u * FF_NT, d - 1);
+        xv[u] = x[i];
+        wv[u] = w[i];
+    }
+    const WaveExpTab tab = WaveExpTab::load(lane);
+    const float bv8 = router ? bias[min(e8, E - 1)] : 0.0f;
+    v4f wr[NST];
+    auto fetch_rows = [&] {
+        const float *rowp = Wp + (size_t)min(e8, E - 1) * d;
+#pragma unroll
+        for (int i = 0; i < NST; ++i) wr[i] = *reinterpret_cast<const v4f *>(rowp + 32 * i + 4 * l8);
+    };
+    float ss = 0.0f;
+#pragma unroll
+    for (uint32_t u = 0; u < XB; ++u) {
+        const uint32_t i = tid + u * FF_NT;
+        if (i < d) {
+            if (EXACT) ps[i] = xv[u] * xv[u];
+            else ss += xv[u] * xv[u];
+        }
+    }
+    if (EXACT) {
+        __syncthreads();
+        if (router && rows && e8 < E) fetch_rows();   // arrives during the chain
+        if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
+    } else {
+        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
+        if (lane == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        if (router && rows && e8 < E) fetch_rows();
+        if (tid == 0) {
+            float t = 0.0f;
+            for (int i = 0; i < (int)(FF_NT / 64); ++i) t += red[i];
+            s_ss = t;
+        }
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf(s_ss / (float)d + eps);
+#pragma unroll
+    for (uint32_t u = 0; u < XB; ++u) {
+        const uint32_t i = tid + u * FF_NT;
+        if (i < d) {
+            const float v = xv[u] * scale * wv[u];
+            hs[i] = v;
+            hp[router_perm(i)] = v;
+        }
+    }
+    __syncthreads();
+    {   // quantization of h for the expert rows (quant.rs:111-123), into this workgroup's LDS
+        const uint32_t nb = d / QK;
+        for (uint32_t b0 = 0; b0 < nb; b0 += FF_NT / 8) {
+            const uint32_t b = b0 + ((uint32_t)tid >> 3);
+            const v4f hv = *reinterpret_cast<const v4f *>(hs + min(b, nb - 1) * QK + j * 4);
+            const float v[4] = {hv.x, hv.y, hv.z, hv.w};
+            quant_block_lane(v, j, min(b, nb - 1), sq, sd, b < nb);
+        }
+        zero_pad(nb, Wg.nc, sq, sd, tid, FF_NT);
+    }
+    float g = 0.0f;   // the gate of this thread's router row
+    if (router) {
+        if (rows) {   // logits: lane l8 of row e8 runs the ops::dot chains l8 + 8 a (uniform per wave)
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (e8 < E) {
+#pragma unroll
+                for (int i = 0; i < NST; ++i) {
+                    const v4f hv = *reinterpret_cast<const v4f *>(hp + 32 * i + 4 * l8);
+                    a[0] = fmaf(wr[i].x, hv.x, a[0]);
+                    a[1] = fmaf(wr[i].y, hv.y, a[1]);
+                    a[2] = fmaf(wr[i].z, hv.z, a[2]);
+                    a[3] = fmaf(wr[i].w, hv.w, a[3]);
+                }
+            }
+            float v = (a[0] + a[1]) + (a[2] + a[3]);
+            {
+                const float dn = dpp_f<0x124>(v), up = dpp_f<0x12C>(v);
+                v = v + ((l8 & 4) ? dn : up);   // lane ^ 4
+            }
+            v = v + dpp_f<0x4E>(v);   // lane ^ 2
+            v = v + dpp_f<0xB1>(v);   // lane ^ 1
+            g = hg_sigmoid_l(v, tab);
+            const float key = (g + bv8) + 0.0f;   // -0 made +0 (the float compare has -0 == +0)
+            const uint32_t mb = __builtin_bit_cast(uint32_t, key);
+            const uint64_t mk = ((uint64_t)((mb & 0x80000000u) ? ~mb : (mb | 0x80000000u)) << 32) | (uint32_t)~e8;
+            if (l8 == 0 && e8 < E) K[e8] = mk;
+        }
+        __syncthreads();
+        if (rows) {   // rank = #{e' : key_e' > key_e or equal with e' < e}: lane l8 counts e' = l8 + 8 q
+            const float key = (g + bv8) + 0.0f;
+            const uint32_t mb = __builtin_bit_cast(uint32_t, key);
+            const uint64_t mk = ((uint64_t)((mb & 0x80000000u) ? ~mb : (mb | 0x80000000u)) << 32) | (uint32_t)~e8;
+            uint64_t kk[8];
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q) kk[q] = K[min(l8 + 8 * q, E - 1)];
+            uint32_t cnt = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q) cnt += (l8 + 8 * q < E) && (kk[q] > mk);
+            {
+                const uint32_t dn = dpp_u<0x124>(cnt), up = dpp_u<0x12C>(cnt);
+                cnt += (l8 & 4) ? dn : up;
+            }
+            cnt += dpp_u<0x4E>(cnt);
+            cnt += dpp_u<0xB1>(cnt);
+            if (l8 == 0 && e8 < E && cnt < top_k) { tk[cnt] = e8; tw[cnt] = g; }
+        }
+    }
+    __syncthreads();
+    if (tid >= (int)(8 * FF_ROWS)) return;   // the router needed every wave, the rows need two
+    // the slot's rows
+    const bool routed = router && slot < top_k;
+    const Q8Mat &G = routed ? Wg : Sg;
+    const Q8Mat &U = routed ? Wu : Su;
+    const uint32_t r = routed ? tk[slot] * f + lrow : lrow;
+    Q8Row<ORDER, SCF32, NCT> rg, ru;
+    rg.begin(row_qs(G, r), row_sc<SCF32>(G, r), G.nb, G.nc, j);
+    ru.begin(row_qs(U, r), row_sc<SCF32>(U, r), U.nb, U.nc, j);
+    if (router && blockIdx.x == 0 && slot == 0 && tid < 64) {   // the picks for the down projection
+        auto rlf = [](float v, uint32_t l) {
+            return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), (int)l));
+        };
+        auto rlu = [](uint32_t v, uint32_t l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l); };
+        const uint32_t rl = min((uint32_t)lane, top_k - 1);
+        const uint32_t ei = tk[rl];
+        const float twl = tw[rl];
+        float sw = 0.0f;   // every lane forms the same sequential sum (f32 iterator sum + 1e-9)
+        if (weights_norm) {
+            for (uint32_t q = 0; q < top_k; ++q) sw = sw + rlf(twl, q);
+            sw = sw + 1e-9f;
+        }
+        uint32_t rk = 0;   // slot order by ascending expert id (the prompt path's accumulation order)
+        for (uint32_t q = 0; q < top_k; ++q) rk += rlu(ei, q) < ei;
+        if ((uint32_t)lane < top_k) {
+            const float wr_ = (weights_norm ? twl / sw : twl) * weights_scale;
+            topk_idx[lane] = ei;
+            topk_w[lane] = wr_;
+            rec_idx[lane] = ei;
+            rec_w[lane] = wr_;
+            order[rk] = (uint32_t)lane;
+        }
+    }
+    const float gv = rg.finish(sq, sd);
+    const float uv = ru.finish(sq, sd);
+    const float av = hg_silu_l(gv, tab) * uv;   // every lane: the table lookup is a lane exchange
+    if (row < f && j == 0) a_out[(size_t)slot * f + row] = av;
 }
 
 // ------------------------------------------------------------------ experts
@@ -2180,6 +2370,53 @@ void launch_ffn_gateup(hipStream_t st, int order, const Q8Mat &Wg, const Q8Mat &
         if (Wg.sc_f32) gateup_launch<ORDER_PREFILL, true>(st, Wg, Wu, Sg, Su, topk_idx, top_k, n_slots, f, q, dq, a);
         else gateup_launch<ORDER_PREFILL, false>(st, Wg, Wu, Sg, Su, topk_idx, top_k, n_slots, f, q, dq, a);
     }
+}
+
+bool launch_ffn_front(hipStream_t st, bool exact, int order, const float *x, const float *w, float eps, uint32_t d,
+                      const float *Wp, const float *bias, uint32_t E, uint32_t top_k, int gating_sigmoid,
+                      int weights_norm, float weights_scale, const Q8Mat &Wg, const Q8Mat &Wu, const Q8Mat &Sg,
+                      const Q8Mat &Su, uint32_t n_slots, uint32_t f, uint32_t *topk_idx, float *topk_w,
+                      uint32_t *ord, uint32_t *rec_idx, float *rec_w, float *a) {
+    if (d % 32 || d > 1024 || (E && (!gating_sigmoid || E > FF_MAXE || top_k > 64 || top_k > E)) ||
+        Wg.nc != Sg.nc || Wg.sc_f32 != Sg.sc_f32)
+        return false;
+    const dim3 grid(div_up(f, FF_ROWS), E ? n_slots : 1);
+    const size_t shm = 3 * (size_t)d * sizeof(float) + (size_t)Wg.nc * CHUNK_BYTES + (size_t)Wg.nc * 4 * sizeof(float);
+    if (!Wp) Wp = x;      // (not read without a router)
+    if (!bias) bias = x;
+#define FFK(EX, O, S, N, NS)                                                                                      \
+    LAUNCH((k_ffn_front<EX, O, S, N, NS>), grid, dim3(FF_NT), shm, st, x, w, eps, d, Wp, bias, E, top_k,          \
+           weights_norm, weights_scale, Wg, Wu, Sg, Su, f, topk_idx, topk_w, ord, rec_idx, rec_w, a)
+#define FFK_S(EX, O, N, NS)                 \
+    do {                                    \
+        if (Wg.sc_f32) FFK(EX, O, true, N, NS);  \
+        else FFK(EX, O, false, N, NS);           \
+    } while (0)
+#define FFK_O(N, NS)                                      \
+    do {                                                  \
+        if (order == ORDER_DECODE) {                      \
+            if (exact) FFK_S(true, ORDER_DECODE, N, NS);  \
+            else FFK_S(false, ORDER_DECODE, N, NS);       \
+        } else {                                          \
+            if (exact) FFK_S(true, ORDER_PREFILL, N, NS); \
+            else FFK_S(false, ORDER_PREFILL, N, NS);      \
+        }                                                 \
+    } while (0)
+    // one instantiation per model width: the chunk batch and the router steps both follow d
+    if (nct_of(Wg.nc) != nct_of(div_up(d, 128))) return false;
+    switch (d) {
+    case 1024: FFK_O(8, 32); break;
+    case 768: FFK_O(4, 24); break;
+    case 512: FFK_O(4, 16); break;
+    case 256: FFK_O(2, 8); break;
+    case 128: FFK_O(1, 4); break;
+    case 64: FFK_O(1, 2); break;
+    default: return false;
+    }
+#undef FFK_O
+#undef FFK_S
+#undef FFK
+    return true;
 }
 
 template <int ORDER, bool SCF32>

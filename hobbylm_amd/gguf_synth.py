@@ -67,6 +67,12 @@ PRESETS: Dict[str, Shape] = {
     "tiny": Shape(128, 3, 1, 4, 2, 32, 256, 96, 8, 2, 1, 1000, context_length=512),
     "tiny_noshared": Shape(64, 2, 1, 2, 1, 32, 128, 64, 6, 3, 0, 300, context_length=256,
                            rope_theta=1e6),
+    # the other router forms: softmax gating with renormalized weights, and sigmoid gating with
+    # renormalized and scaled weights
+    "tiny_softmax": Shape(128, 2, 1, 4, 2, 32, 256, 96, 8, 2, 1, 1000, context_length=512,
+                          gating_sigmoid=False, expert_weights_norm=True),
+    "tiny_wnorm": Shape(256, 2, 1, 4, 2, 64, 256, 96, 12, 4, 1, 1000, context_length=512,
+                        expert_weights_norm=True, expert_weights_scale=2.5),
 }
 
 
