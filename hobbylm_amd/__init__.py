@@ -69,6 +69,7 @@ SIGNATURES = {
     "hg_generate_greedy": (C.c_int, [_vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32,
                                      _u32p, C.POINTER(C.c_uint32)]),
     "hg_last_routing": (C.c_int, [_vp, _u32p, _f32p]),
+    "hg_seq_sum": (C.c_int, [_f32p, C.c_uint32, C.c_uint32, _f32p]),
     "hg_profile_step": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, _f32p, _u32p]),
     "hg_profile_class": (C.c_char_p, [C.c_uint32]),
     "hg_q8_tensor_quantize": (C.c_int, [_f32p, C.c_uint32, C.c_uint32, C.POINTER(_vp)]),
@@ -318,6 +319,15 @@ class Q8Tensor:
         _check(lib().hg_q8_tensor_matvec_gather(self.h, rows_per_mat, ids, ids.size,
                                                 np.ascontiguousarray(x, np.float32), y.reshape(-1)))
         return y
+
+
+def seq_sum(x, method: int = 1) -> np.float32:
+    """((0 + x[0]) + x[1]) + ... in binary32 on the device (the sums of ops.rs:101-104 and
+    ops.rs:119-122): method 1 = the workgroup method of the decode kernels, 0 = one lane."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(1, np.float32)
+    _check(lib().hg_seq_sum(x, x.size, method, out))
+    return out[0]
 
 
 def attention_time(n_heads: int, n_kv: int, hd: int, ctx: int, reps: int = 50, fast: bool = False):

@@ -1007,6 +1007,19 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
     return HG_OK;
 }
 
+int hg_seq_sum(const float *x, uint32_t n, uint32_t method, float *out) {
+    if ((!x && n) || !out || method > 1) return fail(HG_ERR_ARG, "NULL argument or unknown method");
+    int rc = check_device();
+    if (rc) return rc;
+    DevBuf dx, dout;
+    if ((rc = dx.upload(x, (size_t)n * 4)) || (rc = dout.alloc(4))) return rc;
+    launch_seq_sum(nullptr, dx.as<float>(), n, (int)method, dout.as<float>());
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(out, dout.p, 4, hipMemcpyDeviceToHost));
+    return HG_OK;
+}
+
 int hg_attention_time(uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t ctx, uint32_t reps, uint32_t flags,
                       float *us) {
     if (!us || !reps || !ctx) return fail(HG_ERR_ARG, "NULL argument or zero count");

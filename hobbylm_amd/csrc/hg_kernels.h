@@ -72,6 +72,9 @@ bool launch_ffn_front(hipStream_t st, bool exact, int order, const float *x, con
                       int weights_norm, float weights_scale, const Q8Mat &Wg, const Q8Mat &Wu, const Q8Mat &Sg,
                       const Q8Mat &Su, uint32_t n_slots, uint32_t f, uint32_t *topk_idx, float *topk_w,
                       uint32_t *ord, uint32_t *rec_idx, float *rec_w, float *a);
+// One workgroup forms 0 + x[0] + ... + x[n-1] in binary32 (method 1: the parallel exact
+// method, method 0: one lane).
+void launch_seq_sum(hipStream_t st, const float *x, uint32_t n, int method, float *out);
 void launch_ffn_gateup(hipStream_t st, int order, const Q8Mat &Wg, const Q8Mat &Wu, const Q8Mat &Sg,
                        const Q8Mat &Su, const uint32_t *topk_idx, uint32_t top_k, uint32_t n_slots, uint32_t f,
                        const uint8_t *q, const float *dq, float *a);

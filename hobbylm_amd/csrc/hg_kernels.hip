@@ -272,6 +272,291 @@ __device__ inline float seq_sum_lds(const float *a, uint32_t n, float s) {
     return s;
 }
 
+// ------------------------------------------------------------------ exact parallel sum
+// The same sequential binary32 sum 0 + a[0] + ... + a[n-1] of non-negative terms (the
+// reference's `ss += v * v` of rmsnorm, ops.rs:101-104, and `sum += *v` of softmax,
+// ops.rs:119-122), formed by one wave with identical result bits.
+//
+// Why it can be parallel.  While the running sum s stays in one binade [2^e, 2^(e+1)) (binade
+// -126 also holds zero and the subnormals; the quantum is u = 2^(e-23) in both) it is an
+// integer number of quanta, and an add whose result stays in the binade contributes
+// round(a / u) quanta, independent of s, unless a / u is an exact half (a tie: s's parity
+// decides).  So if the binades of the sums before and after each add were known, all but a
+// few adds (those that change the binade, ties, and adds whose binade is uncertain) would be
+// integer increments that a prefix sum adds exactly; the few "events" stay real float adds.
+//
+// Certification.  Each add errs by at most 2^-24 of its result (results below 2^-125 are
+// exact) and s never decreases, so with T_k = a[0] + ... + a[k-1] (real numbers)
+// |s_k - T_k| <= k 2^-24 (T_k + |s_k - T_k|), i.e. <= 1.001 k 2^-24 T_k for k <= 2^14.  The
+// wave forms every T_k in binary32 as (exclusive scan of the lanes' partial sums) + (lane's
+// running sum): relative error below 48 * 2^-24 for EPT <= 32; a margin R = 2^-16 covers it
+// and the rounding of the bound products.  s_k then lies in [T~_k (1 - R - C k),
+// T~_k (1 + R + C k)] with C = 1.01 2^-24.  A lane whose bracket from its first sum to its
+// last lies in one binade (nearly all lanes) needs nothing per term; a lane whose bracket
+// crosses one boundary 2^b classifies each term by its own bracket; otherwise all its terms
+// are events.
+//
+// Schedule (wave 0 only, no workgroup barrier): lane l holds terms l EPT .. l EPT + EPT - 1;
+// (1) running sums and an exclusive scan give every bracket; (2) terms are classified and
+// rounded to quanta, scans give the exclusive quanta prefix IP_k (mod 2^32) and event count;
+// (3) events are written compactly to LDS (IP at the event, the term) with the binade of the
+// run of increments before each; (4) lane j forms incr_j = (IP at event j - IP at event j-1)
+// quanta of its run's binade (an exact add: the run stays in its binade), and the wave adds
+// incr_0, a_(k_0), incr_1, a_(k_1), ..., incr_m in order.  Negative, NaN or infinite terms, a
+// total that may overflow, n > 64 EPT or more than MCAP events fall back to adding every term.
+namespace xsum {
+constexpr uint32_t MCAP = 256;
+struct Scratch {
+    uint32_t sync;   // participant arrivals (zeroed by the caller before a workgroup barrier)
+    float wt[8];
+    uint32_t wbad[8], wd[8], we[8];
+    uint32_t ipev[MCAP];
+    float aev[MCAP];
+    int32_t sege[MCAP + 1];
+    __attribute__((aligned(16))) float c[2 * MCAP + 32];
+};
+}   // namespace xsum
+
+template <int CTRL, int RM>
+__device__ inline uint32_t dpp_zero(uint32_t v) {   // lanes without a source (or masked rows) read 0
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RM, 0xf, true);
+}
+// Inclusive scans over the 64 lanes: row_shr 1, 2, 4, 8 within rows of 16, then row_bcast 15
+// (rows 1, 3) and row_bcast 31 (rows 2, 3).
+__device__ inline uint32_t wave_scan_u(uint32_t v) {
+    v += dpp_zero<0x111, 0xf>(v);
+    v += dpp_zero<0x112, 0xf>(v);
+    v += dpp_zero<0x114, 0xf>(v);
+    v += dpp_zero<0x118, 0xf>(v);
+    v += dpp_zero<0x142, 0xa>(v);
+    v += dpp_zero<0x143, 0xc>(v);
+    return v;
+}
+template <int CTRL, int RM>
+__device__ inline float dpp_zero_f(float v) {
+    return __builtin_bit_cast(float, dpp_zero<CTRL, RM>(__builtin_bit_cast(uint32_t, v)));
+}
+// exclusive scan: wave_shr 1 (lane 0 reads 0), then the inclusive scan
+__device__ inline float wave_excl_scan_f(float v) {
+    v = dpp_zero_f<0x138, 0xf>(v);
+    v += dpp_zero_f<0x111, 0xf>(v);
+    v += dpp_zero_f<0x112, 0xf>(v);
+    v += dpp_zero_f<0x114, 0xf>(v);
+    v += dpp_zero_f<0x118, 0xf>(v);
+    v += dpp_zero_f<0x142, 0xa>(v);
+    v += dpp_zero_f<0x143, 0xc>(v);
+    return v;
+}
+// binade exponent of x >= 0 (x < 2^-126: -126)
+__device__ inline int binade_of(float x) {
+    return x >= 0x1p-126f ? (int)((__builtin_bit_cast(uint32_t, x) >> 23) & 0xff) - 127 : -126;
+}
+__device__ inline float rlane_f(float v, uint32_t l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), (int)l));
+}
+
+// Meeting point of the NPW participant waves only (the other waves of the workgroup are not
+// waited for): arrival count in LDS, phase ph = 1, 2, 3.
+template <int NPW>
+__device__ inline void part_sync(xsum::Scratch &L, uint32_t ph) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(&L.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(&L.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < NPW * ph)
+        __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// a: LDS, 16-byte aligned, readable up to a multiple of 4 terms past n.  The waves with
+// p = 0 .. NPW - 1 call (p uniform per wave; p = 0 is the wave that receives the result); they
+// meet three times among themselves, so the other waves of the workgroup keep working.  L.sync
+// must be 0 on entry (zeroed before a workgroup barrier).  Lane l of wave p holds terms
+// (64 p + l) EPT .. + EPT - 1 (EPT = 4: consecutive lanes read consecutive 16 bytes).
+template <int NPW, int EPT>
+__device__ __forceinline__ float block_seq_sum(const float *a, uint32_t n, xsum::Scratch &L, int p, int lane) {
+    static_assert(NPW >= 1 && NPW <= 8 && (EPT == 4 || EPT == 8), "per-wave totals, term masks");
+    constexpr float C = 1.01f * 0x1p-24f, R = 0x1p-16f;
+    constexpr uint32_t WT = 64 * EPT;   // terms per wave
+    const uint32_t k0 = (uint32_t)(64 * p + lane) * EPT;
+    const bool fits = n <= WT * NPW;                              // (uniform)
+    const bool act = fits && p >= 0 && WT * (uint32_t)p < n;      // (uniform per wave)
+    float v[EPT], pp[EPT + 1];
+    pp[0] = 0.0f;
+    float woff = 0.0f;
+    if (act) {   // (1) terms, running sums, the wave's exclusive scan
+        bool bad = false;
+#pragma unroll
+        for (int u = 0; u < EPT / 4; ++u) {
+            v4f r = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (k0 + 4 * u < n) r = reinterpret_cast<const v4f *>(a)[k0 / 4 + u];
+            v[4 * u] = r.x;
+            v[4 * u + 1] = r.y;
+            v[4 * u + 2] = r.z;
+            v[4 * u + 3] = r.w;
+        }
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            v[i] = k0 + i < n ? v[i] : 0.0f;
+            bad |= !(v[i] >= 0.0f && v[i] <= 0x1.fffffep127f);   // (NaN fails)
+            pp[i + 1] = pp[i] + v[i];
+        }
+        woff = wave_excl_scan_f(pp[EPT]);
+        if (lane == 63) L.wt[p] = woff + pp[EPT];
+        if (lane == 0) L.wbad[p] = __builtin_amdgcn_ballot_w64(bad) != 0;
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            v[i] = 0.0f;
+            pp[i + 1] = 0.0f;
+        }
+    }
+    part_sync<NPW>(L, 1);
+    float off = 0.0f, tot = 0.0f;
+    uint32_t anybad = 0;
+#pragma unroll
+    for (int w = 0; w < NPW; ++w) {
+        const bool has = WT * (uint32_t)w < n;
+        const float t = has ? L.wt[w] : 0.0f;
+        if (w < p) off += t;
+        tot += t;
+        anybad |= has ? L.wbad[w] : 0u;
+    }
+    off += woff;
+    const bool serial0 = !fits || anybad || !(tot < 0x1p126f);   // (uniform)
+    // (2) classification and quanta
+    const int el = binade_of(off * (1.0f - R - C * (float)k0)),
+              eh = binade_of((off + pp[EPT]) * (1.0f + R + C * (float)(k0 + EPT)));
+    uint32_t evm = 0, abm = 0, dsum = 0, esum = 0;
+    auto quanta = [&](int i, bool *tie) {
+        const int e = ((abm >> i) & 1) ? eh : el;
+        const float y = fminf(ldexpf(v[i], 23 - e), 0x1p25f);
+        const float fl = floorf(y), fr = y - fl;
+        *tie = fr == 0.5f;
+        return (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
+    };
+    if (act && !serial0) {
+        // one boundary 2^eh inside the bracket: each term by its own bracket; more: all events
+        const float B = __builtin_bit_cast(float, (uint32_t)(min(eh, 127) + 127) << 23);
+        const bool one = eh == el + 1;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            const float k = (float)(k0 + i);
+            const bool below = (off + pp[i + 1]) * (1.0f + R + C * (k + 1.0f)) < B,
+                       above = (off + pp[i]) * (1.0f - R - C * k) >= B;
+            abm |= (uint32_t)(el != eh && one && above) << i;
+            evm |= (uint32_t)(el != eh && !(one && (below || above))) << i;
+        }
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            bool tie;
+            const uint32_t q = quanta(i, &tie);
+            const bool in = k0 + i < n;
+            const bool ev = in && (((evm >> i) & 1) || tie);
+            evm = (evm & ~(1u << i)) | ((uint32_t)ev << i);
+            dsum += (in && !ev) ? q : 0u;
+            esum += ev ? 1u : 0u;
+        }
+    }
+    uint32_t di = 0, ei = 0;
+    if (act) {
+        di = wave_scan_u(dsum);
+        ei = wave_scan_u(esum);
+        if (lane == 63) {
+            L.wd[p] = di;
+            L.we[p] = ei;
+        }
+    }
+    part_sync<NPW>(L, 2);
+    uint32_t ioff = di - dsum, eoff = ei - esum, itot = 0, m = 0;
+#pragma unroll
+    for (int w = 0; w < NPW; ++w) {
+        const bool has = WT * (uint32_t)w < n;
+        const uint32_t x = has ? L.wd[w] : 0u, y = has ? L.we[w] : 0u;
+        itot += x;
+        m += y;
+        if (w < p) {
+            ioff += x;
+            eoff += y;
+        }
+    }
+    const bool serial = serial0 || m > xsum::MCAP;   // (uniform)
+    // (3) events and run binades (a run's first lane writes its binade; a run can also be
+    // written by an earlier lane of an unclean thread or the first lane of a wave, always with
+    // the same value)
+    const uint32_t eprev = dpp_zero<0x138, 0xf>(eoff);   // the previous lane's eoff (lane 0: 0)
+    if (act && !serial && k0 < n) {
+        if (evm == 0) {
+            if (lane == 0 || eprev != eoff) L.sege[eoff] = el;
+        } else {
+            uint32_t ip = ioff, ec = eoff;
+            bool after = true;
+#pragma unroll
+            for (int i = 0; i < EPT; ++i) {
+                const bool in = k0 + i < n, ev = (evm >> i) & 1;
+                bool tie;
+                const uint32_t q = quanta(i, &tie);
+                if (in && ev) {
+                    L.ipev[ec] = ip;
+                    L.aev[ec] = v[i];
+                }
+                if (in && !ev && after) L.sege[ec] = ((abm >> i) & 1) ? eh : el;
+                ec += (in && ev) ? 1u : 0u;
+                ip += (in && !ev) ? q : 0u;
+                after = in ? ev : after;
+            }
+        }
+    }
+    part_sync<NPW>(L, 3);
+    // (4) incr_0, a_(k_0), ..., incr_m added in order by wave 0, padded with +0 (exact: the sum
+    // is never -0) to whole batches of 32 adds
+    float s = 0.0f;
+    if (p == 0) {
+        if (serial) return rlane_f(lane == 0 ? seq_sum_lds(a, n, 0.0f) : 0.0f, 0);
+        const uint32_t nc = (2 * m + 1 + 31) / 32 * 32;
+        for (uint32_t j = lane; 2 * j < nc; j += 64) {
+            float cj = 0.0f, aj = 0.0f;
+            if (j <= m) {
+                const uint32_t hi = j < m ? L.ipev[j] : itot, lo = j ? L.ipev[j - 1] : 0u;
+                const uint32_t dI = hi - lo;   // < 2^23 quanta: the run stays in its binade
+                const int e = min(max(L.sege[j], -126), 127);   // (unwritten for empty runs)
+                cj = dI ? ldexpf((float)dI, e - 23) : 0.0f;
+            }
+            if (j < m) aj = L.aev[j];
+            L.c[2 * j] = cj;
+            L.c[2 * j + 1] = aj;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        s = rlane_f(lane == 0 ? seq_sum_lds(L.c, nc, 0.0f) : 0.0f, 0);
+    }
+    return s;
+}
+
+// Test entry: one workgroup sums x[0..n) (n <= 4096 in LDS; larger n: one lane over global
+// memory) with the workgroup method (method 1) or one lane (method 0).
+__global__ __launch_bounds__(512) void k_seq_sum(const float *__restrict__ x, uint32_t n, int method, float *out) {
+    __shared__ __align__(16) float a[4096];
+    __shared__ xsum::Scratch L;
+    const int tid = threadIdx.x;
+    if (n > 4096) {
+        if (tid == 0) {
+            float s = 0.0f;
+            for (uint32_t i = 0; i < n; ++i) s = s + x[i];
+            *out = s;
+        }
+        return;
+    }
+    for (uint32_t i = tid; i < 4096; i += 512) a[i] = i < n ? x[i] : 0.0f;
+    if (tid == 0) L.sync = 0;
+    __syncthreads();
+    if (method == 1) {
+        const float r = block_seq_sum<8, 4>(a, n, L, tid >> 6, tid & 63);
+        if (tid == 0) *out = r;
+    } else if (tid == 0) {
+        *out = seq_sum_lds(a, n, 0.0f);
+    }
+}
+
 // ------------------------------------------------------------------ embedding
 // Model::forward (model.rs:154): x = token_embd[token] (F32 table, dequantized at load).
 __global__ void k_embed(const float *__restrict__ emb, uint32_t d, const StepParams *p, float *x) {
@@ -293,31 +578,8 @@ __global__ void k_advance(StepParams *p) {
 // ------------------------------------------------------------------ RMSNorm + quantize
 // rmsnorm (ops.rs:85-96): ss = sum x^2; scale = 1/sqrt(ss/n + eps); h = x*scale*w; then
 // the activation quantization of the consuming matvec (quant.rs:111-123).
-// EXACT: the squares are formed in parallel and summed by one lane in index order (the
-// reference's `ss += v * v`); otherwise a tree.
-template <bool EXACT>
-__device__ inline float sum_squares(const float *xs, float *ps, uint32_t d, int tid, int nthr, float *red,
-                                    float *s_out) {
-    if (EXACT) {
-        for (uint32_t i = tid; i < d; i += nthr) ps[i] = xs[i] * xs[i];
-        __syncthreads();
-        if (tid == 0) *s_out = seq_sum_lds(ps, d, 0.0f);
-    } else {
-        float ss = 0.0f;
-        for (uint32_t i = tid; i < d; i += nthr) ss += xs[i] * xs[i];
-        for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-        __syncthreads();
-        if (tid == 0) {
-            float t = 0.0f;
-            for (int i = 0; i < nthr / 64; ++i) t += red[i];
-            *s_out = t;
-        }
-    }
-    __syncthreads();
-    return *s_out;
-}
-
+// EXACT: the squares are formed in parallel and summed in index order (the reference's
+// `ss += v * v`) by block_seq_sum; otherwise a tree.
 template <bool EXACT>
 __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float *__restrict__ x, const float *__restrict__ w,
                                                        float eps, uint32_t d, float *h_out, uint8_t *q_out,
@@ -325,6 +587,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float *__restrict__
     extern __shared__ __align__(16) float ps[];  // d squares
     __shared__ float red[4];
     __shared__ float s_ss;
+    __shared__ xsum::Scratch xs;
     const int tid = threadIdx.x, j = tid & 7;
     const uint32_t nb = d / QK, nc = div_up(nb, 4), ng = d / 4;
     // thread tid owns the float4 groups g = tid + 256 u: elements 4g..4g+3, i.e. lane j of
@@ -353,8 +616,10 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float *__restrict__
         if (tid + 256 * u < ng) squares(xv[u], tid + 256 * u);
     for (uint32_t g = tid + 256 * RQ; g < ng; g += 256) squares(reinterpret_cast<const v4f *>(x)[g], g);
     if (EXACT) {
+        if (tid == 0) xs.sync = 0;
         __syncthreads();
-        if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
+        const float r = block_seq_sum<4, 4>(ps, d, xs, tid >> 6, tid & 63);   // ss += v * v in index order
+        if (tid == 0) s_ss = r;
     } else {
         for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -651,8 +916,10 @@ struct GroupRaw {
 // reference's order; a separate chain wave (HD <= 64) runs it while the row waves fetch their
 // weights.  Writes q, k (normed and rotated) and v into out (the q | k | v layout).
 template <int HD> struct QkvCfg {
-    static constexpr int CW = HD <= 64 ? 64 : 0;   // threads of the chain wave
-    static constexpr int NT = CW + 8 * HD;         // + 8 lanes per row
+    static constexpr int CW = HD <= 64 ? 64 : 0;   // wave 0: the head's epilogue
+    static constexpr int RE = CW + 8 * HD;         // + 8 lanes per row
+    static constexpr int SW = HD <= 64 ? 192 : 0;  // + waves that only sum (no weight loads)
+    static constexpr int NT = RE + SW;
 };
 template <bool EXACT, int ORDER, bool SCF32, int NCT, int HD>
 __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const float *__restrict__ x,
@@ -661,7 +928,7 @@ __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const floa
                                                             const float *__restrict__ cs, const float *__restrict__ sn,
                                                             const StepParams *p, uint32_t n_heads, uint32_t n_kv,
                                                             float *kc, float *vc, uint32_t cap, float *out) {
-    constexpr int CW = QkvCfg<HD>::CW, NT = QkvCfg<HD>::NT;
+    constexpr int CW = QkvCfg<HD>::CW, RE = QkvCfg<HD>::RE, NT = QkvCfg<HD>::NT;
     extern __shared__ __align__(16) uint8_t smem[];
     uint8_t *sq = smem;
     float *sd = reinterpret_cast<float *>(smem + W.nc * CHUNK_BYTES);
@@ -669,9 +936,14 @@ __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const floa
     __shared__ __align__(16) float hv[HD], ho[HD], tmp[HD];
     __shared__ float red[NT / 64];
     __shared__ float s_ss;
+    __shared__ xsum::Scratch xs;
     const int tid = threadIdx.x, lane = tid & 63, j = tid & 7;
-    const bool rowt = tid >= CW;
+    const bool rowt = tid >= CW && tid < RE;
     const uint32_t hh = blockIdx.x, d = W.K, ng = d / 4;
+    // the waves of the index-order sum: wave 0 and the waves past the rows (or, without those,
+    // the first four waves)
+    const int wave = tid >> 6,
+              sp = QkvCfg<HD>::SW ? (wave == 0 ? 0 : (tid >= RE ? 1 + (tid - RE) / 64 : -1)) : (wave < 4 ? wave : -1);
     const uint32_t kind = hh < n_heads ? 0u : (hh < n_heads + n_kv ? 1u : 2u);   // q, k, v
     // x and the gain first, alone in the memory pipeline (the chain waits for them)
     constexpr uint32_t RQ = (1024 / 4 + NT - 1) / NT;
@@ -703,11 +975,15 @@ __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const floa
         if (tid + NT * u < ng) squares(xv[u], tid + NT * u);
     for (uint32_t g = tid + NT * RQ; g < ng; g += NT) squares(reinterpret_cast<const v4f *>(x)[g], g);
     if (EXACT) {
+        if (tid == 0) xs.sync = 0;
         __syncthreads();
-        // the row waves issue their weights now (arriving during the chain)
+        // the row waves issue their weights now (arriving during the sum)
         if (rowt) rd.begin(row_qs(W, row), row_sc<SCF32>(W, row), W.nb, W.nc, j);
         __builtin_amdgcn_sched_barrier(0);
-        if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
+        if (sp >= 0) {
+            const float r = block_seq_sum<4, 4>(ps, d, xs, sp, lane);   // ss += v * v in index order
+            if (tid == 0) s_ss = r;
+        }
     } else {
         if (rowt) rd.begin(row_qs(W, row), row_sc<SCF32>(W, row), W.nb, W.nc, j);
         for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
@@ -1188,7 +1464,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
     if (tid < (int)C::RMAX) ready[tid] = 0;
     if (tid == 0) done = 0;
     __syncthreads();
-    if (tid == 0) s_inv = 1.0f / seq_sum_lds(e, n, 0.0f);
+    if (tid == 0) s_inv = 1.0f / seq_sum_lds(e, n, 0.0f);   // sum += e_t in index order
     __syncthreads();
     const float inv = s_inv;   // p_t = e_t * inv, formed by the producers
     if (pw >= 0) {
@@ -1274,12 +1550,12 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
 
 // Softmax and P.V of one query head, as k_attn_softmax_pv, for caches whose V slice and
 // products fit in LDS (pv_res_fits): no ring.  Workgroup (h, q), 512 threads:
-//   while lane 0 sums e_t sequentially, waves 1..7 fetch the 16-element V slice of all
-//   positions and write it transposed into LDS P[d][t]; after inv is known, they replace
-//   P[d][t] by the
-//   rounded product p_t * V[d][t] (p_t = e_t * inv; -0 past the context, the exact identity
-//   of the chain's adds) in groups of G positions, each group flagged when written;
-//   wave 0 lanes 0..15 run the 16 sequential chains over P, waiting only for each group's flag.
+//   waves 1..7 fetch the 16-element V slice of all positions into registers, then the
+//   workgroup forms the index-order sum of e_t (block_seq_sum); once inv is known, waves
+//   1..7 write the rounded products p_t * V[d][t] (p_t = e_t * inv; -0 past the context, the
+//   exact identity of the chain's adds) transposed into LDS P[d][t] in groups of G positions,
+//   each group flagged when written; wave 0 lanes 0..15 run the 16 sequential chains over P,
+//   waiting only for each group's flag.
 struct PvResCfg {
     static constexpr uint32_t D = 16;     // output elements per workgroup
     static constexpr uint32_t G = 64;     // positions per product group (two chain chunks)
@@ -1288,9 +1564,11 @@ struct PvResCfg {
 };
 
 __host__ __device__ inline uint32_t pv_res_rows(uint32_t cap) { return div_up(cap, 32) * 32; }
-__host__ __device__ inline size_t pv_res_lds(uint32_t cap) {
+constexpr size_t XSUM_FLOATS = (sizeof(xsum::Scratch) + 15) / 16 * 4;
+__host__ __device__ inline size_t pv_res_lds(uint32_t cap) {   // e, then P (the sum's scratch before)
     const uint32_t rc = pv_res_rows(cap);
-    return ((size_t)rc + (size_t)PvResCfg::D * (rc + 4)) * 4;
+    const size_t p = (size_t)PvResCfg::D * (rc + 4);
+    return ((size_t)rc + (p > XSUM_FLOATS ? p : XSUM_FLOATS)) * 4;
 }
 __host__ __device__ bool pv_res_fits(uint32_t cap) {
     return cap >= 1 && pv_res_lds(cap) <= PV_LDS_BUDGET && 4 * cap <= 448 * PvResCfg::VB &&
@@ -1328,6 +1606,22 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
 #pragma unroll
     for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(u * 512 + tid, n - 1)];
     const WaveExpTab tab = WaveExpTab::load(lane);
+    // V items j = vt + 448 r of thread vt = tid - 64 of waves 1..7 (position j / 4, elements
+    // 4 (j % 4) .. + 3), fetched into registers behind the scores (their issue overlaps the
+    // exps and the sum; wave 0 issues the same loads at one address and ignores them: a load
+    // under a branch would make the waits for the scores also wait for V), turned into the
+    // rounded products p_t v_t[di] once inv is known and written transposed, P[di][t];
+    // positions n .. npad - 1 get -0, the exact identity of an add.  A wave's 64 items of a
+    // round are consecutive, so they fall in at most two groups of 4 G items; the write that
+    // completes a group sets its ready bit.
+    v4f vv[C::VB];
+    const uint32_t vt = tid - 64, vti = wave > 0 ? vt : 0u;
+#pragma unroll
+    for (uint32_t r = 0; r < C::VB; ++r) {
+        const uint32_t j = min(vti + 448 * r, 4 * n - 1), t = j >> 2, dq = j & 3;
+        const float *src = (t == pos) ? vnew + 4 * dq : vcg + (size_t)t * HD + 4 * dq;
+        vv[r] = *reinterpret_cast<const v4f *>(src);
+    }
     for (uint32_t s = lane + 64; s < S; s += 64) m = fmaxf(m, pmax[(size_t)h * S + s]);
     for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));   // max is order-free
     for (uint32_t t0 = 0; t0 < n; t0 += EB * 512) {
@@ -1342,26 +1636,16 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
                 if (t < n) e[t] = ev;
             }
     }
-    if (tid == 0) ready = 0;
+    xsum::Scratch &xs = *reinterpret_cast<xsum::Scratch *>(P);   // (P is not in use yet)
+    if (tid == 0) {
+        ready = 0;
+        xs.sync = 0;
+    }
     if (tid < 64) gcount[tid] = 0;
     __syncthreads();
-    // V items j = vt + 448 r of thread vt = tid - 64 of waves 1..7 (position j / 4, elements
-    // 4 (j % 4) .. + 3), fetched into registers while lane 0 sums (no LDS traffic beside the
-    // chain's reads), turned into the rounded products p_t v_t[di] once inv is known and written
-    // transposed, P[di][t]; positions n .. npad - 1 get -0, the exact identity of an add.  A wave's
-    // 64 items of a round are consecutive, so they fall in at most two groups of 4 G items; the
-    // write that completes a group sets its ready bit.
-    v4f vv[C::VB];
-    const uint32_t vt = tid - 64;
-    if (tid == 0) {
-        s_inv = 1.0f / seq_sum_lds(e, n, 0.0f);
-    } else if (wave > 0) {
-#pragma unroll
-        for (uint32_t r = 0; r < C::VB; ++r) {
-            const uint32_t j = min(vt + 448 * r, 4 * n - 1), t = j >> 2, dq = j & 3;
-            const float *src = (t == pos) ? vnew + 4 * dq : vcg + (size_t)t * HD + 4 * dq;
-            vv[r] = *reinterpret_cast<const v4f *>(src);
-        }
+    {   // sum += e_t in index order
+        const float r = block_seq_sum<8, 4>(e, n, xs, wave, lane);
+        if (tid == 0) s_inv = 1.0f / r;
     }
     __syncthreads();
     const float inv = s_inv;
@@ -1502,6 +1786,7 @@ __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x
     float *hp = hs + d, *ps = hs + 2 * d;
     __shared__ float red[16];
     __shared__ float s_ss;
+    __shared__ xsum::Scratch xs;
     __shared__ __align__(16) float lg[256], scr[256], sel[256];
     __shared__ __align__(16) uint32_t tk[64];
     __shared__ __align__(16) float tw[64];
@@ -1550,9 +1835,17 @@ __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x
             else ss += v * v;
         }
         if (EXACT) {
+            if (tid == 0) xs.sync = 0;
             __syncthreads();
-            if (rows) fetch_rows();   // arrives during the chain
-            if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
+            if (rows) fetch_rows();   // arrives during the sum
+            if (d % 4 == 0) {         // (the squares are 16-byte aligned)
+                if (tid < 256) {
+                    const float r = block_seq_sum<4, 4>(ps, d, xs, tid >> 6, lane);   // ss += v * v in index order
+                    if (tid == 0) s_ss = r;
+                }
+            } else if (tid == 0) {
+                s_ss = seq_sum_lds(ps, d, 0.0f);
+            }
         } else {
             for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
             if (lane == 0) red[tid >> 6] = ss;
@@ -1764,12 +2057,13 @@ __global__ __launch_bounds__(MAXT) void k_ffn_router(const float *__restrict__ x
 // (the same deterministic arithmetic, so every workgroup picks the same experts) and quantizes h
 // into its LDS, so the expert rows are fetched without a kernel boundary and without a round
 // trip through memory; workgroup (0, 0) also writes the picks for the down projection.
-// Threads: wave 0 runs the chain; threads 64 + 8 e .. 64 + 8 e + 7 own router row e (prefetched
-// during the chain in the 16-byte-step layout of k_ffn_router); waves 0-1 own the 16 rows.  Few
+// Threads: waves 0-1 form the index-order sum of squares while threads 128 + 8 e .. + 7 own
+// router row e (prefetched meanwhile in the 16-byte-step layout of k_ffn_router); waves 0-1 then
+// own the 16 gate/up rows.  Few
 // rows per workgroup spread the expert rows, which cannot be fetched before the ranking, over
 // many CUs (one CU issues about 64 bytes a clock).
 constexpr uint32_t FF_NT = 512, FF_ROWS = 16;   // gate/up rows per workgroup: waves 0-1
-constexpr uint32_t FF_MAXE = (FF_NT - 64) / 8;   // 56 experts
+constexpr uint32_t FF_MAXE = (FF_NT - 128) / 8;   // 48 experts
 template <bool EXACT, int ORDER, bool SCF32, int NCT, int NST>
 __global__ __launch_bounds__(512) void k_ffn_front(const float *__restrict__ x, const float *__restrict__ w, float eps,
                                                    uint32_t d, const float *__restrict__ Wp,
@@ -1785,12 +2079,13 @@ __global__ __launch_bounds__(512) void k_ffn_front(const float *__restrict__ x, 
     float *sd = reinterpret_cast<float *>(sq + Wg.nc * CHUNK_BYTES);
     __shared__ float red[FF_NT / 64];
     __shared__ float s_ss;
+    __shared__ xsum::Scratch xs;
     __shared__ uint64_t K[64];
     __shared__ __align__(16) uint32_t tk[64];
     __shared__ __align__(16) float tw[64];
     const int tid = threadIdx.x, lane = tid & 63, j = tid & 7;
-    const bool rows = tid >= 64;
-    const uint32_t e8 = rows ? (uint32_t)(tid - 64) >> 3 : 0u, l8 = (uint32_t)tid & 7;
+    const bool rows = tid >= 128;   // waves 2..7: the router rows (waves 0, 1 sum the squares)
+    const uint32_t e8 = rows ? (uint32_t)(tid - 128) >> 3 : 0u, l8 = (uint32_t)tid & 7;
     const bool router = E > 0;
     const uint32_t slot = blockIdx.y, row = blockIdx.x * FF_ROWS + ((uint32_t)tid >> 3);
     const uint32_t lrow = min(row, f - 1);
@@ -1822,9 +2117,13 @@ __global__ __launch_bounds__(512) void k_ffn_front(const float *__restrict__ x, 
         }
     }
     if (EXACT) {
+        if (tid == 0) xs.sync = 0;
         __syncthreads();
-        if (router && rows && e8 < E) fetch_rows();   // arrives during the chain
-        if (tid == 0) s_ss = seq_sum_lds(ps, d, 0.0f);   // ss += v * v in index order
+        if (router && rows && e8 < E) fetch_rows();   // arrives during the sum
+        if (tid < 128) {
+            const float r = block_seq_sum<2, 8>(ps, d, xs, tid >> 6, lane);   // ss += v * v in index order
+            if (tid == 0) s_ss = r;
+        }
     } else {
         for (int m = 32; m >= 1; m >>= 1) ss += shfl_xor(ss, m);
         if (lane == 0) red[tid >> 6] = ss;
@@ -2130,6 +2429,10 @@ void launch_load_row(hipStream_t st, const float *inputs, uint32_t d, const Step
     LAUNCH(k_load_row, dim3(div_up(d, 256)), dim3(256), 0, st, inputs, d, p, x);
 }
 void launch_advance(hipStream_t st, StepParams *p) { LAUNCH(k_advance, dim3(1), dim3(64), 0, st, p); }
+
+void launch_seq_sum(hipStream_t st, const float *x, uint32_t n, int method, float *out) {
+    LAUNCH(k_seq_sum, dim3(1), dim3(512), 0, st, x, n, method, out);
+}
 
 void launch_rmsnorm_quant(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,
                           float *h, uint8_t *q, float *dq) {

@@ -175,6 +175,13 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
                         uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t pos, float *kc,
                         float *vc, float *out, uint32_t flags);
 
+/* The sequential binary32 sum out = ((0 + x[0]) + x[1]) + ... + x[n-1] that ops::rmsnorm
+ * (`ss += v * v`, ops.rs:101-104) and ops::softmax (`sum += *v`, ops.rs:119-122) form, computed
+ * on the device by the method the decode kernels use for it: method 1 = one workgroup
+ * (identical bits for non-negative terms, n <= 4096; other inputs fall back to one lane),
+ * method 0 = one lane adding in index order. */
+int hg_seq_sum(const float *x, uint32_t n, uint32_t method, float *out);
+
 /* ---- measurement (no counterpart in the reference) ------------------------------------ */
 
 /* Kernel time of t's matvec on device-resident data: x[in] is quantized once on the device,
