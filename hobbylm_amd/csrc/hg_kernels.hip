@@ -373,7 +373,7 @@ __device__ inline void part_sync(xsum::Scratch &L, uint32_t ph) {
 // (64 p + l) EPT .. + EPT - 1 (EPT = 4: consecutive lanes read consecutive 16 bytes).
 template <int NPW, int EPT>
 __device__ __forceinline__ float block_seq_sum(const float *a, uint32_t n, xsum::Scratch &L, int p, int lane) {
-    static_assert(NPW >= 1 && NPW <= 8 && (EPT == 4 || EPT == 8), "per-wave totals, term masks");
+    static_assert(NPW >= 1 && NPW <= 8 && EPT % 4 == 0 && EPT <= 32, "per-wave totals, term masks");
     constexpr float C = 1.01f * 0x1p-24f, R = 0x1p-16f;
     constexpr uint32_t WT = 64 * EPT;   // terms per wave
     const uint32_t k0 = (uint32_t)(64 * p + lane) * EPT;
@@ -1550,29 +1550,29 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
 
 // Softmax and P.V of one query head, as k_attn_softmax_pv, for caches whose V slice and
 // products fit in LDS (pv_res_fits): no ring.  Workgroup (h, q), 512 threads:
-//   waves 1..7 fetch the 16-element V slice of all positions into registers, then the
-//   workgroup forms the index-order sum of e_t (block_seq_sum); once inv is known, waves
-//   1..7 write the rounded products p_t * V[d][t] (p_t = e_t * inv; -0 past the context, the
-//   exact identity of the chain's adds) transposed into LDS P[d][t] in groups of G positions,
-//   each group flagged when written; wave 0 lanes 0..15 run the 16 sequential chains over P,
-//   waiting only for each group's flag.
+//   every wave forms its share of e_t and signals it (no wait); waves 4..7 then stream the
+//   16-element V slice of all positions transposed into LDS, P[d][t], one group of G positions
+//   per round, while waves 0..3 form the index-order sum of e_t (block_seq_sum).  Once inv is
+//   known (a flag, not a barrier), waves 1..7 replace group g (wave 1 + g % 7) by the rounded
+//   products p_t * V[d][t] (p_t = e_t * inv; -0 past the context, the exact identity of the
+//   chain's adds) as soon as its V is in, and flag it; wave 0 lanes 0..15 run the 16
+//   sequential chains over P, waiting only for each group's flag.
 struct PvResCfg {
     static constexpr uint32_t D = 16;     // output elements per workgroup
     static constexpr uint32_t G = 64;     // positions per product group (two chain chunks)
-    static constexpr uint32_t VB = 21;    // V float4 per staging thread: 448 * VB >= 4 * cap
     static constexpr uint32_t NG = 64;    // product groups: one bit each of the ready mask
+    static constexpr uint32_t VB = 8;     // V loads in flight per V thread
 };
 
-__host__ __device__ inline uint32_t pv_res_rows(uint32_t cap) { return div_up(cap, 32) * 32; }
+__host__ __device__ inline uint32_t pv_res_rows(uint32_t cap) { return div_up(cap, 64) * 64; }
 constexpr size_t XSUM_FLOATS = (sizeof(xsum::Scratch) + 15) / 16 * 4;
-__host__ __device__ inline size_t pv_res_lds(uint32_t cap) {   // e, then P (the sum's scratch before)
+__host__ __device__ inline size_t pv_res_lds(uint32_t cap) {   // e, P, the sum's scratch
     const uint32_t rc = pv_res_rows(cap);
-    const size_t p = (size_t)PvResCfg::D * (rc + 4);
-    return ((size_t)rc + (p > XSUM_FLOATS ? p : XSUM_FLOATS)) * 4;
+    return ((size_t)rc + (size_t)PvResCfg::D * (rc + 4) + XSUM_FLOATS) * 4;
 }
 __host__ __device__ bool pv_res_fits(uint32_t cap) {
-    return cap >= 1 && pv_res_lds(cap) <= PV_LDS_BUDGET && 4 * cap <= 448 * PvResCfg::VB &&
-           div_up(pv_res_rows(cap), PvResCfg::G) <= PvResCfg::NG;
+    return cap >= 1 && pv_res_lds(cap) <= PV_LDS_BUDGET && pv_res_rows(cap) / PvResCfg::G <= PvResCfg::NG &&
+           pv_res_rows(cap) <= 3072;
 }
 
 template <int HD>
@@ -1584,8 +1584,10 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     using C = PvResCfg;
     constexpr uint32_t D = C::D, G = C::G, EB = 8;
     extern __shared__ __align__(16) float lds[];
-    __shared__ uint64_t ready;           // bit gi: product group gi written
-    __shared__ uint32_t gcount[64];      // products of group gi written so far (of 4 G)
+    __shared__ uint64_t ready;           // bit g: products of group g written
+    __shared__ uint32_t vdone[4];        // V rounds (groups) written by V wave 4 + i
+    __shared__ uint32_t arrived;         // waves whose e_t are written
+    __shared__ uint32_t inv_ready;
     __shared__ float s_inv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t h, q;
@@ -1595,33 +1597,26 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     const uint32_t rc = pv_res_rows(cap), TPC = rc + 4;   // row stride 4 mod 32 banks
     float *e = lds;                                         // [rc]  e_t
     float *P = lds + rc;                                    // [D][TPC]  V, then the products
+    xsum::Scratch &xs = *reinterpret_cast<xsum::Scratch *>(P + (size_t)D * TPC);
     const float *sc = scores + (size_t)h * cap;
     const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
     const float *vcg = vc + (size_t)g * cap * HD + q * D;
     const float *vnew = qkv + qd + kvd + g * HD + q * D;   // row pos, appended this step
-    const uint32_t npad = div_up(n, 32) * 32, ngroups = div_up(npad, G);
+    const uint32_t ng = div_up(n, G), npad = div_up(n, 32) * 32;   // groups, chain positions
     // loads in issue order: the split maxima, this thread's first scores, the exp table
     float m = pmax[(size_t)h * S + min((uint32_t)lane, S - 1)];
     float sv[EB];
 #pragma unroll
     for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(u * 512 + tid, n - 1)];
     const WaveExpTab tab = WaveExpTab::load(lane);
-    // V items j = vt + 448 r of thread vt = tid - 64 of waves 1..7 (position j / 4, elements
-    // 4 (j % 4) .. + 3), fetched into registers behind the scores (their issue overlaps the
-    // exps and the sum; wave 0 issues the same loads at one address and ignores them: a load
-    // under a branch would make the waits for the scores also wait for V), turned into the
-    // rounded products p_t v_t[di] once inv is known and written transposed, P[di][t];
-    // positions n .. npad - 1 get -0, the exact identity of an add.  A wave's 64 items of a
-    // round are consecutive, so they fall in at most two groups of 4 G items; the write that
-    // completes a group sets its ready bit.
-    v4f vv[C::VB];
-    const uint32_t vt = tid - 64, vti = wave > 0 ? vt : 0u;
-#pragma unroll
-    for (uint32_t r = 0; r < C::VB; ++r) {
-        const uint32_t j = min(vti + 448 * r, 4 * n - 1), t = j >> 2, dq = j & 3;
-        const float *src = (t == pos) ? vnew + 4 * dq : vcg + (size_t)t * HD + 4 * dq;
-        vv[r] = *reinterpret_cast<const v4f *>(src);
+    if (tid == 0) {
+        ready = 0;
+        arrived = 0;
+        inv_ready = 0;
+        xs.sync = 0;
     }
+    if (tid < 4) vdone[tid] = 0;
+    __syncthreads();
     for (uint32_t s = lane + 64; s < S; s += 64) m = fmaxf(m, pmax[(size_t)h * S + s]);
     for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));   // max is order-free
     for (uint32_t t0 = 0; t0 < n; t0 += EB * 512) {
@@ -1636,51 +1631,78 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
                 if (t < n) e[t] = ev;
             }
     }
-    xsum::Scratch &xs = *reinterpret_cast<xsum::Scratch *>(P);   // (P is not in use yet)
-    if (tid == 0) {
-        ready = 0;
-        xs.sync = 0;
-    }
-    if (tid < 64) gcount[tid] = 0;
-    __syncthreads();
-    {   // sum += e_t in index order
-        const float r = block_seq_sum<8, 4>(e, n, xs, wave, lane);
-        if (tid == 0) s_inv = 1.0f / r;
-    }
-    __syncthreads();
-    const float inv = s_inv;
-    if (wave > 0) {
-        static_assert(C::G == 64 && D == 16, "a group is 64 positions x 4 element quads");
-        const uint32_t nitems = 4 * npad;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0) __hip_atomic_fetch_add(&arrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (wave >= 4) {
+        // V streamed into P[d][t]: round r, thread vt = tid - 256 -> position 64 r + vt / 4,
+        // elements 4 (vt % 4) .. + 3 (positions past the context: zeros, replaced by -0 later);
+        // VB rounds of loads in flight, then their LDS writes, then this wave's round count
+        const uint32_t vt = (uint32_t)tid - 256, dq = vt & 3, tl = vt >> 2;
+        for (uint32_t r0 = 0; r0 < ng; r0 += C::VB) {
+            v4f vr[C::VB];
 #pragma unroll
-        for (uint32_t r = 0; r < C::VB; ++r) {
-            const uint32_t jw = 448 * r + 64 * (uint32_t)(wave - 1);   // the wave's first item
-            if (jw >= nitems) break;                                    // (uniform)
-            const uint32_t j = jw + (uint32_t)lane;
-            if (j < nitems) {
-                const uint32_t t = j >> 2, d0 = 4 * (j & 3);
-                const bool in = t < n;
-                const float pt = in ? e[t] * inv : 0.0f;
-                P[(d0 + 0) * TPC + t] = in ? pt * vv[r].x : -0.0f;
-                P[(d0 + 1) * TPC + t] = in ? pt * vv[r].y : -0.0f;
-                P[(d0 + 2) * TPC + t] = in ? pt * vv[r].z : -0.0f;
-                P[(d0 + 3) * TPC + t] = in ? pt * vv[r].w : -0.0f;
+            for (uint32_t u = 0; u < C::VB; ++u) {
+                const uint32_t t = min(G * (r0 + u) + tl, n - 1);
+                const float *src = (t == pos) ? vnew + 4 * dq : vcg + (size_t)t * HD + 4 * dq;
+                vr[u] = *reinterpret_cast<const v4f *>(src);
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane == 0) {
-                const uint32_t je = min(jw + 64, nitems);   // items [jw, je) written by this wave
-                const uint32_t g0 = jw / (4 * G), g1 = (je - 1) / (4 * G);
-                for (uint32_t gi = g0; gi <= g1; ++gi) {
-                    const uint32_t lo = max(jw, gi * 4 * G), hi = min(je, (gi + 1) * 4 * G);
-                    const uint32_t full = min((gi + 1) * 4 * G, nitems) - gi * 4 * G;
-                    const uint32_t before =
-                        __hip_atomic_fetch_add(&gcount[gi], hi - lo, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    if (before + (hi - lo) == full)
-                        __hip_atomic_fetch_or(&ready, 1ull << gi, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll
+            for (uint32_t u = 0; u < C::VB; ++u) {
+                const uint32_t t = G * (r0 + u) + tl;
+                if (r0 + u < ng) {
+                    P[(4 * dq + 0) * TPC + t] = vr[u].x;
+                    P[(4 * dq + 1) * TPC + t] = vr[u].y;
+                    P[(4 * dq + 2) * TPC + t] = vr[u].z;
+                    P[(4 * dq + 3) * TPC + t] = vr[u].w;
                 }
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0)
+                __hip_atomic_store(&vdone[wave - 4], min(r0 + C::VB, ng), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-    } else if (lane < (int)D) {
+    } else {   // sum += e_t in index order, once every wave's e_t are written
+        while (__hip_atomic_load(&arrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 8u)
+            __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        const float r = n <= 2048 ? block_seq_sum<4, 8>(e, n, xs, wave, lane) : block_seq_sum<4, 12>(e, n, xs, wave, lane);
+        if (tid == 0) {
+            s_inv = 1.0f / r;
+            __hip_atomic_store(&inv_ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    }
+    if (wave >= 1) {   // products of groups wave - 1, wave + 6, ...: lane l -> element l / 4,
+                       // positions 16 (l % 4) .. + 15 of the group (four 16-byte steps)
+        while (__hip_atomic_load(&inv_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u)
+            __builtin_amdgcn_s_sleep(1);
+        const float inv = s_inv;
+        const uint32_t di = (uint32_t)lane >> 2, tq = (uint32_t)lane & 3;
+        for (uint32_t gi = (uint32_t)wave - 1; gi < ng; gi += 7) {
+            for (;;) {   // this group's V rows are in once every V wave has passed round gi
+                uint32_t v0 = __hip_atomic_load(&vdone[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                v0 = min(v0, __hip_atomic_load(&vdone[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+                v0 = min(v0, __hip_atomic_load(&vdone[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+                v0 = min(v0, __hip_atomic_load(&vdone[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+                if (v0 > gi) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                const uint32_t t = G * gi + 16 * tq + 4 * u;
+                v4f *pv = reinterpret_cast<v4f *>(P + di * TPC + t);
+                const v4f ev = *reinterpret_cast<const v4f *>(e + t), vv = *pv;
+                v4f pr;
+                pr.x = t + 0 < n ? (ev.x * inv) * vv.x : -0.0f;
+                pr.y = t + 1 < n ? (ev.y * inv) * vv.y : -0.0f;
+                pr.z = t + 2 < n ? (ev.z * inv) * vv.z : -0.0f;
+                pr.w = t + 3 < n ? (ev.w * inv) * vv.w : -0.0f;
+                *pv = pr;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0) __hip_atomic_fetch_or(&ready, 1ull << gi, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    }
+    if (wave == 0 && lane < (int)D) {
         // chains: 32 positions (eight 16-byte reads) per chunk, the next chunk's reads issued
         // before the current chunk's adds (unconditional, index clamped), order pinned
         float o = 0.0f;
