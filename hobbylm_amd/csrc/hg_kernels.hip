@@ -533,11 +533,13 @@ __device__ __forceinline__ float block_seq_sum(const float *a, uint32_t n, xsum:
 }
 
 // Test entry: one workgroup sums x[0..n) (n <= 4096 in LDS; larger n: one lane over global
-// memory) with the workgroup method (method 1) or one lane (method 0).
+// memory) with the layouts the decode kernels use: method 1: 8 waves x 4 terms per lane, 2: 4
+// waves x 4 (waves 0..3), 3: 4 waves x 4 (waves 0, 5, 6, 7), 4: 2 waves x 8, 5: 4 waves x 8,
+// 6: 4 waves x 12; method 0: one lane.
 __global__ __launch_bounds__(512) void k_seq_sum(const float *__restrict__ x, uint32_t n, int method, float *out) {
     __shared__ __align__(16) float a[4096];
     __shared__ xsum::Scratch L;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (n > 4096) {
         if (tid == 0) {
             float s = 0.0f;
@@ -549,12 +551,28 @@ __global__ __launch_bounds__(512) void k_seq_sum(const float *__restrict__ x, ui
     for (uint32_t i = tid; i < 4096; i += 512) a[i] = i < n ? x[i] : 0.0f;
     if (tid == 0) L.sync = 0;
     __syncthreads();
-    if (method == 1) {
-        const float r = block_seq_sum<8, 4>(a, n, L, tid >> 6, tid & 63);
-        if (tid == 0) *out = r;
-    } else if (tid == 0) {
-        *out = seq_sum_lds(a, n, 0.0f);
+    float r = 0.0f;
+    switch (method) {
+    case 1: r = block_seq_sum<8, 4>(a, n, L, wave, lane); break;
+    case 2:
+        if (wave < 4) r = block_seq_sum<4, 4>(a, n, L, wave, lane);
+        break;
+    case 3:
+        if (wave == 0 || wave >= 5) r = block_seq_sum<4, 4>(a, n, L, wave == 0 ? 0 : wave - 4, lane);
+        break;
+    case 4:
+        if (wave < 2) r = block_seq_sum<2, 8>(a, n, L, wave, lane);
+        break;
+    case 5:
+        if (wave < 4) r = block_seq_sum<4, 8>(a, n, L, wave, lane);
+        break;
+    case 6:
+        if (wave < 4) r = block_seq_sum<4, 12>(a, n, L, wave, lane);
+        break;
+    default:
+        if (tid == 0) r = seq_sum_lds(a, n, 0.0f);
     }
+    if (tid == 0) *out = r;
 }
 
 // ------------------------------------------------------------------ embedding

@@ -177,9 +177,10 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
 
 /* The sequential binary32 sum out = ((0 + x[0]) + x[1]) + ... + x[n-1] that ops::rmsnorm
  * (`ss += v * v`, ops.rs:101-104) and ops::softmax (`sum += *v`, ops.rs:119-122) form, computed
- * on the device by the method the decode kernels use for it: method 1 = one workgroup
- * (identical bits for non-negative terms, n <= 4096; other inputs fall back to one lane),
- * method 0 = one lane adding in index order. */
+ * on the device by the method the decode kernels use for it: methods 1..6 = the workgroup
+ * layouts of those kernels (waves x terms per lane: 8x4, 4x4, 4x4 on waves 0,5,6,7, 2x8, 4x8,
+ * 4x12; identical bits for non-negative terms; other inputs or n beyond the layout fall back
+ * to one lane), method 0 = one lane adding in index order (n <= 4096 in LDS). */
 int hg_seq_sum(const float *x, uint32_t n, uint32_t method, float *out);
 
 /* ---- measurement (no counterpart in the reference) ------------------------------------ */

@@ -82,7 +82,22 @@ def _cases():
 @pytest.mark.parametrize("name,x", _cases(), ids=lambda v: v if isinstance(v, str) else "")
 def test_workgroup_sum_matches_sequential(hg, name, x):
     want = _seq(x)
-    for method in (1, 0):
+    for method in (1, 2, 3, 4, 5, 6, 0):   # every wave layout of the decode kernels, one lane
         got = hg.seq_sum(x, method)
         assert np.array_equal(np.float32(got).view(np.uint32), np.float32(want).view(np.uint32)) or (
             np.isnan(got) and np.isnan(want)), (name, method, got, want)
+
+
+def test_norm_inputs_of_the_130m_model(hg):
+    """Sums of squares of real embeddings (the first RMSNorm of a synthetic 130M model), and
+    the same vectors cut to every length the layouts split differently."""
+    from hobbylm_amd import gguf_synth as gs
+    m = hg.Model(gs.synth_path("130M", 0))
+    for t in gs.prompt_ids(7, 4, 50257):
+        x = m.token_embedding(int(t))
+        sq = (x * x).astype(np.float32)
+        for n in (64, 255, 256, 257, 511, 512, len(sq)):
+            want = _seq(sq[:n])
+            for method in (1, 2, 3, 4, 5, 6):
+                got = hg.seq_sum(sq[:n], method)
+                assert np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32), (int(t), n, method)
