@@ -275,51 +275,64 @@ __device__ inline float seq_sum_lds(const float *a, uint32_t n, float s) {
 // ------------------------------------------------------------------ exact parallel sum
 // The same sequential binary32 sum 0 + a[0] + ... + a[n-1] of non-negative terms (the
 // reference's `ss += v * v` of rmsnorm, ops.rs:101-104, and `sum += *v` of softmax,
-// ops.rs:119-122), formed by one wave with identical result bits.
+// ops.rs:119-122), formed by a few waves with identical result bits.
 //
 // Why it can be parallel.  While the running sum s stays in one binade [2^e, 2^(e+1)) (binade
 // -126 also holds zero and the subnormals; the quantum is u = 2^(e-23) in both) it is an
-// integer number of quanta, and an add whose result stays in the binade contributes
-// round(a / u) quanta, independent of s, unless a / u is an exact half (a tie: s's parity
-// decides).  So if the binades of the sums before and after each add were known, all but a
-// few adds (those that change the binade, ties, and adds whose binade is uncertain) would be
-// integer increments that a prefix sum adds exactly; the few "events" stay real float adds.
+// integer number of quanta, and each add rounds to the quantum grid, so what a stretch of adds
+// contributes depends only on the terms and on the parity of s at its start (round half to
+// even is the only place s enters).  A lane that holds EPT consecutive terms and knows their
+// adds stay in binade e replays them from the anchors c = 2^e (even; 0 for binade -126) and
+// c + u (odd): both chains stay in the binade, so each reproduces the true adds for a start of
+// its parity.  If the two increments agree, the lane adds that many quanta whatever s is; they
+// differ exactly when one of its adds is a tie.
 //
 // Certification.  Each add errs by at most 2^-24 of its result (results below 2^-125 are
 // exact) and s never decreases, so with T_k = a[0] + ... + a[k-1] (real numbers)
-// |s_k - T_k| <= k 2^-24 (T_k + |s_k - T_k|), i.e. <= 1.001 k 2^-24 T_k for k <= 2^14.  The
-// wave forms every T_k in binary32 as (exclusive scan of the lanes' partial sums) + (lane's
-// running sum): relative error below 48 * 2^-24 for EPT <= 32; a margin R = 2^-16 covers it
-// and the rounding of the bound products.  s_k then lies in [T~_k (1 - R - C k),
+// |s_k - T_k| <= k 2^-24 (T_k + |s_k - T_k|), i.e. <= 1.001 k 2^-24 T_k for k <= 2^14.  Lanes
+// form T_k in binary32 from their partial sums, a wave scan and the previous waves' terms
+// (at most 64 roundings deep, relative error below 2^-18); a margin R = 2^-16 covers that and
+// the rounding of the bound products.  s_k then lies in [T~_k (1 - R - C k),
 // T~_k (1 + R + C k)] with C = 1.01 2^-24.  A lane whose bracket from its first sum to its
-// last lies in one binade (nearly all lanes) needs nothing per term; a lane whose bracket
-// crosses one boundary 2^b classifies each term by its own bracket; otherwise all its terms
-// are events.
+// last lies in one binade is "clean"; two consecutive clean lanes always share their binade
+// (the brackets at their common boundary both hold s).
 //
-// Schedule (wave 0 only, no workgroup barrier): lane l holds terms l EPT .. l EPT + EPT - 1;
-// (1) running sums and an exclusive scan give every bracket; (2) terms are classified and
-// rounded to quanta, scans give the exclusive quanta prefix IP_k (mod 2^32) and event count;
-// (3) events are written compactly to LDS (IP at the event, the term) with the binade of the
-// run of increments before each; (4) lane j forms incr_j = (IP at event j - IP at event j-1)
-// quanta of its run's binade (an exact add: the run stays in its binade), and the wave adds
-// incr_0, a_(k_0), incr_1, a_(k_1), ..., incr_m in order.  Negative, NaN or infinite terms, a
-// total that may overflow, n > 64 EPT or more than MCAP events fall back to adding every term.
+// Schedule.  Every participant wave, without waiting for the others: lane l of wave p holds
+// terms (64 p + l) EPT .. + EPT - 1 and sums the previous waves' terms at its own position
+// (their wave total is the wave's offset); brackets classify the lanes; clean lanes with
+// agreeing chains contribute their quanta to a wave scan, every other lane (binade crossings,
+// ties) is an "event lane" whose terms stay real float adds; the wave records its event lanes
+// (quanta prefix, position, the binade of the lane before) and totals in LDS.  After one
+// meeting, lane j of wave 0 takes event lane j's terms and incr_j, the clean quanta between
+// event lanes j - 1 and j as one exact float of the run's binade; the ordered adds incr_0, the
+// terms of event lane 0, incr_1, ..., incr_M then run lane by lane, each lane receiving the
+// sum so far from the one before.  Negative, NaN or infinite terms, a total that may overflow,
+// n > NPW 64 EPT, more than EVCAP event lanes in a wave or more than 64 in all fall back to
+// adding every term.
 namespace xsum {
-constexpr uint32_t MCAP = 256;
+constexpr uint32_t EVCAP = 32;    // event lanes recorded per wave
 struct Scratch {
     uint32_t sync;   // participant arrivals (zeroed by the caller before a workgroup barrier)
-    float wt[8];
-    uint32_t wbad[8], wd[8], we[8];
-    uint32_t ipev[MCAP];
-    float aev[MCAP];
-    int32_t sege[MCAP + 1];
-    __attribute__((aligned(16))) float c[2 * MCAP + 32];
+    uint32_t wbad[8], wm[8], wq[8];
+    int32_t wtail[8], efin;
+    uint32_t evip[8][EVCAP];   // quanta before the event lane (wave-local prefix, mod 2^32)
+    uint32_t evk[8][EVCAP];    // lane | (binade of the lane before + 127) << 8 (0: the wave's first lane)
 };
 }   // namespace xsum
 
 template <int CTRL, int RM>
 __device__ inline uint32_t dpp_zero(uint32_t v) {   // lanes without a source (or masked rows) read 0
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RM, 0xf, true);
+}
+// Pins a value computed by lane exchanges to where it is written, so that the compiler cannot
+// move the exchange under a lane-dependent branch (source lanes outside it would read 0).
+__device__ inline uint32_t pin_u(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+__device__ inline float pin_f(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
 }
 // Inclusive scans over the 64 lanes: row_shr 1, 2, 4, 8 within rows of 16, then row_bcast 15
 // (rows 1, 3) and row_bcast 31 (rows 2, 3).
@@ -330,22 +343,24 @@ __device__ inline uint32_t wave_scan_u(uint32_t v) {
     v += dpp_zero<0x118, 0xf>(v);
     v += dpp_zero<0x142, 0xa>(v);
     v += dpp_zero<0x143, 0xc>(v);
-    return v;
+    return pin_u(v);
 }
 template <int CTRL, int RM>
 __device__ inline float dpp_zero_f(float v) {
     return __builtin_bit_cast(float, dpp_zero<CTRL, RM>(__builtin_bit_cast(uint32_t, v)));
 }
-// exclusive scan: wave_shr 1 (lane 0 reads 0), then the inclusive scan
-__device__ inline float wave_excl_scan_f(float v) {
-    v = dpp_zero_f<0x138, 0xf>(v);
+__device__ inline float wave_incl_scan_f(float v) {
     v += dpp_zero_f<0x111, 0xf>(v);
     v += dpp_zero_f<0x112, 0xf>(v);
     v += dpp_zero_f<0x114, 0xf>(v);
     v += dpp_zero_f<0x118, 0xf>(v);
     v += dpp_zero_f<0x142, 0xa>(v);
     v += dpp_zero_f<0x143, 0xc>(v);
-    return v;
+    return pin_f(v);
+}
+// exclusive scan: wave_shr 1 (lane 0 reads 0), then the inclusive scan
+__device__ inline float wave_excl_scan_f(float v) {
+    return wave_incl_scan_f(dpp_zero_f<0x138, 0xf>(v));
 }
 // binade exponent of x >= 0 (x < 2^-126: -126)
 __device__ inline int binade_of(float x) {
@@ -356,7 +371,7 @@ __device__ inline float rlane_f(float v, uint32_t l) {
 }
 
 // Meeting point of the NPW participant waves only (the other waves of the workgroup are not
-// waited for): arrival count in LDS, phase ph = 1, 2, 3.
+// waited for): arrival count in LDS, phase ph = 1, 2, ...
 template <int NPW>
 __device__ inline void part_sync(xsum::Scratch &L, uint32_t ph) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -368,168 +383,142 @@ __device__ inline void part_sync(xsum::Scratch &L, uint32_t ph) {
 
 // a: LDS, 16-byte aligned, readable up to a multiple of 4 terms past n.  The waves with
 // p = 0 .. NPW - 1 call (p uniform per wave; p = 0 is the wave that receives the result); they
-// meet three times among themselves, so the other waves of the workgroup keep working.  L.sync
-// must be 0 on entry (zeroed before a workgroup barrier).  Lane l of wave p holds terms
-// (64 p + l) EPT .. + EPT - 1 (EPT = 4: consecutive lanes read consecutive 16 bytes).
+// meet once among themselves, so the other waves of the workgroup keep working.  L.sync must be
+// 0 on entry (zeroed before a workgroup barrier).
 template <int NPW, int EPT>
-__device__ __forceinline__ float block_seq_sum(const float *a, uint32_t n, xsum::Scratch &L, int p, int lane) {
-    static_assert(NPW >= 1 && NPW <= 8 && EPT % 4 == 0 && EPT <= 32, "per-wave totals, term masks");
+__device__ __forceinline__ float block_seq_sum(const float *a, uint32_t n, xsum::Scratch &L, int p_, int lane) {
+    static_assert(NPW >= 1 && NPW <= 8 && EPT % 4 == 0 && EPT <= 16, "wave tables, offsets depth");
     constexpr float C = 1.01f * 0x1p-24f, R = 0x1p-16f;
     constexpr uint32_t WT = 64 * EPT;   // terms per wave
+    const int p = __builtin_amdgcn_readfirstlane(p_);
     const uint32_t k0 = (uint32_t)(64 * p + lane) * EPT;
-    const bool fits = n <= WT * NPW;                              // (uniform)
-    const bool act = fits && p >= 0 && WT * (uint32_t)p < n;      // (uniform per wave)
-    float v[EPT], pp[EPT + 1];
-    pp[0] = 0.0f;
-    float woff = 0.0f;
-    if (act) {   // (1) terms, running sums, the wave's exclusive scan
-        bool bad = false;
+    const bool fits = n <= WT * NPW;                      // (uniform)
+    const bool act = fits && WT * (uint32_t)p < n;        // (uniform per wave)
+    const v4f *a4 = reinterpret_cast<const v4f *>(a);
+    if (act) {
+        float v[EPT];
 #pragma unroll
         for (int u = 0; u < EPT / 4; ++u) {
             v4f r = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (k0 + 4 * u < n) r = reinterpret_cast<const v4f *>(a)[k0 / 4 + u];
+            if (k0 + 4 * u < n) r = a4[k0 / 4 + u];
             v[4 * u] = r.x;
             v[4 * u + 1] = r.y;
             v[4 * u + 2] = r.z;
             v[4 * u + 3] = r.w;
         }
+        uint32_t mx = 0;   // largest bit pattern: above 0x7f7fffff is negative, -0, inf or NaN
+        float t = 0.0f;
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
             v[i] = k0 + i < n ? v[i] : 0.0f;
-            bad |= !(v[i] >= 0.0f && v[i] <= 0x1.fffffep127f);   // (NaN fails)
-            pp[i + 1] = pp[i] + v[i];
+            mx = max(mx, __builtin_bit_cast(uint32_t, v[i]));
+            t = t + v[i];
         }
-        woff = wave_excl_scan_f(pp[EPT]);
-        if (lane == 63) L.wt[p] = woff + pp[EPT];
-        if (lane == 0) L.wbad[p] = __builtin_amdgcn_ballot_w64(bad) != 0;
-    } else {
+        float x = 0.0f;   // the previous waves' terms at this lane's position (all below n)
+#pragma unroll
+        for (int w = 0; w < NPW - 1; ++w)
+            if (w < p) {
+#pragma unroll
+                for (int u = 0; u < EPT / 4; ++u) {
+                    const v4f r = a4[(uint32_t)(64 * w + lane) * (EPT / 4) + u];
+                    x = ((x + r.x) + (r.y + r.z)) + r.w;
+                }
+            }
+        const float before = p > 0 ? rlane_f(wave_incl_scan_f(x), 63) : 0.0f;
+        const float off = before + wave_excl_scan_f(t);
+        const float lo = off * (1.0f - R - C * (float)k0), hi = (off + t) * (1.0f + R + C * (float)(k0 + EPT));
+        const bool bad = mx > 0x7f7fffffu || !(hi < 0x1p126f);
+        const int el = binade_of(lo), eh = binade_of(hi);
+        const bool in = k0 < n;
+        // both parity chains from the anchors of binade el (meaningful for clean lanes)
+        const float cA = el == -126 ? 0.0f : __builtin_bit_cast(float, (uint32_t)(el + 127) << 23);
+        const float cB = cA + ldexpf(1.0f, el - 23);
+        float A = cA, B = cB;
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
-            v[i] = 0.0f;
-            pp[i + 1] = 0.0f;
+            A = A + v[i];
+            B = B + v[i];
         }
+        const uint32_t qA = (uint32_t)ldexpf(A - cA, 23 - el), qB = (uint32_t)ldexpf(B - cB, 23 - el);
+        const bool ev = in && (el != eh || qA != qB);
+        const uint32_t q = in && !ev ? qA : 0u;
+        const uint32_t qi = wave_scan_u(q);
+        const uint64_t em = __builtin_amdgcn_ballot_w64(ev);
+        const bool anyb = __builtin_amdgcn_ballot_w64(bad) != 0;
+        const uint32_t idx = __builtin_amdgcn_mbcnt_hi((uint32_t)(em >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)em, 0u));
+        const uint32_t ep = pin_u(dpp_zero<0x138, 0xf>((uint32_t)(el + 127)));   // the lane before (lane 0: 0)
+        const uint32_t nev = (uint32_t)__builtin_popcountll(em);
+        if (ev && idx < xsum::EVCAP) {
+            L.evip[p][idx] = qi - q;
+            L.evk[p][idx] = (uint32_t)lane | ep << 8;
+        }
+        if (lane == 63) {
+            L.wq[p] = qi;
+            L.wtail[p] = el;
+        }
+        if (lane == 0) {
+            L.wm[p] = min(nev, xsum::EVCAP);
+            L.wbad[p] = anyb || nev > xsum::EVCAP;
+        }
+        if (in && k0 + EPT >= n) L.efin = el;   // the last lane: binade of the final run
     }
     part_sync<NPW>(L, 1);
-    float off = 0.0f, tot = 0.0f;
-    uint32_t anybad = 0;
+    if (p != 0) return 0.0f;
+    // wave 0: the event lanes' offsets in the list, the quanta before each wave
+    uint32_t mb[NPW], qb[NPW], M = 0, Q = 0, anybad = 0;
 #pragma unroll
     for (int w = 0; w < NPW; ++w) {
         const bool has = WT * (uint32_t)w < n;
-        const float t = has ? L.wt[w] : 0.0f;
-        if (w < p) off += t;
-        tot += t;
+        mb[w] = M;
+        qb[w] = Q;
+        M += has ? L.wm[w] : 0u;
+        Q += has ? L.wq[w] : 0u;
         anybad |= has ? L.wbad[w] : 0u;
     }
-    off += woff;
-    const bool serial0 = !fits || anybad || !(tot < 0x1p126f);   // (uniform)
-    // (2) classification and quanta
-    const int el = binade_of(off * (1.0f - R - C * (float)k0)),
-              eh = binade_of((off + pp[EPT]) * (1.0f + R + C * (float)(k0 + EPT)));
-    uint32_t evm = 0, abm = 0, dsum = 0, esum = 0;
-    auto quanta = [&](int i, bool *tie) {
-        const int e = ((abm >> i) & 1) ? eh : el;
-        const float y = fminf(ldexpf(v[i], 23 - e), 0x1p25f);
-        const float fl = floorf(y), fr = y - fl;
-        *tie = fr == 0.5f;
-        return (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
-    };
-    if (act && !serial0) {
-        // one boundary 2^eh inside the bracket: each term by its own bracket; more: all events
-        const float B = __builtin_bit_cast(float, (uint32_t)(min(eh, 127) + 127) << 23);
-        const bool one = eh == el + 1;
+    if (!fits || anybad || M > 64) return rlane_f(lane == 0 ? seq_sum_lds(a, n, 0.0f) : 0.0f, 0);
+    // lane j < M: event lane j's terms, the quanta before it (mod 2^32) and its run's binade
+    uint32_t ip = 0;
+    int e = -126;
+    float tv[EPT];
 #pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-            const float k = (float)(k0 + i);
-            const bool below = (off + pp[i + 1]) * (1.0f + R + C * (k + 1.0f)) < B,
-                       above = (off + pp[i]) * (1.0f - R - C * k) >= B;
-            abm |= (uint32_t)(el != eh && one && above) << i;
-            evm |= (uint32_t)(el != eh && !(one && (below || above))) << i;
-        }
+    for (int i = 0; i < EPT; ++i) tv[i] = 0.0f;
+    if ((uint32_t)lane < M) {
+        uint32_t w = 0, mw = 0, qw = 0;
 #pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-            bool tie;
-            const uint32_t q = quanta(i, &tie);
-            const bool in = k0 + i < n;
-            const bool ev = in && (((evm >> i) & 1) || tie);
-            evm = (evm & ~(1u << i)) | ((uint32_t)ev << i);
-            dsum += (in && !ev) ? q : 0u;
-            esum += ev ? 1u : 0u;
-        }
-    }
-    uint32_t di = 0, ei = 0;
-    if (act) {
-        di = wave_scan_u(dsum);
-        ei = wave_scan_u(esum);
-        if (lane == 63) {
-            L.wd[p] = di;
-            L.we[p] = ei;
-        }
-    }
-    part_sync<NPW>(L, 2);
-    uint32_t ioff = di - dsum, eoff = ei - esum, itot = 0, m = 0;
-#pragma unroll
-    for (int w = 0; w < NPW; ++w) {
-        const bool has = WT * (uint32_t)w < n;
-        const uint32_t x = has ? L.wd[w] : 0u, y = has ? L.we[w] : 0u;
-        itot += x;
-        m += y;
-        if (w < p) {
-            ioff += x;
-            eoff += y;
-        }
-    }
-    const bool serial = serial0 || m > xsum::MCAP;   // (uniform)
-    // (3) events and run binades (a run's first lane writes its binade; a run can also be
-    // written by an earlier lane of an unclean thread or the first lane of a wave, always with
-    // the same value)
-    const uint32_t eprev = dpp_zero<0x138, 0xf>(eoff);   // the previous lane's eoff (lane 0: 0)
-    if (act && !serial && k0 < n) {
-        if (evm == 0) {
-            if (lane == 0 || eprev != eoff) L.sege[eoff] = el;
-        } else {
-            uint32_t ip = ioff, ec = eoff;
-            bool after = true;
-#pragma unroll
-            for (int i = 0; i < EPT; ++i) {
-                const bool in = k0 + i < n, ev = (evm >> i) & 1;
-                bool tie;
-                const uint32_t q = quanta(i, &tie);
-                if (in && ev) {
-                    L.ipev[ec] = ip;
-                    L.aev[ec] = v[i];
-                }
-                if (in && !ev && after) L.sege[ec] = ((abm >> i) & 1) ? eh : el;
-                ec += (in && ev) ? 1u : 0u;
-                ip += (in && !ev) ? q : 0u;
-                after = in ? ev : after;
+        for (int q = 1; q < NPW; ++q)
+            if (mb[q] <= (uint32_t)lane && WT * (uint32_t)q < n) {
+                w = q;
+                mw = mb[q];
+                qw = qb[q];
             }
+        const uint32_t ix = (uint32_t)lane - mw;
+        ip = L.evip[w][ix] + qw;
+        const uint32_t kw = L.evk[w][ix];
+        const int ep = (int)(kw >> 8) - 127;
+        e = ep == -127 ? (w > 0 ? L.wtail[w - 1] : -126) : ep;
+        const uint32_t kj = (64 * w + (kw & 63)) * EPT;
+#pragma unroll
+        for (int u = 0; u < EPT / 4; ++u) {
+            const v4f r = a4[kj / 4 + u];
+            tv[4 * u] = kj + 4 * u < n ? r.x : 0.0f;
+            tv[4 * u + 1] = kj + 4 * u + 1 < n ? r.y : 0.0f;
+            tv[4 * u + 2] = kj + 4 * u + 2 < n ? r.z : 0.0f;
+            tv[4 * u + 3] = kj + 4 * u + 3 < n ? r.w : 0.0f;
         }
     }
-    part_sync<NPW>(L, 3);
-    // (4) incr_0, a_(k_0), ..., incr_m added in order by wave 0, padded with +0 (exact: the sum
-    // is never -0) to whole batches of 32 adds
-    float s = 0.0f;
-    if (p == 0) {
-        if (serial) return rlane_f(lane == 0 ? seq_sum_lds(a, n, 0.0f) : 0.0f, 0);
-        const uint32_t nc = (2 * m + 1 + 31) / 32 * 32;
-        for (uint32_t j = lane; 2 * j < nc; j += 64) {
-            float cj = 0.0f, aj = 0.0f;
-            if (j <= m) {
-                const uint32_t hi = j < m ? L.ipev[j] : itot, lo = j ? L.ipev[j - 1] : 0u;
-                const uint32_t dI = hi - lo;   // < 2^23 quanta: the run stays in its binade
-                const int e = min(max(L.sege[j], -126), 127);   // (unwritten for empty runs)
-                cj = dI ? ldexpf((float)dI, e - 23) : 0.0f;
-            }
-            if (j < m) aj = L.aev[j];
-            L.c[2 * j] = cj;
-            L.c[2 * j + 1] = aj;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        s = rlane_f(lane == 0 ? seq_sum_lds(L.c, nc, 0.0f) : 0.0f, 0);
+    const uint32_t ipp = pin_u(dpp_zero<0x138, 0xf>(ip));   // event lane j - 1's (lane 0: 0)
+    const uint32_t dI = ip - ipp;   // < 2^24 quanta: the run stays in its binade
+    const float inc = (uint32_t)lane < M && dI ? ldexpf((float)dI, min(max(e, -126), 127) - 23) : 0.0f;
+    const uint32_t dF = Q - (M ? (uint32_t)__builtin_amdgcn_readlane((int)ip, (int)(M - 1)) : 0u);
+    const float incF = dF ? ldexpf((float)dF, min(max(L.efin, -126), 127) - 23) : 0.0f;   // the final run
+    // the ordered adds: step j runs in lane j, which receives the sum so far from lane j - 1
+    float x = 0.0f;
+    for (uint32_t j = 0; j < M; ++j) {
+        x = dpp_zero_f<0x138, 0xf>(x) + inc;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) x = x + tv[i];
     }
-    return s;
+    return (M ? rlane_f(x, M - 1) : 0.0f) + incF;
 }
 
 // Test entry: one workgroup sums x[0..n) (n <= 4096 in LDS; larger n: one lane over global
@@ -2187,15 +2176,16 @@ __global__ __launch_bounds__(512) void k_ffn_front(const float *__restrict__ x, 
         }
     }
     __syncthreads();
-    {   // quantization of h for the expert rows (quant.rs:111-123), into this workgroup's LDS
+    if (tid < 128) {   // quantization of h for the expert rows (quant.rs:111-123), into this
+                       // workgroup's LDS, by waves 0-1 while the router waves form the logits
         const uint32_t nb = d / QK;
-        for (uint32_t b0 = 0; b0 < nb; b0 += FF_NT / 8) {
+        for (uint32_t b0 = 0; b0 < nb; b0 += 16) {
             const uint32_t b = b0 + ((uint32_t)tid >> 3);
             const v4f hv = *reinterpret_cast<const v4f *>(hs + min(b, nb - 1) * QK + j * 4);
             const float v[4] = {hv.x, hv.y, hv.z, hv.w};
             quant_block_lane(v, j, min(b, nb - 1), sq, sd, b < nb);
         }
-        zero_pad(nb, Wg.nc, sq, sd, tid, FF_NT);
+        zero_pad(nb, Wg.nc, sq, sd, tid, 128);
     }
     float g = 0.0f;   // the gate of this thread's router row
     if (router) {
