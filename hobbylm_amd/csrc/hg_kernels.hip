@@ -1556,16 +1556,18 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
 }
 
 // Softmax and P.V of one query head, as k_attn_softmax_pv, for caches whose V slice and
-// products fit in LDS (pv_res_fits): no ring.  Workgroup (h, q), 512 threads:
+// products fit in LDS (pv_res_fits): no ring.  Workgroup (h, q), 512 threads, D = 4 output
+// elements: the grid has a workgroup per CU, and a chain wave with few active lanes adds
+// fastest (measured: about 3.4 ns per add with 4 lanes, 4.5 with 16):
 //   every wave forms its share of e_t and signals it (no wait); waves 4..7 then stream the
-//   16-element V slice of all positions transposed into LDS, P[d][t], one group of G positions
-//   per round, while waves 0..3 form the index-order sum of e_t (block_seq_sum).  Once inv is
-//   known (a flag, not a barrier), waves 1..7 replace group g (wave 1 + g % 7) by the rounded
-//   products p_t * V[d][t] (p_t = e_t * inv; -0 past the context, the exact identity of the
-//   chain's adds) as soon as its V is in, and flag it; wave 0 lanes 0..15 run the 16
-//   sequential chains over P, waiting only for each group's flag.
+//   D-element V slice of all positions transposed into LDS, P[d][t], flagging each round,
+//   while waves 0..3 form the index-order sum of e_t (block_seq_sum).  Once inv is known (a
+//   flag, not a barrier), waves 1..7 replace group g (wave 1 + g % 7) by the rounded products
+//   p_t * V[d][t] (p_t = e_t * inv; -0 past the context, the exact identity of the chain's
+//   adds) as soon as its V is in, and flag it; wave 0 lanes 0..D-1 run the D sequential
+//   chains over P, waiting only for each group's flag.
 struct PvResCfg {
-    static constexpr uint32_t D = 16;     // output elements per workgroup
+    static constexpr uint32_t D = 4;      // output elements per workgroup (4 or 8)
     static constexpr uint32_t G = 64;     // positions per product group (two chain chunks)
     static constexpr uint32_t NG = 64;    // product groups: one bit each of the ready mask
     static constexpr uint32_t VB = 8;     // V loads in flight per V thread
@@ -1592,7 +1594,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     constexpr uint32_t D = C::D, G = C::G, EB = 8;
     extern __shared__ __align__(16) float lds[];
     __shared__ uint64_t ready;           // bit g: products of group g written
-    __shared__ uint32_t vdone[4];        // V rounds (groups) written by V wave 4 + i
+    __shared__ uint32_t vdone[4];        // V rounds written by V wave 4 + i (its groups i, i + 4, ...)
     __shared__ uint32_t arrived;         // waves whose e_t are written
     __shared__ uint32_t inv_ready;
     __shared__ float s_inv;
@@ -1640,32 +1642,36 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0) __hip_atomic_fetch_add(&arrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    constexpr uint32_t LP = D / 4;   // lanes per position of the V slice (16 bytes each)
     if (wave >= 4) {
-        // V streamed into P[d][t]: round r, thread vt = tid - 256 -> position 64 r + vt / 4,
-        // elements 4 (vt % 4) .. + 3 (positions past the context: zeros, replaced by -0 later);
-        // VB rounds of loads in flight, then their LDS writes, then this wave's round count
-        const uint32_t vt = (uint32_t)tid - 256, dq = vt & 3, tl = vt >> 2;
-        for (uint32_t r0 = 0; r0 < ng; r0 += C::VB) {
+        // V into P[d][t]: round r, thread vt = tid - 256 -> position (256 r + vt) / LP,
+        // elements 4 c .. 4 c + 3, c = vt % LP: wave 4 + w covers the group (4 r + w) / LP
+        // (positions past the context read row n - 1, replaced by -0 later); VB rounds of loads
+        // in flight, then per round its LDS writes and this wave's round count
+        const uint32_t vt = (uint32_t)tid - 256, c4 = 4 * (vt % LP), nr = div_up(ng * LP, 4);
+        for (uint32_t r0 = 0; r0 < nr; r0 += C::VB) {
             v4f vr[C::VB];
 #pragma unroll
             for (uint32_t u = 0; u < C::VB; ++u) {
-                const uint32_t t = min(G * (r0 + u) + tl, n - 1);
-                const float *src = (t == pos) ? vnew + 4 * dq : vcg + (size_t)t * HD + 4 * dq;
+                const uint32_t t = min((256 * (r0 + u) + vt) / LP, n - 1);
+                const float *src = ((t == pos) ? vnew : vcg + (size_t)t * HD) + c4;
                 vr[u] = *reinterpret_cast<const v4f *>(src);
             }
 #pragma unroll
             for (uint32_t u = 0; u < C::VB; ++u) {
-                const uint32_t t = G * (r0 + u) + tl;
-                if (r0 + u < ng) {
-                    P[(4 * dq + 0) * TPC + t] = vr[u].x;
-                    P[(4 * dq + 1) * TPC + t] = vr[u].y;
-                    P[(4 * dq + 2) * TPC + t] = vr[u].z;
-                    P[(4 * dq + 3) * TPC + t] = vr[u].w;
+                const uint32_t t = (256 * (r0 + u) + vt) / LP;
+                if (r0 + u < nr) {
+                    if (t < G * ng) {
+                        P[(c4 + 0) * TPC + t] = vr[u].x;
+                        P[(c4 + 1) * TPC + t] = vr[u].y;
+                        P[(c4 + 2) * TPC + t] = vr[u].z;
+                        P[(c4 + 3) * TPC + t] = vr[u].w;
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");   // (the later rounds' loads stay in flight)
+                    if (lane == 0)
+                        __hip_atomic_store(&vdone[wave - 4], r0 + u + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane == 0)
-                __hip_atomic_store(&vdone[wave - 4], min(r0 + C::VB, ng), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     } else {   // sum += e_t in index order, once every wave's e_t are written
         while (__hip_atomic_load(&arrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 8u)
@@ -1677,25 +1683,26 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
             __hip_atomic_store(&inv_ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
-    if (wave >= 1) {   // products of groups wave - 1, wave + 6, ...: lane l -> element l / 4,
-                       // positions 16 (l % 4) .. + 15 of the group (four 16-byte steps)
+    if (wave >= 1) {   // products of groups wave - 1, wave + 6, ...: lane l -> element l / (64 / D),
+                       // positions D (l % (64 / D)) .. + D - 1 of the group
         while (__hip_atomic_load(&inv_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u)
             __builtin_amdgcn_s_sleep(1);
         const float inv = s_inv;
-        const uint32_t di = (uint32_t)lane >> 2, tq = (uint32_t)lane & 3;
+        const uint32_t di = (uint32_t)lane / (64 / D), tq = (uint32_t)lane % (64 / D);
         for (uint32_t gi = (uint32_t)wave - 1; gi < ng; gi += 7) {
-            for (;;) {   // this group's V rows are in once every V wave has passed round gi
-                uint32_t v0 = __hip_atomic_load(&vdone[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                v0 = min(v0, __hip_atomic_load(&vdone[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-                v0 = min(v0, __hip_atomic_load(&vdone[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-                v0 = min(v0, __hip_atomic_load(&vdone[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-                if (v0 > gi) break;
+            // this group's V rows are in once V waves 4 + w, w = LP gi - 4 r .. + LP - 1, have
+            // passed round r = LP gi / 4
+            const uint32_t r = LP * gi / 4, w0 = LP * gi - 4 * r;
+            for (;;) {
+                uint32_t v0 = __hip_atomic_load(&vdone[w0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (LP > 1) v0 = min(v0, __hip_atomic_load(&vdone[w0 + LP - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+                if (v0 > r) break;
                 __builtin_amdgcn_s_sleep(1);
             }
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 #pragma unroll
-            for (uint32_t u = 0; u < 4; ++u) {
-                const uint32_t t = G * gi + 16 * tq + 4 * u;
+            for (uint32_t u = 0; u < D / 4; ++u) {
+                const uint32_t t = G * gi + D * tq + 4 * u;
                 v4f *pv = reinterpret_cast<v4f *>(P + di * TPC + t);
                 const v4f ev = *reinterpret_cast<const v4f *>(e + t), vv = *pv;
                 v4f pr;
