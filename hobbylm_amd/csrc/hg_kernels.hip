@@ -1557,23 +1557,23 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
 
 // Softmax and P.V of one query head, as k_attn_softmax_pv, for caches whose V slice and
 // products fit in LDS (pv_res_fits): no ring.  Workgroup (h, q), 512 threads, D = 4 output
-// elements: the grid has a workgroup per CU, and a chain wave with few active lanes adds
-// fastest (measured: about 3.4 ns per add with 4 lanes, 4.5 with 16):
+// elements, so the grid has a workgroup per CU and the chain wave has few active lanes:
 //   every wave forms its share of e_t and signals it (no wait); waves 4..7 then stream the
 //   D-element V slice of all positions transposed into LDS, P[d][t], flagging each round,
 //   while waves 0..3 form the index-order sum of e_t (block_seq_sum).  Once inv is known (a
-//   flag, not a barrier), waves 1..7 replace group g (wave 1 + g % 7) by the rounded products
-//   p_t * V[d][t] (p_t = e_t * inv; -0 past the context, the exact identity of the chain's
-//   adds) as soon as its V is in, and flag it; wave 0 lanes 0..D-1 run the D sequential
-//   chains over P, waiting only for each group's flag.
+//   flag, not a barrier), waves 1..3 and 5..7 (not wave 4, which shares the chain wave's
+//   SIMD) replace group g by the rounded products p_t * V[d][t] (p_t = e_t * inv; -0 past the
+//   context, the exact identity of the chain's adds) as soon as its V is in, and flag it;
+//   wave 0 lanes 0..D-1 run the D sequential chains over P in blocks of 4 groups, waiting only
+//   for each block's flags.
 struct PvResCfg {
     static constexpr uint32_t D = 4;      // output elements per workgroup (4 or 8)
-    static constexpr uint32_t G = 64;     // positions per product group (two chain chunks)
+    static constexpr uint32_t G = 64;     // positions per product group (two chain chunks of 32)
     static constexpr uint32_t NG = 64;    // product groups: one bit each of the ready mask
     static constexpr uint32_t VB = 8;     // V loads in flight per V thread
 };
 
-__host__ __device__ inline uint32_t pv_res_rows(uint32_t cap) { return div_up(cap, 64) * 64; }
+__host__ __device__ inline uint32_t pv_res_rows(uint32_t cap) { return div_up(cap, 256) * 256; }   // chain blocks
 constexpr size_t XSUM_FLOATS = (sizeof(xsum::Scratch) + 15) / 16 * 4;
 __host__ __device__ inline size_t pv_res_lds(uint32_t cap) {   // e, P, the sum's scratch
     const uint32_t rc = pv_res_rows(cap);
@@ -1611,7 +1611,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
     const float *vcg = vc + (size_t)g * cap * HD + q * D;
     const float *vnew = qkv + qd + kvd + g * HD + q * D;   // row pos, appended this step
-    const uint32_t ng = div_up(n, G), npad = div_up(n, 32) * 32;   // groups, chain positions
+    const uint32_t ng = div_up(n, G), nblk = div_up(n, 4 * G);   // V groups, chain blocks of 4 groups
     // loads in issue order: the split maxima, this thread's first scores, the exp table
     float m = pmax[(size_t)h * S + min((uint32_t)lane, S - 1)];
     float sv[EB];
@@ -1683,17 +1683,20 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
             __hip_atomic_store(&inv_ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
-    if (wave >= 1) {   // products of groups wave - 1, wave + 6, ...: lane l -> element l / (64 / D),
-                       // positions D (l % (64 / D)) .. + D - 1 of the group
+    if (wave >= 1 && wave != 4) {
+        // products by the six waves off the chain wave's SIMD (wave 4 shares it with wave 0):
+        // groups pw, pw + 6, ... (pw = 0..5); lane l -> element l / (64 / D), positions
+        // D (l % (64 / D)) .. + D - 1 of the group
         while (__hip_atomic_load(&inv_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u)
             __builtin_amdgcn_s_sleep(1);
         const float inv = s_inv;
         const uint32_t di = (uint32_t)lane / (64 / D), tq = (uint32_t)lane % (64 / D);
-        for (uint32_t gi = (uint32_t)wave - 1; gi < ng; gi += 7) {
+        const uint32_t pw = (uint32_t)wave - (wave < 4 ? 1 : 2);
+        for (uint32_t gi = pw; gi < 4 * nblk; gi += 6) {   // (groups past the context: all -0)
             // this group's V rows are in once V waves 4 + w, w = LP gi - 4 r .. + LP - 1, have
             // passed round r = LP gi / 4
             const uint32_t r = LP * gi / 4, w0 = LP * gi - 4 * r;
-            for (;;) {
+            while (gi < ng) {
                 uint32_t v0 = __hip_atomic_load(&vdone[w0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 if (LP > 1) v0 = min(v0, __hip_atomic_load(&vdone[w0 + LP - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
                 if (v0 > r) break;
@@ -1717,16 +1720,18 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
         }
     }
     if (wave == 0 && lane < (int)D) {
-        // chains: 32 positions (eight 16-byte reads) per chunk, the next chunk's reads issued
-        // before the current chunk's adds (unconditional, index clamped), order pinned
+        // chains: blocks of 256 positions, 32 positions (eight 16-byte reads) per chunk; the next
+        // chunk's reads are issued before the current chunk's adds, in an order pinned by empty
+        // statements that hold the sum and order memory (reads cannot move above them), and the
+        // next block's product flags are checked once per block, before its first reads (a
+        // block's code has no loop, so the compiler's waits stay partial inside it)
         float o = 0.0f;
         const v4f *row = reinterpret_cast<const v4f *>(P + lane * TPC);
-        const uint32_t nch = npad / 32;
         uint64_t known = 0;   // ready bits seen so far
-        auto ready_wait = [&](uint32_t gi) {
-            while (!((known >> gi) & 1)) {
+        auto block_wait = [&](uint32_t b) {   // groups 4 b .. 4 b + 3
+            while (((known >> (4 * b)) & 0xf) != 0xf) {
                 known = __hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-                if (!((known >> gi) & 1)) __builtin_amdgcn_s_sleep(1);
+                if (((known >> (4 * b)) & 0xf) != 0xf) __builtin_amdgcn_s_sleep(1);
             }
         };
         v4f ca[8], cb[8];
@@ -1743,23 +1748,25 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
                 o = o + c[u].w;
             }
         };
-        static_assert(G == 64, "a group is the chunk pair c, c + 1 (c even)");
-        ready_wait(0);
+        static_assert(G == 64, "a block is 8 chunks of 32 positions");
+        block_wait(0);
         ld(ca, 0);
-        for (uint32_t c = 0; c < nch; c += 2) {
-            const uint32_t c1 = min(c + 1, nch - 1), c2 = min(c + 2, nch - 1);
-            __builtin_amdgcn_sched_barrier(0);
-            ld(cb, c1);
-            __builtin_amdgcn_sched_barrier(0);
-            add(ca);
-            __builtin_amdgcn_sched_barrier(0);
-            if (c + 1 >= nch) break;
-            if (c2 != c1) ready_wait(c2 / 2);
-            __builtin_amdgcn_sched_barrier(0);
-            ld(ca, c2);
+        for (uint32_t b = 0; b < nblk; ++b) {
+            const uint32_t c = 8 * b;
+#define HG_PV_STEP(NX, CUR, NXT)                 \
+    ld(NXT, c + (NX));                           \
+    __builtin_amdgcn_sched_barrier(0);           \
+    add(CUR);                                    \
+    asm volatile("" : "+v"(o) : : "memory");
+            HG_PV_STEP(1, ca, cb) HG_PV_STEP(2, cb, ca) HG_PV_STEP(3, ca, cb) HG_PV_STEP(4, cb, ca)
+            HG_PV_STEP(5, ca, cb) HG_PV_STEP(6, cb, ca) HG_PV_STEP(7, ca, cb)
+#undef HG_PV_STEP
+            const bool more = b + 1 < nblk;
+            if (more) block_wait(b + 1);
+            ld(ca, more ? c + 8 : c);   // (the last block rereads its first chunk, unused)
             __builtin_amdgcn_sched_barrier(0);
             add(cb);
-            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("" : "+v"(o) : : "memory");
         }
         o_out[h * HD + q * D + lane] = o;
     }
