@@ -46,5 +46,12 @@ enum { ORDER_DECODE = 0, ORDER_PREFILL = 1 };
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_LOGITS = 2 };
 
 inline __host__ __device__ uint32_t div_up(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+// The V cache of a layer holds the rows [n_kv][cap][hd] and, after them, the same values
+// transposed, [n_kv][hd][vt_stride(cap)], which the resident P.V kernel reads as contiguous
+// position runs of one element.
+inline __host__ __device__ uint32_t vt_stride(uint32_t cap) { return (cap + 63) / 64 * 64; }
+inline __host__ __device__ size_t v_layer_floats(uint32_t cap, uint32_t n_kv, uint32_t hd) {
+    return (size_t)n_kv * hd * (cap + vt_stride(cap));
+}
 
 }  // namespace hg

@@ -145,7 +145,7 @@ struct hg_kv {
     bool exact = false;
     uint32_t S = 0;         // attention context splits
     uint32_t lm_threads = 256, n_part = 0;
-    DevBuf kc, vc;          // [L][n_kv][cap][hd]
+    DevBuf kc, vc;          // [L][n_kv][cap][hd]; V: each layer also [n_kv][hd][vt_stride(cap)]
     DevBuf x, qkv, o, part, scores, a, logits, pv, pi, qa, da, topk_idx, topk_w, order, rec_idx, rec_w, params,
         out_ids, inputs;
     uint32_t inputs_rows = 0;
@@ -354,7 +354,7 @@ float *layer_k(const hg_kv *kv, uint32_t l) {
 }
 float *layer_v(const hg_kv *kv, uint32_t l) {
     const hg_config &c = kv->m->c;
-    return kv->vc.as<float>() + (size_t)l * c.n_kv_heads * kv->cap * c.head_dim;
+    return kv->vc.as<float>() + (size_t)l * v_layer_floats(kv->cap, c.n_kv_heads, c.head_dim);
 }
 
 void enqueue_layers(hg_kv *kv, int order) {
@@ -546,7 +546,9 @@ int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out) 
     HIP_TRY(hipStreamCreateWithFlags(&kv->st, hipStreamNonBlocking));
     const size_t kvsz = (size_t)c.n_layers * c.n_kv_heads * kv->cap * c.head_dim * 4;
     int rc;
-    if ((rc = kv->kc.alloc(kvsz)) || (rc = kv->vc.alloc(kvsz))) return rc;
+    if ((rc = kv->kc.alloc(kvsz)) ||
+        (rc = kv->vc.alloc((size_t)c.n_layers * v_layer_floats(kv->cap, c.n_kv_heads, c.head_dim) * 4)))
+        return rc;
     const uint32_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
     const uint32_t maxk = std::max(std::max(c.d_model, qd), std::max(c.dense_ffn, c.expert_ffn));
     const uint32_t maxnc = div_up(maxk / QK, 4);
@@ -967,11 +969,14 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
     memcpy(qkv.data(), q, qd * 4);
     memcpy(qkv.data() + qd, k, kvd * 4);
     memcpy(qkv.data() + qd + kvd, v, kvd * 4);
-    std::vector<float> kh((size_t)n_kv * cap * hd, 0.0f), vh(kh.size(), 0.0f);
+    std::vector<float> kh((size_t)n_kv * cap * hd, 0.0f), vh(v_layer_floats(cap, n_kv, hd), 0.0f);
+    float *vth = vh.data() + (size_t)n_kv * cap * hd;   // the transposed copy
     for (uint32_t t = 0; t < pos; ++t)
         for (uint32_t g = 0; g < n_kv; ++g) {
             memcpy(&kh[((size_t)g * cap + t) * hd], kc + ((size_t)t * n_kv + g) * hd, hd * 4);
             memcpy(&vh[((size_t)g * cap + t) * hd], vc + ((size_t)t * n_kv + g) * hd, hd * 4);
+            for (uint32_t i = 0; i < hd; ++i)
+                vth[((size_t)g * hd + i) * vt_stride(cap) + t] = vc[((size_t)t * n_kv + g) * hd + i];
         }
     std::vector<float> cs, sn;
     rope_table(hd, rope_len, theta, cs, sn);
@@ -1037,7 +1042,8 @@ int hg_attention_time(uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t ctx
         st ^= st << 13; st ^= st >> 7; st ^= st << 17;
         return (float)((double)(st >> 11) * 0x1p-53 * 2.0 - 1.0) * 1.7320508f;
     };
-    std::vector<float> qkv(qd + 2 * kvd), kh((size_t)n_kv * cap * hd), vh(kh.size()), ones(hd, 1.0f), cs, sn;
+    std::vector<float> qkv(qd + 2 * kvd), kh((size_t)n_kv * cap * hd), vh(v_layer_floats(cap, n_kv, hd)),
+        ones(hd, 1.0f), cs, sn;   // (vh: the rows and their transposed copy, random alike: timing only)
     for (float &v : qkv) v = rnd();
     for (float &v : kh) v = rnd();
     for (float &v : vh) v = rnd();

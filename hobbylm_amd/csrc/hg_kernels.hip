@@ -1027,9 +1027,11 @@ __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const floa
     if (kind == 2) {
         const uint32_t g = hh - n_heads - n_kv;
         float *vcr = vc + ((size_t)g * cap + pos) * HD;
+        float *vtr = vc + (size_t)n_kv * cap * HD + (size_t)g * HD * vt_stride(cap) + pos;
         for (uint32_t i = lane; i < HD; i += 64) {
             dst[i] = hv[i];
             vcr[i] = hv[i];
+            vtr[(size_t)i * vt_stride(cap)] = hv[i];
         }
         return;
     }
@@ -1064,8 +1066,13 @@ __global__ __launch_bounds__(64) void k_qk_rope_append(float *qkv, const float *
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (hh >= n_heads + n_kv) {
-        float *vcr = vc + ((size_t)(hh - n_heads - n_kv) * cap + pos) * HD;
-        for (uint32_t i = lane; i < HD; i += 64) vcr[i] = u[i];
+        const uint32_t g = hh - n_heads - n_kv;
+        float *vcr = vc + ((size_t)g * cap + pos) * HD;
+        float *vtr = vc + (size_t)n_kv * cap * HD + (size_t)g * HD * vt_stride(cap) + pos;
+        for (uint32_t i = lane; i < HD; i += 64) {
+            vcr[i] = u[i];
+            vtr[(size_t)i * vt_stride(cap)] = u[i];
+        }
         return;
     }
     norm_rope_head<HD>(u, o, hc, hh < n_heads, eps, tmp, lane);
@@ -1559,8 +1566,8 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
 // products fit in LDS (pv_res_fits): no ring.  Workgroup (h, q), 512 threads, D = 4 output
 // elements, so the grid has a workgroup per CU and the chain wave has few active lanes:
 //   every wave forms its share of e_t and signals it (no wait); waves 4..7 then stream the
-//   D-element V slice of all positions transposed into LDS, P[d][t], flagging each round,
-//   while waves 0..3 form the index-order sum of e_t (block_seq_sum).  Once inv is known (a
+//   D rows of V's transposed copy (contiguous positions) into LDS, P[d][t], flagging each
+//   round, while waves 0..3 form the index-order sum of e_t (block_seq_sum).  Once inv is known (a
 //   flag, not a barrier), waves 1..3 and 5..7 (not wave 4, which shares the chain wave's
 //   SIMD) replace group g by the rounded products p_t * V[d][t] (p_t = e_t * inv; -0 past the
 //   context, the exact identity of the chain's adds) as soon as its V is in, and flag it;
@@ -1608,9 +1615,8 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     float *P = lds + rc;                                    // [D][TPC]  V, then the products
     xsum::Scratch &xs = *reinterpret_cast<xsum::Scratch *>(P + (size_t)D * TPC);
     const float *sc = scores + (size_t)h * cap;
-    const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
-    const float *vcg = vc + (size_t)g * cap * HD + q * D;
-    const float *vnew = qkv + qd + kvd + g * HD + q * D;   // row pos, appended this step
+    static_assert(D == 4, "a lane moves 16 bytes of one element's row");
+    const float *vtg = vc + (size_t)n_kv * cap * HD + ((size_t)g * HD + q * D) * vt_stride(cap);   // rows q D ..
     const uint32_t ng = div_up(n, G), nblk = div_up(n, 4 * G);   // V groups, chain blocks of 4 groups
     // loads in issue order: the split maxima, this thread's first scores, the exp table
     float m = pmax[(size_t)h * S + min((uint32_t)lane, S - 1)];
@@ -1642,34 +1648,30 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0) __hip_atomic_fetch_add(&arrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    constexpr uint32_t LP = D / 4;   // lanes per position of the V slice (16 bytes each)
+    constexpr uint32_t LP = 1;   // V waves per group
     if (wave >= 4) {
-        // V into P[d][t]: round r, thread vt = tid - 256 -> position (256 r + vt) / LP,
-        // elements 4 c .. 4 c + 3, c = vt % LP: wave 4 + w covers the group (4 r + w) / LP
-        // (positions past the context read row n - 1, replaced by -0 later); VB rounds of loads
-        // in flight, then per round its LDS writes and this wave's round count
-        const uint32_t vt = (uint32_t)tid - 256, c4 = 4 * (vt % LP), nr = div_up(ng * LP, 4);
+        // V into P[d][t] from the transposed copy: round r, wave 4 + w -> group g = 4 r + w,
+        // lane l -> element l / 16, positions 64 g + 4 (l % 16) .. + 3 (16 contiguous bytes; the
+        // rows run to vt_stride(cap), positions past the context are replaced by -0 later); VB
+        // rounds of loads in flight, then per round its LDS writes and this wave's round count
+        const uint32_t w4 = (uint32_t)wave - 4, d4 = (uint32_t)lane >> 4, t4 = 4 * ((uint32_t)lane & 15);
+        const float *vrow = vtg + (size_t)d4 * vt_stride(cap) + t4;
+        const uint32_t nr = div_up(ng, 4);
         for (uint32_t r0 = 0; r0 < nr; r0 += C::VB) {
             v4f vr[C::VB];
 #pragma unroll
             for (uint32_t u = 0; u < C::VB; ++u) {
-                const uint32_t t = min((256 * (r0 + u) + vt) / LP, n - 1);
-                const float *src = ((t == pos) ? vnew : vcg + (size_t)t * HD) + c4;
-                vr[u] = *reinterpret_cast<const v4f *>(src);
+                const uint32_t gg = min(4 * (r0 + u) + w4, ng - 1);
+                vr[u] = *reinterpret_cast<const v4f *>(vrow + G * gg);
             }
 #pragma unroll
             for (uint32_t u = 0; u < C::VB; ++u) {
-                const uint32_t t = (256 * (r0 + u) + vt) / LP;
+                const uint32_t gg = 4 * (r0 + u) + w4;
                 if (r0 + u < nr) {
-                    if (t < G * ng) {
-                        P[(c4 + 0) * TPC + t] = vr[u].x;
-                        P[(c4 + 1) * TPC + t] = vr[u].y;
-                        P[(c4 + 2) * TPC + t] = vr[u].z;
-                        P[(c4 + 3) * TPC + t] = vr[u].w;
-                    }
+                    if (gg < ng) *reinterpret_cast<v4f *>(P + d4 * TPC + G * gg + t4) = vr[u];
                     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");   // (the later rounds' loads stay in flight)
                     if (lane == 0)
-                        __hip_atomic_store(&vdone[wave - 4], r0 + u + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        __hip_atomic_store(&vdone[w4], r0 + u + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
             }
         }
