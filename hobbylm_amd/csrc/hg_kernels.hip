@@ -135,13 +135,39 @@ struct Q8Row {
     v4i wq[NCT];
     typename ScaleVec<SCF32>::T sq[NCT];
 
+    // A row of exactly 8 full chunks (the single-batch case with NCT = 8) loads its scales once:
+    // lane j takes chunk j's, and chunk u's reach the row's lanes by an LDS-free swizzle
+    // (lane i reads lane (i & ~7) | u), which halves the row's load instructions.
+    __device__ inline bool bcast() const { return NCT == 8 && nc == 8 && nb == 32; }
     __device__ inline void load(uint32_t c0) {
+        const bool bc = bcast() && c0 == 0;
 #pragma unroll
         for (int u = 0; u < NCT; ++u) {
             const uint32_t c = min(c0 + (uint32_t)u, nc - 1);
             wq[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(w + c * CHUNK_BYTES + j * 16));
-            sq[u] = __builtin_nontemporal_load(reinterpret_cast<const typename ScaleVec<SCF32>::T *>(s) + c);
+            if (!bc)
+                sq[u] = __builtin_nontemporal_load(reinterpret_cast<const typename ScaleVec<SCF32>::T *>(s) + c);
         }
+        if (bc) sq[0] = __builtin_nontemporal_load(reinterpret_cast<const typename ScaleVec<SCF32>::T *>(s) + j);
+    }
+    template <int U>
+    __device__ inline typename ScaleVec<SCF32>::T row_scales() const {   // chunk U's, from lane U of the row
+        constexpr int pat = 0x18 | (U << 5);   // and_mask 0x18, or_mask U
+        // (the elements go through scalars: a bit cast of a vector element expression reads
+        // element 0 with this compiler)
+        typename ScaleVec<SCF32>::T r;
+        if constexpr (SCF32) {
+            const float s0 = sq[0].x, s1 = sq[0].y, s2 = sq[0].z, s3 = sq[0].w;
+            r.x = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, s0), pat));
+            r.y = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, s1), pat));
+            r.z = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, s2), pat));
+            r.w = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, s3), pat));
+        } else {
+            const uint32_t h0 = sq[0].x, h1 = sq[0].y;
+            r.x = (uint32_t)__builtin_amdgcn_ds_swizzle((int)h0, pat);
+            r.y = (uint32_t)__builtin_amdgcn_ds_swizzle((int)h1, pat);
+        }
+        return r;
     }
     __device__ inline void begin(const uint8_t *w_, const void *s_, uint32_t nb_, uint32_t nc_, int j_) {
         w = w_;
@@ -153,9 +179,13 @@ struct Q8Row {
     }
     // One chunk c (batch slot u) against the activation chunk x and its scales.
     __device__ inline void chunk(int u, uint32_t c, const v4i x, const v4f dxc, bool guard, float &acc) const {
+        chunk_s(u, c, x, dxc, guard, acc, sq[u]);
+    }
+    __device__ inline void chunk_s(int u, uint32_t c, const v4i x, const v4f dxc, bool guard, float &acc,
+                                   const typename ScaleVec<SCF32>::T scl) const {
         const int p[4] = {sdot4(wq[u].x, x.x), sdot4(wq[u].y, x.y), sdot4(wq[u].z, x.z), sdot4(wq[u].w, x.w)};
         float sv[4];
-        unpack_scales(sq[u], sv);
+        unpack_scales(scl, sv);
         const float dv[4] = {dxc.x, dxc.y, dxc.z, dxc.w};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -187,6 +217,22 @@ struct Q8Row {
                 xa[u] = *reinterpret_cast<const v4i *>(qx + u * CHUNK_BYTES + j * 16);
                 xs[u] = *reinterpret_cast<const v4f *>(dx + u * 4);
             }
+            if constexpr (NCT == 8) {
+                if (bcast()) {
+                    typename ScaleVec<SCF32>::T sc[8];
+                    sc[0] = row_scales<0>();
+                    sc[1] = row_scales<1>();
+                    sc[2] = row_scales<2>();
+                    sc[3] = row_scales<3>();
+                    sc[4] = row_scales<4>();
+                    sc[5] = row_scales<5>();
+                    sc[6] = row_scales<6>();
+                    sc[7] = row_scales<7>();
+#pragma unroll
+                    for (int u = 0; u < NCT; ++u) chunk_s(u, (uint32_t)u, xa[u], xs[u], false, acc, sc[u]);
+                    goto reduce;
+                }
+            }
 #pragma unroll
             for (int u = 0; u < NCT; ++u) chunk(u, (uint32_t)u, xa[u], xs[u], false, acc);
         } else {
@@ -210,6 +256,7 @@ struct Q8Row {
                 load(c0);
             }
         }
+    reduce:
         if (ORDER == ORDER_DECODE) {   // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) in lane 0 (quant.rs:61-65)
             {
                 const float dn = dpp_f<0x124>(acc), up = dpp_f<0x12C>(acc);
