@@ -1722,21 +1722,24 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
                 }
             }
         }
-    } else {   // sum += e_t in index order, once every wave's e_t are written
+    }
+    float inv0 = 0.0f;   // wave 0: 1 / sum
+    if (wave < 4) {   // sum += e_t in index order, once every wave's e_t are written
         while (__hip_atomic_load(&arrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 8u)
             __builtin_amdgcn_s_sleep(1);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         const float r = n <= 2048 ? block_seq_sum<4, 8>(e, n, xs, wave, lane) : block_seq_sum<4, 12>(e, n, xs, wave, lane);
+        inv0 = 1.0f / r;
         if (tid == 0) {
-            s_inv = 1.0f / r;
+            s_inv = inv0;
             __hip_atomic_store(&inv_ready, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
     if (wave >= 1 && wave != 4) {
         // products by the six waves off the chain wave's SIMD (wave 4 shares it with wave 0):
-        // groups pw, pw + 6, ... (pw = 0..5); lane l -> element l / 16, positions
-        // 4 (l % 16) .. + 3 of the group.  The first group alone (the first chain block needs
-        // it soon), then the others together: their reads first, one release, one flag update.
+        // groups pw, pw + 6, ... (pw = 0..5) past the first block; lane l -> element l / 16,
+        // positions 4 (l % 16) .. + 3 of the group.  The first group alone (the chain needs it
+        // soon), then the others together: their reads first, one release, one flag update.
         while (__hip_atomic_load(&inv_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u)
             __builtin_amdgcn_s_sleep(1);
         const float inv = s_inv;
@@ -1761,7 +1764,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
             return pr;
         };
         static_assert(D == 4 && LP == 1, "one 16-byte step per lane and group");
-        if (pw < ngp) {
+        if (pw >= 4 && pw < ngp) {   // (groups 0..3, the first chain block: wave 0 itself)
             if (pw < ng) vwait(pw / 4, pw % 4, pw % 4);
             const uint32_t t = G * pw + 4 * tq;
             v4f *pv = reinterpret_cast<v4f *>(P + di * TPC + t);
@@ -1791,6 +1794,38 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             if (lane == 0) __hip_atomic_fetch_or(&ready, mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
+    }
+    if (wave == 0) {   // the first block's products (groups 0..3), by the chain wave itself
+        const uint32_t di = (uint32_t)lane >> 4, tq = (uint32_t)lane & 15;
+        for (;;) {   // round 0 of every V wave in
+            uint32_t v0 = __hip_atomic_load(&vdone[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            v0 = min(v0, __hip_atomic_load(&vdone[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            v0 = min(v0, __hip_atomic_load(&vdone[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            v0 = min(v0, __hip_atomic_load(&vdone[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            if (v0 > 0) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        v4f ev[4], vv[4];
+#pragma unroll
+        for (uint32_t g4 = 0; g4 < 4; ++g4) {
+            const uint32_t t = G * g4 + 4 * tq;
+            ev[g4] = *reinterpret_cast<const v4f *>(e + t);
+            vv[g4] = *reinterpret_cast<const v4f *>(P + di * TPC + t);
+        }
+#pragma unroll
+        for (uint32_t g4 = 0; g4 < 4; ++g4) {
+            const uint32_t t = G * g4 + 4 * tq;
+            v4f pr;
+            pr.x = t + 0 < n ? (ev[g4].x * inv0) * vv[g4].x : -0.0f;
+            pr.y = t + 1 < n ? (ev[g4].y * inv0) * vv[g4].y : -0.0f;
+            pr.z = t + 2 < n ? (ev[g4].z * inv0) * vv[g4].z : -0.0f;
+            pr.w = t + 3 < n ? (ev[g4].w * inv0) * vv[g4].w : -0.0f;
+            *reinterpret_cast<v4f *>(P + di * TPC + t) = pr;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     if (wave == 0 && lane < (int)D) {
         // chains: blocks of 256 positions, 64 positions (sixteen 16-byte reads) per chunk; the next
@@ -1823,8 +1858,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
             }
         };
         static_assert(G == 64, "a block is 4 chunks of 64 positions");
-        block_wait(0);
-        ld(ca, 0);
+        ld(ca, 0);   // (block 0: this wave's own products)
         for (uint32_t b = 0; b < nblk; ++b) {
             const uint32_t c = 4 * b;
 #define HG_PV_STEP(NX, CUR, NXT)                 \
