@@ -1609,20 +1609,99 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
     }
 }
 
+// o = o + p_0 + p_1 + ... + p_63 in order, for the first lane of each row of 16, where lane i
+// of the row holds p_4i .. p_4i+3 in a: the row's own four, then lane i's four through a row
+// rotation by 16 - i fused into the add.  One asm block, so that no wait states separate the
+// adds: an add whose rotated operand was written long before needs none for its other operand
+// (the previous add's result), which keeps the chain at the rate of register-fed adds (2.0 ns
+// per add, against 2.5-2.9 with the products read from LDS and 5.1 with the compiler's wait
+// states between rotated adds; all three bit-identical).  Every lane of the row must be active.
+__device__ __forceinline__ void pv_adds64(float &o, const v4f a) {
+    const float a0 = a.x, a1 = a.y, a2 = a.z, a3 = a.w;
+    asm volatile(
+                 "v_add_f32 %0, %0, %1\n"
+                 "v_add_f32 %0, %0, %2\n"
+                 "v_add_f32 %0, %0, %3\n"
+                 "v_add_f32 %0, %0, %4\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:15 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:15 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:15 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:15 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:14 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:14 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:14 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:14 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:13 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:13 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:13 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:13 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:12 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:12 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:12 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:12 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:11 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:11 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:11 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:11 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:10 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:9 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:9 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:9 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:9 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:7 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:7 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:7 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:7 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:6 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:6 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:6 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:6 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:5 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:5 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:5 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:5 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:4 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:4 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:4 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:4 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:3 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:3 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:3 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:3 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:2 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:2 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:2 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:2 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %1, %0 row_ror:1 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %2, %0 row_ror:1 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %3, %0 row_ror:1 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 "v_add_f32_dpp %0, %4, %0 row_ror:1 row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+                 : "+v"(o)
+                 : "v"(a0), "v"(a1), "v"(a2), "v"(a3));
+}
+
 // Softmax and P.V of one query head, as k_attn_softmax_pv, for caches whose V slice and
 // products fit in LDS (pv_res_fits): no ring.  Workgroup (h, q), 512 threads, D = 4 output
-// elements, so the grid has a workgroup per CU and the chain wave has few active lanes:
+// elements (one per row of 16 lanes of the chain wave; a workgroup per CU):
 //   every wave forms its share of e_t and signals it (no wait); waves 4..7 then stream the
 //   D rows of V's transposed copy (contiguous positions) into LDS, P[d][t], flagging each
-//   round, while waves 0..3 form the index-order sum of e_t (block_seq_sum).  Once inv is known (a
-//   flag, not a barrier), waves 1..3 and 5..7 (not wave 4, which shares the chain wave's
-//   SIMD) replace group g by the rounded products p_t * V[d][t] (p_t = e_t * inv; -0 past the
-//   context, the exact identity of the chain's adds) as soon as its V is in, and flag it;
-//   wave 0 lanes 0..D-1 run the D sequential chains over P in blocks of 4 groups, waiting only
-//   for each block's flags.
+//   round, while waves 0..3 form the index-order sum of e_t (block_seq_sum).  Once inv is
+//   known (a flag, not a barrier), wave 0 replaces the first 4 groups of G positions by the
+//   rounded products p_t * V[d][t] (p_t = e_t * inv; -0 past the context, the exact identity
+//   of the chain's adds) and waves 1..3 and 5..7 (not wave 4, which shares wave 0's SIMD) the
+//   others, flagging them; wave 0 then runs the D sequential chains, a row's lanes holding a
+//   group's products and its first lane adding them in order through DPP row rotations
+//   (pv_adds64), waiting only for each block of 4 groups' flags.
 struct PvResCfg {
     static constexpr uint32_t D = 4;      // output elements per workgroup (4 or 8)
-    static constexpr uint32_t G = 64;     // positions per product group (two chain chunks of 32)
+    static constexpr uint32_t G = 64;     // positions per product group (16 lanes x 4)
     static constexpr uint32_t NG = 64;    // product groups: one bit each of the ready mask
     static constexpr uint32_t VB = 8;     // V loads in flight per V thread
 };
@@ -1827,55 +1906,32 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    if (wave == 0 && lane < (int)D) {
-        // chains: blocks of 256 positions, 64 positions (sixteen 16-byte reads) per chunk; the next
-        // chunk's reads are issued before the current chunk's adds, in an order pinned by empty
-        // statements that hold the sum and order memory (reads cannot move above them), and the
-        // next block's product flags are checked once per block, before its first reads (a
-        // block's code has no loop, so the compiler's waits stay partial inside it)
-        float o = 0.0f;
-        const v4f *row = reinterpret_cast<const v4f *>(P + lane * TPC);
-        uint64_t known = 0;   // ready bits seen so far
+    if (wave == 0) {
+        // chains: row r of the wave (lanes 16 r .. 16 r + 15) owns element r; lane i of the row
+        // holds the products of positions 4 i .. 4 i + 3 of the current group, and the row's
+        // first lane adds the group's 64 products in order, reading lane i's through a row
+        // rotation fused into the add (pv_adds64).  The next group's products are read before
+        // the current group's adds; the product flags are checked once per block of 4 groups.
+        const uint32_t r4 = (uint32_t)lane >> 4, li = (uint32_t)lane & 15;
+        const float *prow = P + r4 * TPC + 4 * li;
+        uint64_t known = 0xf;   // ready bits seen so far (block 0: this wave's own products)
         auto block_wait = [&](uint32_t b) {   // groups 4 b .. 4 b + 3
             while (((known >> (4 * b)) & 0xf) != 0xf) {
                 known = __hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
                 if (((known >> (4 * b)) & 0xf) != 0xf) __builtin_amdgcn_s_sleep(1);
             }
         };
-        constexpr int QB = 16;   // (measured: 2.8 ns per add with 16 reads per batch, 2.9 with 8)
-        v4f ca[QB], cb[QB];
-        auto ld = [&](v4f(&c)[QB], uint32_t ch) {
-#pragma unroll
-            for (int u = 0; u < QB; ++u) c[u] = row[ch * QB + u];
-        };
-        auto add = [&](const v4f(&c)[QB]) {
-#pragma unroll
-            for (int u = 0; u < QB; ++u) {
-                o = o + c[u].x;
-                o = o + c[u].y;
-                o = o + c[u].z;
-                o = o + c[u].w;
-            }
-        };
-        static_assert(G == 64, "a block is 4 chunks of 64 positions");
-        ld(ca, 0);   // (block 0: this wave's own products)
-        for (uint32_t b = 0; b < nblk; ++b) {
-            const uint32_t c = 4 * b;
-#define HG_PV_STEP(NX, CUR, NXT)                 \
-    ld(NXT, c + (NX));                           \
-    __builtin_amdgcn_sched_barrier(0);           \
-    add(CUR);                                    \
-    asm volatile("" : "+v"(o) : : "memory");
-            HG_PV_STEP(1, ca, cb) HG_PV_STEP(2, cb, ca) HG_PV_STEP(3, ca, cb)
-#undef HG_PV_STEP
-            const bool more = b + 1 < nblk;
-            if (more) block_wait(b + 1);
-            ld(ca, more ? c + 4 : c);   // (the last block rereads its first chunk, unused)
-            __builtin_amdgcn_sched_barrier(0);
-            add(cb);
-            asm volatile("" : "+v"(o) : : "memory");
+        const uint32_t ngp = 4 * nblk;
+        float o = 0.0f;
+        v4f pa = *reinterpret_cast<const v4f *>(prow);
+        for (uint32_t g = 0; g < ngp; ++g) {
+            const uint32_t gn = g + 1;
+            if (gn < ngp && (gn & 3) == 0) block_wait(gn >> 2);
+            const v4f pb = *reinterpret_cast<const v4f *>(prow + G * min(gn, ngp - 1));
+            pv_adds64(o, pa);
+            pa = pb;
         }
-        o_out[h * HD + q * D + lane] = o;
+        if (li == 0) o_out[h * HD + q * D + r4] = o;
     }
 }
 
