@@ -913,7 +913,7 @@ __device__ inline void norm_rope_head(const float *u, float *o, const HeadConst<
         }
         scale = 1.0f / sqrtf(ss / (float)HD + eps);
     }
-    scale = __shfl(scale, 0, 64);
+    scale = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, scale), 0));
 #pragma unroll
     for (int k = 0; k < HeadConst<HD>::NW; ++k) {
         const uint32_t i = lane + 64 * k;
