@@ -383,7 +383,7 @@ void enqueue_layers(hg_kv *kv, int order) {
         mark(kv, P_OPROJ);
         if (kv->exact)  // attn_output quantizes o itself
             launch_matvec(st, order, EPI_RESID, L.o.m, reinterpret_cast<const uint8_t *>(kv->o.as<float>()), nullptr,
-                          x, 64, 0, nullptr, nullptr);
+                          x, 128, 0, nullptr, nullptr);
         else
             launch_matvec(st, order, EPI_RESID, L.o.m, qa, da, x, 64, 0, nullptr, nullptr);
         if (L.moe) mark(kv, P_ROUTER);   // ffn_norm + router (+ gate/up when fused)
