@@ -415,9 +415,9 @@ void enqueue_layers(hg_kv *kv, int order) {
             mark(kv, P_GATEUP);
             launch_ffn_gateup(st, order, L.gate.m, L.up.m, L.gate.m, L.up.m, nullptr, 0, 1, c.dense_ffn, qa, da,
                               kv->a.as<float>());
-            mark(kv, P_DOWN);
-            launch_ffn_down(st, order, L.down.m, L.down.m, nullptr, nullptr, nullptr, 0, 1, 1, d, c.dense_ffn,
-                            kv->a.as<float>(), x);
+            mark(kv, P_DOWN);   // x += down(a): the plain matvec, a quantized in its prologue (model.rs:253-254)
+            launch_matvec(st, order, EPI_RESID, L.down.m, reinterpret_cast<const uint8_t *>(kv->a.as<float>()), nullptr,
+                          x, 128, 0, nullptr, nullptr);
         }
     }
 }
