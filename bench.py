@@ -121,10 +121,24 @@ def cpu_baseline(path, gm, gkv, tokens, start, budget_s, max_steps):
         n += 1
     dt = time.perf_counter() - t0
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": oracle.threads(), "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{n} greedy decode steps at positions {start}..{start + n - 1} (context ~2k) of the "
                       f"same model, continuing from the GPU's KV cache; C restatement of hobby-rs's AVX2 "
                       f"decode path, rows in parallel over {oracle.threads()} OpenMP threads",
             "greedy_match": f"{match}/{n}"}
+
+
+def cpu_model():
+    """The host CPU's model name (as lscpu reports it) and logical CPU count."""
+    name = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return f"{name} ({os.cpu_count()} logical CPUs visible)"
 
 
 def op_matvec():
@@ -299,7 +313,7 @@ def main():
     path = gs.synth_path("500M", 1)
     m = hg.Model(path)
     cfg = m.cfg
-    kv = m.new_cache(max_ctx=CTX_END + 8)  # 8 spare rows for the profiling replay
+    kv = m.new_cache()   # the drop-in default: capacity = context_length (8192)
     prompt = gs.prompt_ids(1, N_PROMPT, 50257)
     emb = np.stack([m.token_embedding(int(t)) for t in prompt])
     _, first = m.prefill(emb, kv)
@@ -333,7 +347,7 @@ def main():
         n = min(len(g["tokens"]), len(stream))
         golden = {"tokens_compared": n, "identical": g["tokens"][:n] == stream[:n]}
 
-    # per-kernel-class split of one step at the window's end (pos 2048, a spare row)
+    # per-kernel-class split of one step at the window's end (pos 2048, a free row of the cache)
     prof = m.profile_step(int(ids[-1]), kv, reps=10)
     step_us = sum(v[0] for v in prof.values())
     dom = max(prof, key=lambda k: prof[k][0])
@@ -378,7 +392,9 @@ def main():
         "config": {"workload": f"hobbylm 500M-shaped sparse MoE, Q8_0, batch 1, greedy decode positions "
                                f"{start}..{CTX_END - 1} after a 16-token prompt",
                    "model": "hobbylm-500M-synthetic", "global_batch": 1, "seq_len": CTX_END,
-                   "parallelism": "none (1 GPU)", "kv_cache": "f32, layer-major, reference-order reductions"},
+                   "parallelism": "none (1 GPU)",
+                   "kv_cache": f"f32, layer-major, capacity {cfg.context_length} (the default), "
+                               f"reference-order reductions"},
         "step_bandwidth": {"algorithmic_bytes_per_token": bytes_step, "achieved_GBps": round(ach / 1e9, 2),
                            "peak_GBps": PEAK_HBM / 1e9, "frac": round(ach / PEAK_HBM, 5)},
         "roofline": roof,

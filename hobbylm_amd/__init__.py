@@ -53,6 +53,7 @@ SIGNATURES = {
     "hg_last_error": (C.c_char_p, []),
     "hg_model_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(_vp)]),
     "hg_model_free": (None, [_vp]),
+    "hg_gguf_load_tensor": (C.c_int, [C.c_char_p, C.c_char_p, _vp, C.c_uint64, C.POINTER(C.c_uint64)]),
     "hg_model_config": (C.c_int, [_vp, C.POINTER(HgConfig)]),
     "hg_weight_bytes": (C.c_uint64, [_vp]),
     "hg_device_weight_bytes": (C.c_uint64, [_vp]),
@@ -62,6 +63,7 @@ SIGNATURES = {
     "hg_kv_len": (C.c_uint32, [_vp]),
     "hg_kv_truncate": (C.c_int, [_vp, C.c_uint32]),
     "hg_kv_read": (C.c_int, [_vp, C.c_uint32, _f32p, _f32p]),
+    "hg_kv_load": (C.c_int, [_vp, C.c_uint32, _f32p, _f32p]),
     "hg_forward": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, _vp, C.POINTER(C.c_uint32)]),
     "hg_forward_x": (C.c_int, [_vp, _vp, _f32p, C.c_uint32, _vp, C.POINTER(C.c_uint32)]),
     "hg_prefill": (C.c_int, [_vp, _vp, _f32p, C.c_uint32, _vp, C.POINTER(C.c_uint32)]),
@@ -238,6 +240,13 @@ class KvCache:
         _check(lib().hg_kv_read(self.h, layer, k.reshape(-1), v.reshape(-1)))
         return k, v
 
+    def load(self, k: np.ndarray, v: np.ndarray):
+        """KvCache.k / .v / .len = (k, v, k.shape[1]) (model.rs:60-64); k, v [n_layers][len][kv_dim]."""
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        assert k.shape == v.shape and k.shape[0] == self.model.cfg.n_layers
+        _check(lib().hg_kv_load(self.h, k.shape[1], k.reshape(-1), v.reshape(-1)))
+
     def routing(self):
         c = self.model.cfg
         idx = np.empty(c.n_layers * c.top_k, np.uint32)
@@ -319,6 +328,15 @@ class Q8Tensor:
         _check(lib().hg_q8_tensor_matvec_gather(self.h, rows_per_mat, ids, ids.size,
                                                 np.ascontiguousarray(x, np.float32), y.reshape(-1)))
         return y
+
+
+def gguf_load_tensor(path: str, name: str) -> np.ndarray:
+    """Gguf::load (gguf.rs:250-269) of one tensor as f32 (host work, no device needed)."""
+    n = C.c_uint64()
+    _check(lib().hg_gguf_load_tensor(str(path).encode(), name.encode(), None, 0, C.byref(n)))
+    out = np.empty(n.value, np.float32)
+    _check(lib().hg_gguf_load_tensor(str(path).encode(), name.encode(), _ptr(out), out.size, C.byref(n)))
+    return out
 
 
 def seq_sum(x, method: int = 1) -> np.float32:

@@ -10,7 +10,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <map>
 #include <memory>
+#include <stdexcept>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -127,6 +129,21 @@ struct Layer {
     DevQ8 qkv, o, gate, up, down, gate_e, up_e, down_e, gate_sh, up_sh, down_sh;
 };
 
+// The model as parsed and packed on the host, before any device call: every format error of
+// the file surfaces here, in the reference's load order (model.rs:79-131).
+struct HostLayer {
+    bool moe = false;
+    std::vector<float> attn_norm, q_norm, k_norm, ffn_norm, router, router_p, bias;
+    PackedQ8 qkv, o, gate, up, down, gate_e, up_e, down_e, gate_sh, up_sh, down_sh;
+};
+struct HostModel {
+    hg_config c{};
+    std::vector<HostLayer> layers;
+    std::vector<float> token_embd, output_norm, rope_cos, rope_sin;
+    PackedQ8 output;
+    uint64_t ref_bytes = 0;
+};
+
 }  // namespace
 
 struct hg_model {
@@ -143,7 +160,7 @@ struct hg_kv {
     hipStream_t st = nullptr;
     uint32_t cap = 0, len = 0, flags = 0;
     bool exact = false;
-    uint32_t S = 0;         // attention context splits
+    uint32_t win = 0;       // attention window of the step being enqueued (see window_of)
     uint32_t lm_threads = 256, n_part = 0;
     DevBuf kc, vc;          // [L][n_kv][cap][hd]; V: each layer also [n_kv][hd][vt_stride(cap)]
     DevBuf x, qkv, o, part, scores, a, logits, pv, pi, qa, da, topk_idx, topk_w, order, rec_idx, rec_w, params,
@@ -152,7 +169,9 @@ struct hg_kv {
     StepParams *h_params = nullptr;
     uint32_t *h_ids = nullptr;
     float *h_logits = nullptr;
-    hipGraphExec_t g_decode = nullptr, g_body = nullptr, g_tail = nullptr;
+    // captured steps, one per attention window (decode, prompt-row body), and the prompt tail
+    std::map<uint32_t, hipGraphExec_t> g_decode, g_body;
+    hipGraphExec_t g_tail = nullptr;
     bool use_graph = true;
     LaunchTimer *timer = nullptr;  // hg_profile_step: per-dispatch timing
     ~hg_kv();
@@ -162,24 +181,26 @@ namespace {
 
 uint32_t slots_of(const hg_config &c) { return c.top_k + (c.n_shared > 0 ? 1 : 0); }
 
-int load_norm(const Gguf &g, const std::string &name, size_t want, DevBuf &dst) {
-    std::vector<float> v;
-    int rc = g.f32(name, v, g_err);
-    if (rc) return rc;
-    if (v.size() != want)
-        return fail(HG_ERR_FORMAT, "tensor `" + name + "` has " + std::to_string(v.size()) + " elements, expected " +
-                                       std::to_string(want));
-    return dst.upload(v.data(), v.size() * 4);
+// Attention window of a step over n = pos + 1 positions of a cache of cap positions: n rounded
+// up to 256 positions (1024 past 3072), at most cap.  The attention launches are sized for the
+// window, not the capacity, so a step costs what its live context needs; each window has its
+// own captured graph.
+uint32_t window_of(uint32_t n, uint32_t cap) {
+    const uint32_t w = n <= 3072 ? div_up(n, 256) * 256 : div_up(n, 1024) * 1024;
+    return std::min(w, cap);
 }
 
-// Matrices packed on the host, uploaded together once the model-wide scale storage is known.
-struct Pending {
-    std::vector<std::pair<PackedQ8, DevQ8 *>> mats;
-};
-thread_local Pending *g_pending = nullptr;
+int load_norm(const Gguf &g, const std::string &name, size_t want, std::vector<float> &dst) {
+    int rc = g.f32(name, dst, g_err);
+    if (rc) return rc;
+    if (dst.size() != want)
+        return fail(HG_ERR_FORMAT, "tensor `" + name + "` has " + std::to_string(dst.size()) + " elements, expected " +
+                                       std::to_string(want));
+    return HG_OK;
+}
 
 // Gguf::load + Mat::build(.., quant = true) (model.rs:87-89, 121): requantize and pack.
-int load_q8(const Gguf &g, const std::string &name, uint32_t N, uint32_t K, DevQ8 &dst, hg_model *m) {
+int load_q8(const Gguf &g, const std::string &name, uint32_t N, uint32_t K, PackedQ8 &dst, HostModel &hm) {
     const TensorInfo *t;
     const uint8_t *raw;
     size_t nbytes;
@@ -189,32 +210,14 @@ int load_q8(const Gguf &g, const std::string &name, uint32_t N, uint32_t K, DevQ
         return fail(HG_ERR_FORMAT, "tensor `" + name + "` has " + std::to_string(t->n_elems()) + " elements, expected " +
                                        std::to_string((uint64_t)N * K));
     if (K % QK) return fail(HG_ERR_UNSUPPORTED, "Q8_0 needs in_ divisible by 32 (got " + std::to_string(K) + ")");
-    PackedQ8 p;
-    if (t->type == 8) pack_q8_from_q8_0(raw, N, K, p);
+    if (t->type == GGML_Q8_0) pack_q8_from_q8_0(raw, N, K, dst);
     else {
         std::vector<float> w;
         rc = g.load(name, w, g_err);
         if (rc) return rc;
-        pack_q8_from_f32(w.data(), N, K, p);
+        pack_q8_from_f32(w.data(), N, K, dst);
     }
-    m->ref_bytes += p.ref_bytes();
-    g_pending->mats.emplace_back(std::move(p), &dst);
-    return HG_OK;
-}
-
-// Upload the pending matrices with f16 scales if every scale of every matrix is an exact
-// f16 value (GGUF Q8_0 files: the on-disk 34 bytes per block), else all with f32 scales.
-int upload_pending(hg_model *m) {
-    bool all_f16 = true;
-    for (auto &pm : g_pending->mats) all_f16 = all_f16 && pm.first.f16_exact;
-    for (auto &pm : g_pending->mats) {
-        pm.first.set_scale_storage(!all_f16);
-        int rc = pm.second->upload(pm.first);
-        if (rc) return rc;
-        m->dev_bytes += pm.second->dev_bytes();
-        pm.first = PackedQ8();
-    }
-    g_pending->mats.clear();
+    hm.ref_bytes += dst.ref_bytes();
     return HG_OK;
 }
 
@@ -230,7 +233,122 @@ int validate(const hg_config &c) {
     if (c.n_experts > 256 || c.top_k > 64 || c.top_k > c.n_experts) return bad("expert count out of range");
     if (c.n_dense < c.n_layers && (slots_of(c) == 0 || slots_of(c) > 16)) return bad("more than 16 expert slots");
     if (!c.context_length) return bad("context_length is 0");
+    if (c.context_length > (1u << 20)) return bad("context_length above 2^20");
     return HG_OK;
+}
+
+// Gguf::open + Config::from_gguf + Model::load on the host (no device call).
+int parse_model(const char *path, HostModel &hm) {
+    Gguf g;
+    int rc = g.open(path, g_err);
+    if (rc) return rc;
+    rc = config_from_gguf(g, hm.c, g_err);
+    if (rc) return rc;
+    rc = validate(hm.c);
+    if (rc) return rc;
+    const hg_config &c = hm.c;
+    const uint32_t d = c.d_model, f = c.expert_ffn, hd = c.head_dim;
+    const uint32_t qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+    hm.layers.resize(c.n_layers);
+    for (uint32_t i = 0; i < c.n_layers; ++i) {
+        HostLayer &L = hm.layers[i];
+        const std::string p = "blk." + std::to_string(i) + ".";
+        L.moe = i >= c.n_dense;
+        if (L.moe) {
+            if ((rc = g.load(p + "ffn_gate_inp.weight", L.router, g_err))) return rc;
+            if (L.router.size() != (size_t)c.n_experts * d)
+                return fail(HG_ERR_FORMAT, "tensor `" + p + "ffn_gate_inp.weight` has wrong size");
+            L.router_p.resize(L.router.size());   // the router kernel's 16-byte-per-step row layout
+            for (size_t e = 0; e < c.n_experts; ++e)
+                for (uint32_t k = 0; k < d; ++k) L.router_p[e * d + router_perm(k)] = L.router[e * d + k];
+            if ((rc = load_norm(g, p + "exp_probs_b.bias", c.n_experts, L.bias))) return rc;
+            if ((rc = load_q8(g, p + "ffn_gate_exps.weight", c.n_experts * f, d, L.gate_e, hm))) return rc;
+            if ((rc = load_q8(g, p + "ffn_up_exps.weight", c.n_experts * f, d, L.up_e, hm))) return rc;
+            if ((rc = load_q8(g, p + "ffn_down_exps.weight", c.n_experts * d, f, L.down_e, hm))) return rc;
+            if ((rc = load_q8(g, p + "ffn_gate_shexp.weight", f, d, L.gate_sh, hm))) return rc;
+            if ((rc = load_q8(g, p + "ffn_up_shexp.weight", f, d, L.up_sh, hm))) return rc;
+            if ((rc = load_q8(g, p + "ffn_down_shexp.weight", d, f, L.down_sh, hm))) return rc;
+        } else {
+            if ((rc = load_q8(g, p + "ffn_gate.weight", c.dense_ffn, d, L.gate, hm))) return rc;
+            if ((rc = load_q8(g, p + "ffn_up.weight", c.dense_ffn, d, L.up, hm))) return rc;
+            if ((rc = load_q8(g, p + "ffn_down.weight", d, c.dense_ffn, L.down, hm))) return rc;
+        }
+        if ((rc = load_norm(g, p + "attn_norm.weight", d, L.attn_norm))) return rc;
+        if ((rc = load_q8(g, p + "attn_qkv.weight", qd + 2 * kvd, d, L.qkv, hm))) return rc;
+        if ((rc = load_norm(g, p + "attn_q_norm.weight", hd, L.q_norm))) return rc;
+        if ((rc = load_norm(g, p + "attn_k_norm.weight", hd, L.k_norm))) return rc;
+        if ((rc = load_q8(g, p + "attn_output.weight", d, qd, L.o, hm))) return rc;
+        if ((rc = load_norm(g, p + "ffn_norm.weight", d, L.ffn_norm))) return rc;
+    }
+    if ((rc = load_q8(g, "output.weight", c.vocab_size, d, hm.output, hm))) return rc;
+    if ((rc = g.load("token_embd.weight", hm.token_embd, g_err))) return rc;
+    if (hm.token_embd.size() != (size_t)c.vocab_size * d)
+        return fail(HG_ERR_FORMAT, "tensor `token_embd.weight` has wrong size");
+    if ((rc = load_norm(g, "output_norm.weight", d, hm.output_norm))) return rc;
+    rope_table(hd, c.context_length, c.rope_theta, hm.rope_cos, hm.rope_sin);
+    return HG_OK;
+}
+
+int upload_vec(const std::vector<float> &v, DevBuf &dst) { return dst.upload(v.data(), v.size() * 4); }
+
+// Device residency of a parsed model.  Matrices keep f16 scales if every scale of every matrix
+// is an exact f16 value (GGUF Q8_0 files: the on-disk 34 bytes per block), else all f32.
+int upload_model(HostModel &hm, hg_model *m) {
+    m->c = hm.c;
+    m->n_slots = slots_of(hm.c);
+    m->ref_bytes = hm.ref_bytes;
+    std::vector<std::pair<PackedQ8 *, DevQ8 *>> mats;
+    m->layers.resize(hm.layers.size());
+    for (size_t i = 0; i < hm.layers.size(); ++i) {
+        HostLayer &H = hm.layers[i];
+        m->layers[i] = std::make_unique<Layer>();
+        Layer &L = *m->layers[i];
+        L.moe = H.moe;
+        PackedQ8 *hp[] = {&H.qkv, &H.o, &H.gate, &H.up, &H.down, &H.gate_e, &H.up_e, &H.down_e, &H.gate_sh,
+                          &H.up_sh, &H.down_sh};
+        DevQ8 *dp[] = {&L.qkv, &L.o, &L.gate, &L.up, &L.down, &L.gate_e, &L.up_e, &L.down_e, &L.gate_sh,
+                       &L.up_sh, &L.down_sh};
+        for (size_t k = 0; k < sizeof hp / sizeof hp[0]; ++k)
+            if (hp[k]->N) mats.emplace_back(hp[k], dp[k]);
+        int rc;
+        if ((rc = upload_vec(H.attn_norm, L.attn_norm)) || (rc = upload_vec(H.q_norm, L.q_norm)) ||
+            (rc = upload_vec(H.k_norm, L.k_norm)) || (rc = upload_vec(H.ffn_norm, L.ffn_norm)) ||
+            (rc = upload_vec(H.router, L.router)) || (rc = upload_vec(H.router_p, L.router_p)) ||
+            (rc = upload_vec(H.bias, L.bias)))
+            return rc;
+    }
+    mats.emplace_back(&hm.output, &m->output);
+    bool all_f16 = true;
+    for (auto &pm : mats) all_f16 = all_f16 && pm.first->f16_exact;
+    for (auto &pm : mats) {
+        pm.first->set_scale_storage(!all_f16);
+        int rc = pm.second->upload(*pm.first);
+        if (rc) return rc;
+        m->dev_bytes += pm.second->dev_bytes();
+        *pm.first = PackedQ8();
+    }
+    int rc;
+    if ((rc = upload_vec(hm.token_embd, m->token_embd)) || (rc = upload_vec(hm.output_norm, m->output_norm)) ||
+        (rc = upload_vec(hm.rope_cos, m->rope_cos)) || (rc = upload_vec(hm.rope_sin, m->rope_sin)))
+        return rc;
+    return HG_OK;
+}
+
+// Every extern "C" body runs inside guard(): a C++ exception (host allocation failure, a
+// container length error) becomes an error code instead of crossing the C boundary.
+template <class F>
+int guard(F &&body) {
+    try {
+        return body();
+    } catch (const std::bad_alloc &) {
+        return fail(HG_ERR_NOMEM, "host allocation failed");
+    } catch (const std::length_error &e) {
+        return fail(HG_ERR_NOMEM, std::string("host allocation failed: ") + e.what());
+    } catch (const std::exception &e) {
+        return fail(HG_ERR_DEVICE, std::string("internal error: ") + e.what());
+    } catch (...) {
+        return fail(HG_ERR_DEVICE, "internal error");
+    }
 }
 
 }  // namespace
@@ -241,95 +359,63 @@ extern "C" {
 const char *hg_last_error(void) { return g_err.c_str(); }
 
 int hg_model_load(const char *path, int quant, hg_model **out) {
-    if (!out) return fail(HG_ERR_ARG, "out is NULL");
-    *out = nullptr;
-    if (!quant) return fail(HG_ERR_UNSUPPORTED, "F32 matrices (quant = false) are not supported by the GPU backend");
-    int rc = check_device();
-    if (rc) return rc;
-    Gguf g;
-    rc = g.open(path, g_err);
-    if (rc) return rc;
-    Pending pending;
-    g_pending = &pending;
-    struct Reset { ~Reset() { g_pending = nullptr; } } reset;
-    auto m = std::make_unique<hg_model>();
-    rc = config_from_gguf(g, m->c, g_err);
-    if (rc) return rc;
-    rc = validate(m->c);
-    if (rc) return rc;
-    const hg_config &c = m->c;
-    const uint32_t d = c.d_model, f = c.expert_ffn, hd = c.head_dim;
-    const uint32_t qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
-    m->n_slots = slots_of(c);
-    for (uint32_t i = 0; i < c.n_layers; ++i) {
-        auto L = std::make_unique<Layer>();
-        const std::string p = "blk." + std::to_string(i) + ".";
-        L->moe = i >= c.n_dense;
-        if (L->moe) {
-            std::vector<float> rw;
-            if ((rc = g.load(p + "ffn_gate_inp.weight", rw, g_err))) return rc;
-            if (rw.size() != (size_t)c.n_experts * d)
-                return fail(HG_ERR_FORMAT, "tensor `" + p + "ffn_gate_inp.weight` has wrong size");
-            if ((rc = L->router.upload(rw.data(), rw.size() * 4))) return rc;
-            if (d % 32) return fail(HG_ERR_FORMAT, "d_model must be a multiple of 32");
-            std::vector<float> rp(rw.size());   // the router kernel's 16-byte-per-step row layout
-            for (size_t e = 0; e < c.n_experts; ++e)
-                for (uint32_t k = 0; k < d; ++k) rp[e * d + router_perm(k)] = rw[e * d + k];
-            if ((rc = L->router_p.upload(rp.data(), rp.size() * 4))) return rc;
-            if ((rc = load_norm(g, p + "exp_probs_b.bias", c.n_experts, L->bias))) return rc;
-            if ((rc = load_q8(g, p + "ffn_gate_exps.weight", c.n_experts * f, d, L->gate_e, m.get()))) return rc;
-            if ((rc = load_q8(g, p + "ffn_up_exps.weight", c.n_experts * f, d, L->up_e, m.get()))) return rc;
-            if ((rc = load_q8(g, p + "ffn_down_exps.weight", c.n_experts * d, f, L->down_e, m.get()))) return rc;
-            if ((rc = load_q8(g, p + "ffn_gate_shexp.weight", f, d, L->gate_sh, m.get()))) return rc;
-            if ((rc = load_q8(g, p + "ffn_up_shexp.weight", f, d, L->up_sh, m.get()))) return rc;
-            if ((rc = load_q8(g, p + "ffn_down_shexp.weight", d, f, L->down_sh, m.get()))) return rc;
-        } else {
-            if ((rc = load_q8(g, p + "ffn_gate.weight", c.dense_ffn, d, L->gate, m.get()))) return rc;
-            if ((rc = load_q8(g, p + "ffn_up.weight", c.dense_ffn, d, L->up, m.get()))) return rc;
-            if ((rc = load_q8(g, p + "ffn_down.weight", d, c.dense_ffn, L->down, m.get()))) return rc;
-        }
-        if ((rc = load_norm(g, p + "attn_norm.weight", d, L->attn_norm))) return rc;
-        if ((rc = load_q8(g, p + "attn_qkv.weight", qd + 2 * kvd, d, L->qkv, m.get()))) return rc;
-        if ((rc = load_norm(g, p + "attn_q_norm.weight", hd, L->q_norm))) return rc;
-        if ((rc = load_norm(g, p + "attn_k_norm.weight", hd, L->k_norm))) return rc;
-        if ((rc = load_q8(g, p + "attn_output.weight", d, qd, L->o, m.get()))) return rc;
-        if ((rc = load_norm(g, p + "ffn_norm.weight", d, L->ffn_norm))) return rc;
-        m->layers.push_back(std::move(L));
-    }
-    if ((rc = load_q8(g, "output.weight", c.vocab_size, d, m->output, m.get()))) return rc;
-    if ((rc = upload_pending(m.get()))) return rc;
-    {
-        std::vector<float> emb;
-        if ((rc = g.load("token_embd.weight", emb, g_err))) return rc;
-        if (emb.size() != (size_t)c.vocab_size * d) return fail(HG_ERR_FORMAT, "tensor `token_embd.weight` has wrong size");
-        if ((rc = m->token_embd.upload(emb.data(), emb.size() * 4))) return rc;
-    }
-    if ((rc = load_norm(g, "output_norm.weight", d, m->output_norm))) return rc;
-    std::vector<float> cs, sn;
-    rope_table(hd, c.context_length, c.rope_theta, cs, sn);
-    if ((rc = m->rope_cos.upload(cs.data(), cs.size() * 4))) return rc;
-    if ((rc = m->rope_sin.upload(sn.data(), sn.size() * 4))) return rc;
-    *out = m.release();
-    return HG_OK;
+    return guard([&]() -> int {
+        if (!out) return fail(HG_ERR_ARG, "out is NULL");
+        *out = nullptr;
+        if (!path) return fail(HG_ERR_ARG, "path is NULL");
+        if (!quant)
+            return fail(HG_ERR_UNSUPPORTED, "F32 matrices (quant = false) are not supported by the GPU backend");
+        auto hm = std::make_unique<HostModel>();
+        int rc = parse_model(path, *hm);
+        if (rc) return rc;
+        if ((rc = check_device())) return rc;
+        auto m = std::make_unique<hg_model>();
+        if ((rc = upload_model(*hm, m.get()))) return rc;
+        *out = m.release();
+        return HG_OK;
+    });
+}
+
+int hg_gguf_load_tensor(const char *path, const char *name, float *out, uint64_t cap, uint64_t *n) {
+    return guard([&]() -> int {
+        if (!path || !name || !n) return fail(HG_ERR_ARG, "NULL argument");
+        *n = 0;
+        Gguf g;
+        int rc = g.open(path, g_err);
+        if (rc) return rc;
+        std::vector<float> v;
+        if ((rc = g.load(name, v, g_err))) return rc;
+        *n = v.size();
+        if (!out) return HG_OK;
+        if (cap < v.size())
+            return fail(HG_ERR_ARG, "output holds " + std::to_string(cap) + " floats, tensor has " +
+                                        std::to_string(v.size()));
+        memcpy(out, v.data(), v.size() * 4);
+        return HG_OK;
+    });
 }
 
 void hg_model_free(hg_model *m) { delete m; }
 
 int hg_model_config(const hg_model *m, hg_config *out) {
-    if (!m || !out) return fail(HG_ERR_ARG, "NULL argument");
-    *out = m->c;
-    return HG_OK;
+    return guard([&]() -> int {
+        if (!m || !out) return fail(HG_ERR_ARG, "NULL argument");
+        *out = m->c;
+        return HG_OK;
+    });
 }
 
 uint64_t hg_weight_bytes(const hg_model *m) { return m ? m->ref_bytes : 0; }
 uint64_t hg_device_weight_bytes(const hg_model *m) { return m ? m->dev_bytes : 0; }
 
 int hg_token_embedding(const hg_model *m, uint32_t id, float *out) {
-    if (!m || !out) return fail(HG_ERR_ARG, "NULL argument");
-    if (id >= m->c.vocab_size) return fail(HG_ERR_ARG, "token " + std::to_string(id) + " out of range");
-    HIP_TRY(hipMemcpy(out, m->token_embd.as<float>() + (size_t)id * m->c.d_model, m->c.d_model * 4,
-                      hipMemcpyDeviceToHost));
-    return HG_OK;
+    return guard([&]() -> int {
+        if (!m || !out) return fail(HG_ERR_ARG, "NULL argument");
+        if (id >= m->c.vocab_size) return fail(HG_ERR_ARG, "token " + std::to_string(id) + " out of range");
+        HIP_TRY(hipMemcpy(out, m->token_embd.as<float>() + (size_t)id * m->c.d_model, m->c.d_model * 4,
+                          hipMemcpyDeviceToHost));
+        return HG_OK;
+    });
 }
 
 }  // extern "C"
@@ -376,8 +462,8 @@ void enqueue_layers(hg_kv *kv, int order) {
             mark(kv, part == 0 ? P_ATTN_A : P_ATTN_B);
             launch_attn(st, kv->exact, part, c.head_dim, kv->qkv.as<float>(), L.q_norm.as<float>(),
                         L.k_norm.as<float>(), c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), p,
-                        layer_k(kv, l), layer_v(kv, l), kv->cap, c.n_heads, c.n_kv_heads, kv->S,
-                        kv->part.as<float>(), kv->scores.as<float>(), kv->o.as<float>(),
+                        layer_k(kv, l), layer_v(kv, l), kv->cap, kv->win, c.n_heads, c.n_kv_heads,
+                        attn_splits(kv->win), kv->part.as<float>(), kv->scores.as<float>(), kv->o.as<float>(),
                         kv->exact ? nullptr : qa, da);
         }
         mark(kv, P_OPROJ);
@@ -452,12 +538,25 @@ void enqueue_body(hg_kv *kv) {
     launch_advance(kv->st, kv->params.as<StepParams>());
 }
 
+// A launch the kernels' host code refused or HIP rejected while `fn` enqueued (sticky per
+// thread, cleared by the check).
+int check_launches(const char *what) {
+    std::string msg;
+    const hipError_t e = take_launch_error(msg);
+    if (e == hipSuccess) return HG_OK;
+    return fail(HG_ERR_DEVICE, std::string(what) + ": " + msg);
+}
+
 // Run `fn`'s kernels on the cache's stream: replay its captured graph (capturing it on
-// first use) or, with HG_GRAPH=0, launch eagerly.
+// first use) or, with HG_GRAPH=0, launch eagerly.  A launch error during capture ends the
+// capture and discards the graph, so no step returns HG_OK without having run.
 template <class F>
 int run(hg_kv *kv, hipGraphExec_t &exec, F fn) {
+    (void)take_launch_error_reset();
     if (!kv->use_graph) {
         fn(kv);
+        int rc = check_launches("kernel launch");
+        if (rc) return rc;
         HIP_TRY(hipGetLastError());
         return HG_OK;
     }
@@ -465,7 +564,12 @@ int run(hg_kv *kv, hipGraphExec_t &exec, F fn) {
         hipGraph_t graph = nullptr;
         HIP_TRY(hipStreamBeginCapture(kv->st, hipStreamCaptureModeThreadLocal));
         fn(kv);
+        const int lrc = check_launches("kernel launch during graph capture");
         hipError_t e = hipStreamEndCapture(kv->st, &graph);
+        if (lrc) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return lrc;
+        }
         if (e != hipSuccess) return fail(HG_ERR_DEVICE, std::string("graph capture: ") + hipGetErrorString(e));
         e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
@@ -476,6 +580,12 @@ int run(hg_kv *kv, hipGraphExec_t &exec, F fn) {
     }
     HIP_TRY(hipGraphLaunch(exec, kv->st));
     return HG_OK;
+}
+
+// The captured step for the window of a step at position pos (kv->win is set for enqueue).
+hipGraphExec_t &graph_for(hg_kv *kv, std::map<uint32_t, hipGraphExec_t> &set, uint32_t pos) {
+    kv->win = window_of(pos + 1, kv->cap);
+    return set[kv->win];
 }
 
 int set_params(hg_kv *kv, uint32_t token, uint32_t pos, uint32_t feedback, uint32_t embed, uint32_t base) {
@@ -517,8 +627,10 @@ int check_step(const hg_model *m, const hg_kv *kv, uint32_t pos, uint32_t n) {
 
 hg_kv::~hg_kv() {
     if (st) (void)hipStreamSynchronize(st);
-    if (g_decode) (void)hipGraphExecDestroy(g_decode);
-    if (g_body) (void)hipGraphExecDestroy(g_body);
+    for (auto &g : g_decode)
+        if (g.second) (void)hipGraphExecDestroy(g.second);
+    for (auto &g : g_body)
+        if (g.second) (void)hipGraphExecDestroy(g.second);
     if (g_tail) (void)hipGraphExecDestroy(g_tail);
     if (h_params) (void)hipHostFree(h_params);
     if (h_ids) (void)hipHostFree(h_ids);
@@ -529,53 +641,55 @@ hg_kv::~hg_kv() {
 extern "C" {
 
 int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out) {
-    if (!m || !out) return fail(HG_ERR_ARG, "NULL argument");
-    *out = nullptr;
-    const hg_config &c = m->c;
-    if (max_ctx == 0 || max_ctx > c.context_length) max_ctx = c.context_length;
-    auto kv = std::make_unique<hg_kv>();
-    kv->m = m;
-    kv->cap = max_ctx;
-    kv->flags = flags;
-    kv->exact = (flags & HG_KV_FAST) == 0;
-    const char *ge = getenv("HG_GRAPH");
-    kv->use_graph = !(ge && ge[0] == '0');
-    kv->S = std::max(64u, div_up(kv->cap, 256));  // splits of at most 256 positions (LDS bound)
-    if (kv->exact && pv_ring_slots(kv->cap) < 2)
-        return fail(HG_ERR_UNSUPPORTED, "a reference-order cache holds at most 32768 positions");
-    HIP_TRY(hipStreamCreateWithFlags(&kv->st, hipStreamNonBlocking));
-    const size_t kvsz = (size_t)c.n_layers * c.n_kv_heads * kv->cap * c.head_dim * 4;
-    int rc;
-    if ((rc = kv->kc.alloc(kvsz)) ||
-        (rc = kv->vc.alloc((size_t)c.n_layers * v_layer_floats(kv->cap, c.n_kv_heads, c.head_dim) * 4)))
-        return rc;
-    const uint32_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
-    const uint32_t maxk = std::max(std::max(c.d_model, qd), std::max(c.dense_ffn, c.expert_ffn));
-    const uint32_t maxnc = div_up(maxk / QK, 4);
-    const uint32_t ffw = std::max(c.dense_ffn, c.expert_ffn) * std::max(m->n_slots, 1u);
-    kv->n_part = matvec_blocks(c.vocab_size, kv->lm_threads);
-    if ((rc = kv->x.alloc(c.d_model * 4)) || (rc = kv->qkv.alloc((size_t)(qd + 2 * kvd) * 4)) ||
-        (rc = kv->o.alloc((size_t)qd * 4)) ||
-        (rc = kv->part.alloc((size_t)c.n_heads * kv->S * (c.head_dim + 2) * 4)) ||
-        (rc = kv->scores.alloc(kv->exact ? (size_t)c.n_heads * kv->cap * 4 : 4)) ||
-        (rc = kv->a.alloc((size_t)ffw * 4)) || (rc = kv->logits.alloc((size_t)c.vocab_size * 4)) ||
-        (rc = kv->pv.alloc((size_t)kv->n_part * 4)) || (rc = kv->pi.alloc((size_t)kv->n_part * 4)) ||
-        (rc = kv->qa.alloc((size_t)maxnc * CHUNK_BYTES)) || (rc = kv->da.alloc((size_t)maxnc * 4 * 4)) ||
-        (rc = kv->topk_idx.alloc(64 * 4)) || (rc = kv->topk_w.alloc(64 * 4)) || (rc = kv->order.alloc(64 * 4)) ||
-        (rc = kv->rec_idx.alloc((size_t)c.n_layers * std::max(c.top_k, 1u) * 4)) ||
-        (rc = kv->rec_w.alloc((size_t)c.n_layers * std::max(c.top_k, 1u) * 4)) ||
-        (rc = kv->params.alloc(sizeof(StepParams))) || (rc = kv->out_ids.alloc((size_t)(kv->cap + 1) * 4)))
-        return rc;
-    HIP_TRY(hipMemset(kv->rec_idx.p, 0xff, kv->rec_idx.n));
-    HIP_TRY(hipMemset(kv->rec_w.p, 0, kv->rec_w.n));
-    HIP_TRY(hipMemset(kv->kc.p, 0, kv->kc.n));
-    HIP_TRY(hipMemset(kv->vc.p, 0, kv->vc.n));
-    HIP_TRY(hipHostMalloc((void **)&kv->h_params, sizeof(StepParams), hipHostMallocDefault));
-    HIP_TRY(hipHostMalloc((void **)&kv->h_ids, (size_t)(kv->cap + 1) * 4, hipHostMallocDefault));
-    HIP_TRY(hipHostMalloc((void **)&kv->h_logits, (size_t)c.vocab_size * 4, hipHostMallocDefault));
-    HIP_TRY(hipDeviceSynchronize());
-    *out = kv.release();
-    return HG_OK;
+    return guard([&]() -> int {
+        if (!m || !out) return fail(HG_ERR_ARG, "NULL argument");
+        *out = nullptr;
+        const hg_config &c = m->c;
+        if (max_ctx == 0 || max_ctx > c.context_length) max_ctx = c.context_length;
+        auto kv = std::make_unique<hg_kv>();
+        kv->m = m;
+        kv->cap = max_ctx;
+        kv->flags = flags;
+        kv->exact = (flags & HG_KV_FAST) == 0;
+        const char *ge = getenv("HG_GRAPH");
+        kv->use_graph = !(ge && ge[0] == '0');
+        kv->win = kv->cap;
+        if (kv->exact && pv_ring_slots(kv->cap) < 2)
+            return fail(HG_ERR_UNSUPPORTED, "a reference-order cache holds at most 32768 positions");
+        HIP_TRY(hipStreamCreateWithFlags(&kv->st, hipStreamNonBlocking));
+        const size_t kvsz = (size_t)c.n_layers * c.n_kv_heads * kv->cap * c.head_dim * 4;
+        int rc;
+        if ((rc = kv->kc.alloc(kvsz)) ||
+            (rc = kv->vc.alloc((size_t)c.n_layers * v_layer_floats(kv->cap, c.n_kv_heads, c.head_dim) * 4)))
+            return rc;
+        const uint32_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+        const uint32_t maxk = std::max(std::max(c.d_model, qd), std::max(c.dense_ffn, c.expert_ffn));
+        const uint32_t maxnc = div_up(maxk / QK, 4);
+        const uint32_t ffw = std::max(c.dense_ffn, c.expert_ffn) * std::max(m->n_slots, 1u);
+        kv->n_part = matvec_blocks(c.vocab_size, kv->lm_threads);
+        if ((rc = kv->x.alloc(c.d_model * 4)) || (rc = kv->qkv.alloc((size_t)(qd + 2 * kvd) * 4)) ||
+            (rc = kv->o.alloc((size_t)qd * 4)) ||
+            (rc = kv->part.alloc((size_t)c.n_heads * attn_splits(kv->cap) * (c.head_dim + 2) * 4)) ||
+            (rc = kv->scores.alloc(kv->exact ? (size_t)c.n_heads * kv->cap * 4 : 4)) ||
+            (rc = kv->a.alloc((size_t)ffw * 4)) || (rc = kv->logits.alloc((size_t)c.vocab_size * 4)) ||
+            (rc = kv->pv.alloc((size_t)kv->n_part * 4)) || (rc = kv->pi.alloc((size_t)kv->n_part * 4)) ||
+            (rc = kv->qa.alloc((size_t)maxnc * CHUNK_BYTES)) || (rc = kv->da.alloc((size_t)maxnc * 4 * 4)) ||
+            (rc = kv->topk_idx.alloc(64 * 4)) || (rc = kv->topk_w.alloc(64 * 4)) || (rc = kv->order.alloc(64 * 4)) ||
+            (rc = kv->rec_idx.alloc((size_t)c.n_layers * std::max(c.top_k, 1u) * 4)) ||
+            (rc = kv->rec_w.alloc((size_t)c.n_layers * std::max(c.top_k, 1u) * 4)) ||
+            (rc = kv->params.alloc(sizeof(StepParams))) || (rc = kv->out_ids.alloc((size_t)(kv->cap + 1) * 4)))
+            return rc;
+        HIP_TRY(hipMemset(kv->rec_idx.p, 0xff, kv->rec_idx.n));
+        HIP_TRY(hipMemset(kv->rec_w.p, 0, kv->rec_w.n));
+        HIP_TRY(hipMemset(kv->kc.p, 0, kv->kc.n));
+        HIP_TRY(hipMemset(kv->vc.p, 0, kv->vc.n));
+        HIP_TRY(hipHostMalloc((void **)&kv->h_params, sizeof(StepParams), hipHostMallocDefault));
+        HIP_TRY(hipHostMalloc((void **)&kv->h_ids, (size_t)(kv->cap + 1) * 4, hipHostMallocDefault));
+        HIP_TRY(hipHostMalloc((void **)&kv->h_logits, (size_t)c.vocab_size * 4, hipHostMallocDefault));
+        HIP_TRY(hipDeviceSynchronize());
+        *out = kv.release();
+        return HG_OK;
+    });
 }
 
 void hg_kv_free(hg_kv *kv) { delete kv; }
@@ -583,174 +697,223 @@ void hg_kv_free(hg_kv *kv) { delete kv; }
 uint32_t hg_kv_len(const hg_kv *kv) { return kv ? kv->len : 0; }
 
 int hg_kv_read(const hg_kv *kv, uint32_t layer, float *k, float *v) {
-    if (!kv || !k || !v) return fail(HG_ERR_ARG, "NULL argument");
-    const hg_config &c = kv->m->c;
-    if (layer >= c.n_layers) return fail(HG_ERR_ARG, "layer out of range");
-    const uint32_t hd = c.head_dim, nkv = c.n_kv_heads, len = kv->len;
-    std::vector<float> kb((size_t)nkv * kv->cap * hd), vb(kb.size());
-    HIP_TRY(hipStreamSynchronize(kv->st));
-    HIP_TRY(hipMemcpy(kb.data(), layer_k(kv, layer), kb.size() * 4, hipMemcpyDeviceToHost));
-    HIP_TRY(hipMemcpy(vb.data(), layer_v(kv, layer), vb.size() * 4, hipMemcpyDeviceToHost));
-    for (uint32_t t = 0; t < len; ++t)
-        for (uint32_t g = 0; g < nkv; ++g) {
-            memcpy(k + ((size_t)t * nkv + g) * hd, kb.data() + ((size_t)g * kv->cap + t) * hd, hd * 4);
-            memcpy(v + ((size_t)t * nkv + g) * hd, vb.data() + ((size_t)g * kv->cap + t) * hd, hd * 4);
-        }
-    return HG_OK;
+    return guard([&]() -> int {
+        if (!kv || !k || !v) return fail(HG_ERR_ARG, "NULL argument");
+        const hg_config &c = kv->m->c;
+        if (layer >= c.n_layers) return fail(HG_ERR_ARG, "layer out of range");
+        const uint32_t hd = c.head_dim, nkv = c.n_kv_heads, len = kv->len;
+        std::vector<float> kb((size_t)nkv * kv->cap * hd), vb(kb.size());
+        HIP_TRY(hipStreamSynchronize(kv->st));
+        HIP_TRY(hipMemcpy(kb.data(), layer_k(kv, layer), kb.size() * 4, hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(vb.data(), layer_v(kv, layer), vb.size() * 4, hipMemcpyDeviceToHost));
+        for (uint32_t t = 0; t < len; ++t)
+            for (uint32_t g = 0; g < nkv; ++g) {
+                memcpy(k + ((size_t)t * nkv + g) * hd, kb.data() + ((size_t)g * kv->cap + t) * hd, hd * 4);
+                memcpy(v + ((size_t)t * nkv + g) * hd, vb.data() + ((size_t)g * kv->cap + t) * hd, hd * 4);
+            }
+        return HG_OK;
+    });
+}
+
+int hg_kv_load(hg_kv *kv, uint32_t len, const float *k, const float *v) {
+    return guard([&]() -> int {
+        if (!kv || (len && (!k || !v))) return fail(HG_ERR_ARG, "NULL argument");
+        if (len > kv->cap)
+            return fail(HG_ERR_ARG, "len " + std::to_string(len) + " exceeds the cache (" + std::to_string(kv->cap) +
+                                        " positions)");
+        const hg_config &c = kv->m->c;
+        const uint32_t hd = c.head_dim, nkv = c.n_kv_heads, kvd = nkv * hd, vts = vt_stride(kv->cap);
+        HIP_TRY(hipStreamSynchronize(kv->st));
+        std::vector<float> kh((size_t)len * hd), vh((size_t)len * hd), vt((size_t)hd * len);
+        for (uint32_t l = 0; l < c.n_layers; ++l)
+            for (uint32_t g = 0; g < nkv; ++g) {
+                const float *ks = k + (size_t)l * len * kvd, *vs = v + (size_t)l * len * kvd;
+                for (uint32_t t = 0; t < len; ++t) {
+                    memcpy(&kh[(size_t)t * hd], ks + (size_t)t * kvd + g * hd, hd * 4);
+                    memcpy(&vh[(size_t)t * hd], vs + (size_t)t * kvd + g * hd, hd * 4);
+                    for (uint32_t i = 0; i < hd; ++i) vt[(size_t)i * len + t] = vs[(size_t)t * kvd + g * hd + i];
+                }
+                if (!len) continue;
+                float *kd = layer_k(kv, l) + (size_t)g * kv->cap * hd, *vd = layer_v(kv, l) + (size_t)g * kv->cap * hd;
+                float *vtd = layer_v(kv, l) + (size_t)nkv * kv->cap * hd + (size_t)g * hd * vts;
+                HIP_TRY(hipMemcpy(kd, kh.data(), (size_t)len * hd * 4, hipMemcpyHostToDevice));
+                HIP_TRY(hipMemcpy(vd, vh.data(), (size_t)len * hd * 4, hipMemcpyHostToDevice));
+                HIP_TRY(hipMemcpy2D(vtd, (size_t)vts * 4, vt.data(), (size_t)len * 4, (size_t)len * 4, hd,
+                                    hipMemcpyHostToDevice));
+            }
+        kv->len = len;
+        return HG_OK;
+    });
 }
 
 int hg_forward(const hg_model *m, hg_kv *kv, uint32_t token, uint32_t pos, float *logits, uint32_t *next) {
-    int rc = check_step(m, kv, pos, 1);
-    if (rc) return rc;
-    if (token >= m->c.vocab_size)
-        return fail(HG_ERR_ARG, "token " + std::to_string(token) + " out of range (vocab " +
-                                    std::to_string(m->c.vocab_size) + ")");
-    if ((rc = set_params(kv, token, pos, 0, 1, pos))) return rc;
-    if ((rc = run(kv, kv->g_decode, enqueue_decode))) return rc;
-    if ((rc = finish(kv, logits, next))) return rc;
-    kv->len = pos + 1;
-    return HG_OK;
+    return guard([&]() -> int {
+        int rc = check_step(m, kv, pos, 1);
+        if (rc) return rc;
+        if (token >= m->c.vocab_size)
+            return fail(HG_ERR_ARG, "token " + std::to_string(token) + " out of range (vocab " +
+                                        std::to_string(m->c.vocab_size) + ")");
+        if ((rc = set_params(kv, token, pos, 0, 1, pos))) return rc;
+        if ((rc = run(kv, graph_for(kv, kv->g_decode, pos), enqueue_decode))) return rc;
+        if ((rc = finish(kv, logits, next))) return rc;
+        kv->len = pos + 1;
+        return HG_OK;
+    });
 }
 
 int hg_forward_x(const hg_model *m, hg_kv *kv, const float *x, uint32_t pos, float *logits, uint32_t *next) {
-    int rc = check_step(m, kv, pos, 1);
-    if (rc) return rc;
-    if (!x) return fail(HG_ERR_ARG, "x is NULL");
-    HIP_TRY(hipMemcpyAsync(kv->x.p, x, (size_t)m->c.d_model * 4, hipMemcpyHostToDevice, kv->st));
-    if ((rc = set_params(kv, 0, pos, 0, 0, pos))) return rc;
-    if ((rc = run(kv, kv->g_decode, enqueue_decode))) return rc;
-    if ((rc = finish(kv, logits, next))) return rc;
-    kv->len = pos + 1;
-    return HG_OK;
+    return guard([&]() -> int {
+        int rc = check_step(m, kv, pos, 1);
+        if (rc) return rc;
+        if (!x) return fail(HG_ERR_ARG, "x is NULL");
+        HIP_TRY(hipMemcpyAsync(kv->x.p, x, (size_t)m->c.d_model * 4, hipMemcpyHostToDevice, kv->st));
+        if ((rc = set_params(kv, 0, pos, 0, 0, pos))) return rc;
+        if ((rc = run(kv, graph_for(kv, kv->g_decode, pos), enqueue_decode))) return rc;
+        if ((rc = finish(kv, logits, next))) return rc;
+        kv->len = pos + 1;
+        return HG_OK;
+    });
 }
 
 int hg_prefill(const hg_model *m, hg_kv *kv, const float *inputs, uint32_t tn, float *logits, uint32_t *next) {
-    if (!kv) return fail(HG_ERR_ARG, "NULL argument");
-    if (tn == 0) return fail(HG_ERR_ARG, "prefill needs at least one input row");
-    if (!inputs) return fail(HG_ERR_ARG, "inputs is NULL");
-    const uint32_t base = kv->len;
-    int rc = check_step(m, kv, base, tn);
-    if (rc) return rc;
-    const size_t rowb = (size_t)m->c.d_model * 4;
-    if (tn > kv->inputs_rows) {
-        HIP_TRY(hipStreamSynchronize(kv->st));
-        if ((rc = kv->inputs.alloc(rowb * tn))) return rc;
-        kv->inputs_rows = tn;
-        if (kv->g_body) {  // the captured body reads the old buffer
-            (void)hipGraphExecDestroy(kv->g_body);
-            kv->g_body = nullptr;
+    return guard([&]() -> int {
+        if (!kv) return fail(HG_ERR_ARG, "NULL argument");
+        if (tn == 0) return fail(HG_ERR_ARG, "prefill needs at least one input row");
+        if (!inputs) return fail(HG_ERR_ARG, "inputs is NULL");
+        const uint32_t base = kv->len;
+        int rc = check_step(m, kv, base, tn);
+        if (rc) return rc;
+        const size_t rowb = (size_t)m->c.d_model * 4;
+        if (tn > kv->inputs_rows) {
+            HIP_TRY(hipStreamSynchronize(kv->st));
+            if ((rc = kv->inputs.alloc(rowb * tn))) return rc;
+            kv->inputs_rows = tn;
+            for (auto &g : kv->g_body)   // the captured bodies read the old buffer
+                if (g.second) (void)hipGraphExecDestroy(g.second);
+            kv->g_body.clear();
         }
-    }
-    HIP_TRY(hipMemcpyAsync(kv->inputs.p, inputs, rowb * tn, hipMemcpyHostToDevice, kv->st));
-    if ((rc = set_params(kv, 0, base, 0, 0, base))) return rc;
-    for (uint32_t t = 0; t < tn; ++t)
-        if ((rc = run(kv, kv->g_body, enqueue_body))) return rc;
-    if ((rc = run(kv, kv->g_tail, enqueue_tail))) return rc;
-    if ((rc = finish(kv, logits, next))) return rc;
-    kv->len = base + tn;
-    return HG_OK;
+        HIP_TRY(hipMemcpyAsync(kv->inputs.p, inputs, rowb * tn, hipMemcpyHostToDevice, kv->st));
+        if ((rc = set_params(kv, 0, base, 0, 0, base))) return rc;
+        for (uint32_t t = 0; t < tn; ++t)
+            if ((rc = run(kv, graph_for(kv, kv->g_body, base + t), enqueue_body))) return rc;
+        if ((rc = run(kv, kv->g_tail, enqueue_tail))) return rc;
+        if ((rc = finish(kv, logits, next))) return rc;
+        kv->len = base + tn;
+        return HG_OK;
+    });
 }
 
 int hg_decode_greedy(const hg_model *m, hg_kv *kv, uint32_t first_token, uint32_t n_steps, uint32_t *out_ids) {
-    if (!kv) return fail(HG_ERR_ARG, "NULL argument");
-    const uint32_t pos = kv->len;
-    int rc = check_step(m, kv, pos, n_steps);
-    if (rc) return rc;
-    if (first_token >= m->c.vocab_size) return fail(HG_ERR_ARG, "token out of range");
-    if (n_steps == 0) return HG_OK;
-    if (!out_ids) return fail(HG_ERR_ARG, "out_ids is NULL");
-    if ((rc = set_params(kv, first_token, pos, 1, 1, pos))) return rc;
-    for (uint32_t i = 0; i < n_steps; ++i)
-        if ((rc = run(kv, kv->g_decode, enqueue_decode))) return rc;
-    HIP_TRY(hipMemcpyAsync(kv->h_ids, kv->out_ids.p, (size_t)n_steps * 4, hipMemcpyDeviceToHost, kv->st));
-    HIP_TRY(hipStreamSynchronize(kv->st));
-    memcpy(out_ids, kv->h_ids, (size_t)n_steps * 4);
-    kv->len = pos + n_steps;
-    return HG_OK;
+    return guard([&]() -> int {
+        if (!kv) return fail(HG_ERR_ARG, "NULL argument");
+        const uint32_t pos = kv->len;
+        int rc = check_step(m, kv, pos, n_steps);
+        if (rc) return rc;
+        if (first_token >= m->c.vocab_size) return fail(HG_ERR_ARG, "token out of range");
+        if (n_steps == 0) return HG_OK;
+        if (!out_ids) return fail(HG_ERR_ARG, "out_ids is NULL");
+        if ((rc = set_params(kv, first_token, pos, 1, 1, pos))) return rc;
+        for (uint32_t i = 0; i < n_steps; ++i)
+            if ((rc = run(kv, graph_for(kv, kv->g_decode, pos + i), enqueue_decode))) return rc;
+        HIP_TRY(hipMemcpyAsync(kv->h_ids, kv->out_ids.p, (size_t)n_steps * 4, hipMemcpyDeviceToHost, kv->st));
+        HIP_TRY(hipStreamSynchronize(kv->st));
+        memcpy(out_ids, kv->h_ids, (size_t)n_steps * 4);
+        kv->len = pos + n_steps;
+        return HG_OK;
+    });
 }
 
 int hg_generate_greedy(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_new,
                        float rep_penalty, uint32_t eos, uint32_t *out_ids, uint32_t *n_out) {
-    if (!m || !kv || !n_out) return fail(HG_ERR_ARG, "NULL argument");
-    *n_out = 0;
-    if (n_prompt == 0) return HG_OK;
-    const hg_config &c = m->c;
-    const uint32_t d = c.d_model, V = c.vocab_size, valid = V < 50257 ? V : 50257;
-    std::vector<float> in((size_t)n_prompt * d);
-    int rc;
-    for (uint32_t i = 0; i < n_prompt; ++i)
-        if ((rc = hg_token_embedding(m, prompt[i], in.data() + (size_t)i * d))) return rc;
-    const bool host_sample = rep_penalty != 1.0f;
-    std::vector<float> logits(host_sample ? V : 0);
-    uint32_t next = 0, pos = kv->len + n_prompt;
-    if ((rc = hg_prefill(m, kv, in.data(), n_prompt, host_sample ? logits.data() : nullptr, &next))) return rc;
-    const uint32_t stop = std::min(c.context_length, kv->cap);
-    uint32_t n = 0;
-    for (uint32_t it = 0; it < max_new; ++it) {
-        if (host_sample) {
-            for (uint32_t i = valid; i < V; ++i) logits[i] = -INFINITY;
-            for (uint32_t q = 0; q < n; ++q) {
-                float &l = logits[out_ids[q]];
-                l = l > 0.0f ? l / rep_penalty : l * rep_penalty;
+    return guard([&]() -> int {
+        if (!m || !kv || !n_out) return fail(HG_ERR_ARG, "NULL argument");
+        *n_out = 0;
+        if (n_prompt > 0 && !prompt) return fail(HG_ERR_ARG, "prompt is NULL");
+        if (max_new > 0 && !out_ids) return fail(HG_ERR_ARG, "out_ids is NULL");
+        if (n_prompt == 0) return HG_OK;
+        const hg_config &c = m->c;
+        const uint32_t d = c.d_model, V = c.vocab_size, valid = V < 50257 ? V : 50257;
+        std::vector<float> in((size_t)n_prompt * d);
+        int rc;
+        for (uint32_t i = 0; i < n_prompt; ++i)
+            if ((rc = hg_token_embedding(m, prompt[i], in.data() + (size_t)i * d))) return rc;
+        const bool host_sample = rep_penalty != 1.0f;
+        std::vector<float> logits(host_sample ? V : 0);
+        uint32_t next = 0, pos = kv->len + n_prompt;
+        if ((rc = hg_prefill(m, kv, in.data(), n_prompt, host_sample ? logits.data() : nullptr, &next))) return rc;
+        const uint32_t stop = std::min(c.context_length, kv->cap);
+        uint32_t n = 0;
+        for (uint32_t it = 0; it < max_new; ++it) {
+            if (host_sample) {
+                for (uint32_t i = valid; i < V; ++i) logits[i] = -INFINITY;
+                for (uint32_t q = 0; q < n; ++q) {
+                    float &l = logits[out_ids[q]];
+                    l = l > 0.0f ? l / rep_penalty : l * rep_penalty;
+                }
+                uint32_t best = 0;
+                float bv = -INFINITY;
+                for (uint32_t i = 0; i < V; ++i)
+                    if (logits[i] > bv) { bv = logits[i]; best = i; }
+                next = best;
             }
-            uint32_t best = 0;
-            float bv = -INFINITY;
-            for (uint32_t i = 0; i < V; ++i)
-                if (logits[i] > bv) { bv = logits[i]; best = i; }
-            next = best;
+            if (next == eos) break;
+            out_ids[n++] = next;
+            if (pos + 1 >= stop) break;
+            if ((rc = hg_forward(m, kv, next, pos, host_sample ? logits.data() : nullptr, &next))) {
+                *n_out = n;
+                return rc;
+            }
+            ++pos;
         }
-        if (next == eos) break;
-        out_ids[n++] = next;
-        if (pos + 1 >= stop) break;
-        if ((rc = hg_forward(m, kv, next, pos, host_sample ? logits.data() : nullptr, &next))) {
-            *n_out = n;
-            return rc;
-        }
-        ++pos;
-    }
-    *n_out = n;
-    return HG_OK;
+        *n_out = n;
+        return HG_OK;
+    });
 }
 
 int hg_profile_step(const hg_model *m, hg_kv *kv, uint32_t token, uint32_t reps, float *us, uint32_t *launches) {
-    if (!m || !kv || kv->m != m || !us || !launches) return fail(HG_ERR_ARG, "NULL argument");
-    if (kv->len >= kv->cap) return fail(HG_ERR_ARG, "the cache is full: no free position to replay a step at");
-    if (token >= m->c.vocab_size) return fail(HG_ERR_ARG, "token out of range");
-    for (int c = 0; c < P_COUNT; ++c) { us[c] = 0.0f; launches[c] = 0; }
-    int rc;
-    for (uint32_t r = 0; r < reps; ++r) {
-        if ((rc = set_params(kv, token, kv->len, 0, 1, kv->len))) return rc;
-        LaunchTimer timer;
-        kv->timer = &timer;
-        set_launch_timer(&timer);
-        enqueue_decode(kv);
-        set_launch_timer(nullptr);
-        kv->timer = nullptr;
-        hipError_t e = hipStreamSynchronize(kv->st);
-        for (size_t i = 0; e == hipSuccess && i < timer.ev.size(); ++i) {
-            float ms = 0.0f;
-            e = hipEventElapsedTime(&ms, timer.ev[i].first, timer.ev[i].second);
-            us[timer.tags[i]] += ms * 1000.0f / reps;
-            if (r == 0) launches[timer.tags[i]] += 1;
+    return guard([&]() -> int {
+        if (!m || !kv || kv->m != m || !us || !launches) return fail(HG_ERR_ARG, "NULL argument");
+        if (kv->len >= kv->cap) return fail(HG_ERR_ARG, "the cache is full: no free position to replay a step at");
+        if (token >= m->c.vocab_size) return fail(HG_ERR_ARG, "token out of range");
+        for (int c = 0; c < P_COUNT; ++c) { us[c] = 0.0f; launches[c] = 0; }
+        int rc;
+        for (uint32_t r = 0; r < reps; ++r) {
+            if ((rc = set_params(kv, token, kv->len, 0, 1, kv->len))) return rc;
+            LaunchTimer timer;
+            kv->timer = &timer;
+            kv->win = window_of(kv->len + 1, kv->cap);
+            set_launch_timer(&timer);
+            enqueue_decode(kv);
+            set_launch_timer(nullptr);
+            kv->timer = nullptr;
+            hipError_t e = hipStreamSynchronize(kv->st);
+            for (size_t i = 0; e == hipSuccess && i < timer.ev.size(); ++i) {
+                float ms = 0.0f;
+                e = hipEventElapsedTime(&ms, timer.ev[i].first, timer.ev[i].second);
+                us[timer.tags[i]] += ms * 1000.0f / reps;
+                if (r == 0) launches[timer.tags[i]] += 1;
+            }
+            for (auto &pr : timer.ev) {
+                (void)hipEventDestroy(pr.first);
+                (void)hipEventDestroy(pr.second);
+            }
+            if (e != hipSuccess) return fail(HG_ERR_DEVICE, std::string("profile: ") + hipGetErrorString(e));
         }
-        for (auto &pr : timer.ev) {
-            (void)hipEventDestroy(pr.first);
-            (void)hipEventDestroy(pr.second);
-        }
-        if (e != hipSuccess) return fail(HG_ERR_DEVICE, std::string("profile: ") + hipGetErrorString(e));
-    }
-    return HG_OK;
+        return HG_OK;
+    });
 }
 
 const char *hg_profile_class(uint32_t c) { return c < P_COUNT ? kProfNames[c] : ""; }
 
 int hg_last_routing(const hg_kv *kv, uint32_t *idx, float *w) {
-    if (!kv) return fail(HG_ERR_ARG, "NULL argument");
-    const size_t n = (size_t)kv->m->c.n_layers * kv->m->c.top_k;
-    HIP_TRY(hipStreamSynchronize(kv->st));
-    if (idx) HIP_TRY(hipMemcpy(idx, kv->rec_idx.p, n * 4, hipMemcpyDeviceToHost));
-    if (w) HIP_TRY(hipMemcpy(w, kv->rec_w.p, n * 4, hipMemcpyDeviceToHost));
-    return HG_OK;
+    return guard([&]() -> int {
+        if (!kv) return fail(HG_ERR_ARG, "NULL argument");
+        const size_t n = (size_t)kv->m->c.n_layers * kv->m->c.top_k;
+        HIP_TRY(hipStreamSynchronize(kv->st));
+        if (idx) HIP_TRY(hipMemcpy(idx, kv->rec_idx.p, n * 4, hipMemcpyDeviceToHost));
+        if (w) HIP_TRY(hipMemcpy(w, kv->rec_w.p, n * 4, hipMemcpyDeviceToHost));
+        return HG_OK;
+    });
 }
 
 }  // extern "C"
@@ -795,23 +958,27 @@ int with_act(const hg_q8_tensor *t, const float *x, uint32_t rows, F body) {
 extern "C" {
 
 int hg_q8_tensor_quantize(const float *w, uint32_t out, uint32_t in, hg_q8_tensor **t) {
-    if (!w || !t) return fail(HG_ERR_ARG, "NULL argument");
-    if (in % QK || !out || !in) return fail(HG_ERR_ARG, "Q8_0 needs in_ divisible by 32 (got " + std::to_string(in) + ")");
-    int rc = check_device();
-    if (rc) return rc;
-    PackedQ8 p;
-    pack_q8_from_f32(w, out, in, p);
-    return make_tensor(p, t);
+    return guard([&]() -> int {
+        if (!w || !t) return fail(HG_ERR_ARG, "NULL argument");
+        if (in % QK || !out || !in) return fail(HG_ERR_ARG, "Q8_0 needs in_ divisible by 32 (got " + std::to_string(in) + ")");
+        int rc = check_device();
+        if (rc) return rc;
+        PackedQ8 p;
+        pack_q8_from_f32(w, out, in, p);
+        return make_tensor(p, t);
+    });
 }
 
 int hg_q8_tensor_from_q8_0(const void *blocks, uint32_t out, uint32_t in, hg_q8_tensor **t) {
-    if (!blocks || !t) return fail(HG_ERR_ARG, "NULL argument");
-    if (in % QK || !out || !in) return fail(HG_ERR_ARG, "Q8_0 needs in_ divisible by 32 (got " + std::to_string(in) + ")");
-    int rc = check_device();
-    if (rc) return rc;
-    PackedQ8 p;
-    pack_q8_from_q8_0(static_cast<const uint8_t *>(blocks), out, in, p);
-    return make_tensor(p, t);
+    return guard([&]() -> int {
+        if (!blocks || !t) return fail(HG_ERR_ARG, "NULL argument");
+        if (in % QK || !out || !in) return fail(HG_ERR_ARG, "Q8_0 needs in_ divisible by 32 (got " + std::to_string(in) + ")");
+        int rc = check_device();
+        if (rc) return rc;
+        PackedQ8 p;
+        pack_q8_from_q8_0(static_cast<const uint8_t *>(blocks), out, in, p);
+        return make_tensor(p, t);
+    });
 }
 
 void hg_q8_tensor_free(hg_q8_tensor *t) { delete t; }
@@ -819,59 +986,65 @@ void hg_q8_tensor_free(hg_q8_tensor *t) { delete t; }
 uint64_t hg_q8_tensor_bytes(const hg_q8_tensor *t) { return t ? t->w.ref_bytes : 0; }
 
 int hg_q8_tensor_matvec(const hg_q8_tensor *t, const float *x, float *y) {
-    if (!t || !x || !y) return fail(HG_ERR_ARG, "NULL argument");
-    const Q8Mat &W = t->w.m;
-    return with_act(t, x, 1, [&](DevBuf &qa, DevBuf &da) -> int {
-        DevBuf dy;
-        int rc = dy.alloc((size_t)W.N * 4);
-        if (rc) return rc;
-        launch_matvec(t->st, ORDER_DECODE, EPI_STORE, W, qa.as<uint8_t>(), da.as<float>(), dy.as<float>(), 64, 0,
-                      nullptr, nullptr);
-        HIP_TRY(hipGetLastError());
-        HIP_TRY(hipMemcpyAsync(y, dy.p, (size_t)W.N * 4, hipMemcpyDeviceToHost, t->st));
-        HIP_TRY(hipStreamSynchronize(t->st));
-        return HG_OK;
+    return guard([&]() -> int {
+        if (!t || !x || !y) return fail(HG_ERR_ARG, "NULL argument");
+        const Q8Mat &W = t->w.m;
+        return with_act(t, x, 1, [&](DevBuf &qa, DevBuf &da) -> int {
+            DevBuf dy;
+            int rc = dy.alloc((size_t)W.N * 4);
+            if (rc) return rc;
+            launch_matvec(t->st, ORDER_DECODE, EPI_STORE, W, qa.as<uint8_t>(), da.as<float>(), dy.as<float>(), 64, 0,
+                          nullptr, nullptr);
+            HIP_TRY(hipGetLastError());
+            HIP_TRY(hipMemcpyAsync(y, dy.p, (size_t)W.N * 4, hipMemcpyDeviceToHost, t->st));
+            HIP_TRY(hipStreamSynchronize(t->st));
+            return HG_OK;
+        });
     });
 }
 
 int hg_q8_tensor_matmul(const hg_q8_tensor *t, const float *x, float *y, uint32_t tn) {
-    if (!t || !x || !y) return fail(HG_ERR_ARG, "NULL argument");
-    if (tn == 0) return HG_OK;
-    const Q8Mat &W = t->w.m;
-    return with_act(t, x, tn, [&](DevBuf &qa, DevBuf &da) -> int {
-        DevBuf dy;
-        int rc = dy.alloc((size_t)W.N * tn * 4);
-        if (rc) return rc;
-        for (uint32_t r = 0; r < tn; ++r)
-            launch_matvec(t->st, ORDER_PREFILL, EPI_STORE, W, qa.as<uint8_t>() + (size_t)r * W.nc * CHUNK_BYTES,
-                          da.as<float>() + (size_t)r * W.nc * 4, dy.as<float>() + (size_t)r * W.N, 64, 0, nullptr,
-                          nullptr);
-        HIP_TRY(hipGetLastError());
-        HIP_TRY(hipMemcpyAsync(y, dy.p, (size_t)W.N * tn * 4, hipMemcpyDeviceToHost, t->st));
-        HIP_TRY(hipStreamSynchronize(t->st));
-        return HG_OK;
+    return guard([&]() -> int {
+        if (!t || !x || !y) return fail(HG_ERR_ARG, "NULL argument");
+        if (tn == 0) return HG_OK;
+        const Q8Mat &W = t->w.m;
+        return with_act(t, x, tn, [&](DevBuf &qa, DevBuf &da) -> int {
+            DevBuf dy;
+            int rc = dy.alloc((size_t)W.N * tn * 4);
+            if (rc) return rc;
+            for (uint32_t r = 0; r < tn; ++r)
+                launch_matvec(t->st, ORDER_PREFILL, EPI_STORE, W, qa.as<uint8_t>() + (size_t)r * W.nc * CHUNK_BYTES,
+                              da.as<float>() + (size_t)r * W.nc * 4, dy.as<float>() + (size_t)r * W.N, 64, 0, nullptr,
+                              nullptr);
+            HIP_TRY(hipGetLastError());
+            HIP_TRY(hipMemcpyAsync(y, dy.p, (size_t)W.N * tn * 4, hipMemcpyDeviceToHost, t->st));
+            HIP_TRY(hipStreamSynchronize(t->st));
+            return HG_OK;
+        });
     });
 }
 
 int hg_q8_tensor_matvec_gather(const hg_q8_tensor *t, uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids,
                                const float *x, float *y) {
-    if (!t || !ids || !x || !y) return fail(HG_ERR_ARG, "NULL argument");
-    const Q8Mat &W = t->w.m;
-    if (rows_per_mat == 0 || W.N % rows_per_mat) return fail(HG_ERR_ARG, "rows_per_mat does not divide the rows");
-    const uint32_t n_mat = W.N / rows_per_mat;
-    for (uint32_t i = 0; i < n_ids; ++i)
-        if (ids[i] >= n_mat) return fail(HG_ERR_ARG, "expert id " + std::to_string(ids[i]) + " out of range");
-    if (n_ids == 0) return HG_OK;
-    return with_act(t, x, 1, [&](DevBuf &qa, DevBuf &da) -> int {
-        DevBuf dy, did;
-        int rc;
-        if ((rc = dy.alloc((size_t)rows_per_mat * n_ids * 4)) || (rc = did.upload(ids, (size_t)n_ids * 4))) return rc;
-        launch_matvec_gather(t->st, W, rows_per_mat, did.as<uint32_t>(), n_ids, qa.as<uint8_t>(), da.as<float>(),
-                             dy.as<float>());
-        HIP_TRY(hipGetLastError());
-        HIP_TRY(hipMemcpyAsync(y, dy.p, (size_t)rows_per_mat * n_ids * 4, hipMemcpyDeviceToHost, t->st));
-        HIP_TRY(hipStreamSynchronize(t->st));
-        return HG_OK;
+    return guard([&]() -> int {
+        if (!t || !ids || !x || !y) return fail(HG_ERR_ARG, "NULL argument");
+        const Q8Mat &W = t->w.m;
+        if (rows_per_mat == 0 || W.N % rows_per_mat) return fail(HG_ERR_ARG, "rows_per_mat does not divide the rows");
+        const uint32_t n_mat = W.N / rows_per_mat;
+        for (uint32_t i = 0; i < n_ids; ++i)
+            if (ids[i] >= n_mat) return fail(HG_ERR_ARG, "expert id " + std::to_string(ids[i]) + " out of range");
+        if (n_ids == 0) return HG_OK;
+        return with_act(t, x, 1, [&](DevBuf &qa, DevBuf &da) -> int {
+            DevBuf dy, did;
+            int rc;
+            if ((rc = dy.alloc((size_t)rows_per_mat * n_ids * 4)) || (rc = did.upload(ids, (size_t)n_ids * 4))) return rc;
+            launch_matvec_gather(t->st, W, rows_per_mat, did.as<uint32_t>(), n_ids, qa.as<uint8_t>(), da.as<float>(),
+                                 dy.as<float>());
+            HIP_TRY(hipGetLastError());
+            HIP_TRY(hipMemcpyAsync(y, dy.p, (size_t)rows_per_mat * n_ids * 4, hipMemcpyDeviceToHost, t->st));
+            HIP_TRY(hipStreamSynchronize(t->st));
+            return HG_OK;
+        });
     });
 }
 
@@ -897,224 +1070,234 @@ int timer_mean_us(LaunchTimer &timer, float *us) {
 
 int hg_q8_tensor_time_matvec(const hg_q8_tensor *t, const float *x, uint32_t reps, uint32_t copies,
                              uint32_t rows_per_mat, const uint32_t *ids, uint32_t n_ids, float *us) {
-    if (!t || !x || !us || !reps || !copies) return fail(HG_ERR_ARG, "NULL argument or zero count");
-    const Q8Mat &W = t->w.m;
-    const bool gather = ids != nullptr;
-    if (gather) {
-        if (rows_per_mat == 0 || W.N % rows_per_mat || n_ids == 0) return fail(HG_ERR_ARG, "bad gather shape");
-        for (uint32_t i = 0; i < n_ids; ++i)
-            if (ids[i] >= W.N / rows_per_mat) return fail(HG_ERR_ARG, "expert id out of range");
-    }
-    const size_t qs_bytes = (size_t)W.N * W.nc * CHUNK_BYTES, sc_bytes = (size_t)W.N * W.nc * 4 * (W.sc_f32 ? 4 : 2);
-    return with_act(t, x, 1, [&](DevBuf &qa, DevBuf &da) -> int {
-        DevBuf dy, did, rep;
-        int rc;
-        const uint32_t rows = gather ? rows_per_mat * n_ids : W.N;
-        if ((rc = dy.alloc((size_t)rows * 4))) return rc;
-        if (gather && (rc = did.upload(ids, (size_t)n_ids * 4))) return rc;
-        if (copies > 1) {   // replicas of the weights, each (qs, scales) 256-byte aligned
-            const size_t one = (qs_bytes + 255) / 256 * 256 + (sc_bytes + 255) / 256 * 256;
-            if ((rc = rep.alloc(one * copies))) return rc;
-            for (uint32_t c = 0; c < copies; ++c) {
-                uint8_t *b = rep.as<uint8_t>() + one * c;
-                HIP_TRY(hipMemcpyAsync(b, W.qs, qs_bytes, hipMemcpyDeviceToDevice, t->st));
-                HIP_TRY(hipMemcpyAsync(b + (qs_bytes + 255) / 256 * 256, W.sc, sc_bytes, hipMemcpyDeviceToDevice, t->st));
-            }
+    return guard([&]() -> int {
+        if (!t || !x || !us || !reps || !copies) return fail(HG_ERR_ARG, "NULL argument or zero count");
+        const Q8Mat &W = t->w.m;
+        const bool gather = ids != nullptr;
+        if (gather) {
+            if (rows_per_mat == 0 || W.N % rows_per_mat || n_ids == 0) return fail(HG_ERR_ARG, "bad gather shape");
+            for (uint32_t i = 0; i < n_ids; ++i)
+                if (ids[i] >= W.N / rows_per_mat) return fail(HG_ERR_ARG, "expert id out of range");
         }
-        const size_t one = (qs_bytes + 255) / 256 * 256 + (sc_bytes + 255) / 256 * 256;
-        auto view = [&](uint32_t c) {
-            Q8Mat v = W;
-            if (copies > 1) {
-                uint8_t *b = rep.as<uint8_t>() + one * c;
-                v.qs = b;
-                v.sc = b + (qs_bytes + 255) / 256 * 256;
+        const size_t qs_bytes = (size_t)W.N * W.nc * CHUNK_BYTES, sc_bytes = (size_t)W.N * W.nc * 4 * (W.sc_f32 ? 4 : 2);
+        return with_act(t, x, 1, [&](DevBuf &qa, DevBuf &da) -> int {
+            DevBuf dy, did, rep;
+            int rc;
+            const uint32_t rows = gather ? rows_per_mat * n_ids : W.N;
+            if ((rc = dy.alloc((size_t)rows * 4))) return rc;
+            if (gather && (rc = did.upload(ids, (size_t)n_ids * 4))) return rc;
+            if (copies > 1) {   // replicas of the weights, each (qs, scales) 256-byte aligned
+                const size_t one = (qs_bytes + 255) / 256 * 256 + (sc_bytes + 255) / 256 * 256;
+                if ((rc = rep.alloc(one * copies))) return rc;
+                for (uint32_t c = 0; c < copies; ++c) {
+                    uint8_t *b = rep.as<uint8_t>() + one * c;
+                    HIP_TRY(hipMemcpyAsync(b, W.qs, qs_bytes, hipMemcpyDeviceToDevice, t->st));
+                    HIP_TRY(hipMemcpyAsync(b + (qs_bytes + 255) / 256 * 256, W.sc, sc_bytes, hipMemcpyDeviceToDevice, t->st));
+                }
             }
-            return v;
-        };
-        auto call = [&](uint32_t r) {
-            const Q8Mat v = view(r % copies);
-            if (gather)
-                launch_matvec_gather(t->st, v, rows_per_mat, did.as<uint32_t>(), n_ids, qa.as<uint8_t>(), da.as<float>(),
-                                     dy.as<float>());
-            else
-                launch_matvec(t->st, ORDER_DECODE, EPI_STORE, v, qa.as<uint8_t>(), da.as<float>(), dy.as<float>(), 64, 0,
-                              nullptr, nullptr);
-        };
-        for (uint32_t r = 0; r < 3; ++r) call(r);   // warm-up
-        HIP_TRY(hipStreamSynchronize(t->st));
-        LaunchTimer timer;
-        set_launch_timer(&timer);
-        for (uint32_t r = 0; r < reps; ++r) call(r);
-        set_launch_timer(nullptr);
-        HIP_TRY(hipGetLastError());
-        HIP_TRY(hipStreamSynchronize(t->st));
-        return timer_mean_us(timer, us);
+            const size_t one = (qs_bytes + 255) / 256 * 256 + (sc_bytes + 255) / 256 * 256;
+            auto view = [&](uint32_t c) {
+                Q8Mat v = W;
+                if (copies > 1) {
+                    uint8_t *b = rep.as<uint8_t>() + one * c;
+                    v.qs = b;
+                    v.sc = b + (qs_bytes + 255) / 256 * 256;
+                }
+                return v;
+            };
+            auto call = [&](uint32_t r) {
+                const Q8Mat v = view(r % copies);
+                if (gather)
+                    launch_matvec_gather(t->st, v, rows_per_mat, did.as<uint32_t>(), n_ids, qa.as<uint8_t>(), da.as<float>(),
+                                         dy.as<float>());
+                else
+                    launch_matvec(t->st, ORDER_DECODE, EPI_STORE, v, qa.as<uint8_t>(), da.as<float>(), dy.as<float>(), 64, 0,
+                                  nullptr, nullptr);
+            };
+            for (uint32_t r = 0; r < 3; ++r) call(r);   // warm-up
+            HIP_TRY(hipStreamSynchronize(t->st));
+            LaunchTimer timer;
+            set_launch_timer(&timer);
+            for (uint32_t r = 0; r < reps; ++r) call(r);
+            set_launch_timer(nullptr);
+            HIP_TRY(hipGetLastError());
+            HIP_TRY(hipStreamSynchronize(t->st));
+            return timer_mean_us(timer, us);
+        });
     });
 }
 
 int hg_attention_decode(const float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
                         float eps, float theta, uint32_t rope_len, uint32_t n_heads, uint32_t n_kv, uint32_t hd,
                         uint32_t pos, float *kc, float *vc, float *out, uint32_t flags) {
-    if (!q || !k || !v || !q_norm || !k_norm || !kc || !vc || !out) return fail(HG_ERR_ARG, "NULL argument");
-    if (hd != 32 && hd != 64 && hd != 128) return fail(HG_ERR_UNSUPPORTED, "head_dim not in {32, 64, 128}");
-    if (!n_kv || n_heads % n_kv || n_heads / n_kv > 8) return fail(HG_ERR_UNSUPPORTED, "unsupported head grouping");
-    if (pos >= rope_len) return fail(HG_ERR_ARG, "pos beyond the RoPE table");
-    if (!(flags & HG_KV_FAST) && pv_ring_slots(pos + 1) < 2)
-        return fail(HG_ERR_UNSUPPORTED, "reference-order attention supports at most 32768 positions");
-    int rc = check_device();
-    if (rc) return rc;
-    const bool exact = (flags & HG_KV_FAST) == 0;
-    const uint32_t qd = n_heads * hd, kvd = n_kv * hd, n = pos + 1, cap = n, S = std::max(64u, div_up(n, 256));
-    std::vector<float> qkv(qd + 2 * kvd);
-    memcpy(qkv.data(), q, qd * 4);
-    memcpy(qkv.data() + qd, k, kvd * 4);
-    memcpy(qkv.data() + qd + kvd, v, kvd * 4);
-    std::vector<float> kh((size_t)n_kv * cap * hd, 0.0f), vh(v_layer_floats(cap, n_kv, hd), 0.0f);
-    float *vth = vh.data() + (size_t)n_kv * cap * hd;   // the transposed copy
-    for (uint32_t t = 0; t < pos; ++t)
-        for (uint32_t g = 0; g < n_kv; ++g) {
-            memcpy(&kh[((size_t)g * cap + t) * hd], kc + ((size_t)t * n_kv + g) * hd, hd * 4);
-            memcpy(&vh[((size_t)g * cap + t) * hd], vc + ((size_t)t * n_kv + g) * hd, hd * 4);
-            for (uint32_t i = 0; i < hd; ++i)
-                vth[((size_t)g * hd + i) * vt_stride(cap) + t] = vc[((size_t)t * n_kv + g) * hd + i];
-        }
-    std::vector<float> cs, sn;
-    rope_table(hd, rope_len, theta, cs, sn);
-    StepParams hp{};
-    hp.pos = pos;
-    DevBuf dqkv, dqn, dkn, dcs, dsn, dk, dv, dp, dpart, dscr, dout, dq, dd;
-    if ((rc = dqkv.upload(qkv.data(), qkv.size() * 4)) || (rc = dqn.upload(q_norm, hd * 4)) ||
-        (rc = dkn.upload(k_norm, hd * 4)) || (rc = dcs.upload(cs.data(), cs.size() * 4)) ||
-        (rc = dsn.upload(sn.data(), sn.size() * 4)) || (rc = dk.upload(kh.data(), kh.size() * 4)) ||
-        (rc = dv.upload(vh.data(), vh.size() * 4)) || (rc = dp.upload(&hp, sizeof hp)) ||
-        (rc = dpart.alloc((size_t)n_heads * S * (hd + 2) * 4)) || (rc = dscr.alloc((size_t)n_heads * cap * 4)) ||
-        (rc = dout.alloc((size_t)qd * 4)) || (rc = dq.alloc((size_t)div_up(qd / QK, 4) * CHUNK_BYTES)) ||
-        (rc = dd.alloc((size_t)div_up(qd / QK, 4) * 16)))
-        return rc;
-    if (!launch_qk_rope_append(nullptr, hd, dqkv.as<float>(), dqn.as<float>(), dkn.as<float>(), eps, dcs.as<float>(),
-                               dsn.as<float>(), dp.as<StepParams>(), n_heads, n_kv, dk.as<float>(), dv.as<float>(), cap))
-        return fail(HG_ERR_UNSUPPORTED, "head_dim not supported");
-    for (int which = 0; which < 2; ++which)
-        if (!launch_attn(nullptr, exact, which, hd, dqkv.as<float>(), dqn.as<float>(), dkn.as<float>(), eps,
-                         dcs.as<float>(), dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap,
-                         n_heads, n_kv, S, dpart.as<float>(), dscr.as<float>(), dout.as<float>(), dq.as<uint8_t>(),
-                         dd.as<float>()))
+    return guard([&]() -> int {
+        if (!q || !k || !v || !q_norm || !k_norm || !kc || !vc || !out) return fail(HG_ERR_ARG, "NULL argument");
+        if (hd != 32 && hd != 64 && hd != 128) return fail(HG_ERR_UNSUPPORTED, "head_dim not in {32, 64, 128}");
+        if (!n_kv || n_heads % n_kv || n_heads / n_kv > 8) return fail(HG_ERR_UNSUPPORTED, "unsupported head grouping");
+        if (pos >= rope_len) return fail(HG_ERR_ARG, "pos beyond the RoPE table");
+        if (!(flags & HG_KV_FAST) && pv_ring_slots(pos + 1) < 2)
+            return fail(HG_ERR_UNSUPPORTED, "reference-order attention supports at most 32768 positions");
+        int rc = check_device();
+        if (rc) return rc;
+        const bool exact = (flags & HG_KV_FAST) == 0;
+        const uint32_t qd = n_heads * hd, kvd = n_kv * hd, n = pos + 1, cap = n, S = attn_splits(cap);
+        std::vector<float> qkv(qd + 2 * kvd);
+        memcpy(qkv.data(), q, qd * 4);
+        memcpy(qkv.data() + qd, k, kvd * 4);
+        memcpy(qkv.data() + qd + kvd, v, kvd * 4);
+        std::vector<float> kh((size_t)n_kv * cap * hd, 0.0f), vh(v_layer_floats(cap, n_kv, hd), 0.0f);
+        float *vth = vh.data() + (size_t)n_kv * cap * hd;   // the transposed copy
+        for (uint32_t t = 0; t < pos; ++t)
+            for (uint32_t g = 0; g < n_kv; ++g) {
+                memcpy(&kh[((size_t)g * cap + t) * hd], kc + ((size_t)t * n_kv + g) * hd, hd * 4);
+                memcpy(&vh[((size_t)g * cap + t) * hd], vc + ((size_t)t * n_kv + g) * hd, hd * 4);
+                for (uint32_t i = 0; i < hd; ++i)
+                    vth[((size_t)g * hd + i) * vt_stride(cap) + t] = vc[((size_t)t * n_kv + g) * hd + i];
+            }
+        std::vector<float> cs, sn;
+        rope_table(hd, rope_len, theta, cs, sn);
+        StepParams hp{};
+        hp.pos = pos;
+        DevBuf dqkv, dqn, dkn, dcs, dsn, dk, dv, dp, dpart, dscr, dout, dq, dd;
+        if ((rc = dqkv.upload(qkv.data(), qkv.size() * 4)) || (rc = dqn.upload(q_norm, hd * 4)) ||
+            (rc = dkn.upload(k_norm, hd * 4)) || (rc = dcs.upload(cs.data(), cs.size() * 4)) ||
+            (rc = dsn.upload(sn.data(), sn.size() * 4)) || (rc = dk.upload(kh.data(), kh.size() * 4)) ||
+            (rc = dv.upload(vh.data(), vh.size() * 4)) || (rc = dp.upload(&hp, sizeof hp)) ||
+            (rc = dpart.alloc((size_t)n_heads * S * (hd + 2) * 4)) || (rc = dscr.alloc((size_t)n_heads * cap * 4)) ||
+            (rc = dout.alloc((size_t)qd * 4)) || (rc = dq.alloc((size_t)div_up(qd / QK, 4) * CHUNK_BYTES)) ||
+            (rc = dd.alloc((size_t)div_up(qd / QK, 4) * 16)))
+            return rc;
+        if (!launch_qk_rope_append(nullptr, hd, dqkv.as<float>(), dqn.as<float>(), dkn.as<float>(), eps, dcs.as<float>(),
+                                   dsn.as<float>(), dp.as<StepParams>(), n_heads, n_kv, dk.as<float>(), dv.as<float>(), cap))
             return fail(HG_ERR_UNSUPPORTED, "head_dim not supported");
-    HIP_TRY(hipGetLastError());
-    HIP_TRY(hipDeviceSynchronize());
-    HIP_TRY(hipMemcpy(out, dout.p, (size_t)qd * 4, hipMemcpyDeviceToHost));
-    HIP_TRY(hipMemcpy(kh.data(), dk.p, kh.size() * 4, hipMemcpyDeviceToHost));
-    HIP_TRY(hipMemcpy(vh.data(), dv.p, vh.size() * 4, hipMemcpyDeviceToHost));
-    for (uint32_t g = 0; g < n_kv; ++g) {
-        memcpy(kc + ((size_t)pos * n_kv + g) * hd, &kh[((size_t)g * cap + pos) * hd], hd * 4);
-        memcpy(vc + ((size_t)pos * n_kv + g) * hd, &vh[((size_t)g * cap + pos) * hd], hd * 4);
-    }
-    return HG_OK;
+        for (int which = 0; which < 2; ++which)
+            if (!launch_attn(nullptr, exact, which, hd, dqkv.as<float>(), dqn.as<float>(), dkn.as<float>(), eps,
+                             dcs.as<float>(), dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap,
+                             cap, n_heads, n_kv, S, dpart.as<float>(), dscr.as<float>(), dout.as<float>(),
+                             dq.as<uint8_t>(), dd.as<float>()))
+                return fail(HG_ERR_UNSUPPORTED, "head_dim not supported");
+        HIP_TRY(hipGetLastError());
+        HIP_TRY(hipDeviceSynchronize());
+        HIP_TRY(hipMemcpy(out, dout.p, (size_t)qd * 4, hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(kh.data(), dk.p, kh.size() * 4, hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(vh.data(), dv.p, vh.size() * 4, hipMemcpyDeviceToHost));
+        for (uint32_t g = 0; g < n_kv; ++g) {
+            memcpy(kc + ((size_t)pos * n_kv + g) * hd, &kh[((size_t)g * cap + pos) * hd], hd * 4);
+            memcpy(vc + ((size_t)pos * n_kv + g) * hd, &vh[((size_t)g * cap + pos) * hd], hd * 4);
+        }
+        return HG_OK;
+    });
 }
 
 int hg_seq_sum(const float *x, uint32_t n, uint32_t method, float *out) {
-    if ((!x && n) || !out || method > 6) return fail(HG_ERR_ARG, "NULL argument or unknown method");
-    int rc = check_device();
-    if (rc) return rc;
-    DevBuf dx, dout;
-    if ((rc = dx.upload(x, (size_t)n * 4)) || (rc = dout.alloc(4))) return rc;
-    launch_seq_sum(nullptr, dx.as<float>(), n, (int)method, dout.as<float>());
-    HIP_TRY(hipGetLastError());
-    HIP_TRY(hipDeviceSynchronize());
-    HIP_TRY(hipMemcpy(out, dout.p, 4, hipMemcpyDeviceToHost));
-    return HG_OK;
+    return guard([&]() -> int {
+        if ((!x && n) || !out || method > 6) return fail(HG_ERR_ARG, "NULL argument or unknown method");
+        int rc = check_device();
+        if (rc) return rc;
+        DevBuf dx, dout;
+        if ((rc = dx.upload(x, (size_t)n * 4)) || (rc = dout.alloc(4))) return rc;
+        launch_seq_sum(nullptr, dx.as<float>(), n, (int)method, dout.as<float>());
+        HIP_TRY(hipGetLastError());
+        HIP_TRY(hipDeviceSynchronize());
+        HIP_TRY(hipMemcpy(out, dout.p, 4, hipMemcpyDeviceToHost));
+        return HG_OK;
+    });
 }
 
 int hg_attention_time(uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t ctx, uint32_t reps, uint32_t flags,
                       float *us) {
-    if (!us || !reps || !ctx) return fail(HG_ERR_ARG, "NULL argument or zero count");
-    if (hd != 32 && hd != 64 && hd != 128) return fail(HG_ERR_UNSUPPORTED, "head_dim not in {32, 64, 128}");
-    if (!n_kv || n_heads % n_kv || n_heads / n_kv > 8) return fail(HG_ERR_UNSUPPORTED, "unsupported head grouping");
-    const bool exact = (flags & HG_KV_FAST) == 0;
-    if (exact && !pv_res_fits(ctx) && pv_ring_slots(ctx) < 2)
-        return fail(HG_ERR_UNSUPPORTED, "reference-order attention supports at most 32768 positions");
-    int rc = check_device();
-    if (rc) return rc;
-    const uint32_t qd = n_heads * hd, kvd = n_kv * hd, cap = ctx, S = std::max(64u, div_up(ctx, 256)), pos = ctx - 1;
-    // seeded N(0,1)-like data: q, k, v and the cache rows 0 .. pos-1; unit QK-norm gains
-    uint64_t st = 0x9e3779b97f4a7c15ull;
-    auto rnd = [&]() {
-        st ^= st << 13; st ^= st >> 7; st ^= st << 17;
-        return (float)((double)(st >> 11) * 0x1p-53 * 2.0 - 1.0) * 1.7320508f;
-    };
-    std::vector<float> qkv(qd + 2 * kvd), kh((size_t)n_kv * cap * hd), vh(v_layer_floats(cap, n_kv, hd)),
-        ones(hd, 1.0f), cs, sn;   // (vh: the rows and their transposed copy, random alike: timing only)
-    for (float &v : qkv) v = rnd();
-    for (float &v : kh) v = rnd();
-    for (float &v : vh) v = rnd();
-    rope_table(hd, ctx, 10000.0f, cs, sn);
-    StepParams hp{};
-    hp.pos = pos;
-    DevBuf dqkv, dqn, dcs, dsn, dk, dv, dp, dpart, dscr, dout, dq, dd;
-    const size_t part_floats = exact ? (size_t)n_heads * S : (size_t)n_heads * S * (hd + 2);
-    // the fast path's merge also writes the quantized o (the exact path leaves it to attn_output)
-    if ((rc = dq.alloc((size_t)div_up(qd / QK, 4) * CHUNK_BYTES)) || (rc = dd.alloc((size_t)div_up(qd / QK, 4) * 16)))
-        return rc;
-    uint8_t *q_out = exact ? nullptr : dq.as<uint8_t>();
-    float *d_out = exact ? nullptr : dd.as<float>();
-    if ((rc = dqkv.upload(qkv.data(), qkv.size() * 4)) || (rc = dqn.upload(ones.data(), hd * 4)) ||
-        (rc = dcs.upload(cs.data(), cs.size() * 4)) || (rc = dsn.upload(sn.data(), sn.size() * 4)) ||
-        (rc = dk.upload(kh.data(), kh.size() * 4)) || (rc = dv.upload(vh.data(), vh.size() * 4)) ||
-        (rc = dp.upload(&hp, sizeof hp)) || (rc = dpart.alloc(std::max(part_floats, (size_t)n_heads * S * (hd + 2)) * 4)) ||
-        (rc = dscr.alloc((size_t)n_heads * cap * 4)) || (rc = dout.alloc((size_t)qd * 4)))
-        return rc;
-    HIP_TRY(hipDeviceSynchronize());
-    hipStream_t s0 = nullptr;
-    HIP_TRY(hipStreamCreateWithFlags(&s0, hipStreamNonBlocking));
-    auto layer = [&]() {
-        for (int which = 0; which < 2; ++which)
-            launch_attn(s0, exact, which, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f,
-                        dcs.as<float>(), dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap,
-                        n_heads, n_kv, S, dpart.as<float>(), dscr.as<float>(), dout.as<float>(), q_out, d_out);
-    };
-    // q, k normed and rotated and the row pos appended once (the QKV step's work, not timed)
-    launch_qk_rope_append(s0, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f, dcs.as<float>(),
-                          dsn.as<float>(), dp.as<StepParams>(), n_heads, n_kv, dk.as<float>(), dv.as<float>(), cap);
-    for (int r = 0; r < 3; ++r) layer();
-    hipError_t e = hipStreamSynchronize(s0);
-    LaunchTimer timer;
-    if (e == hipSuccess) {
-        set_launch_timer(&timer);
-        for (uint32_t r = 0; r < reps; ++r) {
-            timer.cls = 0;
-            launch_attn(s0, exact, 0, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f, dcs.as<float>(),
-                        dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap, n_heads, n_kv, S,
-                        dpart.as<float>(), dscr.as<float>(), dout.as<float>(), q_out, d_out);
-            timer.cls = 1;
-            launch_attn(s0, exact, 1, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f, dcs.as<float>(),
-                        dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap, n_heads, n_kv, S,
-                        dpart.as<float>(), dscr.as<float>(), dout.as<float>(), q_out, d_out);
+    return guard([&]() -> int {
+        if (!us || !reps || !ctx) return fail(HG_ERR_ARG, "NULL argument or zero count");
+        if (hd != 32 && hd != 64 && hd != 128) return fail(HG_ERR_UNSUPPORTED, "head_dim not in {32, 64, 128}");
+        if (!n_kv || n_heads % n_kv || n_heads / n_kv > 8) return fail(HG_ERR_UNSUPPORTED, "unsupported head grouping");
+        const bool exact = (flags & HG_KV_FAST) == 0;
+        if (exact && !pv_res_fits(ctx) && pv_ring_slots(ctx) < 2)
+            return fail(HG_ERR_UNSUPPORTED, "reference-order attention supports at most 32768 positions");
+        int rc = check_device();
+        if (rc) return rc;
+        const uint32_t qd = n_heads * hd, kvd = n_kv * hd, cap = ctx, S = attn_splits(ctx), pos = ctx - 1;
+        // seeded N(0,1)-like data: q, k, v and the cache rows 0 .. pos-1; unit QK-norm gains
+        uint64_t st = 0x9e3779b97f4a7c15ull;
+        auto rnd = [&]() {
+            st ^= st << 13; st ^= st >> 7; st ^= st << 17;
+            return (float)((double)(st >> 11) * 0x1p-53 * 2.0 - 1.0) * 1.7320508f;
+        };
+        std::vector<float> qkv(qd + 2 * kvd), kh((size_t)n_kv * cap * hd), vh(v_layer_floats(cap, n_kv, hd)),
+            ones(hd, 1.0f), cs, sn;   // (vh: the rows and their transposed copy, random alike: timing only)
+        for (float &v : qkv) v = rnd();
+        for (float &v : kh) v = rnd();
+        for (float &v : vh) v = rnd();
+        rope_table(hd, ctx, 10000.0f, cs, sn);
+        StepParams hp{};
+        hp.pos = pos;
+        DevBuf dqkv, dqn, dcs, dsn, dk, dv, dp, dpart, dscr, dout, dq, dd;
+        const size_t part_floats = exact ? (size_t)n_heads * S : (size_t)n_heads * S * (hd + 2);
+        // the fast path's merge also writes the quantized o (the exact path leaves it to attn_output)
+        if ((rc = dq.alloc((size_t)div_up(qd / QK, 4) * CHUNK_BYTES)) || (rc = dd.alloc((size_t)div_up(qd / QK, 4) * 16)))
+            return rc;
+        uint8_t *q_out = exact ? nullptr : dq.as<uint8_t>();
+        float *d_out = exact ? nullptr : dd.as<float>();
+        if ((rc = dqkv.upload(qkv.data(), qkv.size() * 4)) || (rc = dqn.upload(ones.data(), hd * 4)) ||
+            (rc = dcs.upload(cs.data(), cs.size() * 4)) || (rc = dsn.upload(sn.data(), sn.size() * 4)) ||
+            (rc = dk.upload(kh.data(), kh.size() * 4)) || (rc = dv.upload(vh.data(), vh.size() * 4)) ||
+            (rc = dp.upload(&hp, sizeof hp)) || (rc = dpart.alloc(std::max(part_floats, (size_t)n_heads * S * (hd + 2)) * 4)) ||
+            (rc = dscr.alloc((size_t)n_heads * cap * 4)) || (rc = dout.alloc((size_t)qd * 4)))
+            return rc;
+        HIP_TRY(hipDeviceSynchronize());
+        hipStream_t s0 = nullptr;
+        HIP_TRY(hipStreamCreateWithFlags(&s0, hipStreamNonBlocking));
+        auto layer = [&]() {
+            for (int which = 0; which < 2; ++which)
+                launch_attn(s0, exact, which, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f,
+                            dcs.as<float>(), dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap,
+                            cap, n_heads, n_kv, S, dpart.as<float>(), dscr.as<float>(), dout.as<float>(), q_out, d_out);
+        };
+        // q, k normed and rotated and the row pos appended once (the QKV step's work, not timed)
+        launch_qk_rope_append(s0, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f, dcs.as<float>(),
+                              dsn.as<float>(), dp.as<StepParams>(), n_heads, n_kv, dk.as<float>(), dv.as<float>(), cap);
+        for (int r = 0; r < 3; ++r) layer();
+        hipError_t e = hipStreamSynchronize(s0);
+        LaunchTimer timer;
+        if (e == hipSuccess) {
+            set_launch_timer(&timer);
+            for (uint32_t r = 0; r < reps; ++r) {
+                timer.cls = 0;
+                launch_attn(s0, exact, 0, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f, dcs.as<float>(),
+                            dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap, cap, n_heads, n_kv,
+                            S, dpart.as<float>(), dscr.as<float>(), dout.as<float>(), q_out, d_out);
+                timer.cls = 1;
+                launch_attn(s0, exact, 1, hd, dqkv.as<float>(), dqn.as<float>(), dqn.as<float>(), 1e-5f, dcs.as<float>(),
+                            dsn.as<float>(), dp.as<StepParams>(), dk.as<float>(), dv.as<float>(), cap, cap, n_heads, n_kv,
+                            S, dpart.as<float>(), dscr.as<float>(), dout.as<float>(), q_out, d_out);
+            }
+            set_launch_timer(nullptr);
+            e = hipStreamSynchronize(s0);
         }
-        set_launch_timer(nullptr);
-        e = hipStreamSynchronize(s0);
-    }
-    double t[2] = {0.0, 0.0};
-    for (size_t i = 0; e == hipSuccess && i < timer.ev.size(); ++i) {
-        float ms = 0.0f;
-        e = hipEventElapsedTime(&ms, timer.ev[i].first, timer.ev[i].second);
-        t[timer.tags[i] ? 1 : 0] += ms;
-    }
-    for (auto &pr : timer.ev) {
-        (void)hipEventDestroy(pr.first);
-        (void)hipEventDestroy(pr.second);
-    }
-    (void)hipStreamDestroy(s0);
-    if (e != hipSuccess) return fail(HG_ERR_DEVICE, std::string("attention timing: ") + hipGetErrorString(e));
-    us[0] = (float)(t[0] * 1000.0 / reps);
-    us[1] = (float)(t[1] * 1000.0 / reps);
-    return HG_OK;
+        double t[2] = {0.0, 0.0};
+        for (size_t i = 0; e == hipSuccess && i < timer.ev.size(); ++i) {
+            float ms = 0.0f;
+            e = hipEventElapsedTime(&ms, timer.ev[i].first, timer.ev[i].second);
+            t[timer.tags[i] ? 1 : 0] += ms;
+        }
+        for (auto &pr : timer.ev) {
+            (void)hipEventDestroy(pr.first);
+            (void)hipEventDestroy(pr.second);
+        }
+        (void)hipStreamDestroy(s0);
+        if (e != hipSuccess) return fail(HG_ERR_DEVICE, std::string("attention timing: ") + hipGetErrorString(e));
+        us[0] = (float)(t[0] * 1000.0 / reps);
+        us[1] = (float)(t[1] * 1000.0 / reps);
+        return HG_OK;
+    });
 }
 
 int hg_kv_truncate(hg_kv *kv, uint32_t len) {
-    if (!kv) return fail(HG_ERR_ARG, "NULL argument");
-    if (len > kv->len) return fail(HG_ERR_ARG, "truncate can only shorten the cache");
-    kv->len = len;
-    return HG_OK;
+    return guard([&]() -> int {
+        if (!kv) return fail(HG_ERR_ARG, "NULL argument");
+        if (len > kv->len) return fail(HG_ERR_ARG, "truncate can only shorten the cache");
+        kv->len = len;
+        return HG_OK;
+    });
 }
 
 }  // extern "C"

@@ -21,6 +21,13 @@ uint64_t TensorInfo::n_elems() const {
     return n;
 }
 
+bool TensorInfo::n_elems_checked(uint64_t &n) const {
+    n = 1;
+    for (uint64_t v : ne)
+        if (__builtin_mul_overflow(n, v, &n)) return false;
+    return true;
+}
+
 namespace {
 
 struct Cursor {
@@ -96,17 +103,110 @@ bool read_value(Cursor &c, uint32_t ty, Meta &m, std::string &err) {
     return true;
 }
 
+// type_nbytes (gguf.rs:349-359): bytes of n elements of ggml type ty (whole blocks; a partial
+// block is not stored).  ok = false for another type; an unrepresentable size is reported as
+// SIZE_MAX, which no file holds.
 size_t type_nbytes(uint32_t ty, uint64_t n, bool &ok) {
     ok = true;
+    uint64_t unit, per;   // bytes per `per` elements
     switch (ty) {
-    case 0: return (size_t)n * 4;
-    case 1: return (size_t)n * 2;
-    case 8: return (size_t)(n / 32) * 34;
+    case GGML_F32: unit = 4; per = 1; break;
+    case GGML_F16: unit = 2; per = 1; break;
+    case GGML_Q5_0: unit = 22; per = 32; break;    // d(2) qh(4) qs(16)
+    case GGML_Q8_0: unit = 34; per = 32; break;    // d(2) qs(32)
+    case GGML_Q4_K: unit = 144; per = 256; break;  // d(2) dmin(2) scales(12) qs(128)
+    case GGML_Q6_K: unit = 210; per = 256; break;  // ql(128) qh(64) scales(16) d(2)
     default: ok = false; return 0;
+    }
+    uint64_t b;
+    if (__builtin_mul_overflow(n / per, unit, &b) || b > (uint64_t)SIZE_MAX) return SIZE_MAX;
+    return (size_t)b;
+}
+
+inline float rd_half(const uint8_t *b) { return half_to_f32((uint16_t)(b[0] | (b[1] << 8))); }
+
+// scale_min_k4 (gguf.rs:399-408): the 6-bit scale and min of sub-block j of a K-quant super
+// block, packed in 12 bytes (j < 4 in the low 6 bits of bytes j and j + 4; j >= 4 split over
+// a nibble of byte j + 4 and the top 2 bits of bytes j - 4 and j).
+inline void scale_min_k4(uint32_t j, const uint8_t *sc, uint32_t &d, uint32_t &m) {
+    if (j < 4) {
+        d = sc[j] & 63u;
+        m = sc[j + 4] & 63u;
+    } else {
+        d = (sc[j + 4] & 0x0fu) | ((uint32_t)(sc[j - 4] >> 6) << 4);
+        m = (uint32_t)(sc[j + 4] >> 4) | ((uint32_t)(sc[j] >> 6) << 4);
     }
 }
 
 }  // namespace
+
+// dequant_q5_0 (gguf.rs:377-397): block {f16 d; u32 qh; u8 qs[16]}; element j < 16 is the low
+// nibble of qs[j] with bit j of qh as its fifth bit, element 16 + j the high nibble with bit
+// 16 + j of qh, both offset by -16, times d.
+void dequant_q5_0(const uint8_t *b, size_t n, float *y) {
+    for (size_t blk = 0; blk < n / 32; ++blk) {
+        const uint8_t *o = b + blk * 22;
+        const float d = rd_half(o);
+        const uint32_t qh = (uint32_t)o[2] | (uint32_t)o[3] << 8 | (uint32_t)o[4] << 16 | (uint32_t)o[5] << 24;
+        const uint8_t *qs = o + 6;
+        for (uint32_t j = 0; j < 16; ++j) {
+            const uint32_t lo = (qs[j] & 0x0fu) | (((qh >> j) << 4) & 0x10u);
+            const uint32_t hi = (qs[j] >> 4) | ((qh >> (j + 12)) & 0x10u);
+            y[blk * 32 + j] = (float)((int)lo - 16) * d;
+            y[blk * 32 + 16 + j] = (float)((int)hi - 16) * d;
+        }
+    }
+}
+
+// dequant_q4_k (gguf.rs:410-439): super blocks of 256 = 8 sub-blocks of 32; sub-block pair
+// (2i, 2i + 1) uses the low and high nibbles of qs[32 i .. 32 i + 32]:
+// y = (d * sc) * q - dmin * m, each product rounded (no fused multiply-add).
+void dequant_q4_k(const uint8_t *b, size_t n, float *y) {
+    for (size_t blk = 0; blk < n / 256; ++blk) {
+        const uint8_t *o = b + blk * 144;
+        const float d = rd_half(o), dmin = rd_half(o + 2);
+        const uint8_t *scales = o + 4, *qs = o + 16;
+        float *yo = y + blk * 256;
+        for (uint32_t i = 0; i < 4; ++i) {
+            uint32_t sc1, m1, sc2, m2;
+            scale_min_k4(2 * i, scales, sc1, m1);
+            scale_min_k4(2 * i + 1, scales, sc2, m2);
+            const float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
+            const float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
+            for (uint32_t l = 0; l < 32; ++l) yo[64 * i + l] = d1 * (float)(qs[32 * i + l] & 0x0f) - mm1;
+            for (uint32_t l = 0; l < 32; ++l) yo[64 * i + 32 + l] = d2 * (float)(qs[32 * i + l] >> 4) - mm2;
+        }
+    }
+}
+
+// dequant_q6_k (gguf.rs:441-468): super blocks of 256 as two halves of 128; element l (< 32)
+// of quarter k of a half takes 4 low bits from ql and 2 high bits from qh, offset by -32, and
+// the int8 scale of its 16-element group: y = (d * s) * q.
+void dequant_q6_k(const uint8_t *b, size_t n, float *y) {
+    for (size_t blk = 0; blk < n / 256; ++blk) {
+        const uint8_t *o = b + blk * 210;
+        const uint8_t *ql = o, *qh = o + 128;
+        const int8_t *sc = reinterpret_cast<const int8_t *>(o + 192);
+        const float d = rd_half(o + 208);
+        for (uint32_t half = 0; half < 2; ++half) {
+            float *yb = y + blk * 256 + half * 128;
+            const uint8_t *qlb = ql + half * 64, *qhb = qh + half * 32;
+            const int8_t *scb = sc + half * 8;
+            for (uint32_t l = 0; l < 32; ++l) {
+                const uint32_t is = l / 16;
+                const int q1 = (int)((qlb[l] & 0x0fu) | (((qhb[l] >> 0) & 3u) << 4)) - 32;
+                const int q2 = (int)((qlb[l + 32] & 0x0fu) | (((qhb[l] >> 2) & 3u) << 4)) - 32;
+                const int q3 = (int)((uint32_t)(qlb[l] >> 4) | (((qhb[l] >> 4) & 3u) << 4)) - 32;
+                const int q4 = (int)((uint32_t)(qlb[l + 32] >> 4) | (((qhb[l] >> 6) & 3u) << 4)) - 32;
+                yb[l] = d * (float)scb[is + 0] * (float)q1;
+                yb[l + 32] = d * (float)scb[is + 2] * (float)q2;
+                yb[l + 64] = d * (float)scb[is + 4] * (float)q3;
+                yb[l + 96] = d * (float)scb[is + 6] * (float)q4;
+            }
+        }
+    }
+}
+
 
 Gguf::~Gguf() {
     if (map_) munmap(const_cast<uint8_t *>(map_), size_);
@@ -201,14 +301,23 @@ int Gguf::raw(const std::string &name, const TensorInfo *&t, const uint8_t *&dat
               std::string &err) const {
     t = info(name);
     if (!t) { err = "tensor `" + name + "` not found"; return HG_ERR_FORMAT; }
+    uint64_t n;
+    if (!t->n_elems_checked(n) || n > (uint64_t)SIZE_MAX / 4) {
+        err = "tensor `" + name + "`: element count overflows";
+        return HG_ERR_FORMAT;
+    }
     bool ok;
-    nbytes = type_nbytes(t->type, t->n_elems(), ok);
-    if (!ok) {
-        err = "tensor `" + name + "`: unsupported ggml_type " + std::to_string(t->type);
+    nbytes = type_nbytes(t->type, n, ok);
+    if (!ok) {   // gguf.rs:358 (Gguf::raw adds no context)
+        err = "type_nbytes: unsupported ggml_type " + std::to_string(t->type);
         return HG_ERR_UNSUPPORTED;
     }
+    if (t->offset > size_ || data_start_ > size_ - t->offset) {
+        err = "tensor `" + name + "` data out of bounds";
+        return HG_ERR_FORMAT;
+    }
     const size_t off = data_start_ + (size_t)t->offset;
-    if (off > size_ || nbytes > size_ - off) { err = "tensor `" + name + "` data out of bounds"; return HG_ERR_FORMAT; }
+    if (nbytes > size_ - off) { err = "tensor `" + name + "` data out of bounds"; return HG_ERR_FORMAT; }
     data = map_ + off;
     return HG_OK;
 }
@@ -237,16 +346,22 @@ int Gguf::load(const std::string &name, std::vector<float> &out, std::string &er
     size_t nb;
     int rc = raw(name, t, d, nb, err);
     if (rc) return rc;
-    if (t->type == 0) return f32(name, out, err);
+    if (t->type == GGML_F32) return f32(name, out, err);
     const size_t n = (size_t)t->n_elems();
-    out.resize(n);
-    if (t->type == 1) {
-        for (size_t i = 0; i < n; ++i) out[i] = half_to_f32((uint16_t)(d[2 * i] | (d[2 * i + 1] << 8)));
-    } else {  // Q8_0, gguf.rs:365-375
+    out.assign(n, 0.0f);   // (elements of a partial last block stay 0, as in gguf.rs)
+    switch (t->type) {
+    case GGML_F16:   // dequant_f16, gguf.rs:361-363
+        for (size_t i = 0; i < n; ++i) out[i] = rd_half(d + 2 * i);
+        break;
+    case GGML_Q8_0:  // dequant_q8_0, gguf.rs:365-375
         for (size_t b = 0; b < n / 32; ++b) {
-            const float s = half_to_f32((uint16_t)(d[34 * b] | (d[34 * b + 1] << 8)));
+            const float s = rd_half(d + 34 * b);
             for (int j = 0; j < 32; ++j) out[32 * b + j] = (float)(int8_t)d[34 * b + 2 + j] * s;
         }
+        break;
+    case GGML_Q5_0: dequant_q5_0(d, n, out.data()); break;
+    case GGML_Q4_K: dequant_q4_k(d, n, out.data()); break;
+    case GGML_Q6_K: dequant_q6_k(d, n, out.data()); break;
     }
     return HG_OK;
 }

@@ -19,11 +19,15 @@ struct Meta {
     std::string s;
 };
 
+// ggml tensor types the loader reads (gguf.rs:349-359)
+enum : uint32_t { GGML_F32 = 0, GGML_F16 = 1, GGML_Q5_0 = 6, GGML_Q8_0 = 8, GGML_Q4_K = 12, GGML_Q6_K = 14 };
+
 struct TensorInfo {
     std::vector<uint64_t> ne;  // fastest-varying first (gguf.rs:32-34)
     uint32_t type = 0;
     uint64_t offset = 0;
     uint64_t n_elems() const;
+    bool n_elems_checked(uint64_t &n) const;   // false if the product overflows 64 bits
 };
 
 class Gguf {
@@ -38,10 +42,11 @@ class Gguf {
     bool get_str(const std::string &key, std::string &v) const;
     // Gguf::f32 (gguf.rs:215-235): an F32 tensor, any other type is an error.
     int f32(const std::string &name, std::vector<float> &out, std::string &err) const;
-    // Raw bytes of a tensor of a supported ggml type (F32, F16, Q8_0), bounds-checked.
+    // Raw bytes of a tensor of a supported ggml type (F32, F16, Q5_0, Q8_0, Q4_K, Q6_K),
+    // bounds-checked.
     int raw(const std::string &name, const TensorInfo *&t, const uint8_t *&data, size_t &nbytes,
             std::string &err) const;
-    // Gguf::load (gguf.rs:250-269) for F32, F16 and Q8_0: the tensor as f32.
+    // Gguf::load (gguf.rs:250-269): the tensor as f32, dequantized from any supported type.
     int load(const std::string &name, std::vector<float> &out, std::string &err) const;
 
   private:
@@ -53,6 +58,10 @@ class Gguf {
 };
 
 float half_to_f32(uint16_t h);  // gguf.rs:329-341
+// Block dequantizers of the K-quant and 5-bit files (gguf.rs:377-468): n elements into y.
+void dequant_q5_0(const uint8_t *b, size_t n, float *y);
+void dequant_q4_k(const uint8_t *b, size_t n, float *y);
+void dequant_q6_k(const uint8_t *b, size_t n, float *y);
 
 // Config::from_gguf (config.rs:35-97)
 int config_from_gguf(const Gguf &g, hg_config &c, std::string &err);

@@ -2,6 +2,7 @@
 #pragma once
 #include "hg_common.h"
 
+#include <string>
 #include <vector>
 
 namespace hg {
@@ -14,6 +15,11 @@ struct LaunchTimer {
     void add(hipEvent_t a, hipEvent_t b) { ev.emplace_back(a, b); tags.push_back(cls); }
 };
 void set_launch_timer(LaunchTimer *t);
+// First launch error recorded on this thread since the last take (hipSuccess if none), with
+// the kernel it concerns; taking clears it.
+hipError_t take_launch_error(std::string &msg);
+hipError_t take_launch_error_reset();
+void note_launch_error(hipError_t e, const std::string &what);
 
 hipError_t init_kernel_attributes();
 // LDS ring slots of the reference-order P.V kernel for a cache of cap positions (>= 2 needed).
@@ -49,11 +55,18 @@ size_t attn_fast_shm(uint32_t hd, uint32_t rep, uint32_t cap, uint32_t S);
 // which = 0: scores (reference order) or split partials (fast); which = 1: softmax + P.V or merge.
 // qkv holds q and k normed and rotated, and the caches row pos already (launch_qkv_head or
 // launch_qk_rope_append); qn, kn, eps, cs, sn are not read.
+// cap is the cache's row stride; win (pos + 1 <= win <= cap) the context extent the launches
+// are sized for (splits, LDS, kernel choice), so their cost follows the live context.
 // Reference order with q_out == nullptr leaves the quantization of o to its consumer.
 bool launch_attn(hipStream_t st, bool exact, int which, uint32_t hd, const float *qkv, const float *qn,
                  const float *kn, float eps, const float *cs, const float *sn, const StepParams *p, float *kc,
-                 float *vc, uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,
-                 float *o_out, uint8_t *q_out, float *d_out);
+                 float *vc, uint32_t cap, uint32_t win, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part,
+                 float *scratch, float *o_out, uint8_t *q_out, float *d_out);
+// Attention splits of a window of win positions (at most 256 positions per split).
+inline uint32_t attn_splits(uint32_t win) {
+    const uint32_t s = div_up(win, 256);
+    return s > 64 ? s : 64;
+}
 // Router row permutation the kernel expects in Wp (d a multiple of 32): element k of a row is
 // stored at 32 (k / 32) + 4 (k % 8) + (k % 32) / 8, so the chains k % 32 = l, 8 + l, 16 + l,
 // 24 + l of a 32-wide step are the four consecutive floats 4 l .. 4 l + 3.

@@ -1147,7 +1147,8 @@ __global__ __launch_bounds__(256) void k_attn_fast(const float *__restrict__ qkv
                                                    const float *__restrict__ kn, float eps,
                                                    const float *__restrict__ cs, const float *__restrict__ sn,
                                                    const StepParams *p, float *kc, float *vc, uint32_t cap,
-                                                   uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part) {
+                                                   uint32_t win, uint32_t n_heads, uint32_t n_kv, uint32_t S,
+                                                   float *part) {
     constexpr int MAXREP = 8;
     constexpr int TPT = HD / 4;       // threads per token (one float4 each)
     constexpr int TOK = 256 / TPT;    // tokens per pass
@@ -1163,7 +1164,7 @@ __global__ __launch_bounds__(256) void k_attn_fast(const float *__restrict__ qkv
     float *rot = raw + (rep + 2) * HD;       // (rep+1)*HD : (unused)
     float *tmp = rot + (rep + 1) * HD;       // 4*HD : (unused)
     float *sc = tmp + 4 * HD;                // rep * chunk scores
-    const uint32_t maxchunk = attn_maxchunk(cap, S);
+    const uint32_t maxchunk = attn_maxchunk(win, S);
     float *red = sc + rep * maxchunk;        // TOK * rep * HD partial P.V sums
     float *stat = red + TOK * rep * HD;      // 2*rep (max, sum)
     // q and k are normed and rotated, and k, v appended to the caches, by the QKV step
@@ -1347,17 +1348,20 @@ __device__ inline float dot_wide_serial(const float *a, const float *b, uint32_t
 }
 
 // Scores s[h][t] = dot(q_h, K_t) * (1/sqrt(hd)) (model.rs:213-218, ops::dot's order) for the
-// rep query heads of kv head g over split s of the cache (grid n_kv x S; split s covers
-// positions [s c, s c + c) with c = ceil(cap / S), a layout independent of the step, so the K
-// rows are fetched before the step's position is known), and the split maximum of every head.
+// rep query heads of kv head g over split s of the attention window (grid n_kv x S; split s
+// covers positions [s c, s c + c) with c = ceil(win / S), a layout independent of the step
+// within the window, so the K rows are fetched before the step's position is known), and the
+// split maximum of every head.  The window win (<= cap, >= pos + 1) is fixed per captured
+// step; cap is the cache's row stride.
 // q (normed, rotated) comes from the QKV step's output, K (with this step's row appended) from
 // the cache.  Lane l of the workgroup's 256 threads takes head l % R and position
 // t0 + l / R (+ 256 / R, ...), R = rep rounded up to a power of two: the R lanes of a position
 // read the same K row (one memory request per row).
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ qkv, const StepParams *p,
-                                                     const float *__restrict__ kc, uint32_t cap, uint32_t n_heads,
-                                                     uint32_t n_kv, uint32_t S, float *scores, float *pmax) {
+                                                     const float *__restrict__ kc, uint32_t cap, uint32_t win,
+                                                     uint32_t n_heads, uint32_t n_kv, uint32_t S, float *scores,
+                                                     float *pmax) {
     constexpr int MAXREP = 8;
     __shared__ __align__(16) float qs[MAXREP * HD];
     __shared__ float wm[4][MAXREP];
@@ -1366,12 +1370,12 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     const uint32_t rep = n_heads / n_kv;
     const uint32_t R = rep <= 1 ? 1u : rep <= 2 ? 2u : rep <= 4 ? 4u : 8u;   // lanes per position
     const uint32_t r = (uint32_t)tid % R, pp = 256 / R;                      // head, positions per pass
-    const uint32_t chunk = div_up(cap, S), t0 = s * chunk, t1 = min(cap, t0 + chunk);
+    const uint32_t chunk = div_up(win, S), t0 = s * chunk, t1 = min(win, t0 + chunk);
     const float *kcg = kc + (size_t)g * cap * HD;
     // loads in issue order: this lane's first K row, the group's q heads, the position
     float kt[HD];
     {
-        const uint32_t tr = min(t0 + (uint32_t)tid / R, cap - 1);
+        const uint32_t tr = min(t0 + (uint32_t)tid / R, win - 1);
 #pragma unroll
         for (int i = 0; i < HD; i += 4)
             *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kcg + (size_t)tr * HD + i);
@@ -1385,7 +1389,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     for (uint32_t tb = t0; tb < t1; tb += pp) {
         const uint32_t t = tb + (uint32_t)tid / R;
         if (tb != t0) {   // splits longer than 256 / R positions: the next K row
-            const uint32_t tr = min(t, cap - 1);
+            const uint32_t tr = min(t, win - 1);
 #pragma unroll
             for (int i = 0; i < HD; i += 4)
                 *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kcg + (size_t)tr * HD + i);
@@ -1460,8 +1464,8 @@ template <int HD>
 __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict__ scores,
                                                          const float *__restrict__ pmax,
                                                          const float *__restrict__ qkv, const StepParams *p,
-                                                         const float *__restrict__ vc, uint32_t cap, uint32_t S,
-                                                         uint32_t n_heads, uint32_t n_kv, float *o_out,
+                                                         const float *__restrict__ vc, uint32_t cap, uint32_t win,
+                                                         uint32_t S, uint32_t n_heads, uint32_t n_kv, float *o_out,
                                                          uint8_t *q_out, float *d_out) {
     using C = PvCfg;
     constexpr uint32_t T = C::T, TP = C::TP, D = C::D;
@@ -1474,9 +1478,9 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
     pv_head_quarter(blockIdx.x, n_heads, n_kv, HD / D, &h, &q);
     const uint32_t rep = n_heads / n_kv, g = h / rep;
     const uint32_t pos = p->pos, n = pos + 1;
-    const uint32_t R = pv_ring_slots(cap);
-    float *e = lds;                                     // [cap] e_t, then p_t
-    float *ring = lds + (size_t)div_up(cap, 4) * 4;     // [R][D][TP]
+    const uint32_t R = pv_ring_slots(win);
+    float *e = lds;                                     // [win] e_t, then p_t
+    float *ring = lds + (size_t)div_up(win, 4) * 4;     // [R][D][TP]
     const float *sc = scores + (size_t)h * cap;
     const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
     const float *vcg = vc + (size_t)g * cap * HD + q * D;
@@ -1721,8 +1725,8 @@ template <int HD>
 __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__restrict__ scores,
                                                              const float *__restrict__ pmax,
                                                              const float *__restrict__ qkv, const StepParams *p,
-                                                             const float *__restrict__ vc, uint32_t cap, uint32_t S,
-                                                             uint32_t n_heads, uint32_t n_kv, float *o_out) {
+                                                             const float *__restrict__ vc, uint32_t cap, uint32_t win,
+                                                             uint32_t S, uint32_t n_heads, uint32_t n_kv, float *o_out) {
     using C = PvResCfg;
     constexpr uint32_t D = C::D, G = C::G, EB = 8;
     extern __shared__ __align__(16) float lds[];
@@ -1736,7 +1740,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     pv_head_quarter(blockIdx.x, n_heads, n_kv, HD / D, &h, &q);
     const uint32_t rep = n_heads / n_kv, g = h / rep;
     const uint32_t pos = p->pos, n = pos + 1;
-    const uint32_t rc = pv_res_rows(cap), TPC = rc + 4;   // row stride 4 mod 32 banks
+    const uint32_t rc = pv_res_rows(win), TPC = rc + 4;   // row stride 4 mod 32 banks
     float *e = lds;                                         // [rc]  e_t
     float *P = lds + rc;                                    // [D][TPC]  V, then the products
     xsum::Scratch &xs = *reinterpret_cast<xsum::Scratch *>(P + (size_t)D * TPC);
@@ -2586,6 +2590,27 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
 thread_local LaunchTimer *g_timer = nullptr;
 void set_launch_timer(LaunchTimer *t) { g_timer = t; }
 
+// The first launch error since the last take: a launch HIP rejected (its error code) or one
+// the launch helpers refused on the host (hipErrorInvalidConfiguration).
+thread_local hipError_t g_launch_err = hipSuccess;
+thread_local std::string g_launch_msg;
+void note_launch_error(hipError_t e, const std::string &what) {
+    if (g_launch_err != hipSuccess) return;
+    g_launch_err = e;
+    g_launch_msg = what + ": " + hipGetErrorString(e);
+}
+hipError_t take_launch_error(std::string &msg) {
+    const hipError_t e = g_launch_err;
+    msg = g_launch_msg;
+    g_launch_err = hipSuccess;
+    g_launch_msg.clear();
+    return e;
+}
+hipError_t take_launch_error_reset() {
+    std::string m;
+    return take_launch_error(m);
+}
+
 #define LAUNCH(kern, grid, block, shm, st, ...)                                                              \
     do {                                                                                                     \
         if (g_timer) {                                                                                       \
@@ -2597,6 +2622,8 @@ void set_launch_timer(LaunchTimer *t) { g_timer = t; }
         } else {                                                                                             \
             hipLaunchKernelGGL(kern, grid, block, shm, st, __VA_ARGS__);                                     \
         }                                                                                                    \
+        const hipError_t le_ = hipGetLastError();                                                            \
+        if (le_ != hipSuccess) note_launch_error(le_, #kern);                                                \
     } while (0)
 
 // Kernels whose LDS exceeds the 64 KiB default opt in to the larger gfx950 allocation.
@@ -2672,6 +2699,10 @@ static void mv_launch(hipStream_t st, const Q8Mat &W, const uint8_t *q, const fl
 
 void launch_matvec(hipStream_t st, int order, int epi, const Q8Mat &W, const uint8_t *q, const float *dq, float *y,
                    uint32_t threads, uint32_t valid, float *pv, uint32_t *pi) {
+    if (threads < 64 || threads > 256 || threads % 64) {   // k_matvec: __launch_bounds__(256), whole waves
+        note_launch_error(hipErrorInvalidConfiguration, "k_matvec with " + std::to_string(threads) + " threads");
+        return;
+    }
 #define MV(O, E)                                                                   \
     do {                                                                           \
         if (W.sc_f32) mv_launch<O, E, true>(st, W, q, dq, y, threads, valid, pv, pi);  \
@@ -2774,21 +2805,21 @@ size_t attn_fast_shm(uint32_t hd, uint32_t rep, uint32_t cap, uint32_t S) {
 template <int HD>
 static void attn_exact_launch(hipStream_t st, int which, const float *qkv, const float *qn, const float *kn,
                               float eps, const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
-                              uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part,
+                              uint32_t cap, uint32_t win, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part,
                               float *scratch, float *o_out, uint8_t *q_out, float *d_out) {
     const bool fuse_quant = q_out == nullptr;  // the consumer quantizes o itself
     if (which == 0) {
-        LAUNCH(k_attn_scores<HD>, dim3(n_kv, S), dim3(256), 0, st, qkv, p, kc, cap, n_heads, n_kv, S, scratch,
-               part);
+        LAUNCH(k_attn_scores<HD>, dim3(n_kv, S), dim3(256), 0, st, qkv, p, kc, cap, win, n_heads, n_kv, S,
+               scratch, part);
         return;
     }
-    if (pv_res_fits(cap)) {
-        LAUNCH(k_attn_softmax_pv_res<HD>, dim3(n_heads * (HD / PvResCfg::D)), dim3(512), pv_res_lds(cap), st, scratch,
-               part, qkv, p, vc, cap, S, n_heads, n_kv, o_out);
+    if (pv_res_fits(win)) {
+        LAUNCH(k_attn_softmax_pv_res<HD>, dim3(n_heads * (HD / PvResCfg::D)), dim3(512), pv_res_lds(win), st, scratch,
+               part, qkv, p, vc, cap, win, S, n_heads, n_kv, o_out);
     } else {
-        const size_t shm = (size_t)div_up(cap, 4) * 16 + (size_t)pv_ring_slots(cap) * PvCfg::SLOT * 4;
+        const size_t shm = (size_t)div_up(win, 4) * 16 + (size_t)pv_ring_slots(win) * PvCfg::SLOT * 4;
         LAUNCH(k_attn_softmax_pv<HD>, dim3(n_heads * (HD / PvCfg::D)), dim3(PvCfg::NW * 64), shm, st, scratch, part, qkv,
-               p, vc, cap, S, n_heads, n_kv, o_out, q_out, d_out);
+               p, vc, cap, win, S, n_heads, n_kv, o_out, q_out, d_out);
     }
     if (!fuse_quant) LAUNCH(k_quant_o, dim3(1), dim3(256), 0, st, o_out, n_heads * HD, q_out, d_out);
 }
@@ -2796,12 +2827,12 @@ static void attn_exact_launch(hipStream_t st, int which, const float *qkv, const
 template <int HD>
 static void attn_fast_launch(hipStream_t st, int which, const float *qkv, const float *qn, const float *kn, float eps,
                              const float *cs, const float *sn, const StepParams *p, float *kc, float *vc,
-                             uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *o_out,
-                             uint8_t *q_out, float *d_out) {
+                             uint32_t cap, uint32_t win, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part,
+                             float *o_out, uint8_t *q_out, float *d_out) {
     if (which == 0) {
-        const size_t shm = attn_fast_shm(HD, n_heads / n_kv, cap, S);
-        LAUNCH(k_attn_fast<HD>, dim3(n_kv, S), dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads,
-               n_kv, S, part);
+        const size_t shm = attn_fast_shm(HD, n_heads / n_kv, win, S);
+        LAUNCH(k_attn_fast<HD>, dim3(n_kv, S), dim3(256), shm, st, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, win,
+               n_heads, n_kv, S, part);
         return;
     }
     LAUNCH(k_attn_combine<HD>, dim3(n_heads), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
@@ -2809,15 +2840,15 @@ static void attn_fast_launch(hipStream_t st, int which, const float *qkv, const 
 
 bool launch_attn(hipStream_t st, bool exact, int which, uint32_t hd, const float *qkv, const float *qn,
                  const float *kn, float eps, const float *cs, const float *sn, const StepParams *p, float *kc,
-                 float *vc, uint32_t cap, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part, float *scratch,
-                 float *o_out, uint8_t *q_out, float *d_out) {
+                 float *vc, uint32_t cap, uint32_t win, uint32_t n_heads, uint32_t n_kv, uint32_t S, float *part,
+                 float *scratch, float *o_out, uint8_t *q_out, float *d_out) {
 #define ATTN(HD)                                                                                                    \
     do {                                                                                                            \
         if (exact)                                                                                                  \
-            attn_exact_launch<HD>(st, which, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part,      \
+            attn_exact_launch<HD>(st, which, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, win, n_heads, n_kv, S, part, \
                                   scratch, o_out, q_out, d_out);                                                    \
         else                                                                                                        \
-            attn_fast_launch<HD>(st, which, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, n_heads, n_kv, S, part,       \
+            attn_fast_launch<HD>(st, which, qkv, qn, kn, eps, cs, sn, p, kc, vc, cap, win, n_heads, n_kv, S, part,  \
                                  o_out, q_out, d_out);                                                              \
     } while (0)
     if (hd == 64) ATTN(64);

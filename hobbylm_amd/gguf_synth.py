@@ -5,7 +5,9 @@ tensor names, metadata keys and layouts follow the HobbyLM exporter
 (export/to_gguf.py:59-129), the init recipe follows hobbylm/model.py:288-313
 (N(0, 0.02) everywhere, residual projections x (2L)^-1/2, router x 0.1, unit
 norm gains), and matrices are stored as GGML Q8_0 blocks ({f16 d; int8 q[32]},
-d = amax/127, q = round-half-away(x/d)), the format llama-quantize writes.
+d = amax/127, q = round-half-away(x/d)), the format llama-quantize writes, or, with
+qtype="kquant", as the K-quant / 5-bit mix of a Q4_K_M-style file (Q4_K, Q6_K, Q5_0), whose
+block layouts follow ggml's published quantizers (the decoders are gguf.rs:377-468).
 
 Everything is numpy; the same seed gives the same bytes on every machine
 with this numpy version.
@@ -23,7 +25,7 @@ import numpy as np
 
 GENERATOR_VERSION = 1
 
-GGML_F32, GGML_F16, GGML_Q8_0 = 0, 1, 8
+GGML_F32, GGML_F16, GGML_Q5_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 6, 8, 12, 14
 _T_U32, _T_I32, _T_F32, _T_BOOL, _T_STR, _T_ARR = 4, 5, 6, 7, 8, 9
 
 Q8_BLOCK = np.dtype([("d", "<f2"), ("qs", "i1", (32,))])
@@ -98,6 +100,126 @@ def dequantize_q8_0(blocks: np.ndarray) -> np.ndarray:
     return (blocks["qs"].astype(np.float32) * blocks["d"].astype(np.float32)[:, None]).reshape(-1)
 
 
+def _round_away(v):
+    return np.sign(v) * np.floor(np.abs(np.asarray(v, np.float64)) + 0.5)
+
+
+# ---- block packers: logical values -> ggml block bytes (the inverse of the decoders) ----
+def pack_q5_0(d: np.ndarray, q: np.ndarray) -> bytes:
+    """Q5_0 blocks {f16 d; u32 qh; u8 qs[16]} from f16 scales d[nb] and 5-bit codes q[nb][32]
+    (value = (q - 16) * d): code j < 16 in the low nibble of qs[j] with its fifth bit at bit j of
+    qh, code 16 + j in the high nibble with its fifth bit at bit 16 + j."""
+    q = np.asarray(q, np.uint32).reshape(-1, 32)
+    nb = q.shape[0]
+    out = np.zeros((nb, 22), np.uint8)
+    out[:, 0:2] = np.asarray(d, np.float16).reshape(nb, 1).view(np.uint8)
+    lo, hi = q[:, :16], q[:, 16:]
+    qh = (((lo >> 4) & 1) << np.arange(16, dtype=np.uint32)).sum(1) + \
+         (((hi >> 4) & 1) << (np.arange(16, dtype=np.uint32) + 16)).sum(1)
+    out[:, 2:6] = qh.astype("<u4").reshape(nb, 1).view(np.uint8)
+    out[:, 6:22] = ((lo & 0xF) | ((hi & 0xF) << 4)).astype(np.uint8)
+    return out.tobytes()
+
+
+def pack_q4_k(d, dmin, ls, lm, q) -> bytes:
+    """Q4_K super blocks {f16 d, dmin; u8 scales[12]; u8 qs[128]} from f16 d, dmin [nb], 6-bit
+    sub-block scales ls and mins lm [nb][8] and 4-bit codes q [nb][256]
+    (value = (d ls) q - dmin lm): ggml's scale packing (sub-blocks j < 4 in the low 6 bits of
+    bytes j and j + 4; j >= 4 in a nibble of byte j + 4 plus the top bits of bytes j - 4 and
+    j) and codes of sub-blocks 2i / 2i + 1 in the low / high nibbles of qs[32i .. 32i + 32]."""
+    ls = np.asarray(ls, np.uint32).reshape(-1, 8)
+    lm = np.asarray(lm, np.uint32).reshape(-1, 8)
+    q = np.asarray(q, np.uint32).reshape(-1, 256)
+    nb = q.shape[0]
+    out = np.zeros((nb, 144), np.uint8)
+    out[:, 0:2] = np.asarray(d, np.float16).reshape(nb, 1).view(np.uint8)
+    out[:, 2:4] = np.asarray(dmin, np.float16).reshape(nb, 1).view(np.uint8)
+    sc = np.zeros((nb, 12), np.uint32)
+    for j in range(8):
+        if j < 4:
+            sc[:, j] = ls[:, j]
+            sc[:, j + 4] = lm[:, j]
+        else:
+            sc[:, j + 4] = (ls[:, j] & 0xF) | ((lm[:, j] & 0xF) << 4)
+            sc[:, j - 4] |= (ls[:, j] >> 4) << 6
+            sc[:, j] |= (lm[:, j] >> 4) << 6
+    out[:, 4:16] = sc.astype(np.uint8)
+    qs = np.zeros((nb, 128), np.uint32)
+    for i in range(4):
+        qs[:, 32 * i:32 * i + 32] = q[:, 64 * i:64 * i + 32] | (q[:, 64 * i + 32:64 * i + 64] << 4)
+    out[:, 16:144] = qs.astype(np.uint8)
+    return out.tobytes()
+
+
+def pack_q6_k(d, sc, q) -> bytes:
+    """Q6_K super blocks {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d} from f16 d [nb], int8
+    group scales sc [nb][16] (group = element / 16) and 6-bit codes q [nb][256]
+    (value = (d sc) (q - 32)): in half h, element 128 h + 32 k + l (k < 4, l < 32) keeps its low
+    nibble in ql[64 h + l + 32 (k & 1)] (high nibble when k >= 2) and its top 2 bits at bit 2 k
+    of qh[32 h + l]."""
+    sc = np.asarray(sc, np.int8).reshape(-1, 16)
+    q = np.asarray(q, np.uint32).reshape(-1, 256)
+    nb = q.shape[0]
+    out = np.zeros((nb, 210), np.uint8)
+    ql = np.zeros((nb, 128), np.uint32)
+    qh = np.zeros((nb, 64), np.uint32)
+    for h in range(2):
+        e = q[:, 128 * h:128 * h + 128].reshape(nb, 4, 32)
+        ql[:, 64 * h:64 * h + 32] = (e[:, 0] & 0xF) | ((e[:, 2] & 0xF) << 4)
+        ql[:, 64 * h + 32:64 * h + 64] = (e[:, 1] & 0xF) | ((e[:, 3] & 0xF) << 4)
+        qh[:, 32 * h:32 * h + 32] = (e[:, 0] >> 4) | ((e[:, 1] >> 4) << 2) | ((e[:, 2] >> 4) << 4) | \
+            ((e[:, 3] >> 4) << 6)
+    out[:, 0:128] = ql.astype(np.uint8)
+    out[:, 128:192] = qh.astype(np.uint8)
+    out[:, 192:208] = sc.view(np.uint8)
+    out[:, 208:210] = np.asarray(d, np.float16).reshape(nb, 1).view(np.uint8)
+    return out.tobytes()
+
+
+# ---- quantizers: f32 values -> logical codes (any valid encoding; not ggml's error search) ----
+def quantize_q5_0(x: np.ndarray) -> bytes:
+    """ggml quantize_row_q5_0: d = (the value of largest magnitude) / -16,
+    q = min(31, trunc(x / d + 16.5))."""
+    b = np.ascontiguousarray(x, np.float32).reshape(-1, 32)
+    idx = np.argmax(np.abs(b), axis=1)
+    mx = b[np.arange(b.shape[0]), idx]
+    d = (mx / np.float32(-16.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d != 0, np.float32(1.0) / d, np.float32(0.0)).astype(np.float32)
+    q = np.clip(np.trunc((b * idv[:, None]).astype(np.float32) + np.float32(16.5)), 0, 31).astype(np.uint32)
+    return pack_q5_0(d.astype(np.float16), q)
+
+
+def quantize_q4_k(x: np.ndarray) -> bytes:
+    """Per 32-wide sub-block: min and range, 6-bit scale/min relative to the super block's f16
+    d and dmin, 4-bit codes."""
+    b = np.ascontiguousarray(x, np.float32).reshape(-1, 8, 32).astype(np.float64)
+    mn = np.minimum(b.min(2), 0.0)
+    sc = (b.max(2) - mn) / 15.0
+    d = (sc.max(1) / 63.0).astype(np.float16).astype(np.float64)
+    dmin = ((-mn).max(1) / 63.0).astype(np.float16).astype(np.float64)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ls = np.clip(np.where(d[:, None] > 0, np.rint(sc / d[:, None]), 0), 0, 63)
+        lm = np.clip(np.where(dmin[:, None] > 0, np.rint(-mn / dmin[:, None]), 0), 0, 63)
+        step = d[:, None] * ls
+        q = np.where(step[:, :, None] > 0, np.rint((b + (dmin[:, None] * lm)[:, :, None]) / step[:, :, None]), 0)
+    q = np.clip(q, 0, 15).astype(np.uint32)
+    return pack_q4_k(d.astype(np.float16), dmin.astype(np.float16), ls, lm, q.reshape(-1, 256))
+
+
+def quantize_q6_k(x: np.ndarray) -> bytes:
+    """Per 16-element group an int8 scale relative to the super block's f16 d, 6-bit codes."""
+    b = np.ascontiguousarray(x, np.float32).reshape(-1, 16, 16).astype(np.float64)
+    gs = np.abs(b).max(2) / 31.0
+    d = (gs.max(1) / 127.0).astype(np.float16).astype(np.float64)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        sc = np.clip(np.where(d[:, None] > 0, np.rint(gs / d[:, None]), 0), -128, 127)
+        step = d[:, None] * sc
+        q = np.where(step[:, :, None] > 0, np.rint(b / step[:, :, None]), 0)
+    q = (np.clip(q, -32, 31) + 32).astype(np.uint32)
+    return pack_q6_k(d.astype(np.float16), sc.astype(np.int8), q.reshape(-1, 256))
+
+
 class _Writer:
     def __init__(self, arch: str):
         self.arch = arch
@@ -163,9 +285,26 @@ def _rng(seed: int, name: str) -> np.random.Generator:
     return np.random.default_rng([seed, zlib.crc32(name.encode())])
 
 
+# the tensor types of qtype="kquant" by role (the mix a Q4_K_M file uses: 4-bit K-quants for
+# most matrices, 6-bit for the down projections and the embedding, Q5_0 for attn_output)
+_KQUANT_ROLE = {"token_embd": GGML_Q6_K, "attn_qkv": GGML_Q4_K, "attn_output": GGML_Q5_0,
+                "ffn_gate": GGML_Q4_K, "ffn_up": GGML_Q4_K, "ffn_down": GGML_Q6_K}
+
+
+def _encode(ggml_type: int, arr: np.ndarray) -> bytes:
+    if ggml_type == GGML_Q8_0:
+        return quantize_q8_0(arr).tobytes()
+    if ggml_type == GGML_Q5_0:
+        return quantize_q5_0(arr)
+    if ggml_type == GGML_Q4_K:
+        return quantize_q4_k(arr)
+    return quantize_q6_k(arr)
+
+
 def build_gguf(path: str, shape: Shape, seed: int, *, norm_jitter: float = 0.0,
-               bias_std: float = 0.01, init_std: float = 0.02) -> str:
-    """Write a random-init hobbylm GGUF with Q8_0 matrices and F32 norms/router/bias."""
+               bias_std: float = 0.01, init_std: float = 0.02, qtype: str = "q8_0") -> str:
+    """Write a random-init hobbylm GGUF with quantized matrices (qtype "q8_0", or "kquant" for
+    the Q4_K / Q6_K / Q5_0 mix) and F32 norms/router/bias."""
     s = shape
     w = _Writer("hobbylm")
     a = "hobbylm"
@@ -207,8 +346,19 @@ def build_gguf(path: str, shape: Shape, seed: int, *, norm_jitter: float = 0.0,
         return (_rng(seed, name).standard_normal(int(np.prod(shp)), dtype=np.float32)
                 * np.float32(std)).reshape(shp)
 
+    def mat_type(name, n):
+        if qtype == "q8_0":
+            return GGML_Q8_0
+        role = name.split(".")[-2] if name.startswith("blk.") else name.split(".")[0]
+        for key, ty in _KQUANT_ROLE.items():
+            if role.startswith(key):
+                # K-quant super blocks need whole 256-element groups
+                return ty if ty == GGML_Q5_0 or n % 256 == 0 else GGML_Q5_0
+        return GGML_Q8_0
+
     def q8(name, shp, std):
-        w.tensor(name, shp, GGML_Q8_0, quantize_q8_0(normal(name, shp, std)).tobytes())
+        ty = mat_type(name, int(np.prod(shp)))
+        w.tensor(name, shp, ty, _encode(ty, normal(name, shp, std)))
 
     def f32(name, arr):
         w.tensor(name, arr.shape, GGML_F32, np.ascontiguousarray(arr, dtype="<f4").tobytes())
@@ -218,10 +368,11 @@ def build_gguf(path: str, shape: Shape, seed: int, *, norm_jitter: float = 0.0,
             return np.float32(1.0) + normal(name, (n,), norm_jitter)
         return np.ones(n, dtype=np.float32)
 
-    emb = quantize_q8_0(normal("token_embd.weight", (s.vocab_size, s.d_model), init_std)).tobytes()
-    w.tensor("token_embd.weight", (s.vocab_size, s.d_model), GGML_Q8_0, emb)
+    ety = mat_type("token_embd.weight", s.vocab_size * s.d_model)
+    emb = _encode(ety, normal("token_embd.weight", (s.vocab_size, s.d_model), init_std))
+    w.tensor("token_embd.weight", (s.vocab_size, s.d_model), ety, emb)
     f32("output_norm.weight", gain("output_norm.weight", s.d_model))
-    w.tensor("output.weight", (s.vocab_size, s.d_model), GGML_Q8_0, emb)  # tied embeddings
+    w.tensor("output.weight", (s.vocab_size, s.d_model), ety, emb)  # tied embeddings
     for i in range(s.n_layers):
         p = f"blk.{i}."
         f32(p + "attn_norm.weight", gain(p + "attn_norm.weight", s.d_model))
@@ -264,12 +415,15 @@ def cache_dir() -> str:
 
 
 def synth_path(preset: str, seed: int, *, norm_jitter: float = 0.0,
-               directory: Optional[str] = None) -> str:
-    """Path of the cached synthetic GGUF for (preset, seed), written on first use."""
-    tag = f"{preset}_s{seed}" + (f"_j{norm_jitter:g}" if norm_jitter else "") + f"_v{GENERATOR_VERSION}"
+               directory: Optional[str] = None, qtype: str = "q8_0") -> str:
+    """Path of the cached synthetic GGUF for (preset, seed, qtype), written on first use."""
+    tag = f"{preset}_s{seed}" + (f"_j{norm_jitter:g}" if norm_jitter else "") + \
+        ("" if qtype == "q8_0" else f"_{qtype}") + f"_v{GENERATOR_VERSION}"
     path = os.path.join(directory or cache_dir(), tag + ".gguf")
     if not os.path.exists(path):
-        build_gguf(path, PRESETS[preset], seed, norm_jitter=norm_jitter)
+        tmp = path + f".{os.getpid()}.tmp"
+        build_gguf(tmp, PRESETS[preset], seed, norm_jitter=norm_jitter, qtype=qtype)
+        os.replace(tmp, path)
     return path
 
 

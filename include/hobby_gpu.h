@@ -69,10 +69,18 @@ const char *hg_last_error(void);
 /* Engine::load(path, quant) (lib.rs:85-92) -> Gguf::open (gguf.rs:166-212),
  * Config::from_gguf (config.rs:35-97), Model::load (model.rs:79-131).  quant != 0 keeps
  * every matrix as Q8_0 after the load-time requantization of Q8Tensor::quantize
- * (quant.rs:78-102); quant == 0 (F32 matrices) returns HG_ERR_UNSUPPORTED.  The tokenizer
- * is not built: token ids cross this boundary. */
+ * (quant.rs:78-102), from any matrix type Gguf::load reads (F32, F16, Q5_0, Q8_0, Q4_K,
+ * Q6_K); quant == 0 (F32 matrices) returns HG_ERR_UNSUPPORTED.  The file is parsed and
+ * checked on the host before any device call, so format errors are reported (HG_ERR_IO,
+ * HG_ERR_FORMAT, HG_ERR_UNSUPPORTED) on a machine without a GPU too.  The tokenizer is not
+ * built: token ids cross this boundary. */
 int hg_model_load(const char *path, int quant, hg_model **out);
 void hg_model_free(hg_model *m);
+/* Gguf::open (gguf.rs:166-212) + Gguf::load (gguf.rs:250-269): tensor `name` of the file at
+ * `path` as f32, dequantized from F32, F16, Q5_0, Q8_0, Q4_K or Q6_K (gguf.rs:361-468).  *n
+ * receives the element count; out (NULL: query the count only) holds cap floats.  Host work
+ * only: no device is needed. */
+int hg_gguf_load_tensor(const char *path, const char *name, float *out, uint64_t cap, uint64_t *n);
 /* Engine.cfg (lib.rs:79) */
 int hg_model_config(const hg_model *m, hg_config *out);
 /* Engine::weight_bytes (lib.rs:100-102) -> Model::weight_bytes (model.rs:134-149): bytes
@@ -98,6 +106,10 @@ int hg_kv_truncate(hg_kv *kv, uint32_t len);
 /* Cache rows [0, len) of one layer in the reference layout KvCache.k[layer] /
  * KvCache.v[layer] ([len][n_kv_heads*head_dim], model.rs:60-64, 210-211). */
 int hg_kv_read(const hg_kv *kv, uint32_t layer, float *k, float *v);
+/* Assigning the reference's pub fields KvCache.k / .v / .len (model.rs:60-64): rows [0, len)
+ * of every layer from k, v ([n_layers][len][n_kv_heads*head_dim]), then len; later decode
+ * steps continue from len. */
+int hg_kv_load(hg_kv *kv, uint32_t len, const float *k, const float *v);
 
 /* Model::forward(token, pos, cache) (model.rs:152-156).  pos must equal hg_kv_len(kv)
  * and be < max_ctx.  logits (may be NULL) receives vocab_size floats; next (may be NULL)

@@ -52,6 +52,11 @@ def lib():
             "orc_half_to_f32": (C.c_float, [C.c_uint16]),
             "orc_dequant_q8_0": (None, [_u8p, C.c_size_t, _f32p]),
             "orc_dequant_f16": (None, [_u8p, C.c_size_t, _f32p]),
+            "orc_dequant_q5_0": (None, [_u8p, C.c_size_t, _f32p]),
+            "orc_dequant_q4_k": (None, [_u8p, C.c_size_t, _f32p]),
+            "orc_dequant_q6_k": (None, [_u8p, C.c_size_t, _f32p]),
+            "orc_gguf_load_tensor": (C.c_int, [C.c_char_p, C.c_char_p, C.c_void_p, C.c_uint64,
+                                               C.POINTER(C.c_uint64)]),
             "orc_q8_quantize": (None, [_f32p, C.c_size_t, C.c_size_t, _f32p, _i8p]),
             "orc_quantize_act": (None, [_f32p, C.c_size_t, _i8p, _f32p]),
             "orc_qrow_dot": (C.c_float, [_i8p, _i8p, _f32p, _f32p, C.c_size_t]),
@@ -124,6 +129,26 @@ def dequant_q8_0(raw: np.ndarray, n: int) -> np.ndarray:
     y = np.empty(n, np.float32)
     lib().orc_dequant_q8_0(np.ascontiguousarray(raw, np.uint8), n, y)
     return y
+
+
+def dequant(ggml_type: int, raw: np.ndarray, n: int) -> np.ndarray:
+    """Gguf::load's dequantization of n elements of a Q5_0 (6), Q8_0 (8), Q4_K (12) or Q6_K (14)
+    tensor (gguf.rs:365-468)."""
+    fn = {6: lib().orc_dequant_q5_0, 8: lib().orc_dequant_q8_0, 12: lib().orc_dequant_q4_k,
+          14: lib().orc_dequant_q6_k, 1: lib().orc_dequant_f16}[ggml_type]
+    y = np.zeros(n, np.float32)
+    fn(np.ascontiguousarray(raw, np.uint8).reshape(-1), n, y)
+    return y
+
+
+def gguf_load_tensor(path: str, name: str) -> np.ndarray:
+    """Gguf::load (gguf.rs:250-269) of one tensor, as f32."""
+    n = C.c_uint64()
+    _check(lib().orc_gguf_load_tensor(str(path).encode(), name.encode(), None, 0, C.byref(n)))
+    out = np.empty(n.value, np.float32)
+    _check(lib().orc_gguf_load_tensor(str(path).encode(), name.encode(), out.ctypes.data_as(C.c_void_p),
+                                      out.size, C.byref(n)))
+    return out
 
 
 def q8_quantize(w: np.ndarray):

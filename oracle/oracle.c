@@ -94,6 +94,83 @@ void orc_dequant_q8_0(const uint8_t *b, size_t n, float *y) {
     }
 }
 
+/* gguf.rs:377-397: block {f16 d; u32 qh; u8 qs[16]}; 5-bit values offset by -16 */
+void orc_dequant_q5_0(const uint8_t *b, size_t n, float *y) {
+    for (size_t blk = 0; blk < n / 32; blk++) {
+        size_t o = blk * 22;
+        float d = rd_half(b, o);
+        uint32_t qh = (uint32_t)b[o + 2] | ((uint32_t)b[o + 3] << 8) | ((uint32_t)b[o + 4] << 16) |
+                      ((uint32_t)b[o + 5] << 24);
+        const uint8_t *qs = b + o + 6;
+        for (uint32_t j = 0; j < 16; j++) {
+            uint8_t xh0 = (uint8_t)(((qh >> j) << 4) & 0x10);
+            uint8_t xh1 = (uint8_t)((qh >> (j + 12)) & 0x10);
+            int x0 = (int)((qs[j] & 0x0F) | xh0) - 16;
+            int x1 = (int)((qs[j] >> 4) | xh1) - 16;
+            y[blk * 32 + j] = (float)x0 * d;
+            y[blk * 32 + 16 + j] = (float)x1 * d;
+        }
+    }
+}
+
+/* gguf.rs:399-408 */
+static void scale_min_k4(size_t j, const uint8_t *sc, uint8_t *d, uint8_t *m) {
+    if (j < 4) {
+        *d = sc[j] & 63;
+        *m = sc[j + 4] & 63;
+    } else {
+        *d = (uint8_t)((sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4));
+        *m = (uint8_t)((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
+    }
+}
+
+/* gguf.rs:410-439: 256-element super blocks {f16 d, dmin; u8 scales[12]; u8 qs[128]} */
+void orc_dequant_q4_k(const uint8_t *b, size_t n, float *y) {
+    size_t yi = 0;
+    for (size_t blk = 0; blk < n / 256; blk++) {
+        size_t o = blk * 144;
+        float d = rd_half(b, o), dmin = rd_half(b, o + 2);
+        const uint8_t *scales = b + o + 4, *qs = b + o + 16;
+        size_t is = 0, q = 0;
+        for (int it = 0; it < 4; it++) {
+            uint8_t sc1, m1, sc2, m2;
+            scale_min_k4(is, scales, &sc1, &m1);
+            float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
+            scale_min_k4(is + 1, scales, &sc2, &m2);
+            float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
+            for (int l = 0; l < 32; l++) y[yi++] = d1 * (float)(qs[q + l] & 0xF) - mm1;
+            for (int l = 0; l < 32; l++) y[yi++] = d2 * (float)(qs[q + l] >> 4) - mm2;
+            q += 32;
+            is += 2;
+        }
+    }
+}
+
+/* gguf.rs:441-468: 256-element super blocks {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d} */
+void orc_dequant_q6_k(const uint8_t *b, size_t n, float *y) {
+    for (size_t blk = 0; blk < n / 256; blk++) {
+        size_t o = blk * 210;
+        const uint8_t *ql = b + o, *qh = b + o + 128;
+        const int8_t *sc = (const int8_t *)(b + o + 192);
+        float d = rd_half(b, o + 208);
+        size_t ybase = blk * 256;
+        for (int half = 0; half < 2; half++) {
+            size_t yb = ybase + half * 128, qlb = half * 64, qhb = half * 32, scb = half * 8;
+            for (size_t l = 0; l < 32; l++) {
+                size_t is = l / 16;
+                int q1 = (int)((ql[qlb + l] & 0xF) | (((qh[qhb + l] >> 0) & 3) << 4)) - 32;
+                int q2 = (int)((ql[qlb + l + 32] & 0xF) | (((qh[qhb + l] >> 2) & 3) << 4)) - 32;
+                int q3 = (int)((ql[qlb + l] >> 4) | (((qh[qhb + l] >> 4) & 3) << 4)) - 32;
+                int q4 = (int)((ql[qlb + l + 32] >> 4) | (((qh[qhb + l] >> 6) & 3) << 4)) - 32;
+                y[yb + l] = d * (float)sc[scb + is + 0] * (float)q1;
+                y[yb + l + 32] = d * (float)sc[scb + is + 2] * (float)q2;
+                y[yb + l + 64] = d * (float)sc[scb + is + 4] * (float)q3;
+                y[yb + l + 96] = d * (float)sc[scb + is + 6] * (float)q4;
+            }
+        }
+    }
+}
+
 enum { T_U8, T_I8, T_U16, T_I16, T_U32, T_I32, T_F32, T_BOOL, T_STR, T_ARR, T_U64, T_I64, T_F64 };
 enum { M_U32, M_I32, M_F32, M_U64, M_BOOL, M_STR, M_ARRSTR, M_ARRI32, M_ARRF32, M_OTHER };
 
@@ -313,7 +390,8 @@ static const tinfo_t *tensor_get(const gguf_t *g, const char *name) {
 }
 static uint64_t n_elems(const tinfo_t *t) {
     uint64_t n = 1;
-    for (uint32_t d = 0; d < t->nd; d++) n *= t->ne[d];
+    for (uint32_t d = 0; d < t->nd; d++)
+        if (__builtin_mul_overflow(n, t->ne[d], &n)) return UINT64_MAX;
     return n;
 }
 
@@ -326,6 +404,7 @@ static float *gguf_f32(const gguf_t *g, const char *name, size_t *n_out) {
         return NULL;
     }
     size_t n = (size_t)n_elems(t);
+    if (n_elems(t) == UINT64_MAX || n > SIZE_MAX / 4) { fail("tensor `%s`: element count overflows", name); return NULL; }
     size_t off = g->data_start + (size_t)t->offset;
     if (off > g->size || n * 4 > g->size - off) { fail("tensor `%s` data out of bounds", name); return NULL; }
     if (off % 4) { fail("tensor `%s` is not 4-byte aligned", name); return NULL; }
@@ -335,24 +414,55 @@ static float *gguf_f32(const gguf_t *g, const char *name, size_t *n_out) {
     return v;
 }
 
-/* Gguf::load, gguf.rs:250-269 (F32, F16 and Q8_0; other ggml types are rejected) */
+/* Gguf::load, gguf.rs:250-269, with type_nbytes (gguf.rs:349-359) */
 static float *gguf_load(const gguf_t *g, const char *name, size_t *n_out) {
     const tinfo_t *t = tensor_get(g, name);
     if (!t) { fail("tensor `%s` not found", name); return NULL; }
     if (t->type == 0) return gguf_f32(g, name, n_out);
     size_t n = (size_t)n_elems(t), nbytes;
+    if (n_elems(t) == UINT64_MAX || n > SIZE_MAX / 4) { fail("tensor `%s`: element count overflows", name); return NULL; }
     switch (t->type) {
     case 1: nbytes = n * 2; break;
+    case 6: nbytes = (n / 32) * 22; break;
     case 8: nbytes = (n / 32) * 34; break;
-    default: fail("tensor `%s`: unsupported ggml_type %u", name, t->type); return NULL;
+    case 12: nbytes = (n / 256) * 144; break;
+    case 14: nbytes = (n / 256) * 210; break;
+    default: fail("type_nbytes: unsupported ggml_type %u", t->type); return NULL;   /* gguf.rs:358 */
     }
     size_t off = g->data_start + (size_t)t->offset;
     if (off > g->size || nbytes > g->size - off) { fail("tensor `%s` data out of bounds", name); return NULL; }
-    float *v = (float *)malloc(n * 4 + 4);
-    if (t->type == 1) orc_dequant_f16(g->map + off, n, v);
-    else orc_dequant_q8_0(g->map + off, n, v);
+    float *v = (float *)calloc(n + 1, 4);
+    const uint8_t *b = g->map + off;
+    switch (t->type) {
+    case 1: orc_dequant_f16(b, n, v); break;
+    case 6: orc_dequant_q5_0(b, n, v); break;
+    case 8: orc_dequant_q8_0(b, n, v); break;
+    case 12: orc_dequant_q4_k(b, n, v); break;
+    case 14: orc_dequant_q6_k(b, n, v); break;
+    }
     *n_out = n;
     return v;
+}
+
+/* Gguf::open + Gguf::load (gguf.rs:166-212, 250-269) of one tensor; *n = element count, out
+ * (NULL: count only) holds cap floats. */
+int orc_gguf_load_tensor(const char *path, const char *name, float *out, uint64_t cap, uint64_t *n) {
+    gguf_t g;
+    if (gguf_open(path, &g)) return -1;
+    size_t cnt = 0;
+    float *v = gguf_load(&g, name, &cnt);
+    int rc = 0;
+    if (!v) rc = -1;
+    else {
+        *n = cnt;
+        if (out) {
+            if (cap < cnt) rc = fail("output too small");
+            else memcpy(out, v, cnt * 4);
+        }
+        free(v);
+    }
+    gguf_close(&g);
+    return rc;
 }
 
 /* ======================================================================

@@ -39,6 +39,10 @@ int orc_get_threads(void);
 float orc_half_to_f32(uint16_t h);                                  /* gguf.rs:329-341 */
 void orc_dequant_q8_0(const uint8_t *b, size_t n, float *y);        /* gguf.rs:365-375 */
 void orc_dequant_f16(const uint8_t *b, size_t n, float *y);         /* gguf.rs:361-363 */
+void orc_dequant_q5_0(const uint8_t *b, size_t n, float *y);        /* gguf.rs:377-397 */
+void orc_dequant_q4_k(const uint8_t *b, size_t n, float *y);        /* gguf.rs:410-439 */
+void orc_dequant_q6_k(const uint8_t *b, size_t n, float *y);        /* gguf.rs:441-468 */
+int orc_gguf_load_tensor(const char *path, const char *name, float *out, uint64_t cap, uint64_t *n);
 
 /* ---- quant.rs ---- */
 /* Q8Tensor::quantize (quant.rs:78-102): w[out*in] -> scales[out*in/32], qs[out*in] */

@@ -1,0 +1,213 @@
+"""GGUF reading beyond Q8_0: the Q5_0 / Q4_K / Q6_K decoders (gguf.rs:377-468) and the load
+errors of Gguf::open / Config::from_gguf / Model::load (gguf.rs:166-269, config.rs:35-97).
+
+The decoders are pinned against the block packers of gguf_synth (the inverse mapping: logical
+codes and scales -> ggml bytes), with the expected values formed from the logical arrays, so a
+wrong nibble, bit or scale index in a decoder fails.  The product's host-side reader
+(hg_gguf_load_tensor, hg_model_load's parse) runs without a GPU and must agree with the oracle
+bit for bit and raise the reference's messages.
+"""
+import struct
+
+import numpy as np
+import pytest
+
+from hobbylm_amd import gguf_synth as gs
+
+F32 = np.float32
+
+
+def _f16(rng, n, lo=-3, hi=3):
+    return (rng.uniform(0.5, 2.0, n) * np.exp2(rng.integers(lo, hi, n))).astype(np.float16)
+
+
+def test_q5_0_decoder_pinned(orc):
+    rng = np.random.default_rng(0)
+    nb = 64
+    d = _f16(rng, nb) * np.where(rng.random(nb) < 0.5, -1, 1).astype(np.float16)
+    q = rng.integers(0, 32, (nb, 32))
+    raw = np.frombuffer(gs.pack_q5_0(d, q), np.uint8)
+    want = ((q - 16).astype(F32) * d.astype(F32)[:, None]).reshape(-1)
+    got = orc.dequant(6, raw, nb * 32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_q4_k_decoder_pinned(orc):
+    rng = np.random.default_rng(1)
+    nb = 16
+    d, dmin = _f16(rng, nb), _f16(rng, nb)
+    ls, lm = rng.integers(0, 64, (nb, 8)), rng.integers(0, 64, (nb, 8))
+    q = rng.integers(0, 16, (nb, 256))
+    raw = np.frombuffer(gs.pack_q4_k(d, dmin, ls, lm, q), np.uint8)
+    sub = np.arange(256) // 32
+    # y = (d * sc) * q - dmin * m, every product rounded to f32 (no fused multiply-add)
+    d1 = d.astype(F32)[:, None] * ls.astype(F32)
+    m1 = dmin.astype(F32)[:, None] * lm.astype(F32)
+    want = (d1[:, sub] * q.astype(F32) - m1[:, sub]).astype(F32).reshape(-1)
+    got = orc.dequant(12, raw, nb * 256)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the sub-block scale packing: every one of the 8 (scale, min) pairs is distinguishable
+    ls1 = np.tile(np.arange(8) * 7 + 5, (1, 1))
+    lm1 = np.tile(63 - np.arange(8) * 5, (1, 1))
+    raw1 = np.frombuffer(gs.pack_q4_k(np.array([1.0], np.float16), np.array([1.0], np.float16), ls1, lm1,
+                                      np.ones((1, 256), np.int64)), np.uint8)
+    y1 = orc.dequant(12, raw1, 256)
+    assert np.array_equal(y1.reshape(8, 32)[:, 0], (ls1[0] - lm1[0]).astype(F32))
+
+
+def test_q6_k_decoder_pinned(orc):
+    rng = np.random.default_rng(2)
+    nb = 16
+    d = _f16(rng, nb)
+    sc = rng.integers(-128, 128, (nb, 16)).astype(np.int8)
+    q = rng.integers(0, 64, (nb, 256))
+    raw = np.frombuffer(gs.pack_q6_k(d, sc, q), np.uint8)
+    grp = np.arange(256) // 16
+    ds = d.astype(F32)[:, None] * sc.astype(F32)          # (d * s) first
+    want = (ds[:, grp] * (q - 32).astype(F32)).astype(F32).reshape(-1)
+    got = orc.dequant(14, raw, nb * 256)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("ty,quant,tol", [(6, gs.quantize_q5_0, 0.08), (12, gs.quantize_q4_k, 0.12),
+                                          (14, gs.quantize_q6_k, 0.04)])
+def test_synthetic_quantizers_round_trip(orc, ty, quant, tol):
+    """The writer's encoders produce valid blocks that approximate their input."""
+    rng = np.random.default_rng(ty)
+    x = (rng.standard_normal(4096) * 0.02).astype(F32)
+    y = orc.dequant(ty, np.frombuffer(quant(x), np.uint8), x.size)
+    assert np.max(np.abs(y - x)) <= tol * np.max(np.abs(x))
+
+
+@pytest.fixture(scope="module")
+def kquant_path():
+    return gs.synth_path("tiny", 31, norm_jitter=0.1, qtype="kquant")
+
+
+def _tensor_types(path):
+    """{name: ggml_type} from the tensor directory (own minimal parser)."""
+    b = open(path, "rb").read()
+    n_t, n_m = struct.unpack_from("<QQ", b, 8)
+    p = 24
+
+    def skip_val(p, ty):
+        if ty in (0, 1, 7):
+            return p + 1
+        if ty in (2, 3):
+            return p + 2
+        if ty in (4, 5, 6):
+            return p + 4
+        if ty in (10, 11, 12):
+            return p + 8
+        if ty == 8:
+            (n,) = struct.unpack_from("<Q", b, p)
+            return p + 8 + n
+        at, n = struct.unpack_from("<IQ", b, p)
+        p += 12
+        for _ in range(n):
+            p = skip_val(p, at)
+        return p
+
+    for _ in range(n_m):
+        (kl,) = struct.unpack_from("<Q", b, p)
+        p += 8 + kl
+        (ty,) = struct.unpack_from("<I", b, p)
+        p = skip_val(p + 4, ty)
+    out = {}
+    for _ in range(n_t):
+        (nl,) = struct.unpack_from("<Q", b, p)
+        name = b[p + 8:p + 8 + nl].decode()
+        p += 8 + nl
+        (nd,) = struct.unpack_from("<I", b, p)
+        p += 4 + 8 * nd
+        ty, _ = struct.unpack_from("<IQ", b, p)
+        p += 12
+        out[name] = ty
+    return out
+
+
+def test_kquant_file_uses_every_type(kquant_path):
+    types = set(_tensor_types(kquant_path).values())
+    assert {0, 6, 12, 14} <= types
+
+
+def test_product_reader_matches_oracle(orc, kquant_path):
+    """hg_gguf_load_tensor (the product's host reader) against the oracle's gguf_load, every tensor."""
+    import hobbylm_amd as hg
+    hg.lib()
+    om = orc.Model(kquant_path)
+    for name, ty in _tensor_types(kquant_path).items():
+        got = hg.gguf_load_tensor(kquant_path, name)
+        want = orc.gguf_load_tensor(kquant_path, name)
+        assert got.shape == want.shape, name
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (name, ty)
+    del om
+
+
+# ---------------------------------------------------------------- load errors on the host
+def _write(tmp_path, name, data):
+    p = tmp_path / name
+    p.write_bytes(data)
+    return str(p)
+
+
+def _load_rc(hg, path):
+    import ctypes as C
+    h = C.c_void_p()
+    rc = hg.lib().hg_model_load(str(path).encode(), 1, C.byref(h))
+    if rc == 0:
+        hg.lib().hg_model_free(h)
+    return rc, hg.lib().hg_last_error().decode()
+
+
+def _with_ne(good: bytes, tensor: bytes, ne):
+    """The file with tensor's dimensions replaced by ne (same rank)."""
+    i = good.index(struct.pack("<Q", len(tensor)) + tensor) + 8 + len(tensor)
+    (nd,) = struct.unpack_from("<I", good, i)
+    assert nd == len(ne)
+    return good[:i + 4] + struct.pack("<" + "Q" * nd, *ne) + good[i + 4 + 8 * nd:]
+
+
+def test_product_load_errors_match_reference_messages(orc, tmp_path):
+    import hobbylm_amd as hg
+    hg.lib()
+    tiny = gs.synth_path("tiny", 11, norm_jitter=0.1)
+    good = open(tiny, "rb").read()
+    cases = {
+        "magic.gguf": (b"XXXX" + good[4:], -2, "not a GGUF file \\(bad magic\\)"),
+        "ver.gguf": (good[:4] + struct.pack("<I", 2) + good[8:], -2, "unsupported GGUF version 2 \\(expected 3\\)"),
+        "trunc.gguf": (good[:100], -2, "GGUF: unexpected end of file"),
+        "empty.gguf": (b"", -2, "GGUF: unexpected end of file"),
+        "missing_t.gguf": (good.replace(b"blk.1.attn_norm.weight", b"blk.1.attn_norm.weighX", 1), -2,
+                           "tensor `blk.1.attn_norm.weight` not found"),
+        "missing_k.gguf": (good.replace(b"hobbylm.block_count", b"hobbylm.block_counX", 1), -2,
+                           "missing metadata `hobbylm.block_count`"),
+        "overflow.gguf": (_with_ne(good, b"blk.0.attn_qkv.weight", (1 << 62, 1 << 62)), -2,
+                          "element count overflows"),
+        "bigshape.gguf": (_with_ne(good, b"blk.0.attn_qkv.weight", (1 << 31, 1 << 20)), -2,
+                          "data out of bounds"),
+        "type.gguf": (None, -3, "unsupported ggml_type 2"),
+    }
+    # an unsupported tensor type (2 = Q4_0): patch the type word of one directory entry
+    t = b"blk.0.ffn_gate.weight"
+    i = good.index(struct.pack("<Q", len(t)) + t) + 8 + len(t)
+    (nd,) = struct.unpack_from("<I", good, i)
+    j = i + 4 + 8 * nd
+    cases["type.gguf"] = (good[:j] + struct.pack("<I", 2) + good[j + 4:], -3, "unsupported ggml_type 2")
+    import re
+    for name, (data, code, msg) in cases.items():
+        path = _write(tmp_path, name, data)
+        rc, err = _load_rc(hg, path)
+        assert rc == code and re.search(msg, err), (name, rc, err)
+        # the oracle (the reference's messages) fails on the same file
+        with pytest.raises(orc.OracleError, match=msg):
+            orc.Model(path)
+    rc, err = _load_rc(hg, tmp_path / "absent.gguf")
+    assert rc == -1 and "opening" in err
+    # a well-formed file gets past the parse: it loads on a GPU, or stops at the device check
+    rc, err = _load_rc(hg, tiny)
+    assert rc == 0 or (rc == -5 and "device" in err.lower()), (rc, err)
+    # arguments
+    import ctypes as C
+    assert hg.lib().hg_model_load(None, 1, C.byref(C.c_void_p())) == -4
+    assert hg.lib().hg_model_load(tiny.encode(), 0, C.byref(C.c_void_p())) == -3

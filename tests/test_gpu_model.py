@@ -128,3 +128,59 @@ def test_forward_x_and_errors(hg, orc):
     with pytest.raises(hg.HgError):
         gm.forward(1, 2, small)                   # beyond the cache
     assert gm.weight_bytes() == om.weight_bytes()
+
+
+def test_kquant_file_bit_exact(hg, orc):
+    """A Q4_K / Q6_K / Q5_0 file (dequantized then requantized at load, quant.rs:78-102)."""
+    path = gs.synth_path("tiny", 31, norm_jitter=0.1, qtype="kquant")
+    gm, om, gkv, okv, recs = _run_pair(hg, orc, path, 9, 8, forced=True)
+    for i, (gl, ol, gnext, (gi, gw), (oi, ow, _)) in enumerate(recs):
+        assert _bits_equal(gl, ol), f"logits differ at step {i}"
+        assert np.array_equal(gi[1:], oi[1:]), i
+
+
+def test_joint12_shape_bit_exact(hg, orc):
+    """The published joint12 shape: d768, 16 layers, 12q/3kv heads of 128, 36 x 320 experts,
+    theta 1e6, vocab 50304 (hobby-rs/README.md:9,35)."""
+    path = gs.synth_path("joint12", 5)
+    gm, om, gkv, okv, recs = _run_pair(hg, orc, path, 16, 6)
+    for i, (gl, ol, gnext, (gi, gw), (oi, ow, _)) in enumerate(recs):
+        assert _bits_equal(gl, ol), f"logits differ at step {i}"
+        assert np.array_equal(gi[1:], oi[1:]), i
+    for layer in (0, 7, 15):
+        gk, gv = gkv.read(layer)
+        ok, ov = okv.read(layer)
+        assert _bits_equal(gk, ok) and _bits_equal(gv, ov), layer
+
+
+@pytest.mark.parametrize("start", [3050, 8176])
+def test_default_capacity_cache_bit_exact(hg, orc, start):
+    """The drop-in cache (max_ctx = 0: capacity = context_length = 8192) on the 500M model,
+    seeded with the same KV rows on both paths, decoding forced tokens across attention
+    windows: from the LDS-resident softmax/P.V kernel (<= 3072 positions) into the ring kernel
+    (start 3050), and up to the last position of the cache (start 8176)."""
+    path = gs.synth_path("500M", 1)
+    gm, om = hg.Model(path), orc.Model(path)
+    c = gm.cfg
+    gkv, okv = gm.new_cache(), om.new_cache()
+    assert c.context_length == 8192
+    rng = np.random.default_rng(start)
+    kvd = c.n_kv_heads * c.head_dim
+    k = rng.standard_normal((c.n_layers, start, kvd), dtype=np.float32)
+    v = rng.standard_normal((c.n_layers, start, kvd), dtype=np.float32)
+    gkv.load(k, v)
+    okv.load(k, v)
+    del k, v
+    toks = gs.prompt_ids(start, min(24, c.context_length - start), 50257)
+    for i, t in enumerate(toks):
+        pos = start + i
+        gl, gnext = gm.forward(int(t), pos, gkv)
+        ol = om.forward(int(t), pos, okv)
+        assert _bits_equal(gl, ol), f"logits differ at pos {pos}"
+        assert gnext == int(np.argmax(ol[:50257])), pos
+        gi, _ = gkv.routing()
+        oi, _, _ = okv.routing()
+        assert np.array_equal(gi[1:], oi[1:]), pos
+    gk, gv = gkv.read(c.n_layers - 1)
+    ok, ov = okv.read(c.n_layers - 1)
+    assert _bits_equal(gk, ok) and _bits_equal(gv, ov)

@@ -117,9 +117,9 @@ def test_attention_fast_within_tolerance(hg, orc, ctx):
     assert np.max(np.abs(got - want)) <= 1e-4
 
 
-# 2049 and 3072: the resident kernel's 12-terms-per-lane sum and its longest cache; 3073: the
-# LDS product ring
-@pytest.mark.parametrize("ctx", [1, 300, 2048, 2049, 3072, 3073])
+# 512 / 2048 / 8192: the attention layer's contexts; 2049 and 3072: the resident kernel's
+# 12-terms-per-lane sum and its longest window; 3073 and 8192: the LDS product ring
+@pytest.mark.parametrize("ctx", [1, 300, 512, 2048, 2049, 3072, 3073, 8192])
 def test_attention_exact_bit_exact(hg, orc, ctx):
     got, want = _attn_case(orc, hg, ctx, exact=True)
     assert _bits_equal(got, want)
