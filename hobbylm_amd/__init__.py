@@ -80,6 +80,7 @@ SIGNATURES = {
     "hg_q8_tensor_bytes": (C.c_uint64, [_vp]),
     "hg_q8_tensor_matvec": (C.c_int, [_vp, _f32p, _f32p]),
     "hg_q8_tensor_matmul": (C.c_int, [_vp, _f32p, _f32p, C.c_uint32]),
+    "hg_q8_tensor_matvec_noalloc": (C.c_int, [_vp, _vp, _vp, _vp]),
     "hg_q8_tensor_matvec_gather": (C.c_int, [_vp, C.c_uint32, _u32p, C.c_uint32, _f32p, _f32p]),
     "hg_attention_decode": (C.c_int, [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_float, C.c_float, C.c_uint32,
                                       C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _f32p, _f32p, _f32p,
@@ -315,6 +316,11 @@ class Q8Tensor:
             _check(lib().hg_q8_tensor_time_matvec(self.h, np.ascontiguousarray(x, np.float32), reps, copies,
                                                   rows_per_mat, idv.ctypes.data_as(_vp), len(idv), us))
         return float(us[0])
+
+    def matvec_noalloc(self, x_dev_ptr: int, y_dev_ptr: int, stream: int = 0):
+        """The allocation-free matvec on device pointers (x[in] -> y[out]) enqueued on a
+        hipStream_t handle; the caller synchronizes."""
+        _check(lib().hg_q8_tensor_matvec_noalloc(self.h, _vp(x_dev_ptr), _vp(y_dev_ptr), _vp(stream or None)))
 
     def matmul(self, x: np.ndarray) -> np.ndarray:
         tn = x.shape[0]

@@ -69,6 +69,37 @@ struct DevBuf {
     T *as() const { return static_cast<T *>(p); }
 };
 
+// ---- the allocation-free matvec's scratch --------------------------------------------------
+// The quantized activation of hg_q8_tensor_matvec_noalloc (chunks + scales, as k_quant_vec
+// writes them) lives in this fixed device array, one per GPU for the life of the process.  In
+// host code `scratch` only names the symbol: its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and kept in g_scratch_ptr.
+constexpr uint32_t NOALLOC_MAX_IN = HG_NOALLOC_MAX_IN;
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)(NOALLOC_MAX_IN / 128) * (CHUNK_BYTES + 16);
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+static_assert(NOALLOC_SCRATCH_BYTES == HG_NOALLOC_SCRATCH_BYTES, "header and library disagree");
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[MAX_DEVICES] = {};
+
+// The device address of `scratch` on the current device (looked up on first use there).
+int scratch_ptr(void **out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MAX_DEVICES) return fail(HG_ERR_DEVICE, "device ordinal out of range");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(HG_ERR_DEVICE, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return HG_OK;
+}
+
 int check_device() {
     static std::once_flag once;
     static int status = HG_OK;
@@ -96,6 +127,12 @@ int check_device() {
         if (init_kernel_attributes() != hipSuccess) {
             status = HG_ERR_DEVICE;
             msg = "hipFuncSetAttribute failed";
+            return;
+        }
+        void *sp = nullptr;   // set-up of the allocation-free entry point's scratch on this device
+        if (scratch_ptr(&sp) != HG_OK) {
+            status = HG_ERR_DEVICE;
+            msg = g_err;
         }
     });
     if (status) g_err = msg;
@@ -1000,6 +1037,29 @@ int hg_q8_tensor_matvec(const hg_q8_tensor *t, const float *x, float *y) {
             HIP_TRY(hipStreamSynchronize(t->st));
             return HG_OK;
         });
+    });
+}
+
+int hg_q8_tensor_matvec_noalloc(const hg_q8_tensor *t, const float *x_dev, float *y_dev, void *stream) {
+    return guard([&]() -> int {
+        if (!t || !x_dev || !y_dev) return fail(HG_ERR_ARG, "NULL argument");
+        const Q8Mat &W = t->w.m;
+        if (W.K > NOALLOC_MAX_IN)
+            return fail(HG_ERR_ARG, "in = " + std::to_string(W.K) + " exceeds the allocation-free matvec's maximum of " +
+                                        std::to_string(NOALLOC_MAX_IN));
+        void *sp = nullptr;
+        int rc = scratch_ptr(&sp);
+        if (rc) return rc;
+        // [nc][128] activation chunks, then [nc][4] f32 scales: every byte the matvec reads is
+        // written by the quantization of this call (blocks past in are zeroed), so the previous
+        // call's contents never leak into this one
+        uint8_t *qa = static_cast<uint8_t *>(sp);
+        float *da = reinterpret_cast<float *>(qa + (size_t)W.nc * CHUNK_BYTES);
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        (void)take_launch_error_reset();
+        launch_quant_vec(st, x_dev, W.K, qa, da);
+        launch_matvec(st, ORDER_DECODE, EPI_STORE, W, qa, da, y_dev, 64, 0, nullptr, nullptr);
+        return check_launches("hg_q8_tensor_matvec_noalloc");
     });
 }
 

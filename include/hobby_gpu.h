@@ -170,6 +170,18 @@ void hg_q8_tensor_free(hg_q8_tensor *t);
 uint64_t hg_q8_tensor_bytes(const hg_q8_tensor *t);
 /* Q8Tensor::matvec (quant.rs:106-136): y[out] = W x[in]. */
 int hg_q8_tensor_matvec(const hg_q8_tensor *t, const float *x, float *y);
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops and harnesses that forbid hipMalloc).  hg_q8_tensor_matvec
+ * (Q8Tensor::matvec, quant.rs:106-136) on device-resident x_dev[in] and y_dev[out], enqueued on
+ * `stream` (a hipStream_t; NULL = the null stream) with nothing allocated: the quantized
+ * activation is kept in a fixed library-held device buffer of HG_NOALLOC_SCRATCH_BYTES per GPU
+ * (held until the process ends), which bounds in to HG_NOALLOC_MAX_IN (larger tensors:
+ * HG_ERR_ARG).  Results are bit-identical to hg_q8_tensor_matvec.  Every call on one GPU uses
+ * that GPU's one buffer: calls that overlap on a GPU (other streams, other threads) race.
+ * Returns once the work is enqueued; the caller synchronizes the stream. */
+#define HG_NOALLOC_MAX_IN 32768u
+#define HG_NOALLOC_SCRATCH_BYTES ((HG_NOALLOC_MAX_IN / 128u) * 144u)
+int hg_q8_tensor_matvec_noalloc(const hg_q8_tensor *t, const float *x_dev, float *y_dev, void *stream);
 /* Q8Tensor::matmul (quant.rs:144-194): y[tn][out] = x[tn][in] W^T. */
 int hg_q8_tensor_matmul(const hg_q8_tensor *t, const float *x, float *y, uint32_t tn);
 /* The routed-expert matvec: t holds n_mat stacked matrices of rows_per_mat rows each
