@@ -85,6 +85,15 @@ SIGNATURES = {
     "hg_attention_decode": (C.c_int, [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_float, C.c_float, C.c_uint32,
                                       C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _f32p, _f32p, _f32p,
                                       C.c_uint32]),
+    "hg_batch_new": (C.c_int, [_vp, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(_vp)]),
+    "hg_batch_free": (None, [_vp]),
+    "hg_batch_set_pages": (C.c_int, [_vp, C.c_uint32, _u32p, C.c_uint32]),
+    "hg_batch_len": (C.c_uint32, [_vp, C.c_uint32]),
+    "hg_batch_load": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _f32p, _f32p]),
+    "hg_batch_read": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _f32p, _f32p]),
+    "hg_batch_forward": (C.c_int, [_vp, _vp, _u32p, C.c_uint32, _vp, _vp]),
+    "hg_batch_decode_greedy": (C.c_int, [_vp, _vp, _u32p, C.c_uint32, C.c_uint32, _u32p]),
+    "hg_batch_routing": (C.c_int, [_vp, C.c_uint32, _u32p, _f32p]),
     "hg_q8_tensor_time_matvec": (C.c_int, [_vp, _f32p, C.c_uint32, C.c_uint32, C.c_uint32, _vp, C.c_uint32, _f32p]),
     "hg_attention_time": (C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                     _f32p]),
@@ -253,6 +262,78 @@ class KvCache:
         idx = np.empty(c.n_layers * c.top_k, np.uint32)
         w = np.empty(c.n_layers * c.top_k, np.float32)
         _check(lib().hg_last_routing(self.h, idx, w))
+        return idx.reshape(c.n_layers, c.top_k), w.reshape(c.n_layers, c.top_k)
+
+
+class Batch:
+    """Batched decode of many sequences over a paged KV cache (hg_batch_*): each sequence's
+    step is Model::forward on its own cache (model.rs:152-184), bit-identical to hg_forward."""
+
+    PAGE = 16
+
+    def __init__(self, model: Model, max_seqs: int, max_ctx: int = 0, n_pages: int = 0):
+        self.model = model
+        c = model.cfg
+        self.max_ctx = max_ctx or c.context_length
+        self.n_pages = n_pages or max_seqs * -(-self.max_ctx // self.PAGE)
+        h = _vp()
+        _check(lib().hg_batch_new(model.h, max_seqs, max_ctx, self.n_pages, C.byref(h)))
+        self.h = h
+        self.max_seqs = max_seqs
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().hg_batch_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_pages(self, seq: int, pages):
+        p = np.ascontiguousarray(pages, np.uint32)
+        _check(lib().hg_batch_set_pages(self.h, seq, p, p.size))
+
+    def len(self, seq: int) -> int:
+        return int(lib().hg_batch_len(self.h, seq))
+
+    def load(self, seq: int, k: np.ndarray, v: np.ndarray):
+        """Sequence seq's KvCache.k / .v / .len = (k, v, k.shape[1]); k, v [n_layers][len][kv_dim]."""
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        _check(lib().hg_batch_load(self.h, seq, k.shape[1], k.reshape(-1), v.reshape(-1)))
+
+    def read(self, seq: int, layer: int):
+        c = self.model.cfg
+        kvd = c.n_kv_heads * c.head_dim
+        n = self.len(seq)
+        k = np.empty((n, kvd), np.float32)
+        v = np.empty((n, kvd), np.float32)
+        _check(lib().hg_batch_read(self.h, seq, layer, k.reshape(-1), v.reshape(-1)))
+        return k, v
+
+    def forward(self, tokens, want_logits: bool = True):
+        """One step of sequences 0..len(tokens)-1: (logits [n][vocab] or None, next tokens [n])."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        n = t.size
+        lg = np.empty((n, self.model.cfg.vocab_size), np.float32) if want_logits else None
+        nxt = np.empty(n, np.uint32)
+        _check(lib().hg_batch_forward(self.model.h, self.h, t, n, _ptr(lg), _ptr(nxt)))
+        return lg, nxt
+
+    def decode_greedy(self, first, n_steps: int) -> np.ndarray:
+        f = np.ascontiguousarray(first, np.uint32)
+        out = np.empty((max(n_steps, 1), f.size), np.uint32)
+        _check(lib().hg_batch_decode_greedy(self.model.h, self.h, f, f.size, n_steps, out.reshape(-1)))
+        return out[:n_steps]
+
+    def routing(self, seq: int):
+        c = self.model.cfg
+        idx = np.empty(c.n_layers * c.top_k, np.uint32)
+        w = np.empty(c.n_layers * c.top_k, np.float32)
+        _check(lib().hg_batch_routing(self.h, seq, idx, w))
         return idx.reshape(c.n_layers, c.top_k), w.reshape(c.n_layers, c.top_k)
 
 

@@ -40,6 +40,13 @@ struct StepParams {
     uint32_t pad[2];
 };
 
+// Per-row pointer offsets of a batched launch of a one-row kernel (blockIdx.x = row), in
+// elements: x / h rows, quantized chunk bytes, scales, top-k entries, routing records.  All
+// zero for a single row.
+struct RowStrides {
+    uint32_t x, q, d, k, rec;
+};
+
 // Matvec row order of the activation / weight dot.
 enum { ORDER_DECODE = 0, ORDER_PREFILL = 1 };
 // Matvec epilogues.

@@ -21,53 +21,15 @@
 #include "hg_common.h"
 #include "hg_gguf.h"
 #include "hg_kernels.h"
+#include "hg_model.h"
 
 using namespace hg;
 
-namespace {
-
+namespace hg {
 thread_local std::string g_err;
+}  // namespace hg
 
-int fail(int code, const std::string &msg) {
-    g_err = msg;
-    return code;
-}
-
-#define HIP_TRY(expr)                                                                              \
-    do {                                                                                           \
-        hipError_t e_ = (expr);                                                                    \
-        if (e_ != hipSuccess)                                                                      \
-            return fail(e_ == hipErrorOutOfMemory ? HG_ERR_NOMEM : HG_ERR_DEVICE,                  \
-                        std::string(#expr) + ": " + hipGetErrorString(e_));                        \
-    } while (0)
-
-// Device allocation that frees itself.
-struct DevBuf {
-    void *p = nullptr;
-    size_t n = 0;
-    DevBuf() = default;
-    DevBuf(const DevBuf &) = delete;
-    DevBuf &operator=(const DevBuf &) = delete;
-    ~DevBuf() {
-        if (p) (void)hipFree(p);
-    }
-    int alloc(size_t bytes) {
-        if (p) (void)hipFree(p);
-        p = nullptr;
-        n = bytes;
-        if (bytes == 0) return HG_OK;
-        HIP_TRY(hipMalloc(&p, bytes));
-        return HG_OK;
-    }
-    int upload(const void *src, size_t bytes) {
-        int rc = alloc(bytes);
-        if (rc) return rc;
-        if (bytes) HIP_TRY(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice));
-        return HG_OK;
-    }
-    template <class T>
-    T *as() const { return static_cast<T *>(p); }
-};
+namespace {
 
 // ---- the allocation-free matvec's scratch --------------------------------------------------
 // The quantized activation of hg_q8_tensor_matvec_noalloc (chunks + scales, as k_quant_vec
@@ -100,7 +62,10 @@ int scratch_ptr(void **out) {
     return HG_OK;
 }
 
-int check_device() {
+
+}  // namespace
+
+int hg::check_device() {
     static std::once_flag once;
     static int status = HG_OK;
     static std::string msg;
@@ -139,32 +104,7 @@ int check_device() {
     return status;
 }
 
-struct DevQ8 {
-    DevBuf qs, sc;
-    Q8Mat m{};
-    uint64_t ref_bytes = 0;
-    int upload(const PackedQ8 &p) {
-        int rc = qs.upload(p.qs.data(), p.qs.size());
-        if (!rc) rc = sc.upload(p.sc_bytes(), p.sc_size());
-        if (rc) return rc;
-        m.qs = qs.as<uint8_t>();
-        m.sc = sc.p;
-        m.N = p.N;
-        m.K = p.K;
-        m.nb = p.nb;
-        m.nc = p.nc;
-        m.sc_f32 = p.f32sc ? 1u : 0u;
-        ref_bytes = p.ref_bytes();
-        return HG_OK;
-    }
-    uint64_t dev_bytes() const { return qs.n + sc.n; }
-};
-
-struct Layer {
-    bool moe = false;
-    DevBuf attn_norm, q_norm, k_norm, ffn_norm, router, router_p, bias;
-    DevQ8 qkv, o, gate, up, down, gate_e, up_e, down_e, gate_sh, up_sh, down_sh;
-};
+namespace {
 
 // The model as parsed and packed on the host, before any device call: every format error of
 // the file surfaces here, in the reference's load order (model.rs:79-131).
@@ -182,15 +122,6 @@ struct HostModel {
 };
 
 }  // namespace
-
-struct hg_model {
-    hg_config c{};
-    std::vector<std::unique_ptr<Layer>> layers;
-    DevBuf token_embd, output_norm, rope_cos, rope_sin;
-    DevQ8 output;
-    uint64_t ref_bytes = 0, dev_bytes = 0;
-    uint32_t n_slots = 0;  // routed top-k + shared expert slot
-};
 
 struct hg_kv {
     const hg_model *m = nullptr;
@@ -215,8 +146,6 @@ struct hg_kv {
 };
 
 namespace {
-
-uint32_t slots_of(const hg_config &c) { return c.top_k + (c.n_shared > 0 ? 1 : 0); }
 
 // Attention window of a step over n = pos + 1 positions of a cache of cap positions: n rounded
 // up to 256 positions (1024 past 3072), at most cap.  The attention launches are sized for the
@@ -369,23 +298,6 @@ int upload_model(HostModel &hm, hg_model *m) {
         (rc = upload_vec(hm.rope_cos, m->rope_cos)) || (rc = upload_vec(hm.rope_sin, m->rope_sin)))
         return rc;
     return HG_OK;
-}
-
-// Every extern "C" body runs inside guard(): a C++ exception (host allocation failure, a
-// container length error) becomes an error code instead of crossing the C boundary.
-template <class F>
-int guard(F &&body) {
-    try {
-        return body();
-    } catch (const std::bad_alloc &) {
-        return fail(HG_ERR_NOMEM, "host allocation failed");
-    } catch (const std::length_error &e) {
-        return fail(HG_ERR_NOMEM, std::string("host allocation failed: ") + e.what());
-    } catch (const std::exception &e) {
-        return fail(HG_ERR_DEVICE, std::string("internal error: ") + e.what());
-    } catch (...) {
-        return fail(HG_ERR_DEVICE, "internal error");
-    }
 }
 
 }  // namespace

@@ -31,6 +31,9 @@ void launch_load_row(hipStream_t st, const float *inputs, uint32_t d, const Step
 void launch_advance(hipStream_t st, StepParams *p);
 void launch_rmsnorm_quant(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,
                           float *h, uint8_t *q, float *dq);
+// The same for `rows` rows of d floats (x, h row-major; q, dq one quantized row each).
+void launch_rmsnorm_quant_rows(hipStream_t st, bool exact, uint32_t rows, const float *x, const float *w, float eps,
+                               uint32_t d, float *h, uint8_t *q, float *dq);
 void launch_quant_vec(hipStream_t st, const float *x, uint32_t n, uint8_t *q, float *dq);
 uint32_t matvec_blocks(uint32_t N, uint32_t threads);
 // dq == nullptr: q points to an f32 activation that each workgroup quantizes in its prologue.
@@ -77,6 +80,12 @@ void launch_ffn_router(hipStream_t st, bool exact, const float *x, const float *
                        const float *Wr, const float *Wp, const float *bias, uint32_t E, uint32_t top_k,
                        int gating_sigmoid, int weights_norm, float weights_scale, uint8_t *q, float *dq,
                        uint32_t *topk_idx, float *topk_w, uint32_t *order, uint32_t *rec_idx, float *rec_w);
+// The router of `rows` rows: row r reads and writes its pointers advanced by r times rs.
+void launch_ffn_router_rows(hipStream_t st, bool exact, uint32_t rows, RowStrides rs, const float *x, const float *w,
+                            float eps, uint32_t d, const float *Wr, const float *Wp, const float *bias, uint32_t E,
+                            uint32_t top_k, int gating_sigmoid, int weights_norm, float weights_scale, uint8_t *q,
+                            float *dq, uint32_t *topk_idx, float *topk_w, uint32_t *order, uint32_t *rec_idx,
+                            float *rec_w);
 // ffn_norm + router + gate/up of every slot in one launch (E == 0: the dense FFN, slot 0);
 // false when the shapes are outside what it handles (the caller then uses the router and
 // gate/up launches).

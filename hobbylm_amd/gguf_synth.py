@@ -64,6 +64,9 @@ PRESETS: Dict[str, Shape] = {
     # the published joint12 shape (hobby-rs/README.md:9,35): d768 / 16 layers / 12q-3kv hd128 /
     # 36 x 320 top-6 + 1 shared / vocab 50304 / theta 1e6
     "joint12": Shape(768, 16, 1, 12, 3, 128, 2304, 320, 36, 6, 1, 50304, rope_theta=1e6),
+    # the 500M shape with room for the batched-decode workload's contexts (up to 16384 + the
+    # decoded steps); the same tensors as "500M" for the same seed
+    "500M_long": Shape(1024, 24, 1, 16, 4, 64, 4096, 512, 36, 6, 1, 50257, context_length=16896),
     # small shapes that keep every feature (dense layer, routed + shared experts, GQA,
     # a K that is not a multiple of 128) and run in milliseconds on the CPU oracle
     "tiny": Shape(128, 3, 1, 4, 2, 32, 256, 96, 8, 2, 1, 1000, context_length=512),

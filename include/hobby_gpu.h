@@ -144,6 +144,46 @@ int hg_generate_greedy(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uin
  * idx[L*top_k] (UINT32_MAX for dense layers) and the scaled weights w[L*top_k]. */
 int hg_last_routing(const hg_kv *kv, uint32_t *idx, float *w);
 
+/* ---- batched decode over a paged KV cache ------------------------------------------------
+ * hobby-rs serves concurrent generations by giving each its own KvCache (model.rs:60-75) and
+ * calling Model::forward for each (hobby-chat/src-tauri/src/server.rs:21-31 shares one
+ * Arc<Engine> between them); it has no batched step.  An hg_batch runs one decode step of
+ * many sequences at once: every sequence's step is Model::forward (model.rs:152-184) on its
+ * own cache, with logits, expert routing and cache rows bit-identical to its own hg_forward.
+ * The Q8 matrix products of all sequences run as int8 MFMA GEMMs that keep qrow_dot_avx2's
+ * order per sequence; the routed experts' rows run once per expert over the sequences that
+ * picked it (the grouping of ffn_prefill, model.rs:676-731, with each sequence keeping the
+ * decode path's rank-order combine, model.rs:306-323).  Cache rows live in a pool of pages of
+ * HG_PAGE positions; each sequence has a block table of page ids.  An hg_batch owns a HIP
+ * stream and must be used by one thread at a time. */
+#define HG_PAGE 16u
+typedef struct hg_batch hg_batch;
+/* A batch of up to max_seqs sequences of at most max_ctx positions (0 = context_length) over a
+ * pool of n_pages pages (a page holds HG_PAGE positions of one sequence, every layer). */
+int hg_batch_new(const hg_model *m, uint32_t max_seqs, uint32_t max_ctx, uint32_t n_pages, hg_batch **out);
+void hg_batch_free(hg_batch *b);
+/* Sequence seq's block table: pages[i] holds its positions HG_PAGE i .. HG_PAGE i + HG_PAGE - 1.
+ * The sequence's length becomes 0 (an empty KvCache::new, model.rs:67-74). */
+int hg_batch_set_pages(hg_batch *b, uint32_t seq, const uint32_t *pages, uint32_t n);
+/* KvCache.len of sequence seq. */
+uint32_t hg_batch_len(const hg_batch *b, uint32_t seq);
+/* Sequence seq's KvCache.k / .v / .len = rows [0, len) of every layer from k, v
+ * ([n_layers][len][n_kv_heads*head_dim]), as hg_kv_load. */
+int hg_batch_load(hg_batch *b, uint32_t seq, uint32_t len, const float *k, const float *v);
+/* Rows [0, len) of one layer of sequence seq ([len][n_kv_heads*head_dim]), as hg_kv_read. */
+int hg_batch_read(hg_batch *b, uint32_t seq, uint32_t layer, float *k, float *v);
+/* Model::forward(tokens[s], len_s, cache_s) for sequences s = 0 .. n-1 in one step.
+ * logits (may be NULL) receives [n][vocab_size]; next (may be NULL) the greedy token of each
+ * (as hg_forward's next). */
+int hg_batch_forward(const hg_model *m, hg_batch *b, const uint32_t *tokens, uint32_t n, float *logits,
+                     uint32_t *next);
+/* n_steps batched greedy steps of sequences 0 .. n-1 without host round trips: step i forwards
+ * each sequence's previous greedy token (first[s] for i = 0); out_ids receives [n_steps][n]. */
+int hg_batch_decode_greedy(const hg_model *m, hg_batch *b, const uint32_t *first, uint32_t n, uint32_t n_steps,
+                           uint32_t *out_ids);
+/* Routing of sequence seq's last step, as hg_last_routing. */
+int hg_batch_routing(hg_batch *b, uint32_t seq, uint32_t *idx, float *w);
+
 /* ---- instrumentation (no counterpart in the reference) -------------------------------- */
 
 #define HG_PROF_CLASSES 12
