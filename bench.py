@@ -196,6 +196,111 @@ def op_attention():
                       "higher_is_better": False, "reps": 50, "data": "synthetic seeded", "rows": rows}))
 
 
+def batched_bytes(cfg, ctxs, experts_read):
+    """Algorithmic HBM bytes of one batched decode step: every sequence's K/V rows read and its
+    new row appended (49,152 B per position for the 500M shape), the matrices every step reads
+    once for the whole batch (QKV, O, dense FFN, shared experts, lm_head, routers, norms), and
+    the routed experts' matrices, each distinct (layer, expert) picked in the step read once."""
+    d, L, hd = cfg.d_model, cfg.n_layers, cfg.head_dim
+    qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    q8 = lambda n, k: n * k // 32 * 34
+    b = L * (q8(qd + 2 * kvd, d) + q8(d, qd))
+    b += cfg.n_dense * (2 * q8(cfg.dense_ffn, d) + q8(d, cfg.dense_ffn))
+    n_moe = L - cfg.n_dense
+    one_expert = 2 * q8(cfg.expert_ffn, d) + q8(d, cfg.expert_ffn)
+    b += n_moe * (1 if cfg.n_shared else 0) * one_expert + experts_read * one_expert
+    b += q8(cfg.vocab_size, d)
+    b += n_moe * (cfg.n_experts * d + cfg.n_experts) * 4 + (2 * L + 1) * d * 4 + L * 2 * hd * 4
+    kv_pos = L * 2 * kvd * 4
+    b += sum(kv_pos * (c + 1) for c in ctxs) + len(ctxs) * d * 4
+    return b
+
+
+def batched(args):
+    """Batched decode of the 500M model: 32 sequences with contexts drawn from U[256, 16384]
+    (seed 7), paged KV (16-position pages, a seeded permutation of the pool as block tables),
+    seeded cache rows written on the device; `warmup` greedy steps, then `steps` timed greedy
+    steps of all sequences (each step one token per sequence, the step loop on the device)."""
+    import hobbylm_amd as hg
+    from hobbylm_amd import gguf_synth as gs
+    rng = np.random.default_rng(7)
+    n_seq, steps, warmup = args.batch, args.steps, args.warmup
+    ctxs = [int(x) for x in rng.integers(256, 16385, n_seq)]
+    path = gs.synth_path("500M_long", 1)
+    m = hg.Model(path)
+    cfg = m.cfg
+    max_ctx = max(ctxs) + warmup + steps + 1
+    need = [-(-(c + warmup + steps + 1) // 16) for c in ctxs]
+    n_pages = sum(need)
+    b = hg.Batch(m, n_seq, max_ctx=max_ctx, n_pages=n_pages)
+    perm = rng.permutation(n_pages).astype(np.uint32)
+    if args.contiguous_pages:
+        perm = np.arange(n_pages, dtype=np.uint32)
+    at = 0
+    for s_, c in enumerate(ctxs):
+        b.set_pages(s_, perm[at:at + need[s_]])
+        at += need[s_]
+        b.fill(s_, c, 1000 + s_)
+    first = rng.integers(0, 50257, n_seq).astype(np.uint32)
+    warm = b.decode_greedy(first, warmup) if warmup else first[None, :]
+    start = [c + warmup for c in ctxs]
+    # parity sample: the caches of two sequences (the longest and the shortest) before the window
+    chk = [int(np.argmax(ctxs)), int(np.argmin(ctxs))]
+    snaps = {s_: [b.read(s_, l) for l in range(cfg.n_layers)] for s_ in chk} if not args.no_cpu else {}
+    # (hg_batch_decode_greedy returns once its stream has drained: the window is bracketed by
+    # device synchronizations)
+    t0 = time.perf_counter()
+    ids = b.decode_greedy(warm[-1], steps)
+    dt = time.perf_counter() - t0
+    tok_s = n_seq * steps / dt
+    # the distinct (layer, expert) pairs of the last step, over all sequences
+    picks = set()
+    for s_ in range(n_seq):
+        idx, _ = b.routing(s_)
+        for l in range(cfg.n_dense, cfg.n_layers):
+            picks.update((l, int(e)) for e in idx[l])
+    mean_ctx = [c + (steps - 1) / 2.0 for c in start]
+    by = batched_bytes(cfg, mean_ctx, len(picks))
+    ach = by * steps / dt
+    parity = None
+    if snaps:
+        import oracle
+        om = oracle.Model(path)
+        kvd = cfg.n_kv_heads * cfg.head_dim
+        n_chk = min(steps, args.parity_steps)
+        ok = 0
+        for s_ in chk:
+            okv = om.new_cache()
+            K = np.stack([kv[0] for kv in snaps[s_]])
+            V = np.stack([kv[1] for kv in snaps[s_]])
+            okv.load(K, V)
+            del K, V
+            tok = int(warm[-1][s_])
+            for i in range(n_chk):
+                lg = om.forward(tok, start[s_] + i, okv)
+                tok = int(np.argmax(lg[:50257]))
+                ok += tok == int(ids[i][s_])
+        parity = {"sequences": [{"seq": s_, "context": start[s_]} for s_ in chk], "steps_each": n_chk,
+                  "greedy_tokens_identical": f"{ok}/{len(chk) * n_chk}",
+                  "oracle": "C restatement of hobby-rs's decode path, one Model::forward per sequence"}
+    out = {
+        "metric": "batched decode tok/s (500M Q8_0, 32 ragged sequences, paged KV) + achieved HBM GB/s vs peak",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(dt * 1e3 / steps, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8 MFMA (i32 block sums) -> f32, f32 attention",
+        "data": "synthetic: random-init 500M-shaped Q8_0 GGUF (seed 1, context_length 16896), seeded cache rows",
+        "config": {"workload": f"{n_seq} sequences, contexts U[256,16384] (seed 7, sum {sum(ctxs)}), "
+                               f"pages of 16 positions ({'in pool order' if args.contiguous_pages else 'shuffled'}), "
+                               f"greedy decode of {steps} steps after {warmup}",
+                   "model": "hobbylm-500M-synthetic", "global_batch": n_seq, "parallelism": "none (1 GPU)"},
+        "step_bandwidth": {"algorithmic_bytes_per_step": by, "achieved_GBps": round(ach / 1e9, 1),
+                           "peak_GBps": PEAK_HBM / 1e9, "frac": round(ach / PEAK_HBM, 4),
+                           "experts_read": len(picks)},
+        "parity": parity,
+    }
+    print(json.dumps(out))
+
+
 COPY_BYTES = 256 * 2**20
 
 
@@ -277,6 +382,12 @@ def main():
     ap.add_argument("--repeats", type=int, default=3, help="timed windows; the median is reported")
     ap.add_argument("--window-stats", metavar="ROCPROF_DIR")
     ap.add_argument("--op", choices=["matvec", "attention"], help="operator-level measurement instead")
+    ap.add_argument("--batched", action="store_true",
+                    help="the batched workload: 32 ragged sequences over a paged cache (its own JSON line)")
+    ap.add_argument("--batch", type=int, default=32, help="sequences of --batched")
+    ap.add_argument("--parity-steps", type=int, default=3, help="oracle-checked steps per sequence (--batched)")
+    ap.add_argument("--contiguous-pages", action="store_true",
+                    help="--batched: each sequence's pages in pool order instead of a seeded shuffle")
     ap.add_argument("--pmc-calib", action="store_true",
                     help="a copy of known size, then a short decode window (for rocprofv3 --pmc runs)")
     ap.add_argument("--pmc-stats", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -296,6 +407,11 @@ def main():
         return
     if args.pmc_calib:
         pmc_calib()
+        return
+    if args.batched:
+        if args.gpus != 1:
+            sys.exit("bench.py measures one GPU")
+        batched(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this decode path does not shard (--gpus {args.gpus} requested)",

@@ -91,6 +91,7 @@ SIGNATURES = {
     "hg_batch_len": (C.c_uint32, [_vp, C.c_uint32]),
     "hg_batch_load": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _f32p, _f32p]),
     "hg_batch_read": (C.c_int, [_vp, C.c_uint32, C.c_uint32, _f32p, _f32p]),
+    "hg_batch_fill": (C.c_int, [_vp, C.c_uint32, C.c_uint32, C.c_uint64]),
     "hg_batch_forward": (C.c_int, [_vp, _vp, _u32p, C.c_uint32, _vp, _vp]),
     "hg_batch_decode_greedy": (C.c_int, [_vp, _vp, _u32p, C.c_uint32, C.c_uint32, _u32p]),
     "hg_batch_routing": (C.c_int, [_vp, C.c_uint32, _u32p, _f32p]),
@@ -304,6 +305,10 @@ class Batch:
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
         _check(lib().hg_batch_load(self.h, seq, k.shape[1], k.reshape(-1), v.reshape(-1)))
+
+    def fill(self, seq: int, length: int, seed: int):
+        """Seeded pseudo-random cache rows [0, length) on the device (timing workloads)."""
+        _check(lib().hg_batch_fill(self.h, seq, length, seed))
 
     def read(self, seq: int, layer: int):
         c = self.model.cfg

@@ -9,18 +9,26 @@ namespace hg {
 constexpr uint32_t PAGE = 16;                   // positions per KV page
 constexpr uint32_t ACH = 256;                   // positions per attention score chunk
 constexpr uint32_t MAX_GROUPS = 256;            // experts + the shared expert
-constexpr size_t BPV_LDS_BUDGET = 150 * 1024;   // softmax + P.V: e_t and the product ring
+constexpr size_t BSM_LDS_MAX = 150 * 1024;      // softmax: e_t of the longest context
 
-// The KV pages of one layer: [page][kv head][PAGE][hd] floats for K and for V, and the block
-// tables [sequence][bt_stride] (position t of sequence s is in page bt[s][t / PAGE]).
+// The KV pages of one layer: per page and kv head a tile of PAGE * hd floats for K and one for
+// V, and the block tables [sequence][bt_stride] (position t of sequence s is in page
+// bt[s][t / PAGE]).  Tiles are laid out for 16-byte loads whose lanes cover contiguous memory:
+// K [element quad][slot][4 elements] (lane = position: a row in hd/4 loads, a page's 16 lanes
+// reading 256 contiguous bytes), V [slot quad][element][4 slots] (lane = element: 16
+// positions in 4 loads, 64 lanes reading 1 KiB contiguous).
 struct PagedKV {
     float *k, *v;
     const uint32_t *bt;
     uint32_t bt_stride, n_heads, n_kv;
 };
 
-__host__ __device__ inline size_t kv_row_off(uint32_t page, uint32_t g, uint32_t slot, uint32_t n_kv, uint32_t hd) {
-    return (((size_t)page * n_kv + g) * PAGE + slot) * hd;
+__host__ __device__ inline size_t kv_tile(uint32_t page, uint32_t g, uint32_t n_kv, uint32_t hd) {
+    return ((size_t)page * n_kv + g) * PAGE * hd;
+}
+__host__ __device__ inline uint32_t k_el(uint32_t e, uint32_t slot) { return ((e / 4) * PAGE + slot) * 4 + e % 4; }
+__host__ __device__ inline uint32_t v_el(uint32_t e, uint32_t slot, uint32_t hd) {
+    return ((slot / 4) * hd + e) * 4 + slot % 4;
 }
 
 // One column tile of a batched GEMM: entries entry0 .. entry0 + count - 1 of the entry tables
@@ -56,13 +64,18 @@ bool launch_b_gemm(hipStream_t st, int mode, uint32_t tt, const GemmArgs &a, uin
 bool launch_b_qk_rope_append(hipStream_t st, uint32_t hd, float *qkv, uint32_t qkv_stride, const float *qn,
                              const float *kn, float eps, const float *cs, const float *sn, const uint32_t *pos,
                              const PagedKV &kv, uint32_t n);
-// Scores and softmax + P.V of n sequences over their pages; o [n][n_heads * hd].  false if
+// Scores, softmax and P.V of n sequences over their pages; o [n][n_heads * hd].  false if
 // the head size or the context bound is not supported.
 bool launch_b_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t qkv_stride, const uint32_t *pos,
-                        const PagedKV &kv, uint32_t n, uint32_t max_ctx, float *scores, float *pmax, float *o,
-                        uint32_t *err);
-// LDS product-ring slots of the softmax + P.V kernel for contexts up to max_ctx (>= 2 needed).
-uint32_t bpv_slots(uint32_t max_ctx, uint32_t hd);
+                        const uint32_t *order, const PagedKV &kv, uint32_t n, uint32_t max_ctx, float *scores,
+                        float *pmax, float *o);
+// order[r] = the sequence of rank r by length, longest first.
+void launch_b_order(hipStream_t st, const uint32_t *pos, uint32_t n, uint32_t *order);
+// Floats per row of attention scores (one row per (sequence, query head)): max_ctx rounded up
+// to 64, so that rows are 16-byte aligned and 16-byte loads near the end stay in the row.
+inline uint32_t b_sc_stride(uint32_t max_ctx) { return (max_ctx + 63) / 64 * 64; }
+// Whether the attention kernels hold contexts of max_ctx positions (LDS).
+bool batch_ctx_ok(uint32_t max_ctx);
 // Group the (sequence, rank) picks of n sequences by expert into entry tables and column
 // tiles of at most tt entries (the shared expert last, slot top_k of every sequence).
 void launch_b_group(hipStream_t st, const uint32_t *topk_idx, uint32_t n, uint32_t top_k, uint32_t E,
@@ -70,6 +83,8 @@ void launch_b_group(hipStream_t st, const uint32_t *topk_idx, uint32_t n, uint32
                     uint32_t *n_tiles);
 void launch_b_page_copy(hipStream_t st, float *flat, float *pool, const uint32_t *bt, uint32_t npg,
                         uint32_t page_floats, int dir);
+void launch_b_page_fill(hipStream_t st, float *kpool, float *vpool, const uint32_t *bt, uint32_t len, uint32_t n_layers,
+                        uint32_t n_kv, uint32_t hd, size_t layer_floats, uint64_t seed);
 void launch_b_combine(hipStream_t st, const float *y, const float *topk_w, uint32_t top_k, uint32_t n_slots,
                       uint32_t d, uint32_t n, float *x);
 void launch_b_argmax(hipStream_t st, const float *logits, uint32_t V, uint32_t valid, uint32_t *pos, uint32_t *tokens,

@@ -12,6 +12,7 @@
 // sequence's arithmetic is that of its own single-sequence step (model.rs:152-327), so logits,
 // routing and cache rows equal separate hg_forward calls bit for bit.  The step reads tokens
 // and positions from device memory and is captured once per batch size as a HIP graph.
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -38,7 +39,7 @@ struct hg_batch {
     std::vector<uint32_t> lens, bt_host;   // per sequence: length, block table [max_seqs][bt_stride]
     std::vector<uint32_t> n_bt;            // pages assigned per sequence
     DevBuf kpool, vpool;                   // [L][n_pages][n_kv][PAGE][hd]
-    DevBuf bt, pos, tokens, step, err;
+    DevBuf bt, pos, tokens, step, seq_order;
     DevBuf x, xq, xd, qkv, scores, pmax, o, oq, od;
     DevBuf topk_idx, topk_w, order, rec_idx, rec_w;
     DevBuf ent_act, ent_out, etiles, n_etiles;
@@ -104,6 +105,7 @@ void enqueue_step(hg_batch *b) {
     float *xd = b->xd.as<float>();
     uint32_t *pos = b->pos.as<uint32_t>();
     launch_b_embed(st, m->token_embd.as<float>(), d, b->tokens.as<uint32_t>(), n, x);
+    launch_b_order(st, pos, n, b->seq_order.as<uint32_t>());
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const Layer &L = *m->layers[l];
         const PagedKV kv = layer_kv(b, l);
@@ -114,8 +116,8 @@ void enqueue_step(hg_batch *b) {
         if (!launch_b_qk_rope_append(st, hd, b->qkv.as<float>(), qw, L.q_norm.as<float>(), L.k_norm.as<float>(),
                                      c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), pos, kv, n))
             note_launch_error(hipErrorInvalidConfiguration, "QK-norm / RoPE");
-        if (!launch_b_attention(st, hd, b->qkv.as<float>(), qw, pos, kv, n, b->max_ctx, b->scores.as<float>(),
-                                b->pmax.as<float>(), b->o.as<float>(), b->err.as<uint32_t>()))
+        if (!launch_b_attention(st, hd, b->qkv.as<float>(), qw, pos, b->seq_order.as<uint32_t>(), kv, n, b->max_ctx,
+                                b->scores.as<float>(), b->pmax.as<float>(), b->o.as<float>()))
             note_launch_error(hipErrorInvalidConfiguration, "paged attention");
         launch_b_quant_rows(st, b->o.as<float>(), qd, qd, n, b->oq.as<uint8_t>(), ncq * CHUNK_BYTES, b->od.as<float>(),
                             ncq * 4);
@@ -197,12 +199,22 @@ void enqueue_step(hg_batch *b) {
     launch_b_step_advance(st, b->step.as<uint32_t>());
 }
 
-// Replay the step for batch size n (capturing it on first use).
+// Replay the step for batch size n (capturing it on first use), or with HG_GRAPH=0 launch it
+// eagerly (for tracers that do not follow graph launches).
 int run_step(hg_batch *b, uint32_t n) {
     b->cur_n = n;
-    hipGraphExec_t &exec = b->graphs[n];
     std::string msg;
     (void)take_launch_error(msg);
+    static const bool eager = [] {
+        const char *ge = getenv("HG_GRAPH");
+        return ge && ge[0] == '0';
+    }();
+    if (eager) {
+        enqueue_step(b);
+        if (take_launch_error(msg) != hipSuccess) return fail(HG_ERR_DEVICE, "batched step: " + msg);
+        return HG_OK;
+    }
+    hipGraphExec_t &exec = b->graphs[n];
     if (!exec) {
         hipGraph_t graph = nullptr;
         HIP_TRY(hipStreamBeginCapture(b->st, hipStreamCaptureModeThreadLocal));
@@ -250,17 +262,6 @@ int upload_state(hg_batch *b, const uint32_t *tokens, uint32_t n) {
     return HG_OK;
 }
 
-int check_err(hg_batch *b) {
-    uint32_t e = 0;
-    HIP_TRY(hipMemcpyAsync(&e, b->err.p, 4, hipMemcpyDeviceToHost, b->st));
-    HIP_TRY(hipStreamSynchronize(b->st));
-    if (e) {
-        (void)hipMemsetAsync(b->err.p, 0, 4, b->st);
-        return fail(HG_ERR_DEVICE, "a batched attention wait exceeded its bound (flag protocol error)");
-    }
-    return HG_OK;
-}
-
 }  // namespace
 
 extern "C" {
@@ -274,7 +275,7 @@ int hg_batch_new(const hg_model *m, uint32_t max_seqs, uint32_t max_ctx, uint32_
         if (max_ctx == 0 || max_ctx > c.context_length) max_ctx = c.context_length;
         if (c.head_dim != 64 && c.head_dim != 128) return fail(HG_ERR_UNSUPPORTED, "batched decode: head_dim 64 or 128");
         if (c.n_experts + 1 > MAX_GROUPS) return fail(HG_ERR_UNSUPPORTED, "batched decode: too many experts");
-        if (bpv_slots(max_ctx, c.head_dim) < 2)
+        if (!batch_ctx_ok(max_ctx))
             return fail(HG_ERR_UNSUPPORTED, "batched decode: max_ctx " + std::to_string(max_ctx) + " too long");
         if (n_pages == 0) return fail(HG_ERR_ARG, "the page pool is empty");
         int rc = check_device();
@@ -301,10 +302,11 @@ int hg_batch_new(const hg_model *m, uint32_t max_seqs, uint32_t max_ctx, uint32_
         const uint32_t nch = div_up(max_ctx, ACH);
         if ((rc = b->kpool.alloc(pool)) || (rc = b->vpool.alloc(pool)) ||
             (rc = b->bt.alloc((size_t)S * b->bt_stride * 4)) || (rc = b->pos.alloc((size_t)S * 4)) ||
-            (rc = b->tokens.alloc((size_t)S * 4)) || (rc = b->step.alloc(4)) || (rc = b->err.alloc(4)) ||
+            (rc = b->tokens.alloc((size_t)S * 4)) || (rc = b->step.alloc(4)) ||
+            (rc = b->seq_order.alloc((size_t)S * 4)) ||
             (rc = b->x.alloc((size_t)S * d * 4)) || (rc = b->xq.alloc((size_t)S * ncd * CHUNK_BYTES)) ||
             (rc = b->xd.alloc((size_t)S * ncd * 16)) || (rc = b->qkv.alloc((size_t)S * (qd + 2 * kvd) * 4)) ||
-            (rc = b->scores.alloc((size_t)S * c.n_heads * max_ctx * 4)) ||
+            (rc = b->scores.alloc((size_t)S * c.n_heads * b_sc_stride(max_ctx) * 4)) ||
             (rc = b->pmax.alloc((size_t)S * c.n_heads * nch * 4)) || (rc = b->o.alloc((size_t)S * qd * 4)) ||
             (rc = b->oq.alloc((size_t)S * ncq * CHUNK_BYTES)) || (rc = b->od.alloc((size_t)S * ncq * 16)) ||
             (rc = b->topk_idx.alloc((size_t)S * std::max(c.top_k, 1u) * 4)) ||
@@ -322,7 +324,6 @@ int hg_batch_new(const hg_model *m, uint32_t max_seqs, uint32_t max_ctx, uint32_
         HIP_TRY(hipMemset(b->kpool.p, 0, b->kpool.n));
         HIP_TRY(hipMemset(b->vpool.p, 0, b->vpool.n));
         HIP_TRY(hipMemset(b->bt.p, 0, b->bt.n));
-        HIP_TRY(hipMemset(b->err.p, 0, 4));
         HIP_TRY(hipMemset(b->rec_idx.p, 0xff, b->rec_idx.n));
         HIP_TRY(hipMemset(b->rec_w.p, 0, b->rec_w.n));
         // identity entries and the plain column tiles of every batch size
@@ -396,9 +397,11 @@ static int batch_rows(hg_batch *b, uint32_t seq, uint32_t len, float *k, float *
             float *pool = (which ? b->vpool : b->kpool).as<float>() + per * l;
             if (write) {
                 for (uint32_t t = 0; t < len; ++t)
-                    for (uint32_t g = 0; g < nkv; ++g)
-                        memcpy(&host[(size_t)(t / PAGE) * pf + ((size_t)g * PAGE + t % PAGE) * hd],
-                               src + (size_t)t * kvd + g * hd, hd * 4);
+                    for (uint32_t g = 0; g < nkv; ++g) {
+                        const float *row = src + (size_t)t * kvd + g * hd;
+                        float *tile = &host[(size_t)(t / PAGE) * pf + kv_tile(0, g, nkv, hd)];
+                        for (uint32_t e = 0; e < hd; ++e) tile[which ? v_el(e, t % PAGE, hd) : k_el(e, t % PAGE)] = row[e];
+                    }
                 HIP_TRY(hipMemcpyAsync(b->flat.p, host.data(), host.size() * 4, hipMemcpyHostToDevice, b->st));
                 launch_b_page_copy(b->st, b->flat.as<float>(), pool, bt, npg, pf, 0);
                 HIP_TRY(hipStreamSynchronize(b->st));
@@ -407,9 +410,11 @@ static int batch_rows(hg_batch *b, uint32_t seq, uint32_t len, float *k, float *
                 HIP_TRY(hipMemcpyAsync(host.data(), b->flat.p, host.size() * 4, hipMemcpyDeviceToHost, b->st));
                 HIP_TRY(hipStreamSynchronize(b->st));
                 for (uint32_t t = 0; t < len; ++t)
-                    for (uint32_t g = 0; g < nkv; ++g)
-                        memcpy(src + (size_t)t * kvd + g * hd,
-                               &host[(size_t)(t / PAGE) * pf + ((size_t)g * PAGE + t % PAGE) * hd], hd * 4);
+                    for (uint32_t g = 0; g < nkv; ++g) {
+                        float *row = src + (size_t)t * kvd + g * hd;
+                        const float *tile = &host[(size_t)(t / PAGE) * pf + kv_tile(0, g, nkv, hd)];
+                        for (uint32_t e = 0; e < hd; ++e) row[e] = tile[which ? v_el(e, t % PAGE, hd) : k_el(e, t % PAGE)];
+                    }
             }
         }
     std::string msg;
@@ -426,6 +431,25 @@ int hg_batch_load(hg_batch *b, uint32_t seq, uint32_t len, const float *k, const
         HIP_TRY(hipStreamSynchronize(b->st));
         int rc = batch_rows(b, seq, len, const_cast<float *>(k), const_cast<float *>(v), true, -1);
         if (rc) return rc;
+        b->lens[seq] = len;
+        return HG_OK;
+    });
+}
+
+int hg_batch_fill(hg_batch *b, uint32_t seq, uint32_t len, uint64_t seed) {
+    return guard([&]() -> int {
+        if (!b) return fail(HG_ERR_ARG, "NULL argument");
+        if (seq >= b->max_seqs) return fail(HG_ERR_ARG, "sequence index out of range");
+        if (len > b->max_ctx || len > b->n_bt[seq] * PAGE)
+            return fail(HG_ERR_ARG, "len " + std::to_string(len) + " beyond the sequence's pages");
+        const hg_config &c = b->m->c;
+        const size_t layer_floats = (size_t)b->n_pages * c.n_kv_heads * PAGE * c.head_dim;
+        std::string msg;
+        (void)take_launch_error(msg);
+        launch_b_page_fill(b->st, b->kpool.as<float>(), b->vpool.as<float>(), b->bt.as<uint32_t>() + (size_t)seq * b->bt_stride,
+                           len, c.n_layers, c.n_kv_heads, c.head_dim, layer_floats, seed);
+        if (take_launch_error(msg) != hipSuccess) return fail(HG_ERR_DEVICE, msg);
+        HIP_TRY(hipStreamSynchronize(b->st));
         b->lens[seq] = len;
         return HG_OK;
     });
@@ -453,7 +477,7 @@ int hg_batch_forward(const hg_model *m, hg_batch *b, const uint32_t *tokens, uin
             HIP_TRY(hipMemcpyAsync(logits, b->logits.p, (size_t)n * m->c.vocab_size * 4, hipMemcpyDeviceToHost, b->st));
         std::vector<uint32_t> ids(n);
         HIP_TRY(hipMemcpyAsync(ids.data(), b->out_ids.p, (size_t)n * 4, hipMemcpyDeviceToHost, b->st));
-        if ((rc = check_err(b))) return rc;
+        HIP_TRY(hipStreamSynchronize(b->st));
         if (next) memcpy(next, ids.data(), (size_t)n * 4);
         for (uint32_t s = 0; s < n; ++s) b->lens[s] += 1;
         return HG_OK;
@@ -474,7 +498,7 @@ int hg_batch_decode_greedy(const hg_model *m, hg_batch *b, const uint32_t *first
         for (uint32_t i = 0; i < n_steps; ++i)
             if ((rc = run_step(b, n))) return rc;
         HIP_TRY(hipMemcpyAsync(out_ids, b->out_ids.p, (size_t)n_steps * n * 4, hipMemcpyDeviceToHost, b->st));
-        if ((rc = check_err(b))) return rc;
+        HIP_TRY(hipStreamSynchronize(b->st));
         for (uint32_t s = 0; s < n; ++s) b->lens[s] += n_steps;
         return HG_OK;
     });

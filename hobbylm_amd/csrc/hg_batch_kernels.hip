@@ -17,8 +17,9 @@
 // so a lane's A operand for the 4 blocks of a chunk is the chunk's contiguous 64 bytes at 64 h
 // (4 x 16 bytes, word t of each piece = block t).
 //
-// KV rows live in pages of PAGE positions (a pool per layer, [page][kv head][PAGE][hd]); each
-// sequence's block table maps position t to page bt[t / PAGE].
+// KV rows live in pages of PAGE positions (a pool per layer; per page and kv head a K tile and a
+// V tile laid out for 16-byte loads, see PagedKV); each sequence's block table maps position t
+// to page bt[t / PAGE].
 #include <hip/hip_ext.h>
 
 #include "hg_batch.h"
@@ -34,10 +35,6 @@ __device__ inline v16i mfma_i8(v4i a, v4i b) {
     const v16i z = {};
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 }
-
-// A bounded wait: the flag protocol of a kernel guarantees progress, and the cap turns a
-// protocol slip into an error report (*err = 1 and the wait ends) instead of a hang.
-constexpr uint32_t SPIN_CAP = 1u << 22;
 
 // ------------------------------------------------------------------ embedding
 // x[s] = token_embd[tokens[s]] (model.rs:152-154).  grid (d / 256, n).
@@ -229,8 +226,8 @@ __global__ __launch_bounds__(64) void k_b_qk_rope_append(float *qkv, uint32_t qk
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const uint32_t page = kv.bt[(size_t)s * kv.bt_stride + p / PAGE];
     if (hh >= n_heads + n_kv) {
-        float *vr = kv.v + kv_row_off(page, hh - n_heads - n_kv, p % PAGE, n_kv, HD);
-        for (uint32_t i = lane; i < HD; i += 64) vr[i] = u[i];
+        float *vr = kv.v + kv_tile(page, hh - n_heads - n_kv, n_kv, HD);
+        for (uint32_t i = lane; i < HD; i += 64) vr[v_el(i, p % PAGE, HD)] = u[i];
         return;
     }
     norm_rope_head<HD>(u, o, hc, hh < n_heads, eps, tmp, lane);
@@ -239,8 +236,8 @@ __global__ __launch_bounds__(64) void k_b_qk_rope_append(float *qkv, uint32_t qk
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     for (uint32_t i = lane; i < HD; i += 64) src[i] = o[i];
     if (hh >= n_heads) {
-        float *kr = kv.k + kv_row_off(page, hh - n_heads, p % PAGE, n_kv, HD);
-        for (uint32_t i = lane; i < HD; i += 64) kr[i] = o[i];
+        float *kr = kv.k + kv_tile(page, hh - n_heads, n_kv, HD);
+        for (uint32_t i = lane; i < HD; i += 64) kr[k_el(i, p % PAGE)] = o[i];
     }
 }
 
@@ -248,8 +245,8 @@ __global__ __launch_bounds__(64) void k_b_qk_rope_append(float *qkv, uint32_t qk
 // s_t = dot(q_h, K_t) * (1/sqrt(hd)) (model.rs:213-218, ops::dot's order) for the rep query
 // heads of kv head g (blockIdx.y) of sequence s (blockIdx.z) over positions
 // [256 c, 256 c + 256) of its context (c = blockIdx.x; chunks past the context exit), and each
-// head's chunk maximum.  Lanes as k_attn_scores: R lanes (rep rounded up to a power of two)
-// share a position, one K row fetch per position.
+// head's chunk maximum.  Lane = position: its K row is read once (hd/4 16-byte loads, k_el) and
+// dotted with every query head of the group (q broadcast from LDS).
 template <int HD>
 __global__ __launch_bounds__(256) void k_b_scores(const float *__restrict__ qkv, uint32_t qkv_stride,
                                                   const uint32_t *__restrict__ pos, PagedKV kv, float *scores,
@@ -262,117 +259,94 @@ __global__ __launch_bounds__(256) void k_b_scores(const float *__restrict__ qkv,
     const uint32_t n = pos[s] + 1, t0 = c * ACH;
     if (t0 >= n) return;   // (uniform)
     const uint32_t n_heads = kv.n_heads, rep = n_heads / kv.n_kv;
-    const uint32_t R = rep <= 1 ? 1u : rep <= 2 ? 2u : rep <= 4 ? 4u : 8u;
-    const uint32_t r = (uint32_t)tid % R, pp = 256 / R, t1 = min(n, t0 + ACH);
-    const uint32_t *bts = kv.bt + (size_t)s * kv.bt_stride;
-    auto krow = [&](uint32_t t) { return kv.k + kv_row_off(bts[t / PAGE], g, t % PAGE, kv.n_kv, HD); };
-    float kt[HD];
-    {
-        const float *kp = krow(min(t0 + (uint32_t)tid / R, n - 1));
+    const uint32_t t = t0 + 64 * (uint32_t)wave + (uint32_t)lane;
+    const bool live = t0 + 64 * (uint32_t)wave < n;   // (uniform per wave)
+    v4f kt[HD / 4];
+    if (live) {
+        const uint32_t tc = min(t, n - 1);
+        const v4f *kp = reinterpret_cast<const v4f *>(kv.k + kv_tile(kv.bt[(size_t)s * kv.bt_stride + tc / PAGE], g,
+                                                                     kv.n_kv, HD)) + tc % PAGE;
 #pragma unroll
-        for (int i = 0; i < HD; i += 4) *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kp + i);
+        for (int i = 0; i < HD / 4; ++i) kt[i] = kp[i * PAGE];
     }
     const float *qsrc = qkv + (size_t)s * qkv_stride + (size_t)g * rep * HD;
     for (uint32_t i = tid; i < rep * HD; i += 256) qs[i] = qsrc[i];
     __syncthreads();
     const float scale = 1.0f / sqrtf((float)HD);
-    float mx = -__builtin_huge_valf();
-    const float *qr = qs + min(r, rep - 1) * HD;
-    float *sc = scores + ((size_t)s * n_heads + g * rep + r) * sc_stride;
-    for (uint32_t tb = t0; tb < t1; tb += pp) {
-        const uint32_t t = tb + (uint32_t)tid / R;
-        if (tb != t0) {
-            const float *kp = krow(min(t, n - 1));
+    float *scb = scores + ((size_t)s * n_heads + g * rep) * sc_stride;
+    for (uint32_t r = 0; r < rep; ++r) {
+        float mx = -__builtin_huge_valf();
+        if (live) {
+            const float *qr = qs + r * HD;
+            float acc[4][8];   // ops::dot: four 8-lane FMA accumulators over 32-wide steps
 #pragma unroll
-            for (int i = 0; i < HD; i += 4) *reinterpret_cast<v4f *>(kt + i) = *reinterpret_cast<const v4f *>(kp + i);
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int l = 0; l < 8; ++l) acc[a][l] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < HD; i += 32)
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) {
+                        const int e = i + 8 * a + l;
+                        acc[a][l] = fmaf(qr[e], kt[e / 4][e % 4], acc[a][l]);
+                    }
+            float v[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) v[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+            const float sv = (((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]))) * scale;
+            if (t < n) {
+                scb[(size_t)r * sc_stride + t] = sv;
+                mx = sv;
+            }
         }
-        if (r < rep && t < t1) {
-            const float v = dot_wide_serial(qr, kt, HD) * scale;
-            sc[t] = v;
-            mx = fmaxf(mx, v);
-        }
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, shfl_xor(mx, o));
+        if (lane == 0) wm[wave][r] = mx;
     }
-    for (uint32_t o = R; o < 64; o <<= 1) mx = fmaxf(mx, shfl_xor(mx, (int)o));
-    if ((uint32_t)lane < R) wm[wave][lane] = mx;
     __syncthreads();
     if ((uint32_t)tid < rep)
         pmax[((size_t)s * n_heads + g * rep + tid) * pm_stride + c] =
             fmaxf(fmaxf(wm[0][tid], wm[1][tid]), fmaxf(wm[2][tid], wm[3][tid]));
 }
 
-// ------------------------------------------------------------------ paged attention: softmax + P.V
-// One workgroup per (sequence, query head) (ops.rs:112-128, model.rs:226-232):
-//   m = max of the chunk maxima; e_t = exp(s_t - m) (the reference expf) into LDS; sum = the
-//   index-order sum of e_t (block_seq_sum up to 3072 terms, else one lane); p_t = e_t (1/sum);
-//   o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ..., one chain per element di.
-// P.V: the chain wave(s) (lane = di; HD / 64 waves) add the products in position order;
-// producer waves (not on a chain wave's SIMD) read the V rows of 64-position groups from the
-// pages, form the rounded products p_t v_t[di] and store them [di][t] into a ring of LDS slots
-// (positions past the context: -0, the exact identity of the adds).  Slot hand-offs are LDS
-// flags with bounded waits.  Workgroups of one (sequence, kv head) get ids equal mod 8, so the
-// query heads sharing V rows run on one XCD's L2.
-struct PvCfgB {
-    static constexpr uint32_t G = 64;        // positions per ring slot
-    static constexpr uint32_t GP = G + 4;    // padded row of a slot
-    static constexpr uint32_t NW = 8;        // waves
-    static constexpr uint32_t RMAX = 8;
-};
+// ------------------------------------------------------------------ paged attention: softmax
+// The softmax of one (sequence, query head) row of scores (ops.rs:112-128): m = max of the
+// chunk maxima (order-free); e_t = exp(s_t - m) with the reference expf, into LDS; sum = the
+// index-order sum of e_t (block_seq_sum: 4 waves up to 3072 terms, 8 waves x 32 up to 16384,
+// else one lane); p_t = e_t * (1 / sum) written over the scores.  Workgroups are dealt longest
+// sequence first (order[] ranks the sequences by length).  512 threads.
+__host__ __device__ inline size_t bsm_lds(uint32_t max_ctx) { return ((size_t)div_up(max_ctx, 4) * 4 + 64) * 4; }
 
-uint32_t bpv_slots(uint32_t max_ctx, uint32_t hd) {
-    const size_t e_bytes = (size_t)div_up(max_ctx, 4) * 16 + 64 * 4;
-    const size_t slot = (size_t)hd * PvCfgB::GP * 4;
-    const size_t budget = BPV_LDS_BUDGET - sizeof(xsum::Scratch) - 64;
-    const size_t r = budget > e_bytes ? (budget - e_bytes) / slot : 0;
-    return (uint32_t)(r > PvCfgB::RMAX ? PvCfgB::RMAX : r);
-}
-static size_t bpv_lds(uint32_t max_ctx, uint32_t hd, uint32_t slots) {
-    return (size_t)div_up(max_ctx, 4) * 16 + 64 * 4 + (size_t)slots * hd * PvCfgB::GP * 4;
-}
-
-template <int HD>
-__global__ __launch_bounds__(512) void k_b_attn_pv(const float *__restrict__ scores, uint32_t sc_stride,
-                                                   const float *__restrict__ pmax, uint32_t pm_stride,
-                                                   const uint32_t *__restrict__ pos, PagedKV kv, uint32_t n_seq,
-                                                   uint32_t max_ctx, uint32_t R, float *o_out, uint32_t *err) {
-    using C = PvCfgB;
-    constexpr uint32_t NCW = HD / 64;   // chain waves
-    static_assert(HD % 64 == 0 && NCW <= 2, "head_dim 64 or 128");
-    extern __shared__ __align__(16) float lds[];
+__global__ __launch_bounds__(512) void k_b_softmax(float *scores, uint32_t sc_stride, const float *__restrict__ pmax,
+                                                   uint32_t pm_stride, const uint32_t *__restrict__ pos,
+                                                   const uint32_t *__restrict__ order, uint32_t n_heads) {
+    extern __shared__ __align__(16) float e[];   // [max_ctx + 64]
     __shared__ xsum::Scratch xs;
-    __shared__ uint32_t ready[C::RMAX], done[NCW];
     __shared__ float s_inv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t n_heads = kv.n_heads, n_kv = kv.n_kv, rep = n_heads / n_kv;
-    // workgroup -> (sequence, head): the rep heads of a (sequence, kv head) key get ids equal mod 8
-    uint32_t s, h;
-    {
-        const uint32_t L = blockIdx.x, nkeys = n_seq * n_kv;
-        if (nkeys % 8 == 0) {
-            const uint32_t slot = L / 8, key = L % 8 + 8 * (slot / rep), r = slot % rep;
-            s = key / n_kv;
-            h = (key % n_kv) * rep + r;
-        } else {
-            s = L / n_heads;
-            h = L % n_heads;
-        }
-    }
-    const uint32_t g = h / rep, n = pos[s] + 1, nch = div_up(n, ACH);
-    float *e = lds;                                                        // [max_ctx] e_t
-    float *ring = lds + (size_t)div_up(max_ctx, 4) * 4 + 64;               // [R][HD][GP]
-    const float *sc = scores + ((size_t)s * n_heads + h) * sc_stride;
+    const uint32_t s = order[blockIdx.x / n_heads], h = blockIdx.x % n_heads;
+    const uint32_t n = pos[s] + 1, nch = div_up(n, ACH);
+    float *sc = scores + ((size_t)s * n_heads + h) * sc_stride;
     const float *pm = pmax + ((size_t)s * n_heads + h) * pm_stride;
-    const uint32_t *bts = kv.bt + (size_t)s * kv.bt_stride;
     const WaveExpTab tab = WaveExpTab::load(lane);
     float m = -__builtin_huge_valf();
     for (uint32_t c = lane; c < nch; c += 64) m = fmaxf(m, pm[c]);
-    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));   // max is order-free
-    if (tid < (int)C::RMAX) ready[tid] = 0;
-    if (tid < (int)NCW) done[tid] = 0;
+    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
     if (tid == 0) xs.sync = 0;
-    for (uint32_t t0 = 0; t0 < n; t0 += 512) {   // (uniform: every lane calls the exp)
-        const uint32_t t = t0 + (uint32_t)tid;
-        const float ev = hg_expf_l(sc[min(t, n - 1)] - m, tab);
-        if (t < n) e[t] = ev;
+    constexpr uint32_t EB = 8;   // score loads in flight per thread
+    for (uint32_t t0 = 0; t0 < n; t0 += EB * 512) {   // (uniform: every lane calls the exp)
+        float sv[EB];
+#pragma unroll
+        for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(t0 + u * 512 + (uint32_t)tid, n - 1)];
+#pragma unroll
+        for (uint32_t u = 0; u < EB; ++u) {
+            const uint32_t t = t0 + u * 512 + (uint32_t)tid;
+            if (t0 + u * 512 < n) {
+                const float ev = hg_expf_l(sv[u] - m, tab);
+                if (t < n) e[t] = ev;
+            }
+        }
     }
     if (tid < 4) e[n + tid] = 0.0f;   // readable up to a multiple of 4 past n
     __syncthreads();
@@ -381,81 +355,224 @@ __global__ __launch_bounds__(512) void k_b_attn_pv(const float *__restrict__ sco
             const float r = n <= 2048 ? block_seq_sum<4, 8>(e, n, xs, wave, lane) : block_seq_sum<4, 12>(e, n, xs, wave, lane);
             if (tid == 0) s_inv = 1.0f / r;
         }
+    } else if (n <= 16384) {
+        const float r = block_seq_sum<8, 32>(e, n, xs, wave, lane);
+        if (tid == 0) s_inv = 1.0f / r;
     } else if (tid == 0) {
         s_inv = 1.0f / seq_sum_lds(e, n, 0.0f);
     }
     __syncthreads();
     const float inv = s_inv;
-    const uint32_t ngr = div_up(n, C::G);
-    // waves on SIMD wave % 4: the chain waves 0 .. NCW - 1 run alone on their SIMDs
-    const bool chain = (uint32_t)wave < NCW;
-    const bool idle = !chain && (uint32_t)(wave % 4) < NCW;
-    if (!chain && !idle) {
-        // producer index among the producer waves
-        uint32_t pw = 0, np = 0;
-        for (uint32_t w = 0; w < C::NW; ++w) {
-            const bool pr = w >= NCW && (w % 4) >= NCW;
-            if (pr && w < (uint32_t)wave) ++pw;
-            if (pr) ++np;
+    for (uint32_t t = tid; t < n; t += 512) sc[t] = e[t] * inv;   // p_t (x *= inv, ops.rs:124-126)
+}
+
+// ------------------------------------------------------------------ paged attention: P.V
+// o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ... (model.rs:227-232).  One wave per (kv head,
+// group of HPW query heads sharing it, slice of EW = 64 / HPW elements): lane = (head, element),
+// each lane running its chain itself (a rounded product, then the add).  Packing the heads of a
+// kv head into one wave lets the lanes of one element share each V load, so a sequence's V is
+// streamed once per kv head by hd / EW waves, each on its own CU (a wave's stream rate is
+// bounded by the loads it keeps in flight).  A lane's 16 values of a page are four 16-byte
+// loads (v_el), pages prefetched 11 ahead in a register ring of 12 (constant slot indices: the
+// body is unrolled over a 192-position block).  Each head's probabilities of a block are loaded
+// one block ahead, one per lane per 64 positions, and broadcast through the wave's LDS rows.
+// Positions past the context contribute a product of +0 (the chain never holds -0: it starts
+// at +0 and x + (-x) rounds to +0), so o + 0 = o keeps the chain exact.  One wave per
+// workgroup; the waves of one (sequence, kv head) get ids equal mod 8 (one XCD's L2), and
+// workgroups are dealt longest sequence first.
+// o = (((o + p0 v0) + p1 v1) + ...) + p7 v7 with each product rounded (no FMA): the products are
+// interleaved with the adds (mul, mul, add, mul, add, ...) so that no add waits on the one
+// before it with nothing issued in between.
+__device__ __forceinline__ float chain8(float o, v4f pa, v4f pb, v4f va, v4f vb) {
+    float t0, t1;
+    asm("v_mul_f32 %[t0], %[p0], %[v0]\n\t"
+        "v_mul_f32 %[t1], %[p1], %[v1]\n\t"
+        "v_add_f32 %[o], %[o], %[t0]\n\t"
+        "v_mul_f32 %[t0], %[p2], %[v2]\n\t"
+        "v_add_f32 %[o], %[o], %[t1]\n\t"
+        "v_mul_f32 %[t1], %[p3], %[v3]\n\t"
+        "v_add_f32 %[o], %[o], %[t0]\n\t"
+        "v_mul_f32 %[t0], %[p4], %[v4]\n\t"
+        "v_add_f32 %[o], %[o], %[t1]\n\t"
+        "v_mul_f32 %[t1], %[p5], %[v5]\n\t"
+        "v_add_f32 %[o], %[o], %[t0]\n\t"
+        "v_mul_f32 %[t0], %[p6], %[v6]\n\t"
+        "v_add_f32 %[o], %[o], %[t1]\n\t"
+        "v_mul_f32 %[t1], %[p7], %[v7]\n\t"
+        "v_add_f32 %[o], %[o], %[t0]\n\t"
+        "v_add_f32 %[o], %[o], %[t1]"
+        : [o] "+v"(o), [t0] "=&v"(t0), [t1] "=&v"(t1)
+        : [p0] "v"(pa.x), [p1] "v"(pa.y), [p2] "v"(pa.z), [p3] "v"(pa.w), [p4] "v"(pb.x), [p5] "v"(pb.y),
+          [p6] "v"(pb.z), [p7] "v"(pb.w), [v0] "v"(va.x), [v1] "v"(va.y), [v2] "v"(va.z), [v3] "v"(va.w),
+          [v4] "v"(vb.x), [v5] "v"(vb.y), [v6] "v"(vb.z), [v7] "v"(vb.w));
+    return o;
+}
+
+template <int HD, int HPW>
+__global__ __launch_bounds__(64) void k_b_pv(const float *__restrict__ probs, uint32_t sc_stride,
+                                             const uint32_t *__restrict__ pos, const uint32_t *__restrict__ order,
+                                             PagedKV kv, uint32_t n_seq, float *o_out) {
+    // EW elements per wave, WPE waves per head group, LPP 16-byte loads per lane per page
+    constexpr uint32_t EW = 64 / HPW, WPE = HD / EW, LPP = 4 / HPW;
+    // a register ring of R pages (24 loads in flight), probabilities in blocks of half a ring
+    constexpr uint32_t R = 24 / LPP, NPB = R / 2, PB = NPB * PAGE, SB = R * PAGE;
+    constexpr uint32_t PV4 = HPW * PB / 4, PU = (PV4 + 63) / 64;   // 16-byte probability loads per block, per lane
+    constexpr uint32_t PLS = PB + 4;   // LDS row of one head (padded: the heads' rows on other banks)
+    __shared__ __align__(16) float pw[HPW * PLS];
+    __shared__ __align__(16) v4f stg[2][4 * EW];   // a page slice, [quad][element]
+    extern __shared__ uint32_t btl[];             // [pages of the longest context]
+    const int lane = threadIdx.x;
+    const uint32_t n_heads = kv.n_heads, n_kv = kv.n_kv, rep = n_heads / n_kv;
+    const uint32_t wpk = div_up(rep, HPW) * WPE;   // waves per (sequence, kv head)
+    uint32_t key, w;
+    {
+        const uint32_t L = blockIdx.x, nkeys = n_seq * n_kv;
+        if (nkeys % 8 == 0) {
+            const uint32_t slot = L / 8;
+            key = L % 8 + 8 * (slot / wpk);
+            w = slot % wpk;
+        } else {
+            key = L / wpk;
+            w = L % wpk;
         }
-        // lane -> (position sub within a pass, 4 elements): HD / 4 lanes per row
-        constexpr uint32_t LPR = HD / 4, PPI = 64 / LPR;
-        const uint32_t sub = (uint32_t)lane / LPR, d4 = ((uint32_t)lane % LPR) * 4;
-        for (uint32_t k = pw; k < ngr; k += np) {
-            if (k >= R) {   // slot k % R is free once every chain wave finished group k - R
-                uint32_t it = 0;
-                for (;;) {
-                    uint32_t dmin = __hip_atomic_load(&done[0], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    if (NCW > 1) dmin = min(dmin, __hip_atomic_load(&done[NCW - 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
-                    if (dmin >= k - R + 1) break;
-                    if (++it > SPIN_CAP) { if (lane == 0) atomicOr(err, 1u); break; }
-                    __builtin_amdgcn_s_sleep(1);
-                }
-            }
-            float *slot = ring + (size_t)(k % R) * HD * C::GP;
-            v4f vr[C::G / PPI];
+    }
+    const uint32_t s = order[key / n_kv], g = key % n_kv, n = pos[s] + 1, npg = div_up(n, PAGE);
+    const uint32_t *bts = kv.bt + (size_t)s * kv.bt_stride;
+    for (uint32_t i = lane; i < npg; i += 64) btl[i] = bts[i];   // the block table
+    __syncthreads();
+    const uint32_t hb = (w / WPE) * HPW, es = (w % WPE) * EW;   // head group, element slice
+    const uint32_t hl = (uint32_t)lane / EW, el = (uint32_t)lane % EW, hr = hb + hl;   // hr >= rep: idle lanes
+    const float *prb = probs + ((size_t)s * n_heads + g * rep) * sc_stride;
+    const float *vg = kv.v + kv_tile(0, g, n_kv, HD);   // (uniform) + page * pstride
+    const size_t pstride = (size_t)n_kv * HD * PAGE;
+    v4f vr[R][LPP];
+    // the slice of a page: load u of lane l is entry c = 64 u + l of [quad][element] (64
+    // lanes: contiguous runs of EW * 16 bytes)
+    auto load_page = [&](v4f (&d)[LPP], uint32_t page) {
+        const v4f *src = reinterpret_cast<const v4f *>(vg + (size_t)page * pstride);
 #pragma unroll
-            for (uint32_t i = 0; i < C::G / PPI; ++i) {
-                const uint32_t t = min(k * C::G + i * PPI + sub, n - 1);
-                vr[i] = *reinterpret_cast<const v4f *>(kv.v + kv_row_off(bts[t / PAGE], g, t % PAGE, n_kv, HD) + d4);
-            }
-#pragma unroll
-            for (uint32_t i = 0; i < C::G / PPI; ++i) {
-                const uint32_t tt = i * PPI + sub, t = k * C::G + tt;
-                const bool in = t < n;
-                const float pt = in ? e[t] * inv : 0.0f;
-                slot[(d4 + 0) * C::GP + tt] = in ? pt * vr[i].x : -0.0f;
-                slot[(d4 + 1) * C::GP + tt] = in ? pt * vr[i].y : -0.0f;
-                slot[(d4 + 2) * C::GP + tt] = in ? pt * vr[i].z : -0.0f;
-                slot[(d4 + 3) * C::GP + tt] = in ? pt * vr[i].w : -0.0f;
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane == 0) __hip_atomic_store(&ready[k % R], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        for (uint32_t u = 0; u < LPP; ++u) {
+            const uint32_t c = 64 * u + (uint32_t)lane;
+            d[u] = src[(c / EW) * HD + es + c % EW];
         }
-    } else if (chain) {
-        const uint32_t di = (uint32_t)wave * 64 + (uint32_t)lane;
-        float o = 0.0f;
-        for (uint32_t k = 0; k < ngr; ++k) {
-            uint32_t it = 0;
-            while (__hip_atomic_load(&ready[k % R], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != k + 1) {
-                if (++it > SPIN_CAP) { if (lane == 0) atomicOr(err, 1u); break; }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            const v4f *row = reinterpret_cast<const v4f *>(ring + (size_t)(k % R) * HD * C::GP + (size_t)di * C::GP);
-            v4f a[C::G / 4];
+    };
+    auto stage = [&](const v4f (&d)[LPP], uint32_t buf) {
 #pragma unroll
-            for (uint32_t u = 0; u < C::G / 4; ++u) a[u] = row[u];
+        for (uint32_t u = 0; u < LPP; ++u) stg[buf][64 * u + lane] = d[u];
+    };
+    auto id_of = [&](uint32_t p) { return btl[min(p, npg - 1)]; };   // (clamped to the sequence's pages)
+    // probabilities of block B: entry c = 64 u + lane is head c / (PB / 4), positions
+    // B PB + 4 (c % (PB / 4)) .. + 3 (clamped into the row; past the context they are masked)
+    v4f pn[2][PU];
+    auto load_probs = [&](v4f (&d)[PU], uint32_t B) {
 #pragma unroll
-            for (uint32_t u = 0; u < C::G / 4; ++u) {
-                o = o + a[u].x;
-                o = o + a[u].y;
-                o = o + a[u].z;
-                o = o + a[u].w;
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane == 0) __hip_atomic_store(&done[wave], k + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        for (uint32_t u = 0; u < PU; ++u) {
+            const uint32_t c = PV4 % 64 == 0 ? 64 * u + (uint32_t)lane : min(64 * u + (uint32_t)lane, PV4 - 1);
+            const uint32_t r = c / (PB / 4), i = c % (PB / 4);
+            d[u] = *reinterpret_cast<const v4f *>(prb + (size_t)min(hb + r, rep - 1) * sc_stride +
+                                                  min(B * PB + 4 * i, sc_stride - 4));
         }
-        o_out[((size_t)s * n_heads + h) * HD + di] = o;
+    };
+    auto stage_probs = [&](const v4f (&d)[PU]) {
+#pragma unroll
+        for (uint32_t u = 0; u < PU; ++u) {
+            const uint32_t c = 64 * u + (uint32_t)lane;
+            if (PV4 % 64 == 0 || c < PV4)   // (all lanes when the block fills them)
+                *reinterpret_cast<v4f *>(pw + (c / (PB / 4)) * PLS + 4 * (c % (PB / 4))) = d[u];
+        }
+    };
+    // a page's operands in registers: probabilities of the lane's head, values of its element
+    struct Ops {
+        v4f p[4], v[4];
+    };
+    auto read_ops = [&](Ops &d, uint32_t k) {   // page k (its slice staged in stg[k & 1])
+        const v4f *pj = reinterpret_cast<const v4f *>(pw + hl * PLS + 16 * (k % NPB));
+        const v4f *vj = stg[k & 1] + el;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            d.p[q] = pj[q];
+            d.v[q] = vj[q * EW];
+        }
+    };
+    // Pipeline over pages k (ring slot k % R holds page k, loaded R pages ahead).  Step k:
+    // stage page k + 2 into stg[k & 1] and reload its slot with page k + 2 + R; stage the
+    // probabilities if page k + 1 starts a block; read page k + 1's operands from LDS; run the
+    // chain over page k (operands read in the step before).  No fences: the LDS executes one
+    // wave's operations in order, so each write lands after the reads of the data it replaces
+    // and each read sees the writes before it (the compiler keeps the order of accesses to the
+    // same buffer).  Page ids of the pages a
+    // superblock (R pages) loads come from the LDS table one superblock ahead (lane j: page
+    // (sb + 1) R + j + 2).  The probabilities of block B are loaded two blocks ahead into
+    // pn[B & 1] (loads retire in order: the wait for them leaves the newer page loads in flight).
+    const uint32_t ids0 = id_of(min((uint32_t)lane, R + 1));   // pages 0 .. R + 1
+    load_probs(pn[0], 0);
+    load_probs(pn[1], 1);
+    uint32_t ids_nx = id_of(R + 2 + (uint32_t)lane);
+#pragma unroll
+    for (uint32_t j = 0; j < R; ++j) load_page(vr[j], __builtin_amdgcn_readlane(ids0, j));
+    stage_probs(pn[0]);
+    load_probs(pn[0], 2);
+    stage(vr[0], 0);
+    load_page(vr[0], __builtin_amdgcn_readlane(ids0, R));
+    stage(vr[1], 1);
+    load_page(vr[1], __builtin_amdgcn_readlane(ids0, R + 1));
+    Ops ops[2];
+    read_ops(ops[0], 0);
+    float o = 0.0f;
+    const uint32_t nfull = n / SB, nsb = div_up(n, SB);
+    auto step = [&](uint32_t sb, uint32_t j, uint32_t ids, auto full_tag) {
+        constexpr bool full = decltype(full_tag)::value;
+        stage(vr[(j + 2) % R], j & 1);
+        if constexpr (full) load_page(vr[(j + 2) % R], __builtin_amdgcn_readlane(ids, j));
+        if ((j + 1) % NPB == 0) {
+            const uint32_t nb = (j + 1) / NPB;   // block 2 sb + nb starts at page j + 1
+            stage_probs(pn[nb & 1]);
+            if constexpr (full) load_probs(pn[nb & 1], 2 * sb + nb + 2);
+        }
+        read_ops(ops[(j + 1) & 1], j + 1);
+        const Ops &c = ops[j & 1];
+        if constexpr (full) {
+            o = chain8(o, c.p[0], c.p[1], c.v[0], c.v[1]);
+            o = chain8(o, c.p[2], c.p[3], c.v[2], c.v[3]);
+        } else {   // positions t = sb SB + 16 j + 4 q + u < n only
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+                const uint32_t t = sb * SB + 16 * j + 4 * q;
+                o = o + (t < n ? c.p[q].x * c.v[q].x : 0.0f);
+                o = o + (t + 1 < n ? c.p[q].y * c.v[q].y : 0.0f);
+                o = o + (t + 2 < n ? c.p[q].z * c.v[q].z : 0.0f);
+                o = o + (t + 3 < n ? c.p[q].w * c.v[q].w : 0.0f);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);   // keep the step's order
+    };
+    // full superblocks: a straight-line body; then the last one, masked and loading nothing
+    for (uint32_t sb = 0; sb < nfull; ++sb) {
+        const uint32_t ids = ids_nx;
+        ids_nx = id_of((sb + 2) * R + 2 + (uint32_t)lane);
+#pragma unroll
+        for (uint32_t j = 0; j < R; ++j) step(sb, j, ids, std::true_type{});
+    }
+    if (nfull < nsb) {
+#pragma unroll
+        for (uint32_t j = 0; j < R; ++j) step(nfull, j, 0u, std::false_type{});
+    }
+    if (hr < rep) o_out[((size_t)s * n_heads + g * rep + hr) * HD + es + el] = o;
+}
+
+// Heads per P.V wave for rep query heads per kv head.
+inline uint32_t pv_hpw(uint32_t rep) { return rep >= 4 ? 4u : rep >= 2 ? 2u : 1u; }
+
+// Sequences ranked by length, longest first (equal lengths: lower index first).  One workgroup.
+__global__ void k_b_order(const uint32_t *__restrict__ pos, uint32_t n, uint32_t *order) {
+    for (uint32_t s = threadIdx.x; s < n; s += blockDim.x) {
+        const uint32_t p = pos[s];
+        uint32_t r = 0;
+        for (uint32_t q = 0; q < n; ++q) {
+            const uint32_t pq = pos[q];
+            r += pq > p || (pq == p && q < s);
+        }
+        order[r] = s;
     }
 }
 
@@ -470,55 +587,76 @@ __global__ __launch_bounds__(256) void k_b_group(const uint32_t *__restrict__ to
                                                  uint32_t E, uint32_t n_slots, uint32_t TT,
                                                  uint32_t *act_row, uint32_t *out_row, GemmTile *tiles,
                                                  uint32_t *n_tiles) {
-    __shared__ uint32_t cnt[MAX_GROUPS + 1], off[MAX_GROUPS + 1], toff[MAX_GROUPS + 1];
-    const uint32_t tid = threadIdx.x;
+    __shared__ uint32_t cnt[MAX_GROUPS], base[MAX_GROUPS], wc[4][MAX_GROUPS], wa[4], wt[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NP = n * top_k;
     const uint32_t NG = E + (n_slots > top_k ? 1 : 0);
-    for (uint32_t e = tid; e < NG; e += 256) {
-        uint32_t c = 0;
-        if (e < E) {
-            for (uint32_t s = 0; s < n; ++s)
-                for (uint32_t r = 0; r < top_k; ++r) c += topk_idx[s * top_k + r] == e;
-        } else {
-            c = n;
-        }
-        cnt[e] = c;
+    cnt[tid] = 0;   // (256 threads = MAX_GROUPS)
+    __syncthreads();
+    for (uint32_t i = tid; i < NP; i += 256) {
+        const uint32_t e = topk_idx[i];   // (< E: the router's output; anything else is dropped)
+        if (e < E) atomicAdd(&cnt[e], 1u);
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t a = 0, t = 0;
-        for (uint32_t e = 0; e < NG; ++e) {
-            off[e] = a;
-            toff[e] = t;
-            a += cnt[e];
-            t += div_up(cnt[e], TT);
-        }
-        *n_tiles = t;
+    // exclusive scans of the entry and tile counts over the groups (thread = group)
+    const uint32_t c = tid < E ? cnt[tid] : tid < NG ? n : 0u, tc = div_up(c, TT);
+    const uint32_t ia = wave_scan_u(c), it = wave_scan_u(tc);
+    if (lane == 63) {
+        wa[wave] = ia;
+        wt[wave] = it;
     }
     __syncthreads();
-    for (uint32_t e = tid; e < NG; e += 256) {
-        uint32_t i = off[e];
-        if (e < E) {
-            for (uint32_t s = 0; s < n; ++s)
-                for (uint32_t r = 0; r < top_k; ++r)
-                    if (topk_idx[s * top_k + r] == e) {
-                        act_row[i] = s;
-                        out_row[i] = s * n_slots + r;
-                        ++i;
-                    }
-        } else {
-            for (uint32_t s = 0; s < n; ++s, ++i) {
-                act_row[i] = s;
-                out_row[i] = s * n_slots + top_k;
+    uint32_t ba = 0, bt = 0;
+    for (uint32_t w = 0; w < wave; ++w) {
+        ba += wa[w];
+        bt += wt[w];
+    }
+    const uint32_t off = ba + ia - c, toff = bt + it - tc;
+    base[tid] = off;
+    if (tid == 255) *n_tiles = bt + it;
+    if (tid < NG) {
+        for (uint32_t q = 0; q < tc; ++q) {
+            GemmTile tl;
+            tl.grp = tid < E ? tid : 0u;
+            tl.entry0 = off + q * TT;
+            tl.count = min(TT, c - q * TT);
+            tl.mat = tid < E ? 0u : 1u;
+            tiles[toff + q] = tl;
+        }
+        if (tid == E)   // the shared expert: every sequence, slot top_k
+            for (uint32_t sq = 0; sq < n; ++sq) {
+                act_row[off + sq] = sq;
+                out_row[off + sq] = sq * n_slots + top_k;
+            }
+    }
+    // the routed picks in (sequence, rank) order, 256 at a time: a pick's entry is its expert's
+    // base + the picks of that expert in earlier waves of the chunk + its rank within its wave
+    for (uint32_t c0 = 0; c0 < NP; c0 += 256) {
+        const uint32_t i = c0 + tid;
+        const uint32_t e = i < NP ? topk_idx[i] : 0xffffffffu;
+        const bool live = e < E;
+        for (uint32_t w = 0; w < 4; ++w) wc[w][tid] = 0;
+        __syncthreads();
+        uint32_t r = 0, m_all = 0;
+        for (uint32_t k = 0; k < 64; ++k) {   // rank among the wave's lanes with the same expert
+            const uint32_t ek = __builtin_amdgcn_readlane(e, k);
+            const uint64_t m = __builtin_amdgcn_ballot_w64(e == ek);
+            if (k == lane) {
+                r = (uint32_t)__builtin_popcountll(m & ((1ull << lane) - 1));
+                m_all = (uint32_t)__builtin_popcountll(m);
             }
         }
-        for (uint32_t q = 0; q < div_up(cnt[e], TT); ++q) {
-            GemmTile tl;
-            tl.grp = e < E ? e : 0u;
-            tl.entry0 = off[e] + q * TT;
-            tl.count = min(TT, cnt[e] - q * TT);
-            tl.mat = e < E ? 0u : 1u;
-            tiles[toff[e] + q] = tl;
+        if (live && r + 1 == m_all) wc[wave][e] = m_all;   // the wave's last pick of e
+        __syncthreads();
+        if (live) {
+            uint32_t at = base[e] + r;
+            for (uint32_t w = 0; w < wave; ++w) at += wc[w][e];
+            const uint32_t sq = i / top_k;
+            act_row[at] = sq;
+            out_row[at] = sq * n_slots + (i - sq * top_k);
         }
+        __syncthreads();
+        if (tid < E) base[tid] += wc[0][tid] + wc[1][tid] + wc[2][tid] + wc[3][tid];
+        __syncthreads();
     }
 }
 
@@ -583,15 +721,11 @@ __global__ void k_b_step_advance(uint32_t *step) {
         if (le_ != hipSuccess) note_launch_error(le_, #kern);                                                \
     } while (0)
 
+bool batch_ctx_ok(uint32_t max_ctx) { return bsm_lds(max_ctx) <= BSM_LDS_MAX && (size_t)div_up(max_ctx, PAGE) * 4 <= 48 * 1024; }
+
 hipError_t init_batch_kernel_attributes() {
-    hipError_t e = hipSuccess;
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_b_attn_pv<64>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)BPV_LDS_BUDGET);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_b_attn_pv<128>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)BPV_LDS_BUDGET);
-    return e;
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(&k_b_softmax), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)BSM_LDS_MAX);
 }
 
 void launch_b_embed(hipStream_t st, const float *emb, uint32_t d, const uint32_t *tokens, uint32_t n, float *x) {
@@ -650,24 +784,28 @@ bool launch_b_qk_rope_append(hipStream_t st, uint32_t hd, float *qkv, uint32_t q
     return true;
 }
 
+void launch_b_order(hipStream_t st, const uint32_t *pos, uint32_t n, uint32_t *order) {
+    BLAUNCH(k_b_order, dim3(1), dim3(256), 0, st, pos, n, order);
+}
+
 bool launch_b_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t qkv_stride, const uint32_t *pos,
-                        const PagedKV &kv, uint32_t n, uint32_t max_ctx, float *scores, float *pmax, float *o,
-                        uint32_t *err) {
-    const uint32_t nch = div_up(max_ctx, ACH), R = bpv_slots(max_ctx, hd);
-    if (R < 2) return false;
-    const size_t shm = bpv_lds(max_ctx, hd, R);
-    const dim3 gs(nch, kv.n_kv, n), gp(n * kv.n_heads);
-    switch (hd) {
-    case 64:
-        BLAUNCH(k_b_scores<64>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, kv, scores, max_ctx, pmax, nch);
-        BLAUNCH(k_b_attn_pv<64>, gp, dim3(512), shm, st, scores, max_ctx, pmax, nch, pos, kv, n, max_ctx, R, o, err);
-        break;
-    case 128:
-        BLAUNCH(k_b_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, kv, scores, max_ctx, pmax, nch);
-        BLAUNCH(k_b_attn_pv<128>, gp, dim3(512), shm, st, scores, max_ctx, pmax, nch, pos, kv, n, max_ctx, R, o, err);
-        break;
-    default: return false;
-    }
+                        const uint32_t *order, const PagedKV &kv, uint32_t n, uint32_t max_ctx, float *scores,
+                        float *pmax, float *o) {
+    if (!batch_ctx_ok(max_ctx) || (hd != 64 && hd != 128)) return false;
+    const uint32_t nch = div_up(max_ctx, ACH), rep = kv.n_heads / kv.n_kv, hpw = pv_hpw(rep);
+    const uint32_t wpk = div_up(rep, hpw) * (hd / (64 / hpw));
+    const dim3 gs(nch, kv.n_kv, n), gm(n * kv.n_heads), gp(n * kv.n_kv * wpk);
+    const size_t btb = (size_t)div_up(max_ctx, PAGE) * 4;
+    const uint32_t ss = b_sc_stride(max_ctx);
+    if (hd == 64)
+        BLAUNCH(k_b_scores<64>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, kv, scores, ss, pmax, nch);
+    else
+        BLAUNCH(k_b_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, kv, scores, ss, pmax, nch);
+    BLAUNCH(k_b_softmax, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
+#define PV_CASE(H, P) \
+    if (hd == H && hpw == P) BLAUNCH((k_b_pv<H, P>), gp, dim3(64), btb, st, scores, ss, pos, order, kv, n, o);
+    PV_CASE(64, 1) PV_CASE(64, 2) PV_CASE(64, 4) PV_CASE(128, 1) PV_CASE(128, 2) PV_CASE(128, 4)
+#undef PV_CASE
     return true;
 }
 
@@ -688,6 +826,34 @@ __global__ void k_b_page_copy(float *flat, float *pool, const uint32_t *__restri
         if (dir == 0) p[q] = f[q];
         else f[q] = p[q];
     }
+}
+
+// Seeded pseudo-random rows for positions [0, len) of one sequence in every layer's K and V
+// pages (timing workloads): element value = a hash of (seed, layer, which, position, element)
+// mapped to [-sqrt 3, sqrt 3) (unit variance).  grid (npg, n_layers, 2).
+__global__ void k_b_page_fill(float *kpool, float *vpool, const uint32_t *__restrict__ bt, uint32_t len,
+                              uint32_t n_kv, uint32_t hd, size_t layer_floats, uint64_t seed) {
+    const uint32_t i = blockIdx.x, l = blockIdx.y, which = blockIdx.z, pf = n_kv * PAGE * hd;
+    float *p = (which ? vpool : kpool) + layer_floats * l + (size_t)bt[i] * pf;
+    for (uint32_t q = threadIdx.x; q < pf; q += blockDim.x) {
+        // the inverse of k_el / v_el within the kv head's tile
+        const uint32_t g = q / (PAGE * hd), r = q % (PAGE * hd);
+        const uint32_t slot = which ? (r / 4 / hd) * 4 + r % 4 : (r / 4) % PAGE;
+        const uint32_t e = which ? (r / 4) % hd : (r / (4 * PAGE)) * 4 + r % 4, t = i * PAGE + slot;
+        uint64_t z = seed ^ ((uint64_t)l << 40) ^ ((uint64_t)which << 39) ^ ((uint64_t)t << 12) ^ (uint64_t)(g * hd + e);
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;   // splitmix64 finalizer
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        z ^= z >> 31;
+        const float u = (float)(z >> 40) * 0x1p-24f;
+        p[q] = t < len ? (u * 2.0f - 1.0f) * 1.7320508f : 0.0f;
+    }
+}
+
+void launch_b_page_fill(hipStream_t st, float *kpool, float *vpool, const uint32_t *bt, uint32_t len, uint32_t n_layers,
+                        uint32_t n_kv, uint32_t hd, size_t layer_floats, uint64_t seed) {
+    const uint32_t npg = div_up(len, PAGE);
+    if (npg) BLAUNCH(k_b_page_fill, dim3(npg, n_layers, 2), dim3(256), 0, st, kpool, vpool, bt, len, n_kv, hd,
+                     layer_floats, seed);
 }
 
 void launch_b_page_copy(hipStream_t st, float *flat, float *pool, const uint32_t *bt, uint32_t npg,

@@ -333,10 +333,13 @@ __device__ inline float seq_sum_lds(const float *a, uint32_t n, float s) {
 // Certification.  Each add errs by at most 2^-24 of its result (results below 2^-125 are
 // exact) and s never decreases, so with T_k = a[0] + ... + a[k-1] (real numbers)
 // |s_k - T_k| <= k 2^-24 (T_k + |s_k - T_k|), i.e. <= 1.001 k 2^-24 T_k for k <= 2^14.  Lanes
-// form T_k in binary32 from their partial sums, a wave scan and the previous waves' terms
-// (at most 64 roundings deep, relative error below 2^-18); a margin R = 2^-16 covers that and
-// the rounding of the bound products.  s_k then lies in [T~_k (1 - R - C k),
-// T~_k (1 + R + C k)] with C = 1.01 2^-24.  A lane whose bracket from its first sum to its
+// form T_k in binary32 from their partial sums, a wave scan and the previous waves' terms: a
+// sum of non-negative terms D roundings deep errs by at most D 2^-24 relative, with
+// D <= (NPW - 1) 3 EPT / 4 (the previous waves' terms at the lane's position) + 6 (the scan of
+// those) + EPT + 6 (the lane's own terms and their scan) + 2.  A margin R covers that and the
+// rounding of the bound products: 2^-16 while D <= 64 (relative error below 2^-18), else
+// 2^-13 (D <= 512).  s_k then lies in [T~_k (1 - R - C k), T~_k (1 + R + C k)] with
+// C = 1.01 2^-24.  A lane whose bracket from its first sum to its
 // last lies in one binade is "clean"; two consecutive clean lanes always share their binade
 // (the brackets at their common boundary both hold s).
 //
@@ -430,8 +433,11 @@ __device__ inline void part_sync(xsum::Scratch &L, uint32_t ph) {
 // 0 on entry (zeroed before a workgroup barrier).
 template <int NPW, int EPT>
 __device__ __forceinline__ float block_seq_sum(const float *a, uint32_t n, xsum::Scratch &L, int p_, int lane) {
-    static_assert(NPW >= 1 && NPW <= 8 && EPT % 4 == 0 && EPT <= 16, "wave tables, offsets depth");
-    constexpr float C = 1.01f * 0x1p-24f, R = 0x1p-16f;
+    static_assert(NPW >= 1 && NPW <= 8 && EPT % 4 == 0 && EPT <= 32 && NPW * 64 * EPT <= (1 << 14),
+                  "wave tables, offsets depth, terms within the certified count");
+    constexpr int D = (NPW - 1) * 3 * EPT / 4 + EPT + 14;   // rounding depth of the lanes' T~
+    static_assert(D <= 512, "margin");
+    constexpr float C = 1.01f * 0x1p-24f, R = D <= 64 ? 0x1p-16f : 0x1p-13f;
     constexpr uint32_t WT = 64 * EPT;   // terms per wave
     const int p = __builtin_amdgcn_readfirstlane(p_);
     const uint32_t k0 = (uint32_t)(64 * p + lane) * EPT;

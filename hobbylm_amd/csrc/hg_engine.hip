@@ -1163,7 +1163,7 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
 
 int hg_seq_sum(const float *x, uint32_t n, uint32_t method, float *out) {
     return guard([&]() -> int {
-        if ((!x && n) || !out || method > 6) return fail(HG_ERR_ARG, "NULL argument or unknown method");
+        if ((!x && n) || !out || method > 7) return fail(HG_ERR_ARG, "NULL argument or unknown method");
         int rc = check_device();
         if (rc) return rc;
         DevBuf dx, dout;

@@ -15,15 +15,17 @@
 
 namespace hg {
 
-// Test entry: one workgroup sums x[0..n) (n <= 4096 in LDS; larger n: one lane over global
-// memory) with the layouts the decode kernels use: method 1: 8 waves x 4 terms per lane, 2: 4
-// waves x 4 (waves 0..3), 3: 4 waves x 4 (waves 0, 5, 6, 7), 4: 2 waves x 8, 5: 4 waves x 8,
-// 6: 4 waves x 12; method 0: one lane.
+// Test entry: one workgroup sums x[0..n) (n <= 4096, method 7: n <= 16384, in LDS; larger n:
+// one lane over global memory) with the layouts the decode kernels use: method 1: 8 waves x 4
+// terms per lane, 2: 4 waves x 4 (waves 0..3), 3: 4 waves x 4 (waves 0, 5, 6, 7), 4: 2 waves x
+// 8, 5: 4 waves x 8, 6: 4 waves x 12, 7: 8 waves x 32; method 0: one lane.
+constexpr uint32_t SEQSUM_MAX = 16384;
 __global__ __launch_bounds__(512) void k_seq_sum(const float *__restrict__ x, uint32_t n, int method, float *out) {
-    __shared__ __align__(16) float a[4096];
+    extern __shared__ __align__(16) float a[];   // SEQSUM_MAX floats (+4)
     __shared__ xsum::Scratch L;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    if (n > 4096) {
+    const uint32_t cap = method == 7 ? SEQSUM_MAX : 4096;
+    if (n > cap) {
         if (tid == 0) {
             float s = 0.0f;
             for (uint32_t i = 0; i < n; ++i) s = s + x[i];
@@ -31,7 +33,7 @@ __global__ __launch_bounds__(512) void k_seq_sum(const float *__restrict__ x, ui
         }
         return;
     }
-    for (uint32_t i = tid; i < 4096; i += 512) a[i] = i < n ? x[i] : 0.0f;
+    for (uint32_t i = tid; i < cap + 4; i += 512) a[i] = i < n ? x[i] : 0.0f;
     if (tid == 0) L.sync = 0;
     __syncthreads();
     float r = 0.0f;
@@ -52,6 +54,7 @@ __global__ __launch_bounds__(512) void k_seq_sum(const float *__restrict__ x, ui
     case 6:
         if (wave < 4) r = block_seq_sum<4, 12>(a, n, L, wave, lane);
         break;
+    case 7: r = block_seq_sum<8, 32>(a, n, L, wave, lane); break;
     default:
         if (tid == 0) r = seq_sum_lds(a, n, 0.0f);
     }
@@ -2010,6 +2013,9 @@ hipError_t init_kernel_attributes() {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_LDS_BUDGET);
     PVR_ATTR(32) PVR_ATTR(64) PVR_ATTR(128)
 #undef PVR_ATTR
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_seq_sum), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)((SEQSUM_MAX + 4) * sizeof(float)));
     return e;
 }
 
@@ -2034,7 +2040,8 @@ void launch_load_row(hipStream_t st, const float *inputs, uint32_t d, const Step
 void launch_advance(hipStream_t st, StepParams *p) { LAUNCH(k_advance, dim3(1), dim3(64), 0, st, p); }
 
 void launch_seq_sum(hipStream_t st, const float *x, uint32_t n, int method, float *out) {
-    LAUNCH(k_seq_sum, dim3(1), dim3(512), 0, st, x, n, method, out);
+    const size_t shm = ((method == 7 ? SEQSUM_MAX : 4096) + 4) * sizeof(float);
+    LAUNCH(k_seq_sum, dim3(1), dim3(512), shm, st, x, n, method, out);
 }
 
 void launch_rmsnorm_quant(hipStream_t st, bool exact, const float *x, const float *w, float eps, uint32_t d,

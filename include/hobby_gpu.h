@@ -187,6 +187,10 @@ int hg_batch_routing(hg_batch *b, uint32_t seq, uint32_t *idx, float *w);
 /* ---- instrumentation (no counterpart in the reference) -------------------------------- */
 
 #define HG_PROF_CLASSES 12
+/* Rows [0, len) of every layer of batch sequence seq set to seeded pseudo-random values of unit
+ * variance (a hash of seed, layer, position and element), written on the device; the length
+ * becomes len.  For timing workloads whose caches would take long to upload. */
+int hg_batch_fill(hg_batch *b, uint32_t seq, uint32_t len, uint64_t seed);
 /* Time one decode step per kernel class, for measurement tools: the step at pos = len is
  * replayed `reps` times on the cache's own stream, every kernel launched with a start/stop
  * HIP event pair recorded by its own dispatch (hipExtLaunchKernelGGL), i.e. kernel execution
@@ -241,10 +245,11 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
 
 /* The sequential binary32 sum out = ((0 + x[0]) + x[1]) + ... + x[n-1] that ops::rmsnorm
  * (`ss += v * v`, ops.rs:101-104) and ops::softmax (`sum += *v`, ops.rs:119-122) form, computed
- * on the device by the method the decode kernels use for it: methods 1..6 = the workgroup
+ * on the device by the method the decode kernels use for it: methods 1..7 = the workgroup
  * layouts of those kernels (waves x terms per lane: 8x4, 4x4, 4x4 on waves 0,5,6,7, 2x8, 4x8,
- * 4x12; identical bits for non-negative terms; other inputs or n beyond the layout fall back
- * to one lane), method 0 = one lane adding in index order (n <= 4096 in LDS). */
+ * 4x12, 8x32; identical bits for non-negative terms; other inputs or n beyond the layout fall
+ * back to one lane), method 0 = one lane adding in index order (n <= 4096 in LDS; method 7:
+ * n <= 16384). */
 int hg_seq_sum(const float *x, uint32_t n, uint32_t method, float *out);
 
 /* ---- measurement (no counterpart in the reference) ------------------------------------ */

@@ -79,10 +79,41 @@ def _cases():
     return out
 
 
+def _long_cases():
+    """Up to 16384 terms: the batched attention's softmax sums (8 waves x 32 terms per lane)."""
+    rng = np.random.default_rng(11)
+    f = np.float32
+    out = []
+    for n, sc in ((16384, 0.5), (16384, 4.0), (16383, 2.0), (9000, 8.0), (3100, 1.0), (12345, 20.0)):
+        z = rng.standard_normal(n).astype(f) * f(sc)
+        out.append((f"softmax{n}_{sc}", np.exp(z - z.max()).astype(f)))
+    z = rng.standard_normal(16384).astype(f)
+    z[-1] = z.max() + 9
+    out.append(("softmax_late_peak16384", np.exp(z - z.max()).astype(f)))
+    out.append(("ties_long", np.concatenate([[f(2 ** 24)], np.ones(16383, f)])))
+    out.append(("constant_third_long", np.full(16384, f(1 / 3), f)))
+    out.append(("geometric_long", (2.0 ** np.linspace(-80, 20, 16384)).astype(f)))
+    out.append(("unif_long", rng.random(16384, dtype=f)))
+    out.append(("beyond_the_layout", rng.random(16385, dtype=f)))
+    for k in range(8):
+        n = int(rng.integers(4097, 16385))
+        v = np.exp(np.minimum(rng.standard_normal(n) * rng.random() * 30, 80)).astype(f) if k % 2 else \
+            (rng.integers(0, 4, n) * 2.0 ** rng.integers(-30, 5, n)).astype(f)
+        out.append((f"long_random{k}", v))
+    return out
+
+
+@pytest.mark.parametrize("name,x", _long_cases(), ids=lambda v: v if isinstance(v, str) else "")
+def test_long_sum_matches_sequential(hg, name, x):
+    want = _seq(x)
+    got = hg.seq_sum(x, 7)
+    assert np.array_equal(np.float32(got).view(np.uint32), np.float32(want).view(np.uint32)), (name, got, want)
+
+
 @pytest.mark.parametrize("name,x", _cases(), ids=lambda v: v if isinstance(v, str) else "")
 def test_workgroup_sum_matches_sequential(hg, name, x):
     want = _seq(x)
-    for method in (1, 2, 3, 4, 5, 6, 0):   # every wave layout of the decode kernels, one lane
+    for method in (1, 2, 3, 4, 5, 6, 7, 0):   # every wave layout of the decode kernels, one lane
         got = hg.seq_sum(x, method)
         assert np.array_equal(np.float32(got).view(np.uint32), np.float32(want).view(np.uint32)) or (
             np.isnan(got) and np.isnan(want)), (name, method, got, want)
@@ -98,6 +129,6 @@ def test_norm_inputs_of_the_130m_model(hg):
         sq = (x * x).astype(np.float32)
         for n in (64, 255, 256, 257, 511, 512, len(sq)):
             want = _seq(sq[:n])
-            for method in (1, 2, 3, 4, 5, 6):
+            for method in (1, 2, 3, 4, 5, 6, 7):
                 got = hg.seq_sum(sq[:n], method)
                 assert np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32), (int(t), n, method)
