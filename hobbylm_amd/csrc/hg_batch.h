@@ -31,7 +31,7 @@ __host__ __device__ inline uint32_t v_el(uint32_t e, uint32_t slot, uint32_t hd)
     return ((slot / 4) * hd + e) * 4 + slot % 4;
 }
 
-// One column tile of a batched GEMM: entries entry0 .. entry0 + count - 1 of the entry tables
+// One column tile of a batched GEMM: entries entry0 .. entry0 + count - 1 (count <= 8) of the entry tables
 // (act_row: which activation row, out_row: which output row) against matrix group grp of
 // matrix set `mat` (rows grp * rows .. + rows - 1; set 0: the plain or routed matrices, set 1:
 // the shared expert's).
@@ -60,7 +60,8 @@ hipError_t init_batch_kernel_attributes();
 void launch_b_embed(hipStream_t st, const float *emb, uint32_t d, const uint32_t *tokens, uint32_t n, float *x);
 void launch_b_quant_rows(hipStream_t st, const float *x, uint32_t xs, uint32_t n_elems, uint32_t rows, uint8_t *q,
                          uint32_t qs, float *dq, uint32_t ds);
-bool launch_b_gemm(hipStream_t st, int mode, uint32_t tt, const GemmArgs &a, uint32_t max_tiles);
+// A GEMM over column tiles of at most 8 entries (max_tiles: the grid's bound on *n_tiles).
+bool launch_b_gemm(hipStream_t st, int mode, const GemmArgs &a, uint32_t max_tiles);
 bool launch_b_qk_rope_append(hipStream_t st, uint32_t hd, float *qkv, uint32_t qkv_stride, const float *qn,
                              const float *kn, float eps, const float *cs, const float *sn, const uint32_t *pos,
                              const PagedKV &kv, uint32_t n);

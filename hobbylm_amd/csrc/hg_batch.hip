@@ -43,7 +43,7 @@ struct hg_batch {
     DevBuf x, xq, xd, qkv, scores, pmax, o, oq, od;
     DevBuf topk_idx, topk_w, order, rec_idx, rec_w;
     DevBuf ent_act, ent_out, etiles, n_etiles;
-    DevBuf ident, ptiles, pn;              // identity entries; plain tiles per batch size (tt 8, 16)
+    DevBuf ident, ptiles, pn;              // identity entries; plain tiles of 8 entries per batch size
     DevBuf a, aq, ad, y, logits, out_ids, flat;
     std::map<uint32_t, hipGraphExec_t> graphs;   // captured step per batch size
     uint32_t cur_n = 0;                          // batch size of the step being enqueued
@@ -51,16 +51,12 @@ struct hg_batch {
 
 namespace {
 
-constexpr uint32_t PT_MAX = 64;   // plain tiles per batch size and tile width (>= max_seqs / 8)
+constexpr uint32_t PT_MAX = 64;   // plain tiles per batch size (>= max_seqs / 8)
 
-// Plain tile tables: for batch size n and width tt (8 or 16), tiles at
-// ptiles[((n * 2) + (tt == 16)) * PT_MAX], counts at pn[n * 2 + (tt == 16)].
-const GemmTile *plain_tiles(const hg_batch *b, uint32_t n, uint32_t tt) {
-    return b->ptiles.as<GemmTile>() + ((size_t)n * 2 + (tt == 16 ? 1 : 0)) * PT_MAX;
-}
-const uint32_t *plain_count(const hg_batch *b, uint32_t n, uint32_t tt) {
-    return b->pn.as<uint32_t>() + (size_t)n * 2 + (tt == 16 ? 1 : 0);
-}
+// Plain tile tables: for batch size n, the div_up(n, 8) tiles of 8 entries at
+// ptiles[n * PT_MAX], their count at pn[n].
+const GemmTile *plain_tiles(const hg_batch *b, uint32_t n) { return b->ptiles.as<GemmTile>() + (size_t)n * PT_MAX; }
+const uint32_t *plain_count(const hg_batch *b, uint32_t n) { return b->pn.as<uint32_t>() + n; }
 
 PagedKV layer_kv(const hg_batch *b, uint32_t l) {
     const hg_config &c = b->m->c;
@@ -75,14 +71,13 @@ PagedKV layer_kv(const hg_batch *b, uint32_t l) {
     return kv;
 }
 
-// A GEMM over all n sequences of the step (identity entries) with column tiles of tt.
-GemmArgs plain_gemm(const hg_batch *b, const Q8Mat &W, uint32_t tt, const uint8_t *aq, const float *ad, float *y,
-                    uint32_t ys) {
+// A GEMM over all n sequences of the step (identity entries) in column tiles of 8.
+GemmArgs plain_gemm(const hg_batch *b, const Q8Mat &W, const uint8_t *aq, const float *ad, float *y, uint32_t ys) {
     GemmArgs g{};
     g.W[0] = W;
     g.rows = W.N;
-    g.n_tiles = plain_count(b, b->cur_n, tt);
-    g.tiles = plain_tiles(b, b->cur_n, tt);
+    g.n_tiles = plain_count(b, b->cur_n);
+    g.tiles = plain_tiles(b, b->cur_n);
     g.act_row = g.out_row = b->ident.as<uint32_t>();
     g.aq = aq;
     g.ad = ad;
@@ -99,7 +94,7 @@ void enqueue_step(hg_batch *b) {
     hipStream_t st = b->st;
     const uint32_t n = b->cur_n, d = c.d_model, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
     const uint32_t qw = qd + 2 * kvd, f = c.expert_ffn, ns = m->n_slots;
-    const uint32_t ncd = div_up(d / QK, 4), ncq = div_up(qd / QK, 4);
+    const uint32_t ncd = div_up(d / QK, 4), ncq = div_up(qd / QK, 4), pt = div_up(n, 8);   // plain tiles
     float *x = b->x.as<float>();
     uint8_t *xq = b->xq.as<uint8_t>();
     float *xd = b->xd.as<float>();
@@ -111,7 +106,7 @@ void enqueue_step(hg_batch *b) {
         const PagedKV kv = layer_kv(b, l);
         // attention (model.rs:164-171, 186-234)
         launch_rmsnorm_quant_rows(st, true, n, x, L.attn_norm.as<float>(), c.rms_eps, d, nullptr, xq, xd);
-        if (!launch_b_gemm(st, GM_STORE, 16, plain_gemm(b, L.qkv.m, 16, xq, xd, b->qkv.as<float>(), qw), PT_MAX))
+        if (!launch_b_gemm(st, GM_STORE, plain_gemm(b, L.qkv.m, xq, xd, b->qkv.as<float>(), qw), pt))
             note_launch_error(hipErrorInvalidConfiguration, "QKV GEMM");
         if (!launch_b_qk_rope_append(st, hd, b->qkv.as<float>(), qw, L.q_norm.as<float>(), L.k_norm.as<float>(),
                                      c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), pos, kv, n))
@@ -121,8 +116,7 @@ void enqueue_step(hg_batch *b) {
             note_launch_error(hipErrorInvalidConfiguration, "paged attention");
         launch_b_quant_rows(st, b->o.as<float>(), qd, qd, n, b->oq.as<uint8_t>(), ncq * CHUNK_BYTES, b->od.as<float>(),
                             ncq * 4);
-        if (!launch_b_gemm(st, GM_RESID, 16, plain_gemm(b, L.o.m, 16, b->oq.as<uint8_t>(), b->od.as<float>(), x, d),
-                           PT_MAX))
+        if (!launch_b_gemm(st, GM_RESID, plain_gemm(b, L.o.m, b->oq.as<uint8_t>(), b->od.as<float>(), x, d), pt))
             note_launch_error(hipErrorInvalidConfiguration, "O GEMM");
         if (L.moe) {
             // ffn_norm + router + top-k per sequence (model.rs:259-293), h quantized into xq
@@ -153,7 +147,7 @@ void enqueue_step(hg_batch *b) {
             gu.ads = ncd * 4;
             gu.y = b->a.as<float>();
             gu.ys = f;
-            if (!launch_b_gemm(st, GM_GATEUP, 8, gu, b->max_tiles_e))
+            if (!launch_b_gemm(st, GM_GATEUP, gu, b->max_tiles_e))
                 note_launch_error(hipErrorInvalidConfiguration, "expert gate/up GEMM");
             const uint32_t ncf = div_up(f / QK, 4);
             launch_b_quant_rows(st, b->a.as<float>(), f, f, n * ns, b->aq.as<uint8_t>(), ncf * CHUNK_BYTES,
@@ -171,28 +165,26 @@ void enqueue_step(hg_batch *b) {
             dn.ads = ncf * 4;
             dn.y = b->y.as<float>();
             dn.ys = d;
-            if (!launch_b_gemm(st, GM_STORE, 8, dn, b->max_tiles_e))
+            if (!launch_b_gemm(st, GM_STORE, dn, b->max_tiles_e))
                 note_launch_error(hipErrorInvalidConfiguration, "expert down GEMM");
             launch_b_combine(st, b->y.as<float>(), b->topk_w.as<float>(), c.top_k, ns, d, n, x);
         } else {
             // dense FFN (model.rs:243-255)
             const uint32_t df = c.dense_ffn, ncf = div_up(df / QK, 4);
             launch_rmsnorm_quant_rows(st, true, n, x, L.ffn_norm.as<float>(), c.rms_eps, d, nullptr, xq, xd);
-            GemmArgs gu = plain_gemm(b, L.gate.m, 8, xq, xd, b->a.as<float>(), df);
+            GemmArgs gu = plain_gemm(b, L.gate.m, xq, xd, b->a.as<float>(), df);
             gu.U[0] = L.up.m;
-            if (!launch_b_gemm(st, GM_GATEUP, 8, gu, PT_MAX))
+            if (!launch_b_gemm(st, GM_GATEUP, gu, pt))
                 note_launch_error(hipErrorInvalidConfiguration, "dense gate/up GEMM");
             launch_b_quant_rows(st, b->a.as<float>(), df, df, n, b->aq.as<uint8_t>(), ncf * CHUNK_BYTES,
                                 b->ad.as<float>(), ncf * 4);
-            if (!launch_b_gemm(st, GM_RESID, 16,
-                               plain_gemm(b, L.down.m, 16, b->aq.as<uint8_t>(), b->ad.as<float>(), x, d), PT_MAX))
+            if (!launch_b_gemm(st, GM_RESID, plain_gemm(b, L.down.m, b->aq.as<uint8_t>(), b->ad.as<float>(), x, d), pt))
                 note_launch_error(hipErrorInvalidConfiguration, "dense down GEMM");
         }
     }
     // output_norm + lm_head + greedy pick (model.rs:180-183, lib.rs:132-142)
     launch_rmsnorm_quant_rows(st, true, n, x, m->output_norm.as<float>(), c.rms_eps, d, nullptr, xq, xd);
-    if (!launch_b_gemm(st, GM_STORE, 16, plain_gemm(b, m->output.m, 16, xq, xd, b->logits.as<float>(), c.vocab_size),
-                       PT_MAX))
+    if (!launch_b_gemm(st, GM_STORE, plain_gemm(b, m->output.m, xq, xd, b->logits.as<float>(), c.vocab_size), pt))
         note_launch_error(hipErrorInvalidConfiguration, "lm_head GEMM");
     launch_b_argmax(st, b->logits.as<float>(), c.vocab_size, std::min(c.vocab_size, 50257u), pos,
                     b->tokens.as<uint32_t>(), b->out_ids.as<uint32_t>(), b->step.as<uint32_t>(), n, 1);
@@ -329,15 +321,12 @@ int hg_batch_new(const hg_model *m, uint32_t max_seqs, uint32_t max_ctx, uint32_
         // identity entries and the plain column tiles of every batch size
         std::vector<uint32_t> ident(S);
         for (uint32_t i = 0; i < S; ++i) ident[i] = i;
-        std::vector<GemmTile> pt((size_t)(S + 1) * 2 * PT_MAX);
-        std::vector<uint32_t> pn((size_t)(S + 1) * 2);
-        for (uint32_t n = 1; n <= S; ++n)
-            for (uint32_t w = 0; w < 2; ++w) {
-                const uint32_t tt = w ? 16 : 8, nt = div_up(n, tt);
-                pn[n * 2 + w] = nt;
-                for (uint32_t q = 0; q < nt; ++q)
-                    pt[((size_t)n * 2 + w) * PT_MAX + q] = GemmTile{0, q * tt, std::min(tt, n - q * tt), 0};
-            }
+        std::vector<GemmTile> pt((size_t)(S + 1) * PT_MAX);
+        std::vector<uint32_t> pn(S + 1);
+        for (uint32_t n = 1; n <= S; ++n) {
+            pn[n] = div_up(n, 8);
+            for (uint32_t q = 0; q < pn[n]; ++q) pt[(size_t)n * PT_MAX + q] = GemmTile{0, q * 8, std::min(8u, n - q * 8), 0};
+        }
         if ((rc = b->ident.upload(ident.data(), ident.size() * 4)) ||
             (rc = b->ptiles.upload(pt.data(), pt.size() * sizeof(GemmTile))) ||
             (rc = b->pn.upload(pn.data(), pn.size() * 4)))

@@ -1,21 +1,16 @@
 // hg_batch_kernels.hip -- gfx950 kernels of the batched decode step: many sequences, one token
 // each, every sequence's arithmetic identical to its own single-sequence step.
 //
-// The Q8 matrix products of the step run as int8 MFMA GEMMs (v_mfma_i32_32x32x32_i8) that keep
+// The Q8 matrix products of the step run as int8 MFMA GEMMs (v_mfma_i32_16x16x32_i8) that keep
 // the per-sequence operation order of the reference:
 //   decode order, qrow_dot_avx2 (quant.rs:44-67): lane j of a row's 8 accumulators takes
 //     acc_j = fma(sw[b] * dx[b], isum_{b,j}, acc_j) over blocks b, where isum_{b,j} is the int8
 //     dot of the 4 elements 32b + 4j .. 32b + 4j + 3 only.  An MFMA sums over all 32 K slots
 //     of its block, so the activation operand is masked: column (token, j) holds token's 4
 //     elements of lane j and zeros elsewhere, and C[row][(token, j)] is exactly isum_{b,j}.
-//     One MFMA covers 32 rows x 4 tokens x 8 lanes; the 8 lane accumulators are then reduced
+//     One MFMA covers 16 rows x 2 tokens x 8 lanes; the 8 lane accumulators are then reduced
 //     ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) across lanes, as the reference's hsum.
-// MFMA operand layout (probed on gfx950): lane l supplies row (A) / column (B) l % 32, K half
-// l / 32 (16 bytes, the same K slots in A and B); C register v of lane l is row
-// 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32.  K slot (h, i) here carries block element
-// 16 h + i: in the device row layout (hg_common.h) that is lanes j = 4h .. 4h + 3 of the chunk,
-// so a lane's A operand for the 4 blocks of a chunk is the chunk's contiguous 64 bytes at 64 h
-// (4 x 16 bytes, word t of each piece = block t).
+// The operand layout is given at k_gemm16.
 //
 // KV rows live in pages of PAGE positions (a pool per layer; per page and kv head a K tile and a
 // V tile laid out for 16-byte loads, see PagedKV); each sequence's block table maps position t
@@ -28,13 +23,6 @@
 #include "hg_expf.h"
 
 namespace hg {
-
-typedef int v16i __attribute__((ext_vector_type(16)));
-
-__device__ inline v16i mfma_i8(v4i a, v4i b) {
-    const v16i z = {};
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
-}
 
 // ------------------------------------------------------------------ embedding
 // x[s] = token_embd[tokens[s]] (model.rs:152-154).  grid (d / 256, n).
@@ -65,140 +53,173 @@ __global__ __launch_bounds__(256) void k_b_quant_rows(const float *__restrict__ 
 }
 
 // ------------------------------------------------------------------ MFMA GEMM, decode order
-// y[out_row[e]][row] (+)= (W x_{act_row[e]})[row] for the entries e of each column tile and the
-// rows of its matrix group, in qrow_dot_avx2's order (see the file comment).  Workgroup =
-// 4 waves; blockIdx.y = column tile (tiles past *n_tiles exit), blockIdx.x = a block of rows.
-//   GM_STORE / GM_RESID: waves = WR row tiles of 32 rows x 4 / WR column groups of 4 entries.
-//   GM_GATEUP: wave w = (matrix w & 1: gate / up) x (column group w >> 1), 32 rows; the up
-//     wave hands its sums to the gate wave, which stores silu(g) * u (model.rs:301-305).
-// Per chunk, lanes 0..31 fetch the 4 block scales of row rbase + lane with the weights and
-// stage them in LDS (double-buffered by chunk parity; within one wave LDS accesses complete in
-// program order), from where every lane reads those of its 16 output rows.
+// y[out_row[e]][row] (+)= (W x_{act_row[e]})[row] for the entries e of each column tile (at most
+// 8) and the rows of its matrix group, in qrow_dot_avx2's order (see the file comment).
+// Workgroup = 4 waves over 64 rows (blockIdx.x) of one column tile (blockIdx.y; tiles past
+// *n_tiles exit); each wave owns 16 rows and computes every entry of the tile, so its weight
+// loads are its own (a CU streams distinct rows) and each is used by the 4 entry pairs.  The
+// tile's activations (quants and block scales of its <= 8 entries) are staged in LDS first; the
+// wave streams its rows' chunks through a register ring of D chunks.  One
+// v_mfma_i32_16x16x32_i8 per (block, entry pair): lane l supplies A row l % 16 and B column
+// l % 16 = (entry 2p + (l % 16) / 8, lane j = l % 8) for K group g = l / 16 (8 bytes: block
+// elements 8g .. 8g + 7, i.e. the reference lanes 2g and 2g + 1 -- in the device row layout the
+// chunk's 32 bytes at 32 g, word t of each 16-byte half = block t); C register v of lane l is
+// row 4 g + v, column l % 16 (probed on gfx950).  The B operand is masked to the 4 elements of
+// lane j (only group g = j / 2 is nonzero), so C[v] = isum_{b,j} exactly, and each lane runs
+// acc = fma(sw * dx, isum, acc) over the blocks in order for its (row, entry, lane-j)
+// accumulators.  GM_GATEUP: each wave runs the gate and the up matrices and stores silu(g) * u
+// (model.rs:301-305).  D divides nc; FULLK: every chunk has 4 blocks (else D = 1 and the last
+// chunk's padding blocks are skipped).
+__host__ __device__ inline size_t gemm_lds(uint32_t nc) { return (size_t)8 * nc * (CHUNK_BYTES + 16); }
 
-template <bool SCF32, int MODE, int WR>
-__global__ __launch_bounds__(256) void k_gemm_dec(GemmArgs g) {
-    static_assert(MODE != GM_GATEUP || WR == 1, "gate/up: one row tile per workgroup");
-    __shared__ __align__(16) float scl_all[4][2][32][4];
-    __shared__ float up_sum[2][16][64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (blockIdx.y >= *g.n_tiles) return;   // (uniform)
-    const GemmTile tile = g.tiles[blockIdx.y];
-    const int mat = MODE == GM_GATEUP ? (wave & 1) : 0;
-    const int rt = MODE == GM_GATEUP ? 0 : wave % WR;
-    const int cg = MODE == GM_GATEUP ? (wave >> 1) : wave / WR;
-    const Q8Mat &M = MODE == GM_GATEUP && mat == 1 ? g.U[tile.mat] : g.W[tile.mat];
-    const uint32_t r0 = blockIdx.x * 32 * WR + rt * 32;   // first row of the wave within the group
-    const uint32_t gbase = tile.grp * g.rows, rbase = gbase + r0, rlim = gbase + g.rows - 1;
-    const uint32_t nc = M.nc, nb = M.nb;
-    const WaveExpTab tab = WaveExpTab::load(lane);
-    // this lane's operands: A row rbase + lane % 32 (K half lane / 32); B column lane % 32 =
-    // (entry k = (lane % 32) / 8 of the column group, lane j = lane % 8)
-    const uint32_t h = (uint32_t)lane >> 5, j = (uint32_t)lane & 7, k = ((uint32_t)lane & 31) >> 3;
-    const uint32_t arow = min(rbase + ((uint32_t)lane & 31), rlim);
-    const uint32_t ent = (uint32_t)cg * 4 + k;
-    const bool valid = ent < tile.count;
-    const uint32_t e = tile.entry0 + min(ent, tile.count - 1);
-    const uint32_t xr = g.act_row[e];
-    const bool bact = valid && h == (j >> 2);   // the lane whose 16 B hold the column's 4 elements
-    const uint8_t *wrow = M.qs + (size_t)arow * nc * CHUNK_BYTES + 64 * h;
+template <bool SCF32, int MODE, int D, bool FULLK>
+__global__ __launch_bounds__(256) void k_gemm16(GemmArgs g) {
+    static_assert(FULLK || D == 1, "a partial last chunk: one chunk per group");
+    constexpr int NM = MODE == GM_GATEUP ? 2 : 1;   // matrices per wave
     typedef typename ScaleVec<SCF32>::T SV;
-    const SV *srow = reinterpret_cast<const SV *>(row_sc<SCF32>(M, arow));   // (lanes 0..31: its row's)
-    const uint8_t *xq = g.aq + (size_t)xr * g.aqs + j * 16;
-    const float *xd = g.ad + (size_t)xr * g.ads;
-    float acc[16];
+    extern __shared__ __align__(16) uint8_t xs[];   // [8 entries][nc][128] quants, then [8][nc][4] scales
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t ntl = *g.n_tiles;
+    const GemmTile tile = g.tiles[blockIdx.y];   // (read with the count: the table has gridDim.y entries)
+    if (blockIdx.y >= ntl) return;   // (uniform)
+    Q8Mat M[NM];
+    M[0] = g.W[tile.mat];
+    if constexpr (NM == 2) M[1] = g.U[tile.mat];
+    const uint32_t nc = M[0].nc, nb = M[0].nb, ne = tile.count;
+    float *xds = reinterpret_cast<float *>(xs + (size_t)8 * nc * CHUNK_BYTES);
+    // the tile's activations (entries past the count: zeros)
+    for (uint32_t i = tid; i < 8 * nc * 8; i += 256) {   // 16-byte pieces: entry i / (8 nc)
+        const uint32_t e = i / (nc * 8), p = i % (nc * 8);
+        v4i v = {0, 0, 0, 0};
+        if (e < ne) v = *reinterpret_cast<const v4i *>(g.aq + (size_t)g.act_row[tile.entry0 + e] * g.aqs + p * 16);
+        *reinterpret_cast<v4i *>(xs + (size_t)i * 16) = v;
+    }
+    for (uint32_t i = tid; i < 8 * nc; i += 256) {   // block scales: entry i / nc, chunk i % nc
+        const uint32_t e = i / nc, c = i % nc;
+        v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (e < ne) v = *reinterpret_cast<const v4f *>(g.ad + (size_t)g.act_row[tile.entry0 + e] * g.ads + 4 * c);
+        *reinterpret_cast<v4f *>(xds + 4 * i) = v;
+    }
+    __syncthreads();
+    const uint32_t r0 = blockIdx.x * 64 + (uint32_t)wave * 16;   // this wave's rows within the group
+    if (r0 >= g.rows) return;   // (uniform per wave; after the workgroup's only barrier)
+    const WaveExpTab tab = WaveExpTab::load(lane);
+    const uint32_t gq = (uint32_t)lane >> 4, cc = (uint32_t)lane & 15, k = cc >> 3, j = cc & 7;
+    const uint32_t gbase = tile.grp * g.rows, rlim = gbase + g.rows - 1, np = div_up(ne, 2);
+    const bool bact = gq == (j >> 1);   // the lane whose K group holds lane j's 4 elements
+    const uint8_t *wrow[NM];
+    const SV *srow[NM][4];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
-    v4i P[4], Pn[4], bp, bpn;
-    v4f dx, dxn;
-    SV sv, svn;
-    auto load = [&](uint32_t c, v4i (&p)[4], v4i &b, v4f &d, SV &sc) {
-        const v4i *wp = reinterpret_cast<const v4i *>(wrow + (size_t)c * CHUNK_BYTES);
+    for (int m = 0; m < NM; ++m) {
+        wrow[m] = M[m].qs + (size_t)min(gbase + r0 + cc, rlim) * nc * CHUNK_BYTES + 32 * gq;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = __builtin_nontemporal_load(wp + i);
-        sc = srow[c];
-        b = *reinterpret_cast<const v4i *>(xq + (size_t)c * CHUNK_BYTES);
-        d = *reinterpret_cast<const v4f *>(xd + 4 * c);
+        for (int v = 0; v < 4; ++v)
+            srow[m][v] = reinterpret_cast<const SV *>(row_sc<SCF32>(M[m], min(gbase + r0 + 4 * gq + v, rlim)));
+    }
+    struct Ch {
+        v4i w[NM][2];
+        SV s[NM][4];
     };
-    load(0, P, bp, dx, sv);
-    for (uint32_t c = 0; c < nc; ++c) {
-        if (c + 1 < nc) load(c + 1, Pn, bpn, dxn, svn);
-        // the 4 block scales of this wave's 32 rows through LDS; lane reads its 16 rows'
-        // (C register v is row 8 (v / 4) + 4 h + v % 4)
-        float (*scl)[4] = scl_all[wave][c & 1];
-        if (lane < 32) {
-            float f[4];
-            unpack_scales(sv, f);
-            *reinterpret_cast<v4f *>(scl[lane]) = v4f{f[0], f[1], f[2], f[3]};
+    auto load = [&](Ch &d, uint32_t c) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const v4i *wp = reinterpret_cast<const v4i *>(wrow[m] + (size_t)c * CHUNK_BYTES);
+            d.w[m][0] = __builtin_nontemporal_load(wp);
+            d.w[m][1] = __builtin_nontemporal_load(wp + 1);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) d.s[m][v] = srow[m][v][c];
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        v4f s16[16];
+    };
+    float acc[NM][4][4];   // [matrix][entry pair][row v]
 #pragma unroll
-        for (int v = 0; v < 16; ++v) s16[v] = *reinterpret_cast<const v4f *>(scl[8 * (v / 4) + 4 * h + v % 4]);
-        const int pa[4] = {P[0].x, P[1].x, P[2].x, P[3].x}, pb[4] = {P[0].y, P[1].y, P[2].y, P[3].y},
-                  pc[4] = {P[0].z, P[1].z, P[2].z, P[3].z}, pd[4] = {P[0].w, P[1].w, P[2].w, P[3].w};
-        const int bw[4] = {bp.x, bp.y, bp.z, bp.w};
-        const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int *pt = t == 0 ? pa : t == 1 ? pb : t == 2 ? pc : pd;
-            const v4i A = {pt[0], pt[1], pt[2], pt[3]};
-            const int w = bact ? bw[t] : 0;
-            const uint32_t jj = j & 3;
-            const v4i B = {jj == 0 ? w : 0, jj == 1 ? w : 0, jj == 2 ? w : 0, jj == 3 ? w : 0};
-            const v16i C = mfma_i8(A, B);
-            if (4 * c + t < nb) {   // (padding blocks of a partial last chunk: no add)
+        for (int p = 0; p < 4; ++p)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const float sw = t == 0 ? s16[v].x : t == 1 ? s16[v].y : t == 2 ? s16[v].z : s16[v].w;
-                    acc[v] = fmaf(sw * dxs[t], (float)C[v], acc[v]);
+            for (int v = 0; v < 4; ++v) acc[m][p][v] = 0.0f;
+    auto compute = [&](const Ch &d, uint32_t c) {
+        float sw[NM][4][4];
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) unpack_scales(d.s[m][v], sw[m][v]);
+#pragma unroll
+        for (uint32_t p = 0; p < 4; ++p) {
+            if (p < np) {   // (uniform)
+                const uint32_t ei = 2 * p + k;   // this lane's entry of the pair
+                const v4i b4 = *reinterpret_cast<const v4i *>(xs + ((size_t)ei * nc + c) * CHUNK_BYTES + j * 16);
+                const v4f dx4 = *reinterpret_cast<const v4f *>(xds + ((size_t)ei * nc + c) * 4);
+                const int bw[4] = {b4.x, b4.y, b4.z, b4.w};
+                const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    if (FULLK || 4 * c + t < nb) {   // (uniform; padding blocks of a partial last chunk: no add)
+                        const uint32_t w = bact ? (uint32_t)bw[t] : 0u;
+                        const long B = (long)((j & 1) ? (uint64_t)w << 32 : (uint64_t)w);
+#pragma unroll
+                        for (int m = 0; m < NM; ++m) {
+                            const int lo = t == 0 ? d.w[m][0].x : t == 1 ? d.w[m][0].y : t == 2 ? d.w[m][0].z : d.w[m][0].w;
+                            const int hi = t == 0 ? d.w[m][1].x : t == 1 ? d.w[m][1].y : t == 2 ? d.w[m][1].z : d.w[m][1].w;
+                            const long A = (long)((uint64_t)(uint32_t)lo | (uint64_t)(uint32_t)hi << 32);
+                            const v4i z = {0, 0, 0, 0};
+                            const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, z, 0, 0, 0);
+#pragma unroll
+                            for (int v = 0; v < 4; ++v)
+                                acc[m][p][v] = fmaf(sw[m][v][t] * dxs[t], (float)C[v], acc[m][p][v]);
+                        }
+                    }
                 }
             }
         }
-        if (c + 1 < nc) {
+    };
+    Ch ring[D];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) P[i] = Pn[i];
-            bp = bpn;
-            dx = dxn;
-            sv = svn;
+    for (uint32_t u = 0; u < D; ++u) {
+        load(ring[u], min(u, nc - 1));
+        __builtin_amdgcn_sched_barrier(0);   // (slot order as in the loop: the loop's waits hold for its first pass)
+    }
+    // groups of D chunks; each group refills its slots with the chunks D ahead (the last group's
+    // refills re-read the last chunk: cache hits, issued without a branch so that each chunk's
+    // wait counts only the loads after its own)
+    for (uint32_t c0 = 0; c0 < nc; c0 += D) {
+#pragma unroll
+        for (uint32_t u = 0; u < D; ++u) {
+            compute(ring[u], c0 + u);
+            load(ring[u], min(c0 + D + u, nc - 1));
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
-    // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) over the 8 lanes j of each (row, entry)
+    // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) over the 8 lanes j of each (row, entry), then the stores
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        float a = acc[v];
-        {
-            const float dn = dpp_f<0x124>(a), up = dpp_f<0x12C>(a);
-            a = a + ((j & 4) ? dn : up);
+    for (uint32_t p = 0; p < 4; ++p) {
+        if (p >= np) break;   // (uniform)
+        float out[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            float r[NM];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                float a = acc[m][p][v];
+                {
+                    const float dn = dpp_f<0x124>(a), up = dpp_f<0x12C>(a);
+                    a = a + ((j & 4) ? dn : up);
+                }
+                a = a + dpp_f<0x4E>(a);
+                a = a + dpp_f<0xB1>(a);
+                r[m] = a;
+            }
+            out[v] = MODE == GM_GATEUP ? hg_silu_l(r[0], tab) * r[NM - 1] : r[0];   // (every lane)
         }
-        a = a + dpp_f<0x4E>(a);
-        a = a + dpp_f<0xB1>(a);
-        acc[v] = a;
-    }
-    if constexpr (MODE == GM_GATEUP) {
-        if (mat == 1) {
+        const uint32_t ei = 2 * p + k;
+        if (j == 0 && ei < ne) {
+            float *yo = g.y + (size_t)g.out_row[tile.entry0 + ei] * g.ys;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) up_sum[cg][v][lane] = acc[v];
-        }
-        __syncthreads();
-        if (mat == 1) return;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const float a = hg_silu_l(acc[v], tab) * up_sum[cg][v][lane];   // every lane (a lane exchange)
-            const uint32_t rl = r0 + 8 * (v / 4) + 4 * h + v % 4;
-            if (j == 0 && valid && rl < g.rows) g.y[(size_t)g.out_row[e] * g.ys + rl] = a;
-        }
-        return;
-    }
-    if (j == 0 && valid) {
-        float *yo = g.y + (size_t)g.out_row[e] * g.ys;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const uint32_t rl = r0 + 8 * (v / 4) + 4 * h + v % 4;
-            if (rl < g.rows) {
-                if (MODE == GM_RESID) yo[rl] = yo[rl] + acc[v];
-                else yo[rl] = acc[v];
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t rl = r0 + 4 * gq + v;
+                if (rl < g.rows) {
+                    if (MODE == GM_RESID) yo[rl] = yo[rl] + out[v];
+                    else yo[rl] = out[v];
+                }
             }
         }
     }
@@ -738,36 +759,34 @@ void launch_b_quant_rows(hipStream_t st, const float *x, uint32_t xs, uint32_t n
 }
 
 // Column tiles of tt entries: 8 (two row tiles per workgroup; gate/up: both matrices) or 16.
-bool launch_b_gemm(hipStream_t st, int mode, uint32_t tt, const GemmArgs &a, uint32_t max_tiles) {
+bool launch_b_gemm(hipStream_t st, int mode, const GemmArgs &a, uint32_t max_tiles) {
     const Q8Mat &M = a.W[0];
     if (a.W[1].qs && a.W[1].sc_f32 != M.sc_f32) return false;
+    if (mode == GM_GATEUP && (a.U[0].sc_f32 != M.sc_f32 || (a.U[1].qs && a.U[1].sc_f32 != M.sc_f32))) return false;
+    const size_t lds = gemm_lds(M.nc);
+    if (lds > 64 * 1024) return false;
+    const dim3 grid(div_up(a.rows, 64), max_tiles);
+#define GEMM_L(S, MD, DD, FK) BLAUNCH((k_gemm16<S, MD, DD, FK>), grid, dim3(256), lds, st, a)
+#define GEMM_D(S, MD, DMAX)                                                                                  \
+    if (M.nb % 4 != 0) GEMM_L(S, MD, 1, false);                                                              \
+    else if (DMAX >= 8 && M.nc % 8 == 0) GEMM_L(S, MD, (DMAX >= 8 ? 8 : 4), true);                          \
+    else if (DMAX >= 4 && M.nc % 4 == 0) GEMM_L(S, MD, 4, true);                                             \
+    else if (M.nc % 2 == 0) GEMM_L(S, MD, 2, true);                                                          \
+    else GEMM_L(S, MD, 1, true);
     const bool f32s = M.sc_f32 != 0;
-#define GEMM_L(S, MD, WR)                                                                                     \
-    BLAUNCH((k_gemm_dec<S, MD, WR>), dim3(div_up(a.rows, 32 * (WR)), max_tiles), dim3(256), 0, st, a)
-    if (mode == GM_GATEUP) {
-        if (tt != 8) return false;
-        if (f32s) GEMM_L(true, GM_GATEUP, 1);
-        else GEMM_L(false, GM_GATEUP, 1);
-        return true;
+    switch (mode) {
+    case GM_GATEUP:
+        if (f32s) { GEMM_D(true, GM_GATEUP, 2) } else { GEMM_D(false, GM_GATEUP, 2) }   // (two matrices: a shallower ring, two waves per SIMD)
+        break;
+    case GM_STORE:
+        if (f32s) { GEMM_D(true, GM_STORE, 4) } else { GEMM_D(false, GM_STORE, 8) }
+        break;
+    case GM_RESID:
+        if (f32s) { GEMM_D(true, GM_RESID, 4) } else { GEMM_D(false, GM_RESID, 8) }
+        break;
+    default: return false;
     }
-    if (tt != 8 && tt != 16) return false;
-    if (mode == GM_STORE) {
-        if (tt == 8) {
-            if (f32s) GEMM_L(true, GM_STORE, 2);
-            else GEMM_L(false, GM_STORE, 2);
-        } else {
-            if (f32s) GEMM_L(true, GM_STORE, 1);
-            else GEMM_L(false, GM_STORE, 1);
-        }
-    } else {
-        if (tt == 8) {
-            if (f32s) GEMM_L(true, GM_RESID, 2);
-            else GEMM_L(false, GM_RESID, 2);
-        } else {
-            if (f32s) GEMM_L(true, GM_RESID, 1);
-            else GEMM_L(false, GM_RESID, 1);
-        }
-    }
+#undef GEMM_D
 #undef GEMM_L
     return true;
 }
