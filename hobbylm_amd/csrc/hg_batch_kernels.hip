@@ -55,11 +55,12 @@ __global__ __launch_bounds__(256) void k_b_quant_rows(const float *__restrict__ 
 // ------------------------------------------------------------------ MFMA GEMM, decode order
 // y[out_row[e]][row] (+)= (W x_{act_row[e]})[row] for the entries e of each column tile (at most
 // 8) and the rows of its matrix group, in qrow_dot_avx2's order (see the file comment).
-// Workgroup = 4 waves over 64 rows (blockIdx.x) of one column tile (blockIdx.y; tiles past
-// *n_tiles exit); each wave owns 16 rows and computes every entry of the tile, so its weight
-// loads are its own (a CU streams distinct rows) and each is used by the 4 entry pairs.  The
-// tile's activations (quants and block scales of its <= 8 entries) are staged in LDS first; the
-// wave streams its rows' chunks through a register ring of D chunks.  One
+// Workgroup = 4 waves over 16 PPW rows (blockIdx.x) of one column tile (blockIdx.y; tiles past
+// *n_tiles exit); a wave owns 16 rows and PPW of the tile's 4 entry pairs (4 / PPW waves share a
+// row tile through L1), so with PPW = 4 its weight loads are its own and each serves all the
+// tile's entries, and smaller PPW spread small GEMMs over more waves.  The tile's activations
+// (quants and block scales of its <= 8 entries) are staged in LDS first; the wave streams its
+// rows' chunks through a register ring of D chunks.  One
 // v_mfma_i32_16x16x32_i8 per (block, entry pair): lane l supplies A row l % 16 and B column
 // l % 16 = (entry 2p + (l % 16) / 8, lane j = l % 8) for K group g = l / 16 (8 bytes: block
 // elements 8g .. 8g + 7, i.e. the reference lanes 2g and 2g + 1 -- in the device row layout the
@@ -72,9 +73,11 @@ __global__ __launch_bounds__(256) void k_b_quant_rows(const float *__restrict__ 
 // chunk's padding blocks are skipped).
 __host__ __device__ inline size_t gemm_lds(uint32_t nc) { return (size_t)8 * nc * (CHUNK_BYTES + 16); }
 
-template <bool SCF32, int MODE, int D, bool FULLK>
+template <bool SCF32, int MODE, int D, bool FULLK, int PPW>
 __global__ __launch_bounds__(256) void k_gemm16(GemmArgs g) {
     static_assert(FULLK || D == 1, "a partial last chunk: one chunk per group");
+    static_assert(PPW == 1 || PPW == 2 || PPW == 4, "entry pairs per wave");
+    constexpr uint32_t WPR = 4 / PPW;   // waves per row tile
     constexpr int NM = MODE == GM_GATEUP ? 2 : 1;   // matrices per wave
     typedef typename ScaleVec<SCF32>::T SV;
     extern __shared__ __align__(16) uint8_t xs[];   // [8 entries][nc][128] quants, then [8][nc][4] scales
@@ -101,7 +104,8 @@ __global__ __launch_bounds__(256) void k_gemm16(GemmArgs g) {
         *reinterpret_cast<v4f *>(xds + 4 * i) = v;
     }
     __syncthreads();
-    const uint32_t r0 = blockIdx.x * 64 + (uint32_t)wave * 16;   // this wave's rows within the group
+    const uint32_t r0 = blockIdx.x * 16 * PPW + ((uint32_t)wave / WPR) * 16;   // this wave's rows within the group
+    const uint32_t p0 = ((uint32_t)wave % WPR) * PPW;                           // and its first entry pair
     if (r0 >= g.rows) return;   // (uniform per wave; after the workgroup's only barrier)
     const WaveExpTab tab = WaveExpTab::load(lane);
     const uint32_t gq = (uint32_t)lane >> 4, cc = (uint32_t)lane & 15, k = cc >> 3, j = cc & 7;
@@ -130,11 +134,11 @@ __global__ __launch_bounds__(256) void k_gemm16(GemmArgs g) {
             for (int v = 0; v < 4; ++v) d.s[m][v] = srow[m][v][c];
         }
     };
-    float acc[NM][4][4];   // [matrix][entry pair][row v]
+    float acc[NM][PPW][4];   // [matrix][entry pair][row v]
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
+        for (int p = 0; p < PPW; ++p)
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[m][p][v] = 0.0f;
     auto compute = [&](const Ch &d, uint32_t c) {
@@ -144,9 +148,9 @@ __global__ __launch_bounds__(256) void k_gemm16(GemmArgs g) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) unpack_scales(d.s[m][v], sw[m][v]);
 #pragma unroll
-        for (uint32_t p = 0; p < 4; ++p) {
-            if (p < np) {   // (uniform)
-                const uint32_t ei = 2 * p + k;   // this lane's entry of the pair
+        for (uint32_t p = 0; p < PPW; ++p) {
+            if (p0 + p < np) {   // (uniform)
+                const uint32_t ei = 2 * (p0 + p) + k;   // this lane's entry of the pair
                 const v4i b4 = *reinterpret_cast<const v4i *>(xs + ((size_t)ei * nc + c) * CHUNK_BYTES + j * 16);
                 const v4f dx4 = *reinterpret_cast<const v4f *>(xds + ((size_t)ei * nc + c) * 4);
                 const int bw[4] = {b4.x, b4.y, b4.z, b4.w};
@@ -191,8 +195,8 @@ __global__ __launch_bounds__(256) void k_gemm16(GemmArgs g) {
     }
     // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) over the 8 lanes j of each (row, entry), then the stores
 #pragma unroll
-    for (uint32_t p = 0; p < 4; ++p) {
-        if (p >= np) break;   // (uniform)
+    for (uint32_t p = 0; p < PPW; ++p) {
+        if (p0 + p >= np) break;   // (uniform)
         float out[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -210,7 +214,7 @@ __global__ __launch_bounds__(256) void k_gemm16(GemmArgs g) {
             }
             out[v] = MODE == GM_GATEUP ? hg_silu_l(r[0], tab) * r[NM - 1] : r[0];   // (every lane)
         }
-        const uint32_t ei = 2 * p + k;
+        const uint32_t ei = 2 * (p0 + p) + k;
         if (j == 0 && ei < ne) {
             float *yo = g.y + (size_t)g.out_row[tile.entry0 + ei] * g.ys;
 #pragma unroll
@@ -758,31 +762,37 @@ void launch_b_quant_rows(hipStream_t st, const float *x, uint32_t xs, uint32_t n
     BLAUNCH(k_b_quant_rows, dim3(div_up(n_elems / QK, 32), rows), dim3(256), 0, st, x, xs, n_elems, q, qs, dq, ds);
 }
 
-// Column tiles of tt entries: 8 (two row tiles per workgroup; gate/up: both matrices) or 16.
 bool launch_b_gemm(hipStream_t st, int mode, const GemmArgs &a, uint32_t max_tiles) {
     const Q8Mat &M = a.W[0];
     if (a.W[1].qs && a.W[1].sc_f32 != M.sc_f32) return false;
     if (mode == GM_GATEUP && (a.U[0].sc_f32 != M.sc_f32 || (a.U[1].qs && a.U[1].sc_f32 != M.sc_f32))) return false;
     const size_t lds = gemm_lds(M.nc);
     if (lds > 64 * 1024) return false;
-    const dim3 grid(div_up(a.rows, 64), max_tiles);
-#define GEMM_L(S, MD, DD, FK) BLAUNCH((k_gemm16<S, MD, DD, FK>), grid, dim3(256), lds, st, a)
-#define GEMM_D(S, MD, DMAX)                                                                                  \
+    // entry pairs per wave: 4 (each weight load serves the whole tile) unless that leaves fewer
+    // than 1024 waves, then 2; a ring of 2 chunks (occupancy over depth: measured on the 500M
+    // shapes, 2 beats 4 and 8 for every GEMM of the step)
+    const uint32_t nrt = div_up(a.rows, 16), cap = max_tiles * nrt;
+    const uint32_t ppw = cap >= 1024 ? 4u : 2u;
+    const dim3 grid(div_up(a.rows, 16 * ppw), max_tiles);
+#define GEMM_L(S, MD, DD, FK)                                                                                \
+    do {                                                                                                     \
+        if (ppw == 4) BLAUNCH((k_gemm16<S, MD, DD, FK, 4>), grid, dim3(256), lds, st, a);                    \
+        else BLAUNCH((k_gemm16<S, MD, DD, FK, 2>), grid, dim3(256), lds, st, a);                             \
+    } while (0)
+#define GEMM_D(S, MD)                                                                                        \
     if (M.nb % 4 != 0) GEMM_L(S, MD, 1, false);                                                              \
-    else if (DMAX >= 8 && M.nc % 8 == 0) GEMM_L(S, MD, (DMAX >= 8 ? 8 : 4), true);                          \
-    else if (DMAX >= 4 && M.nc % 4 == 0) GEMM_L(S, MD, 4, true);                                             \
     else if (M.nc % 2 == 0) GEMM_L(S, MD, 2, true);                                                          \
     else GEMM_L(S, MD, 1, true);
     const bool f32s = M.sc_f32 != 0;
     switch (mode) {
     case GM_GATEUP:
-        if (f32s) { GEMM_D(true, GM_GATEUP, 2) } else { GEMM_D(false, GM_GATEUP, 2) }   // (two matrices: a shallower ring, two waves per SIMD)
+        if (f32s) { GEMM_D(true, GM_GATEUP) } else { GEMM_D(false, GM_GATEUP) }
         break;
     case GM_STORE:
-        if (f32s) { GEMM_D(true, GM_STORE, 4) } else { GEMM_D(false, GM_STORE, 8) }
+        if (f32s) { GEMM_D(true, GM_STORE) } else { GEMM_D(false, GM_STORE) }
         break;
     case GM_RESID:
-        if (f32s) { GEMM_D(true, GM_RESID, 4) } else { GEMM_D(false, GM_RESID, 8) }
+        if (f32s) { GEMM_D(true, GM_RESID) } else { GEMM_D(false, GM_RESID) }
         break;
     default: return false;
     }
