@@ -65,11 +65,12 @@ bool launch_b_gemm(hipStream_t st, int mode, const GemmArgs &a, uint32_t max_til
 bool launch_b_qk_rope_append(hipStream_t st, uint32_t hd, float *qkv, uint32_t qkv_stride, const float *qn,
                              const float *kn, float eps, const float *cs, const float *sn, const uint32_t *pos,
                              const PagedKV &kv, uint32_t n);
-// Scores, softmax and P.V of n sequences over their pages; o [n][n_heads * hd].  false if
-// the head size or the context bound is not supported.
+// Scores, softmax and P.V of n sequences over their pages; o [n][n_heads * hd]; *err |= 1 if
+// a bounded wait of the P.V hand-off ran out.  false if the head size or the context bound is
+// not supported.
 bool launch_b_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t qkv_stride, const uint32_t *pos,
                         const uint32_t *order, const PagedKV &kv, uint32_t n, uint32_t max_ctx, float *scores,
-                        float *pmax, float *o);
+                        float *pmax, float *o, uint32_t *err);
 // order[r] = the sequence of rank r by length, longest first.
 void launch_b_order(hipStream_t st, const uint32_t *pos, uint32_t n, uint32_t *order);
 // Floats per row of attention scores (one row per (sequence, query head)): max_ctx rounded up

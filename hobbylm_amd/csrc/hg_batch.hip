@@ -39,7 +39,7 @@ struct hg_batch {
     std::vector<uint32_t> lens, bt_host;   // per sequence: length, block table [max_seqs][bt_stride]
     std::vector<uint32_t> n_bt;            // pages assigned per sequence
     DevBuf kpool, vpool;                   // [L][n_pages][n_kv][PAGE][hd]
-    DevBuf bt, pos, tokens, step, seq_order;
+    DevBuf bt, pos, tokens, step, err, seq_order;
     DevBuf x, xq, xd, qkv, scores, pmax, o, oq, od;
     DevBuf topk_idx, topk_w, order, rec_idx, rec_w;
     DevBuf ent_act, ent_out, etiles, n_etiles;
@@ -112,7 +112,7 @@ void enqueue_step(hg_batch *b) {
                                      c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), pos, kv, n))
             note_launch_error(hipErrorInvalidConfiguration, "QK-norm / RoPE");
         if (!launch_b_attention(st, hd, b->qkv.as<float>(), qw, pos, b->seq_order.as<uint32_t>(), kv, n, b->max_ctx,
-                                b->scores.as<float>(), b->pmax.as<float>(), b->o.as<float>()))
+                                b->scores.as<float>(), b->pmax.as<float>(), b->o.as<float>(), b->err.as<uint32_t>()))
             note_launch_error(hipErrorInvalidConfiguration, "paged attention");
         launch_b_quant_rows(st, b->o.as<float>(), qd, qd, n, b->oq.as<uint8_t>(), ncq * CHUNK_BYTES, b->od.as<float>(),
                             ncq * 4);
@@ -254,6 +254,19 @@ int upload_state(hg_batch *b, const uint32_t *tokens, uint32_t n) {
     return HG_OK;
 }
 
+// The device error word of the step's bounded waits (then cleared).
+int check_err(hg_batch *b) {
+    uint32_t e = 0;
+    HIP_TRY(hipMemcpyAsync(&e, b->err.p, 4, hipMemcpyDeviceToHost, b->st));
+    HIP_TRY(hipStreamSynchronize(b->st));
+    if (e) {
+        HIP_TRY(hipMemsetAsync(b->err.p, 0, 4, b->st));
+        HIP_TRY(hipStreamSynchronize(b->st));
+        return fail(HG_ERR_DEVICE, "a batched attention hand-off wait exceeded its bound");
+    }
+    return HG_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -294,7 +307,7 @@ int hg_batch_new(const hg_model *m, uint32_t max_seqs, uint32_t max_ctx, uint32_
         const uint32_t nch = div_up(max_ctx, ACH);
         if ((rc = b->kpool.alloc(pool)) || (rc = b->vpool.alloc(pool)) ||
             (rc = b->bt.alloc((size_t)S * b->bt_stride * 4)) || (rc = b->pos.alloc((size_t)S * 4)) ||
-            (rc = b->tokens.alloc((size_t)S * 4)) || (rc = b->step.alloc(4)) ||
+            (rc = b->tokens.alloc((size_t)S * 4)) || (rc = b->step.alloc(4)) || (rc = b->err.alloc(4)) ||
             (rc = b->seq_order.alloc((size_t)S * 4)) ||
             (rc = b->x.alloc((size_t)S * d * 4)) || (rc = b->xq.alloc((size_t)S * ncd * CHUNK_BYTES)) ||
             (rc = b->xd.alloc((size_t)S * ncd * 16)) || (rc = b->qkv.alloc((size_t)S * (qd + 2 * kvd) * 4)) ||
@@ -316,6 +329,7 @@ int hg_batch_new(const hg_model *m, uint32_t max_seqs, uint32_t max_ctx, uint32_
         HIP_TRY(hipMemset(b->kpool.p, 0, b->kpool.n));
         HIP_TRY(hipMemset(b->vpool.p, 0, b->vpool.n));
         HIP_TRY(hipMemset(b->bt.p, 0, b->bt.n));
+        HIP_TRY(hipMemset(b->err.p, 0, 4));
         HIP_TRY(hipMemset(b->rec_idx.p, 0xff, b->rec_idx.n));
         HIP_TRY(hipMemset(b->rec_w.p, 0, b->rec_w.n));
         // identity entries and the plain column tiles of every batch size
@@ -466,7 +480,7 @@ int hg_batch_forward(const hg_model *m, hg_batch *b, const uint32_t *tokens, uin
             HIP_TRY(hipMemcpyAsync(logits, b->logits.p, (size_t)n * m->c.vocab_size * 4, hipMemcpyDeviceToHost, b->st));
         std::vector<uint32_t> ids(n);
         HIP_TRY(hipMemcpyAsync(ids.data(), b->out_ids.p, (size_t)n * 4, hipMemcpyDeviceToHost, b->st));
-        HIP_TRY(hipStreamSynchronize(b->st));
+        if ((rc = check_err(b))) return rc;
         if (next) memcpy(next, ids.data(), (size_t)n * 4);
         for (uint32_t s = 0; s < n; ++s) b->lens[s] += 1;
         return HG_OK;
@@ -487,7 +501,7 @@ int hg_batch_decode_greedy(const hg_model *m, hg_batch *b, const uint32_t *first
         for (uint32_t i = 0; i < n_steps; ++i)
             if ((rc = run_step(b, n))) return rc;
         HIP_TRY(hipMemcpyAsync(out_ids, b->out_ids.p, (size_t)n_steps * n * 4, hipMemcpyDeviceToHost, b->st));
-        HIP_TRY(hipStreamSynchronize(b->st));
+        if ((rc = check_err(b))) return rc;
         for (uint32_t s = 0; s < n; ++s) b->lens[s] += n_steps;
         return HG_OK;
     });

@@ -585,6 +585,232 @@ __global__ __launch_bounds__(64) void k_b_pv(const float *__restrict__ probs, ui
     if (hr < rep) o_out[((size_t)s * n_heads + g * rep + hr) * HD + es + el] = o;
 }
 
+// ------------------------------------------------------------------ paged attention: P.V, split
+// The same chains as k_b_pv with the rounded products formed by a second wave: workgroup = 2
+// waves for one (sequence, kv head, group of 4 query heads, slice of 16 elements).  The
+// producer (wave 1, lane = (slot quad q, element e)) loads each page's V slice (one 16-byte load:
+// 4 positions of element e) and the 4 heads' probabilities of those positions, and writes the
+// 16 products p * v (+0 past the context) into an LDS ring of PV2_NS slots of PV2_G pages, laid
+// out [q][head][element][4 positions]; the chain wave (lane = (head, element)) reads 16
+// positions of its chain per page with 4 conflict-free 16-byte reads and only adds.  Hand-offs:
+// ready[slot] = group + 1 (producer), done = groups consumed (chain), both plain LDS words --
+// the LDS executes one wave's operations in order, so a flag written after the data (and read
+// before it) orders them without waits; only the compiler is fenced.  Every wait is bounded and
+// reports *err.  Workgroups are dealt longest sequence first; the slices of one (sequence,
+// kv head) get ids equal mod 8.
+constexpr uint32_t PV2_G = 4, PV2_NS = 4, PV2_R = 32;   // pages per slot, ring slots, producer V ring (pages)
+constexpr uint32_t PV2_NP = 3;                          // producer waves
+constexpr size_t PV2_LDS_MAX = 96 * 1024;
+constexpr uint32_t PV_SPIN_CAP = 1u << 22;
+constexpr uint32_t PV2_PROB_FLOATS = PV2_NP * 2 * 4 * (PV2_G * PAGE + 4);   // the producers' probability rows
+__host__ __device__ inline size_t pv2_lds(uint32_t max_ctx) {
+    return (size_t)PV2_NS * PV2_G * 4096 + (size_t)div_up(div_up(max_ctx, PAGE), 4) * 16 + PV2_PROB_FLOATS * 4;
+}
+#define PV2_COMPILER_FENCE() asm volatile("" ::: "memory")
+
+template <int HD>
+__global__ __launch_bounds__(64 * (PV2_NP + 1)) void k_b_pv2(const float *__restrict__ probs, uint32_t sc_stride,
+                                               const uint32_t *__restrict__ pos, const uint32_t *__restrict__ order,
+                                               PagedKV kv, uint32_t n_seq, float *o_out, uint32_t *err) {
+    constexpr uint32_t EW = 16, WPE = HD / EW, G = PV2_G, NS = PV2_NS, R = PV2_R;
+    static_assert(R % G == 0, "whole slots per register ring");
+    extern __shared__ __align__(16) float lds[];
+    v4f *ring = reinterpret_cast<v4f *>(lds);   // [NS][G][q 4][head 4][element 16] x 4 positions
+    float *pw_base = lds + NS * G * 1024;                                   // the producer's probability rows
+    uint32_t *btl = reinterpret_cast<uint32_t *>(pw_base + PV2_PROB_FLOATS);   // the block table
+    __shared__ uint32_t ready[NS], done;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n_heads = kv.n_heads, n_kv = kv.n_kv, rep = n_heads / n_kv;
+    const uint32_t wpk = div_up(rep, 4) * WPE;   // workgroups per (sequence, kv head)
+    uint32_t key, w;
+    {
+        const uint32_t L = blockIdx.x, nkeys = n_seq * n_kv;
+        if (nkeys % 8 == 0) {
+            const uint32_t slot = L / 8;
+            key = L % 8 + 8 * (slot / wpk);
+            w = slot % wpk;
+        } else {
+            key = L / wpk;
+            w = L % wpk;
+        }
+    }
+    const uint32_t s = order[key / n_kv], g = key % n_kv, n = pos[s] + 1, npg = div_up(n, PAGE), ngr = div_up(npg, G);
+    const uint32_t *bts = kv.bt + (size_t)s * kv.bt_stride;
+    for (uint32_t i = threadIdx.x; i < npg; i += 64 * (PV2_NP + 1)) btl[i] = bts[i];
+    if (threadIdx.x < NS) ready[threadIdx.x] = 0;
+    if (threadIdx.x == 0) done = 0;
+    __syncthreads();
+    const uint32_t hb = (w / WPE) * 4, es = (w % WPE) * EW;   // head group, element slice
+    if (wave >= 1) {
+        // ---------------- producers: wave 1 + pp (pp < NP) writes the groups gi = pp, pp + NP, ...
+        // lane = (slot quad q, element e).  A producer's local page k is page k % G of its
+        // local group m = k / G (global group NP m + pp).  V: one 16-byte load per page through a
+        // register ring of R local pages.  Probabilities: per local group (G pages, 16 G
+        // positions), each lane loading 4 of its 4 x 16 G values two groups ahead, staged into an
+        // LDS row per head (double buffered) at the end of the group before, and read back one
+        // page ahead (4 broadcast 16-byte reads).
+        constexpr uint32_t PB = G * PAGE, PLS = PB + 4;   // positions per group, padded row
+        constexpr uint32_t NP = PV2_NP;
+        static_assert(PB == 64 && NP * 2 * 4 * PLS == PV2_PROB_FLOATS, "probability rows");
+        static_assert(R % (2 * G) == 0, "group parity constant across ring passes");
+        const uint32_t pp = (uint32_t)wave - 1;
+        float *pw = pw_base + pp * 2 * 4 * PLS;   // [2][4 heads][PLS]
+        const uint32_t q = (uint32_t)lane >> 4, e = (uint32_t)lane & 15;
+        const float *prb = probs + ((size_t)s * n_heads + g * rep) * sc_stride;
+        const float *vg = kv.v + kv_tile(0, g, n_kv, HD) + (size_t)(q * HD + es + e) * 4;
+        const size_t pstride = (size_t)n_kv * HD * PAGE;
+        auto gpage = [&](uint32_t k) { return (NP * (k / G) + pp) * G + k % G; };   // local page -> page
+        v4f vr[R];
+        float pn[2][4];
+        auto load_probs = [&](float (&d)[4], uint32_t m) {   // local group m; value i: head i, position lane
+            const uint32_t t = min((NP * m + pp) * PB + (uint32_t)lane, n - 1);
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) d[i] = prb[(size_t)min(hb + i, rep - 1) * sc_stride + t];
+        };
+        auto stage_probs = [&](const float (&d)[4], uint32_t buf) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) pw[(buf * 4 + i) * PLS + lane] = d[i];
+        };
+        auto read_probs = [&](v4f (&d)[4], uint32_t k) {   // local page k's 4 positions 4q .. of each head
+            const float *src = pw + ((k / G) % 2) * 4 * PLS + (k % G) * 16 + 4 * q;
+#pragma unroll
+            for (uint32_t h = 0; h < 4; ++h) d[h] = *reinterpret_cast<const v4f *>(src + h * PLS);
+        };
+        auto id_of = [&](uint32_t k) { return btl[min(gpage(k), npg - 1)]; };   // (clamped to the context's pages)
+        // (issue order as in the loop: the loop's waits hold for its first pass)
+        load_probs(pn[0], 0);
+        load_probs(pn[1], 1);
+        const uint32_t ids0 = id_of(lane);   // local pages 0 .. R - 1
+#pragma unroll
+        for (uint32_t u = 0; u < R; ++u) {
+            vr[u] = *reinterpret_cast<const v4f *>(vg + (size_t)__builtin_amdgcn_readlane(ids0, u) * pstride);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        uint32_t ids_nx = id_of(R + lane);
+        stage_probs(pn[0], 0);
+        load_probs(pn[0], 2);
+        v4f pc[4], pn4[4];
+        read_probs(pc, 0);
+        // local pages in blocks of R (the ring's loads run past the producer's last group; those
+        // pages are not written)
+        const uint32_t npr = (ngr > pp ? div_up(ngr - pp, NP) : 0u) * G;
+        uint32_t dc = 0;
+        for (uint32_t k0 = 0; k0 < npr; k0 += R) {
+            const uint32_t ids = ids_nx;
+            ids_nx = id_of(k0 + 2 * R + lane);
+#pragma unroll
+            for (uint32_t u = 0; u < R; ++u) {
+                const uint32_t k = k0 + u, gi = NP * (k / G) + pp, sl = gi % NS, kg = gpage(k);
+                if (u % G == G - 1) {   // the next local page starts local group m: stage it, load m + 2
+                    const uint32_t m = (k + 1) / G;
+                    stage_probs(pn[(u / G + 1) % 2], (u / G + 1) % 2);
+                    load_probs(pn[(u / G + 1) % 2], m + 2);
+                }
+                read_probs(pn4, k + 1);
+                if (gi < ngr) {   // (uniform; pages of groups past the last one are only loaded)
+                    if (u % G == 0 && gi >= NS && dc < gi - NS + 1) {   // the slot's previous group consumed
+                        uint32_t it = 0;   // (dc: the last count read; read again only when it is too low)
+                        while ((dc = __hip_atomic_load(&done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < gi - NS + 1) {
+                            if (++it > PV_SPIN_CAP) {
+                                if (lane == 0) atomicOr(err, 1u);
+                                break;
+                            }
+                            __builtin_amdgcn_s_sleep(1);
+                        }
+                        PV2_COMPILER_FENCE();
+                    }
+                    v4f *dst = ring + (size_t)(sl * G + u % G) * 256 + q * 64 + e;
+                    const v4f vv = vr[u];
+                    if (16 * kg + 16 <= n) {   // (uniform) a full page
+#pragma unroll
+                        for (uint32_t h = 0; h < 4; ++h)
+                            dst[h * 16] = v4f{pc[h].x * vv.x, pc[h].y * vv.y, pc[h].z * vv.z, pc[h].w * vv.w};
+                    } else {   // positions t = 16 k + 4 q + c < n only
+                        const uint32_t t = 16 * kg + 4 * q;
+#pragma unroll
+                        for (uint32_t h = 0; h < 4; ++h)
+                            dst[h * 16] = v4f{t < n ? pc[h].x * vv.x : 0.0f, t + 1 < n ? pc[h].y * vv.y : 0.0f,
+                                              t + 2 < n ? pc[h].z * vv.z : 0.0f, t + 3 < n ? pc[h].w * vv.w : 0.0f};
+                    }
+                    if (u % G == G - 1) {
+                        PV2_COMPILER_FENCE();   // (the slot's data written before its flag)
+                        if (lane == 0)
+                            __hip_atomic_store(&ready[sl], gi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    }
+                }
+                vr[u] = *reinterpret_cast<const v4f *>(vg + (size_t)__builtin_amdgcn_readlane(ids, u) * pstride);
+#pragma unroll
+                for (uint32_t h = 0; h < 4; ++h) pc[h] = pn4[h];
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        return;
+    }
+    // ---------------- chain
+    const uint32_t hl = (uint32_t)lane >> 4;
+    float o = 0.0f;
+    auto poll = [&](uint32_t gi) {
+        return __hip_atomic_load(&ready[gi % NS], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    };
+    auto wait_from = [&](uint32_t f, uint32_t gi) {   // f: the flag read early; spin only if not yet set
+        uint32_t it = 0;
+        while (f != gi + 1) {
+            if (++it > PV_SPIN_CAP) {
+                if (lane == 0) atomicOr(err, 1u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            f = poll(gi);
+        }
+        PV2_COMPILER_FENCE();
+    };
+    auto read_group = [&](v4f (&a)[G * 4], uint32_t gi) {
+        const v4f *src = ring + (size_t)(gi % NS) * G * 256 + lane;
+#pragma unroll
+        for (uint32_t i = 0; i < G * 4; ++i) a[i] = src[i * 64];   // page i / 4, quad i % 4
+    };
+    auto adds = [&](const v4f (&a)[G * 4], uint32_t i0, uint32_t i1) {
+#pragma unroll
+        for (uint32_t i = i0; i < i1; ++i) {
+            o = o + a[i].x;
+            o = o + a[i].y;
+            o = o + a[i].z;
+            o = o + a[i].w;
+        }
+    };
+    v4f A[G * 4], B[G * 4];
+    wait_from(poll(0), 0);
+    read_group(A, 0);
+    // two groups per iteration (A, B alternate): the next group's flag is read before the current
+    // group's adds and its data read half-way through them; done is raised once a group's reads
+    // are issued (the LDS executes them before the store)
+    for (uint32_t gi = 0; gi < ngr; gi += 2) {
+        const bool m1 = gi + 1 < ngr, m2 = gi + 2 < ngr;
+        const uint32_t f1 = poll(gi + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        adds(A, 0, G * 2);
+        if (m1) {
+            wait_from(f1, gi + 1);
+            read_group(B, gi + 1);
+        }
+        PV2_COMPILER_FENCE();
+        if (lane == 0) __hip_atomic_store(&done, gi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        adds(A, G * 2, G * 4);
+        if (!m1) break;
+        const uint32_t f2 = poll(gi + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        adds(B, 0, G * 2);
+        if (m2) {
+            wait_from(f2, gi + 2);
+            read_group(A, gi + 2);
+        }
+        PV2_COMPILER_FENCE();
+        if (lane == 0) __hip_atomic_store(&done, gi + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        adds(B, G * 2, G * 4);
+    }
+    if (hb + hl < rep) o_out[((size_t)s * n_heads + g * rep + hb + hl) * HD + es + (uint32_t)lane % 16] = o;
+}
+
 // Heads per P.V wave for rep query heads per kv head.
 inline uint32_t pv_hpw(uint32_t rep) { return rep >= 4 ? 4u : rep >= 2 ? 2u : 1u; }
 
@@ -746,11 +972,18 @@ __global__ void k_b_step_advance(uint32_t *step) {
         if (le_ != hipSuccess) note_launch_error(le_, #kern);                                                \
     } while (0)
 
-bool batch_ctx_ok(uint32_t max_ctx) { return bsm_lds(max_ctx) <= BSM_LDS_MAX && (size_t)div_up(max_ctx, PAGE) * 4 <= 48 * 1024; }
+bool batch_ctx_ok(uint32_t max_ctx) { return bsm_lds(max_ctx) <= BSM_LDS_MAX && pv2_lds(max_ctx) <= PV2_LDS_MAX; }
 
 hipError_t init_batch_kernel_attributes() {
-    return hipFuncSetAttribute(reinterpret_cast<const void *>(&k_b_softmax), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)BSM_LDS_MAX);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_b_softmax),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)BSM_LDS_MAX);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_b_pv2<64>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)PV2_LDS_MAX);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_b_pv2<128>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)PV2_LDS_MAX);
+    return e;
 }
 
 void launch_b_embed(hipStream_t st, const float *emb, uint32_t d, const uint32_t *tokens, uint32_t n, float *x) {
@@ -819,22 +1052,21 @@ void launch_b_order(hipStream_t st, const uint32_t *pos, uint32_t n, uint32_t *o
 
 bool launch_b_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t qkv_stride, const uint32_t *pos,
                         const uint32_t *order, const PagedKV &kv, uint32_t n, uint32_t max_ctx, float *scores,
-                        float *pmax, float *o) {
+                        float *pmax, float *o, uint32_t *err) {
     if (!batch_ctx_ok(max_ctx) || (hd != 64 && hd != 128)) return false;
-    const uint32_t nch = div_up(max_ctx, ACH), rep = kv.n_heads / kv.n_kv, hpw = pv_hpw(rep);
-    const uint32_t wpk = div_up(rep, hpw) * (hd / (64 / hpw));
+    const uint32_t nch = div_up(max_ctx, ACH), rep = kv.n_heads / kv.n_kv;
+    const uint32_t wpk = div_up(rep, 4) * (hd / 16);
     const dim3 gs(nch, kv.n_kv, n), gm(n * kv.n_heads), gp(n * kv.n_kv * wpk);
-    const size_t btb = (size_t)div_up(max_ctx, PAGE) * 4;
     const uint32_t ss = b_sc_stride(max_ctx);
     if (hd == 64)
         BLAUNCH(k_b_scores<64>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, kv, scores, ss, pmax, nch);
     else
         BLAUNCH(k_b_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, kv, scores, ss, pmax, nch);
     BLAUNCH(k_b_softmax, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
-#define PV_CASE(H, P) \
-    if (hd == H && hpw == P) BLAUNCH((k_b_pv<H, P>), gp, dim3(64), btb, st, scores, ss, pos, order, kv, n, o);
-    PV_CASE(64, 1) PV_CASE(64, 2) PV_CASE(64, 4) PV_CASE(128, 1) PV_CASE(128, 2) PV_CASE(128, 4)
-#undef PV_CASE
+    if (hd == 64)
+        BLAUNCH(k_b_pv2<64>, gp, dim3(64 * (PV2_NP + 1)), pv2_lds(max_ctx), st, scores, ss, pos, order, kv, n, o, err);
+    else
+        BLAUNCH(k_b_pv2<128>, gp, dim3(64 * (PV2_NP + 1)), pv2_lds(max_ctx), st, scores, ss, pos, order, kv, n, o, err);
     return true;
 }
 
