@@ -87,11 +87,24 @@ void launch_b_page_copy(hipStream_t st, float *flat, float *pool, const uint32_t
                         uint32_t page_floats, int dir);
 void launch_b_page_fill(hipStream_t st, float *kpool, float *vpool, const uint32_t *bt, uint32_t len, uint32_t n_layers,
                         uint32_t n_kv, uint32_t hd, size_t layer_floats, uint64_t seed);
-void launch_b_combine(hipStream_t st, const float *y, const float *topk_w, uint32_t top_k, uint32_t n_slots,
-                      uint32_t d, uint32_t n, float *x);
+// order == nullptr: rank order (decode); else the ranks in ascending expert id per sequence (prompt).
+void launch_b_combine(hipStream_t st, const float *y, const float *topk_w, const uint32_t *order, uint32_t top_k,
+                      uint32_t n_slots, uint32_t d, uint32_t n, float *x);
 void launch_b_argmax(hipStream_t st, const float *logits, uint32_t V, uint32_t valid, uint32_t *pos, uint32_t *tokens,
                      uint32_t *out_ids, const uint32_t *step, uint32_t n, uint32_t feedback);
 void launch_b_step_advance(hipStream_t st, uint32_t *step);
 void note_launch_error(hipError_t e, const std::string &what);
+
+// ---- prompt path (Model::prefill, model.rs:340-439, 653-750) on the same kernels
+constexpr size_t PGEMM_LDS_MAX = 96 * 1024;   // prompt GEMM: staged activations of one column tile
+// Entries per column tile of a prompt-order GEMM over K = 128 nc (64, 32 or 16; 0: too long).
+uint32_t pgemm_tile(uint32_t nc);
+// A GEMM in Q8Tensor::matmul's order over column tiles of at most tt entries (16, 32 or 64).
+bool launch_p_gemm(hipStream_t st, int mode, const GemmArgs &a, uint32_t max_tiles, uint32_t tt);
+void launch_p_kv_store(hipStream_t st, const float *qkv, uint32_t qw, uint32_t qd, uint32_t kvd, uint32_t hd,
+                       uint32_t n_kv, uint32_t base, uint32_t rows, uint32_t cap, float *kc, float *vc);
+void launch_p_kv_pages(hipStream_t st, const float *kc, const float *vc, uint32_t cap, uint32_t n_kv, uint32_t hd,
+                       uint32_t npos, float *kpg, float *vpg);
+void launch_p_rev(hipStream_t st, uint32_t n, uint32_t *order);
 
 }  // namespace hg

@@ -167,7 +167,7 @@ void enqueue_step(hg_batch *b) {
             dn.ys = d;
             if (!launch_b_gemm(st, GM_STORE, dn, b->max_tiles_e))
                 note_launch_error(hipErrorInvalidConfiguration, "expert down GEMM");
-            launch_b_combine(st, b->y.as<float>(), b->topk_w.as<float>(), c.top_k, ns, d, n, x);
+            launch_b_combine(st, b->y.as<float>(), b->topk_w.as<float>(), nullptr, c.top_k, ns, d, n, x);
         } else {
             // dense FFN (model.rs:243-255)
             const uint32_t df = c.dense_ffn, ncf = div_up(df / QK, 4);

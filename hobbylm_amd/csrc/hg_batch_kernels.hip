@@ -229,6 +229,164 @@ __global__ __launch_bounds__(256) void k_gemm16(GemmArgs g) {
     }
 }
 
+// ------------------------------------------------------------------ MFMA GEMM, prompt order
+// y[out_row[e]][row] (+)= (W x_{act_row[e]})[row] in Q8Tensor::matmul's order (quant.rs:164-184):
+// acc = acc + (sw[b] * dx[b]) * isum_b over the blocks b in order from 0, isum_b the int8 dot of
+// the whole block (exact in any order).  One v_mfma_i32_16x16x32_i8 yields isum_b for 16 rows x
+// 16 entries with no masking: lane l supplies A row l % 16 and B column (entry) l % 16 for K
+// group g = l / 16 (block elements 8g .. 8g + 7: word t of the 16-byte halves at 32 g and
+// 32 g + 16 of a chunk, t the block within the chunk); C register v of lane l is row 4 g + v,
+// column l % 16.  Workgroup = 4 waves over 64 rows (blockIdx.x) of one column tile of at most
+// 16 NG entries (blockIdx.y; tiles past *n_tiles exit).  The tile's activations are staged in
+// LDS with entry strides of an odd number of 16-byte units, so the 16 entries read at one chunk
+// offset fall in distinct banks; each wave owns 16 rows and all of the tile's entries and streams
+// its rows' chunks through a register ring of D chunks.  The epilogue is 4 VALU operations per
+// (row, entry, block) against one MFMA per 256 of them, so the kernel is VALU-bound.
+__host__ __device__ inline uint32_t pgemm_qstride(uint32_t nc) { return nc * CHUNK_BYTES + 16; }
+__host__ __device__ inline uint32_t pgemm_sstride(uint32_t nc) { return nc * 4 + 4; }
+__host__ __device__ inline size_t pgemm_lds(uint32_t nc, uint32_t tt) {
+    return (size_t)tt * (pgemm_qstride(nc) + 4 * pgemm_sstride(nc));
+}
+
+template <bool SCF32, int MODE, int D, bool FULLK, int NG>
+__global__ __launch_bounds__(256) void k_gemm_p(GemmArgs g) {
+    static_assert(FULLK || D == 1, "a partial last chunk: one chunk per group");
+    constexpr int NM = MODE == GM_GATEUP ? 2 : 1;   // matrices per wave
+    constexpr uint32_t TT = 16 * NG;                // entries per column tile
+    typedef typename ScaleVec<SCF32>::T SV;
+    extern __shared__ __align__(16) uint8_t xs[];   // [TT][qstride] quants, then [TT][sstride] scales
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t ntl = *g.n_tiles;
+    const GemmTile tile = g.tiles[blockIdx.y];   // (read with the count: the table has gridDim.y entries)
+    if (blockIdx.y >= ntl) return;   // (uniform)
+    Q8Mat M[NM];
+    M[0] = g.W[tile.mat];
+    if constexpr (NM == 2) M[1] = g.U[tile.mat];
+    const uint32_t nc = M[0].nc, nb = M[0].nb, ne = tile.count;
+    const uint32_t qst = pgemm_qstride(nc), sst = pgemm_sstride(nc);
+    float *xds = reinterpret_cast<float *>(xs + (size_t)TT * qst);
+    for (uint32_t i = tid; i < TT * nc * 8; i += 256) {   // 16-byte pieces: entry i / (8 nc)
+        const uint32_t e = i / (nc * 8), p = i % (nc * 8);
+        v4i v = {0, 0, 0, 0};
+        if (e < ne) v = *reinterpret_cast<const v4i *>(g.aq + (size_t)g.act_row[tile.entry0 + e] * g.aqs + p * 16);
+        *reinterpret_cast<v4i *>(xs + (size_t)e * qst + p * 16) = v;
+    }
+    for (uint32_t i = tid; i < TT * nc; i += 256) {   // block scales: entry i / nc, chunk i % nc
+        const uint32_t e = i / nc, c = i % nc;
+        v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (e < ne) v = *reinterpret_cast<const v4f *>(g.ad + (size_t)g.act_row[tile.entry0 + e] * g.ads + 4 * c);
+        *reinterpret_cast<v4f *>(xds + (size_t)e * sst + 4 * c) = v;
+    }
+    __syncthreads();
+    const uint32_t r0 = blockIdx.x * 64 + (uint32_t)wave * 16;   // this wave's rows within the group
+    if (r0 >= g.rows) return;   // (uniform per wave; after the workgroup's only barrier)
+    const WaveExpTab tab = WaveExpTab::load(lane);
+    const uint32_t gq = (uint32_t)lane >> 4, cc = (uint32_t)lane & 15;
+    const uint32_t gbase = tile.grp * g.rows, rlim = gbase + g.rows - 1, ngr = div_up(ne, 16);
+    const uint8_t *wrow[NM];
+    const SV *srow[NM][4];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        wrow[m] = M[m].qs + (size_t)min(gbase + r0 + cc, rlim) * nc * CHUNK_BYTES + 32 * gq;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            srow[m][v] = reinterpret_cast<const SV *>(row_sc<SCF32>(M[m], min(gbase + r0 + 4 * gq + v, rlim)));
+    }
+    struct Ch {
+        v4i w[NM][2];
+        SV s[NM][4];
+    };
+    auto load = [&](Ch &d, uint32_t c) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const v4i *wp = reinterpret_cast<const v4i *>(wrow[m] + (size_t)c * CHUNK_BYTES);
+            d.w[m][0] = wp[0];
+            d.w[m][1] = wp[1];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) d.s[m][v] = srow[m][v][c];
+        }
+    };
+    const uint8_t *xb = xs + (size_t)cc * qst + 32 * gq;   // this lane's entry of group 0, its K group
+    const float *xd = xds + (size_t)cc * sst;
+    float acc[NM][NG][4];   // [matrix][entry group][row v]
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int q = 0; q < NG; ++q)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[m][q][v] = 0.0f;
+    auto compute = [&](const Ch &d, uint32_t c) {
+        float sw[NM][4][4];
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) unpack_scales(d.s[m][v], sw[m][v]);
+#pragma unroll
+        for (int q = 0; q < NG; ++q) {
+            if ((uint32_t)q < ngr) {   // (uniform)
+                const uint8_t *bp = xb + (size_t)q * 16 * qst + (size_t)c * CHUNK_BYTES;
+                const v4i b0 = *reinterpret_cast<const v4i *>(bp), b1 = *reinterpret_cast<const v4i *>(bp + 16);
+                const v4f dx4 = *reinterpret_cast<const v4f *>(xd + (size_t)q * 16 * sst + 4 * c);
+                const int bl[4] = {b0.x, b0.y, b0.z, b0.w}, bh[4] = {b1.x, b1.y, b1.z, b1.w};
+                const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    if (FULLK || 4 * c + t < nb) {   // (uniform; padding blocks of a partial last chunk: no add)
+                        const long B = (long)((uint64_t)(uint32_t)bl[t] | (uint64_t)(uint32_t)bh[t] << 32);
+#pragma unroll
+                        for (int m = 0; m < NM; ++m) {
+                            const int lo = t == 0 ? d.w[m][0].x : t == 1 ? d.w[m][0].y : t == 2 ? d.w[m][0].z : d.w[m][0].w;
+                            const int hi = t == 0 ? d.w[m][1].x : t == 1 ? d.w[m][1].y : t == 2 ? d.w[m][1].z : d.w[m][1].w;
+                            const long A = (long)((uint64_t)(uint32_t)lo | (uint64_t)(uint32_t)hi << 32);
+                            const v4i z = {0, 0, 0, 0};
+                            const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, z, 0, 0, 0);
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) {
+                                const float dd = sw[m][v][t] * dxs[t];
+                                acc[m][q][v] = acc[m][q][v] + dd * (float)C[v];
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    };
+    Ch ring[D];
+#pragma unroll
+    for (uint32_t u = 0; u < D; ++u) {
+        load(ring[u], min(u, nc - 1));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (uint32_t c0 = 0; c0 < nc; c0 += D) {
+#pragma unroll
+        for (uint32_t u = 0; u < D; ++u) {
+            compute(ring[u], c0 + u);
+            load(ring[u], min(c0 + D + u, nc - 1));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        if ((uint32_t)q >= ngr) break;   // (uniform)
+        float out[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            out[v] = MODE == GM_GATEUP ? hg_silu_l(acc[0][q][v], tab) * acc[NM - 1][q][v] : acc[0][q][v];   // (every lane)
+        const uint32_t ei = (uint32_t)q * 16 + cc;
+        if (ei < ne) {
+            float *yo = g.y + (size_t)g.out_row[tile.entry0 + ei] * g.ys;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t rl = r0 + 4 * gq + v;
+                if (rl < g.rows) {
+                    if (MODE == GM_RESID) yo[rl] = yo[rl] + out[v];
+                    else yo[rl] = out[v];
+                }
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ QK-norm, RoPE, paged append
 // For each sequence s (blockIdx.y) and head hh (blockIdx.x, q | k | v as the QKV rows): q and k
 // heads normed (model.rs:753-763) and rotated at pos[s] (ops.rs:155-166) in place; k and v rows
@@ -873,11 +1031,14 @@ __global__ __launch_bounds__(256) void k_b_group(const uint32_t *__restrict__ to
             tl.mat = tid < E ? 0u : 1u;
             tiles[toff + q] = tl;
         }
-        if (tid == E)   // the shared expert: every sequence, slot top_k
-            for (uint32_t sq = 0; sq < n; ++sq) {
-                act_row[off + sq] = sq;
-                out_row[off + sq] = sq * n_slots + top_k;
-            }
+    }
+    __syncthreads();
+    if (NG > E) {   // the shared expert: every sequence, slot top_k
+        const uint32_t sb = base[E];
+        for (uint32_t sq = tid; sq < n; sq += 256) {
+            act_row[sb + sq] = sq;
+            out_row[sb + sq] = sq * n_slots + top_k;
+        }
     }
     // the routed picks in (sequence, rank) order, 256 at a time: a pick's entry is its expert's
     // base + the picks of that expert in earlier waves of the chunk + its rank within its wave
@@ -912,15 +1073,20 @@ __global__ __launch_bounds__(256) void k_b_group(const uint32_t *__restrict__ to
 }
 
 // ------------------------------------------------------------------ expert combine + residual
-// x[s] += ((0 + w_0 y_0) + w_1 y_1 + ...) + y_shared (rank order; model.rs:306-323 and
-// 173-176 as k_ffn_down's decode combine).  grid (d / 256, n).
-__global__ void k_b_combine(const float *__restrict__ y, const float *__restrict__ topk_w, uint32_t top_k,
-                            uint32_t n_slots, uint32_t d, float *x) {
+// x[s] += ((0 + w_0 y_0) + w_1 y_1 + ...) + y_shared: rank order (model.rs:306-323 and 173-176,
+// as k_ffn_down's decode combine), or with `order` (the router's ranks in ascending expert id)
+// the prompt path's expert-id order (model.rs:707-731).  grid (d / 256, n).
+__global__ void k_b_combine(const float *__restrict__ y, const float *__restrict__ topk_w,
+                            const uint32_t *__restrict__ order, uint32_t top_k, uint32_t n_slots, uint32_t d,
+                            float *x) {
     const uint32_t s = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= d) return;
     const float *ys = y + (size_t)s * n_slots * d + i;
     float acc = 0.0f;
-    for (uint32_t q = 0; q < top_k; ++q) acc = acc + topk_w[s * top_k + q] * ys[(size_t)q * d];
+    for (uint32_t q = 0; q < top_k; ++q) {
+        const uint32_t r = order ? order[s * top_k + q] : q;
+        acc = acc + topk_w[s * top_k + r] * ys[(size_t)r * d];
+    }
     if (n_slots > top_k) acc = acc + ys[(size_t)top_k * d];
     x[(size_t)s * d + i] = x[(size_t)s * d + i] + acc;
 }
@@ -1122,9 +1288,111 @@ void launch_b_page_copy(hipStream_t st, float *flat, float *pool, const uint32_t
     if (npg) BLAUNCH(k_b_page_copy, dim3(npg), dim3(256), 0, st, flat, pool, bt, page_floats, dir);
 }
 
-void launch_b_combine(hipStream_t st, const float *y, const float *topk_w, uint32_t top_k, uint32_t n_slots,
-                      uint32_t d, uint32_t n, float *x) {
-    BLAUNCH(k_b_combine, dim3(div_up(d, 256), n), dim3(256), 0, st, y, topk_w, top_k, n_slots, d, x);
+void launch_b_combine(hipStream_t st, const float *y, const float *topk_w, const uint32_t *order, uint32_t top_k,
+                      uint32_t n_slots, uint32_t d, uint32_t n, float *x) {
+    BLAUNCH(k_b_combine, dim3(div_up(d, 256), n), dim3(256), 0, st, y, topk_w, order, top_k, n_slots, d, x);
+}
+
+// ====================================================================== prompt path
+// Prompt rows r = blockIdx.y at positions base + r, their k (normed and rotated) and v rows from
+// the QKV output, into a single-sequence cache layer: K [n_kv][cap][hd], V [n_kv][cap][hd] and
+// V's transposed copy [n_kv][hd][vt_stride(cap)] after it (the appends of model.rs:384-389).
+__global__ void k_p_kv_store(const float *__restrict__ qkv, uint32_t qw, uint32_t qd, uint32_t kvd, uint32_t hd,
+                             uint32_t n_kv, uint32_t base, uint32_t cap, float *kc, float *vc) {
+    const uint32_t r = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= kvd) return;
+    const uint32_t g = i / hd, e = i % hd, p = base + r;
+    const float *row = qkv + (size_t)r * qw + qd;
+    const size_t at = ((size_t)g * cap + p) * hd + e;
+    kc[at] = row[i];
+    const float v = row[kvd + i];
+    vc[at] = v;
+    vc[(size_t)n_kv * cap * hd + ((size_t)g * hd + e) * vt_stride(cap) + p] = v;
+}
+
+// Positions [0, npos) of a single-sequence cache layer into pages 0, 1, ... of PAGE positions
+// (the identity block table).  grid (div_up(npos hd, 256), n_kv).
+__global__ void k_p_kv_pages(const float *__restrict__ kc, const float *__restrict__ vc, uint32_t cap, uint32_t n_kv,
+                             uint32_t hd, uint32_t npos, float *kpg, float *vpg) {
+    const uint32_t g = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= npos * hd) return;
+    const uint32_t p = i / hd, e = i % hd;
+    const size_t src = ((size_t)g * cap + p) * hd + e, t = kv_tile(p / PAGE, g, n_kv, hd);
+    kpg[t + k_el(e, p % PAGE)] = kc[src];
+    vpg[t + v_el(e, p % PAGE, hd)] = vc[src];
+}
+
+// order[i] = n - 1 - i: prompt rows by context length, longest first.
+__global__ void k_p_rev(uint32_t n, uint32_t *order) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) order[i] = n - 1 - i;
+}
+
+void launch_p_kv_store(hipStream_t st, const float *qkv, uint32_t qw, uint32_t qd, uint32_t kvd, uint32_t hd,
+                       uint32_t n_kv, uint32_t base, uint32_t rows, uint32_t cap, float *kc, float *vc) {
+    BLAUNCH(k_p_kv_store, dim3(div_up(kvd, 256), rows), dim3(256), 0, st, qkv, qw, qd, kvd, hd, n_kv, base, cap, kc, vc);
+}
+
+void launch_p_kv_pages(hipStream_t st, const float *kc, const float *vc, uint32_t cap, uint32_t n_kv, uint32_t hd,
+                       uint32_t npos, float *kpg, float *vpg) {
+    if (npos == 0) return;
+    BLAUNCH(k_p_kv_pages, dim3(div_up(npos * hd, 256), n_kv), dim3(256), 0, st, kc, vc, cap, n_kv, hd, npos, kpg, vpg);
+}
+
+void launch_p_rev(hipStream_t st, uint32_t n, uint32_t *order) {
+    BLAUNCH(k_p_rev, dim3(div_up(n, 256)), dim3(256), 0, st, n, order);
+}
+
+uint32_t pgemm_tile(uint32_t nc) {
+    for (uint32_t tt = 64; tt >= 16; tt /= 2)
+        if (pgemm_lds(nc, tt) <= PGEMM_LDS_MAX) return tt;
+    return 0;
+}
+
+bool launch_p_gemm(hipStream_t st, int mode, const GemmArgs &a, uint32_t max_tiles, uint32_t tt) {
+    const Q8Mat &M = a.W[0];
+    if (a.W[1].qs && a.W[1].sc_f32 != M.sc_f32) return false;
+    if (mode == GM_GATEUP && (a.U[0].sc_f32 != M.sc_f32 || (a.U[1].qs && a.U[1].sc_f32 != M.sc_f32))) return false;
+    if (tt != 16 && tt != 32 && tt != 64) return false;
+    const size_t lds = pgemm_lds(M.nc, tt);
+    if (lds > PGEMM_LDS_MAX || max_tiles == 0) return false;
+    const dim3 grid(div_up(a.rows, 64), max_tiles);
+    // (each instantiation raises its dynamic LDS limit on first use)
+#define PG_L(S, MD, DD, FK, N)                                                                               \
+    do {                                                                                                     \
+        auto kf_ = k_gemm_p<S, MD, DD, FK, N>;                                                               \
+        static const hipError_t ae_ = hipFuncSetAttribute(reinterpret_cast<const void *>(kf_),               \
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize,        \
+                                                          (int)PGEMM_LDS_MAX);                               \
+        if (ae_ != hipSuccess) {                                                                             \
+            note_launch_error(ae_, "k_gemm_p LDS limit");                                                    \
+            return false;                                                                                    \
+        }                                                                                                    \
+        BLAUNCH(kf_, grid, dim3(256), lds, st, a);                                                           \
+    } while (0)
+#define PG_N(S, MD, DD, FK)                                                                                  \
+    if (tt == 64) PG_L(S, MD, DD, FK, 4);                                                                    \
+    else if (tt == 32) PG_L(S, MD, DD, FK, 2);                                                               \
+    else PG_L(S, MD, DD, FK, 1);
+#define PG_D(S, MD)                                                                                          \
+    if (M.nb % 4 == 0 && M.nc % 2 == 0) { PG_N(S, MD, 2, true) }                                             \
+    else { PG_N(S, MD, 1, false) }
+    const bool f32s = M.sc_f32 != 0;
+    switch (mode) {
+    case GM_GATEUP:
+        if (f32s) { PG_D(true, GM_GATEUP) } else { PG_D(false, GM_GATEUP) }
+        break;
+    case GM_STORE:
+        if (f32s) { PG_D(true, GM_STORE) } else { PG_D(false, GM_STORE) }
+        break;
+    case GM_RESID:
+        if (f32s) { PG_D(true, GM_RESID) } else { PG_D(false, GM_RESID) }
+        break;
+    default: return false;
+    }
+#undef PG_D
+#undef PG_N
+#undef PG_L
+    return true;
 }
 
 void launch_b_argmax(hipStream_t st, const float *logits, uint32_t V, uint32_t valid, uint32_t *pos, uint32_t *tokens,

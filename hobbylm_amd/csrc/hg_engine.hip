@@ -22,6 +22,7 @@
 #include "hg_gguf.h"
 #include "hg_kernels.h"
 #include "hg_model.h"
+#include "hg_prefill.h"
 
 using namespace hg;
 
@@ -142,6 +143,7 @@ struct hg_kv {
     hipGraphExec_t g_tail = nullptr;
     bool use_graph = true;
     LaunchTimer *timer = nullptr;  // hg_profile_step: per-dispatch timing
+    std::unique_ptr<PrefillWork> pw;   // the batched prompt path's buffers (on first use)
     ~hg_kv();
 };
 
@@ -561,6 +563,16 @@ int finish(hg_kv *kv, float *logits, uint32_t *next) {
     return HG_OK;
 }
 
+// The prompt path: all rows at once (default), or with HG_PREFILL=rows one replayed decode-shaped
+// step per row (the reference-order kernels of the decode step in prompt order).
+bool batched_prefill() {
+    static const bool rows = [] {
+        const char *e = getenv("HG_PREFILL");
+        return e && strcmp(e, "rows") == 0;
+    }();
+    return !rows;
+}
+
 int check_step(const hg_model *m, const hg_kv *kv, uint32_t pos, uint32_t n) {
     if (!m || !kv || kv->m != m) return fail(HG_ERR_ARG, "cache does not belong to this model");
     if (pos != kv->len)
@@ -740,6 +752,17 @@ int hg_prefill(const hg_model *m, hg_kv *kv, const float *inputs, uint32_t tn, f
             for (auto &g : kv->g_body)   // the captured bodies read the old buffer
                 if (g.second) (void)hipGraphExecDestroy(g.second);
             kv->g_body.clear();
+        }
+        if (kv->exact && batched_prefill() && prefill_batched_ok(m, base + tn)) {
+            if (!kv->pw) kv->pw = std::make_unique<PrefillWork>();
+            if ((rc = prefill_batched(m, *kv->pw, kv->st, inputs, base, tn, kv->kc.as<float>(), kv->vc.as<float>(),
+                                      kv->cap, kv->x.as<float>(), kv->rec_idx.as<uint32_t>(), kv->rec_w.as<float>())))
+                return rc;
+            if ((rc = set_params(kv, 0, base + tn, 0, 0, base))) return rc;
+            if ((rc = run(kv, kv->g_tail, enqueue_tail))) return rc;
+            if ((rc = finish(kv, logits, next))) return rc;
+            kv->len = base + tn;
+            return HG_OK;
         }
         HIP_TRY(hipMemcpyAsync(kv->inputs.p, inputs, rowb * tn, hipMemcpyHostToDevice, kv->st));
         if ((rc = set_params(kv, 0, base, 0, 0, base))) return rc;

@@ -70,6 +70,8 @@ PRESETS: Dict[str, Shape] = {
     # small shapes that keep every feature (dense layer, routed + shared experts, GQA,
     # a K that is not a multiple of 128) and run in milliseconds on the CPU oracle
     "tiny": Shape(128, 3, 1, 4, 2, 32, 256, 96, 8, 2, 1, 1000, context_length=512),
+    # the tiny shape with room for prompts of thousands of rows
+    "tiny_long": Shape(128, 3, 1, 4, 2, 32, 256, 96, 8, 2, 1, 1000, context_length=4096),
     "tiny_noshared": Shape(64, 2, 1, 2, 1, 32, 128, 64, 6, 3, 0, 300, context_length=256,
                            rope_theta=1e6),
     # the other router forms: softmax gating with renormalized weights, and sigmoid gating with
