@@ -301,6 +301,70 @@ def batched(args):
     print(json.dumps(out))
 
 
+def prefill_work(cfg, n):
+    """Int8 multiply-accumulates of a prompt of n rows through the Q8 matrices (each row through
+    QKV, O, the dense FFN or its top-k routed + shared experts), and the f32 multiply-adds of its
+    causal attention (q.k and p.v over positions 0..t for row t, every query head)."""
+    d, L, hd = cfg.d_model, cfg.n_layers, cfg.head_dim
+    qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    per_row = L * ((qd + 2 * kvd) * d + d * qd)
+    per_row += cfg.n_dense * 3 * cfg.dense_ffn * d
+    per_row += (L - cfg.n_dense) * (cfg.top_k + (1 if cfg.n_shared else 0)) * 3 * cfg.expert_ffn * d
+    attn = L * cfg.n_heads * hd * 2 * (n * (n + 1) // 2)
+    return per_row * n, attn
+
+
+def prefill_bench(args):
+    """Prompt processing of the 500M model into the drop-in cache (capacity = context_length):
+    a seeded prompt of --prefill rows, `warmup` untimed prompts, then the median of `repeats`
+    timed ones, each into a fresh cache (host input rows to the last row's logits)."""
+    import hobbylm_amd as hg
+    from hobbylm_amd import gguf_synth as gs
+    n = args.prefill
+    path = gs.synth_path("500M", 1)
+    m = hg.Model(path)
+    cfg = m.cfg
+    emb = np.stack([m.token_embedding(int(t)) for t in gs.prompt_ids(77, n, 50257)])
+    for _ in range(max(min(args.warmup, 2), 1)):
+        m.prefill(emb, m.new_cache())
+    times = []
+    for _ in range(args.repeats):
+        kv = m.new_cache()
+        t0 = time.perf_counter()
+        lg, _ = m.prefill(emb, kv)
+        times.append(time.perf_counter() - t0)
+        del kv
+    dt = float(np.median(times))
+    macs, attn = prefill_work(cfg, n)
+    out = {
+        "metric": "prefill tok/s (500M Q8_0, one prompt into the default cache)",
+        "value": round(n / dt, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.repeats, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 MFMA (i32 block sums) -> f32, f32 attention",
+        "data": "synthetic: random-init 500M-shaped Q8_0 GGUF (seed 1), seeded prompt rows",
+        "config": {"workload": f"prompt of {n} rows from position 0, cache capacity {cfg.context_length}",
+                   "model": "hobbylm-500M-synthetic", "parallelism": "none (1 GPU)"},
+        "work": {"int8_macs": macs, "attention_fmas": attn,
+                 "int8_TOPs": round(2 * macs / dt / 1e12, 2), "int8_peak_TOPs": 5000.0,
+                 "int8_frac": round(2 * macs / dt / 5.0e15, 5)},
+        "times_ms": [round(t * 1e3, 3) for t in times],
+    }
+    if not args.no_cpu:
+        import oracle
+        om = oracle.Model(path)
+        k = min(n, args.prefill_cpu_rows)
+        okv = om.new_cache()
+        t0 = time.perf_counter()
+        ol = om.prefill(emb[:k], okv)
+        cdt = time.perf_counter() - t0
+        gl, _ = m.prefill(emb[:k], m.new_cache())
+        out["cpu_baseline"] = {"value": round(k / cdt, 2), "unit": "tok/s", "cores": oracle.threads(),
+                               "kind": "port", "sample": f"prefill of the first {k} rows of the prompt",
+                               "model": cpu_model()}
+        out["parity"] = {"rows": k, "logits_identical": bool(np.array_equal(gl.view(np.uint32), ol.view(np.uint32)))}
+    print(json.dumps(out))
+
+
 COPY_BYTES = 256 * 2**20
 
 
@@ -385,6 +449,8 @@ def main():
     ap.add_argument("--batched", action="store_true",
                     help="the batched workload: 32 ragged sequences over a paged cache (its own JSON line)")
     ap.add_argument("--batch", type=int, default=32, help="sequences of --batched")
+    ap.add_argument("--prefill", type=int, metavar="ROWS", help="prompt-processing measurement of ROWS rows instead")
+    ap.add_argument("--prefill-cpu-rows", type=int, default=128, help="oracle-timed rows of --prefill")
     ap.add_argument("--parity-steps", type=int, default=3, help="oracle-checked steps per sequence (--batched)")
     ap.add_argument("--contiguous-pages", action="store_true",
                     help="--batched: each sequence's pages in pool order instead of a seeded shuffle")
@@ -407,6 +473,11 @@ def main():
         return
     if args.pmc_calib:
         pmc_calib()
+        return
+    if args.prefill:
+        if args.gpus != 1:
+            sys.exit("bench.py measures one GPU")
+        prefill_bench(args)
         return
     if args.batched:
         if args.gpus != 1:

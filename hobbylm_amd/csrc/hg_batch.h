@@ -106,5 +106,11 @@ void launch_p_kv_store(hipStream_t st, const float *qkv, uint32_t qw, uint32_t q
 void launch_p_kv_pages(hipStream_t st, const float *kc, const float *vc, uint32_t cap, uint32_t n_kv, uint32_t hd,
                        uint32_t npos, float *kpg, float *vpg);
 void launch_p_rev(hipStream_t st, uint32_t n, uint32_t *order);
+// Causal attention of n prompt rows (row r: positions 0 .. pos[r]) over pages shared by the
+// rows: the decode step's scores and softmax, then a P.V kernel that shares each V load
+// among the rows and heads of a wave.  Arguments as launch_b_attention.
+bool launch_p_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t qkv_stride, const uint32_t *pos,
+                        const uint32_t *order, const PagedKV &kv, uint32_t n, uint32_t max_ctx, float *scores,
+                        float *pmax, float *o, uint32_t *err);
 
 }  // namespace hg

@@ -986,9 +986,9 @@ __global__ void k_b_order(const uint32_t *__restrict__ pos, uint32_t n, uint32_t
 }
 
 // ------------------------------------------------------------------ expert grouping
-// The ffn_prefill grouping (model.rs:676-731) for one decode step of n sequences: for every
-// expert e (ascending), the (sequence, rank) pairs that picked it (sequences ascending), then
-// the shared expert with every sequence (slot top_k).  Entry i of the table: act_row = the
+// The ffn_prefill grouping (model.rs:676-731) for one step of n rows (sequences, or prompt
+// rows): for every expert e (ascending), the (row, rank) pairs that picked it, then the shared
+// expert with every row (slot top_k).  Entry i of the table: act_row = the
 // sequence (its quantized h), out_row = sequence * n_slots + slot (its row of a and y).
 // Column tiles of at most TT entries cover each expert's entries (matrix group e of set 0; the
 // shared expert's tiles use group 0 of set 1).  One workgroup.
@@ -996,7 +996,7 @@ __global__ __launch_bounds__(256) void k_b_group(const uint32_t *__restrict__ to
                                                  uint32_t E, uint32_t n_slots, uint32_t TT,
                                                  uint32_t *act_row, uint32_t *out_row, GemmTile *tiles,
                                                  uint32_t *n_tiles) {
-    __shared__ uint32_t cnt[MAX_GROUPS], base[MAX_GROUPS], wc[4][MAX_GROUPS], wa[4], wt[4];
+    __shared__ uint32_t cnt[MAX_GROUPS], base[MAX_GROUPS], wa[4], wt[4];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NP = n * top_k;
     const uint32_t NG = E + (n_slots > top_k ? 1 : 0);
     cnt[tid] = 0;   // (256 threads = MAX_GROUPS)
@@ -1008,6 +1008,7 @@ __global__ __launch_bounds__(256) void k_b_group(const uint32_t *__restrict__ to
     __syncthreads();
     // exclusive scans of the entry and tile counts over the groups (thread = group)
     const uint32_t c = tid < E ? cnt[tid] : tid < NG ? n : 0u, tc = div_up(c, TT);
+    cnt[tid] = 0;   // (now the fill count of the placement below)
     const uint32_t ia = wave_scan_u(c), it = wave_scan_u(tc);
     if (lane == 63) {
         wa[wave] = ia;
@@ -1040,35 +1041,16 @@ __global__ __launch_bounds__(256) void k_b_group(const uint32_t *__restrict__ to
             out_row[sb + sq] = sq * n_slots + top_k;
         }
     }
-    // the routed picks in (sequence, rank) order, 256 at a time: a pick's entry is its expert's
-    // base + the picks of that expert in earlier waves of the chunk + its rank within its wave
-    for (uint32_t c0 = 0; c0 < NP; c0 += 256) {
-        const uint32_t i = c0 + tid;
-        const uint32_t e = i < NP ? topk_idx[i] : 0xffffffffu;
-        const bool live = e < E;
-        for (uint32_t w = 0; w < 4; ++w) wc[w][tid] = 0;
-        __syncthreads();
-        uint32_t r = 0, m_all = 0;
-        for (uint32_t k = 0; k < 64; ++k) {   // rank among the wave's lanes with the same expert
-            const uint32_t ek = __builtin_amdgcn_readlane(e, k);
-            const uint64_t m = __builtin_amdgcn_ballot_w64(e == ek);
-            if (k == lane) {
-                r = (uint32_t)__builtin_popcountll(m & ((1ull << lane) - 1));
-                m_all = (uint32_t)__builtin_popcountll(m);
-            }
-        }
-        if (live && r + 1 == m_all) wc[wave][e] = m_all;   // the wave's last pick of e
-        __syncthreads();
-        if (live) {
-            uint32_t at = base[e] + r;
-            for (uint32_t w = 0; w < wave; ++w) at += wc[w][e];
+    // the routed picks: a pick's entry is its expert's base + a slot taken with an LDS atomic
+    // (the order of an expert's entries is arbitrary: each entry's GEMM column is its own)
+    for (uint32_t i = tid; i < NP; i += 256) {
+        const uint32_t e = topk_idx[i];
+        if (e < E) {
+            const uint32_t at = base[e] + atomicAdd(&cnt[e], 1u);
             const uint32_t sq = i / top_k;
             act_row[at] = sq;
             out_row[at] = sq * n_slots + (i - sq * top_k);
         }
-        __syncthreads();
-        if (tid < E) base[tid] += wc[0][tid] + wc[1][tid] + wc[2][tid] + wc[3][tid];
-        __syncthreads();
     }
 }
 
@@ -1325,6 +1307,184 @@ __global__ void k_p_kv_pages(const float *__restrict__ kc, const float *__restri
 // order[i] = n - 1 - i: prompt rows by context length, longest first.
 __global__ void k_p_rev(uint32_t n, uint32_t *order) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) order[i] = n - 1 - i;
+}
+
+// Scores of prompt rows (model.rs:386-391): s_t = dot(q_{r,h}, K_t) * (1/sqrt(hd)) in ops::dot's
+// order, as k_b_scores, for a block of PRB consecutive rows (blockIdx.z, longest block first)
+// and the rep query heads of kv head g (blockIdx.y) over positions [256 c, 256 c + 256)
+// (c = blockIdx.x; chunks past the block's longest row exit), and each (row, head)'s chunk
+// maximum.  Lane = position: its K row is read once and dotted with the block's rep PRB query
+// heads (scalar operands), so K is read once per block of rows instead of once per row.
+constexpr uint32_t PRB = 16;
+template <int HD>
+__global__ __launch_bounds__(256) void k_p_scores(const float *__restrict__ qkv, uint32_t qkv_stride,
+                                                  const uint32_t *__restrict__ pos, uint32_t R, PagedKV kv,
+                                                  float *scores, uint32_t sc_stride, float *pmax, uint32_t pm_stride) {
+    constexpr int MAXREP = 8;
+    __shared__ float wm[4][PRB * MAXREP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t c = blockIdx.x, g = blockIdx.y, rb0 = (gridDim.z - 1 - blockIdx.z) * PRB;
+    const uint32_t nrow = min(PRB, R - rb0), nlast = pos[rb0 + nrow - 1] + 1, t0 = c * ACH;
+    if (t0 >= nlast) return;   // (uniform)
+    const uint32_t n_heads = kv.n_heads, rep = n_heads / kv.n_kv;
+    const uint32_t t = t0 + 64 * (uint32_t)wave + (uint32_t)lane, tw = t0 + 64 * (uint32_t)wave;
+    v4f kt[HD / 4];
+    if (tw < nlast) {
+        const uint32_t tc = min(t, nlast - 1);
+        const v4f *kp = reinterpret_cast<const v4f *>(kv.k + kv_tile(kv.bt[tc / PAGE], g, kv.n_kv, HD)) + tc % PAGE;
+#pragma unroll
+        for (int i = 0; i < HD / 4; ++i) kt[i] = kp[i * PAGE];
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
+    for (uint32_t k = 0; k < nrow; ++k) {
+        const uint32_t n = pos[rb0 + k] + 1;
+        float *scb = scores + ((size_t)(rb0 + k) * n_heads + g * rep) * sc_stride;
+        for (uint32_t r = 0; r < rep; ++r) {
+            float mx = -__builtin_huge_valf();
+            if (tw < n) {   // (uniform per wave)
+                // (a wave-uniform address of read-only memory: the query comes in scalar loads)
+                const float *qr = qkv + (size_t)(rb0 + k) * qkv_stride + (size_t)(g * rep + r) * HD;
+                float acc[4][8];   // ops::dot: four 8-lane FMA accumulators over 32-wide steps
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) acc[a][l] = 0.0f;
+#pragma unroll
+                for (int i = 0; i < HD; i += 32)
+#pragma unroll
+                    for (int a = 0; a < 4; ++a)
+#pragma unroll
+                        for (int l = 0; l < 8; ++l) {
+                            const int e = i + 8 * a + l;
+                            acc[a][l] = fmaf(qr[e], kt[e / 4][e % 4], acc[a][l]);
+                        }
+                float v[8];
+#pragma unroll
+                for (int l = 0; l < 8; ++l) v[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+                const float sv = (((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]))) * scale;
+                if (t < n) {
+                    scb[(size_t)r * sc_stride + t] = sv;
+                    mx = sv;
+                }
+            }
+            for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, shfl_xor(mx, o));
+            if (lane == 0) wm[wave][k * rep + r] = mx;
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < nrow * rep; i += 256)
+        pmax[((size_t)(rb0 + i / rep) * n_heads + g * rep + i % rep) * pm_stride + c] =
+            fmaxf(fmaxf(wm[0][i], wm[1][i]), fmaxf(wm[2][i], wm[3][i]));
+}
+
+// P.V of prompt rows (model.rs:392-397): o[r][h][e] = ((0 + p_0 v_0[e]) + p_1 v_1[e]) + ... over
+// positions 0 .. n_r - 1 (n_r = pos[r] + 1), every (row, head, element) its own chain: a rounded
+// product, then the add.  A wave takes one row and the REP query heads of kv head g
+// (blockIdx.y): lane = element (HD / 64 of them per lane), REP chains per element sharing each V
+// load (16-byte loads of a page tile: 4 positions).  The probabilities are scalar operands
+// (wave-uniform loads of read-only memory), PB = 64 / REP positions of every chain per block
+// (64 scalar registers).  Workgroups of 4 waves (4 rows) are dealt longest rows first.
+template <int HD, int REP>
+__global__ __launch_bounds__(256) void k_p_pv(const float *__restrict__ probs, uint32_t ss,
+                                              const uint32_t *__restrict__ pos, uint32_t R, PagedKV kv, float *o) {
+    constexpr int EPL = HD / 64, PB = 64 / REP;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ngrp = div_up(R, 4u), g = blockIdx.y;
+    const uint32_t r = (ngrp - 1 - blockIdx.x) * 4 + (uint32_t)wave;
+    if (r >= R) return;   // (uniform per wave)
+    const uint32_t n_heads = kv.n_heads, n = pos[r] + 1;
+    const float *pb[REP];
+#pragma unroll
+    for (int c = 0; c < REP; ++c) pb[c] = probs + ((size_t)r * n_heads + g * REP + c) * ss;
+    float acc[REP][EPL];
+#pragma unroll
+    for (int c = 0; c < REP; ++c)
+#pragma unroll
+        for (int q = 0; q < EPL; ++q) acc[c][q] = 0.0f;
+    uint32_t t0 = 0;
+    for (; t0 + PB <= n; t0 += PB) {   // blocks of PB positions
+        v4f vv[PB / 4][EPL];
+#pragma unroll
+        for (int j = 0; j < PB / 4; ++j) {
+            const uint32_t t = t0 + 4 * j;
+            const float *vt = kv.v + kv_tile(kv.bt[t / PAGE], g, kv.n_kv, HD) + (size_t)((t % PAGE) / 4) * HD * 4;
+#pragma unroll
+            for (int q = 0; q < EPL; ++q) vv[j][q] = *reinterpret_cast<const v4f *>(vt + (size_t)(lane + 64 * q) * 4);
+        }
+        v4f pp[REP][PB / 4];
+#pragma unroll
+        for (int c = 0; c < REP; ++c)
+#pragma unroll
+            for (int j = 0; j < PB / 4; ++j) pp[c][j] = *reinterpret_cast<const v4f *>(pb[c] + t0 + 4 * j);
+#pragma unroll
+        for (int c = 0; c < REP; ++c)
+#pragma unroll
+            for (int j = 0; j < PB / 4; ++j)
+#pragma unroll
+                for (int q = 0; q < EPL; ++q) {
+                    float a = acc[c][q];
+                    a = a + pp[c][j].x * vv[j][q].x;
+                    a = a + pp[c][j].y * vv[j][q].y;
+                    a = a + pp[c][j].z * vv[j][q].z;
+                    a = a + pp[c][j].w * vv[j][q].w;
+                    acc[c][q] = a;
+                }
+    }
+    for (; t0 < n; t0 += 4) {   // the rest, 4 positions at a time
+        const float *vt = kv.v + kv_tile(kv.bt[t0 / PAGE], g, kv.n_kv, HD) + (size_t)((t0 % PAGE) / 4) * HD * 4;
+        v4f vv[EPL];
+#pragma unroll
+        for (int q = 0; q < EPL; ++q) vv[q] = *reinterpret_cast<const v4f *>(vt + (size_t)(lane + 64 * q) * 4);
+#pragma unroll
+        for (int c = 0; c < REP; ++c) {
+            const v4f pp = *reinterpret_cast<const v4f *>(pb[c] + t0);   // (t0 + 3 < ss)
+#pragma unroll
+            for (int q = 0; q < EPL; ++q) {
+                float a = acc[c][q];
+                a = a + pp.x * vv[q].x;
+                if (t0 + 1 < n) a = a + pp.y * vv[q].y;
+                if (t0 + 2 < n) a = a + pp.z * vv[q].z;
+                if (t0 + 3 < n) a = a + pp.w * vv[q].w;
+                acc[c][q] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < REP; ++c)
+#pragma unroll
+        for (int q = 0; q < EPL; ++q) o[((size_t)r * n_heads + g * REP + c) * HD + lane + 64 * q] = acc[c][q];
+}
+
+bool launch_p_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t qkv_stride, const uint32_t *pos,
+                        const uint32_t *order, const PagedKV &kv, uint32_t n, uint32_t max_ctx, float *scores,
+                        float *pmax, float *o, uint32_t *err) {
+    if (!batch_ctx_ok(max_ctx) || (hd != 64 && hd != 128)) return false;
+    const uint32_t rep = kv.n_heads / kv.n_kv;
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8)   // other groupings: the decode step's P.V kernel
+        return launch_b_attention(st, hd, qkv, qkv_stride, pos, order, kv, n, max_ctx, scores, pmax, o, err);
+    const uint32_t nch = div_up(max_ctx, ACH);
+    const dim3 gs(nch, kv.n_kv, div_up(n, PRB)), gm(n * kv.n_heads);
+    const uint32_t ss = b_sc_stride(max_ctx);
+    if (hd == 64)
+        BLAUNCH(k_p_scores<64>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
+    else
+        BLAUNCH(k_p_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
+    BLAUNCH(k_b_softmax, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
+    const dim3 gp(div_up(n, 4u), kv.n_kv);
+#define PPV(H, P) BLAUNCH((k_p_pv<H, P>), gp, dim3(256), 0, st, scores, ss, pos, n, kv, o)
+    if (hd == 64) {
+        if (rep == 1) PPV(64, 1);
+        else if (rep == 2) PPV(64, 2);
+        else if (rep == 4) PPV(64, 4);
+        else PPV(64, 8);
+    } else {
+        if (rep == 1) PPV(128, 1);
+        else if (rep == 2) PPV(128, 2);
+        else if (rep == 4) PPV(128, 4);
+        else PPV(128, 8);
+    }
+#undef PPV
+    return true;
 }
 
 void launch_p_kv_store(hipStream_t st, const float *qkv, uint32_t qw, uint32_t qd, uint32_t kvd, uint32_t hd,

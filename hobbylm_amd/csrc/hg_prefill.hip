@@ -210,7 +210,7 @@ void enqueue_chunk(const hg_model *m, PrefillWork &w, const Shapes &s, hipStream
                                      c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), pos, kvp, R))
             note_launch_error(hipErrorInvalidConfiguration, "QK-norm / RoPE");
         launch_p_kv_store(st, w.qkv.as<float>(), s.qw, s.qd, s.kvd, hd, nkv, base0, R, cap, Lk, Lv);
-        if (!launch_b_attention(st, hd, w.qkv.as<float>(), s.qw, pos, w.order.as<uint32_t>(), kvp, R, win,
+        if (!launch_p_attention(st, hd, w.qkv.as<float>(), s.qw, pos, w.order.as<uint32_t>(), kvp, R, win,
                                 w.scores.as<float>(), w.pmax.as<float>(), w.o.as<float>(), w.err.as<uint32_t>()))
             note_launch_error(hipErrorInvalidConfiguration, "causal attention");
         launch_b_quant_rows(st, w.o.as<float>(), s.qd, s.qd, R, w.oq.as<uint8_t>(), s.ncq * CHUNK_BYTES,
