@@ -498,12 +498,14 @@ __global__ __launch_bounds__(256) void k_b_scores(const float *__restrict__ qkv,
 // chunk maxima (order-free); e_t = exp(s_t - m) with the reference expf, into LDS; sum = the
 // index-order sum of e_t (block_seq_sum: 4 waves up to 3072 terms, 8 waves x 32 up to 16384,
 // else one lane); p_t = e_t * (1 / sum) written over the scores.  Workgroups are dealt longest
-// sequence first (order[] ranks the sequences by length).  512 threads.
+// sequence first (order[] ranks the sequences by length).  NT = 512 threads, or 256 for
+// contexts of at most 3072 positions (the 4-wave sums; twice the workgroups per CU).
 __host__ __device__ inline size_t bsm_lds(uint32_t max_ctx) { return ((size_t)div_up(max_ctx, 4) * 4 + 64) * 4; }
 
-__global__ __launch_bounds__(512) void k_b_softmax(float *scores, uint32_t sc_stride, const float *__restrict__ pmax,
-                                                   uint32_t pm_stride, const uint32_t *__restrict__ pos,
-                                                   const uint32_t *__restrict__ order, uint32_t n_heads) {
+template <int NT>
+__global__ __launch_bounds__(NT) void k_b_softmax(float *scores, uint32_t sc_stride, const float *__restrict__ pmax,
+                                                  uint32_t pm_stride, const uint32_t *__restrict__ pos,
+                                                  const uint32_t *__restrict__ order, uint32_t n_heads) {
     extern __shared__ __align__(16) float e[];   // [max_ctx + 64]
     __shared__ xsum::Scratch xs;
     __shared__ float s_inv;
@@ -518,14 +520,14 @@ __global__ __launch_bounds__(512) void k_b_softmax(float *scores, uint32_t sc_st
     for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
     if (tid == 0) xs.sync = 0;
     constexpr uint32_t EB = 8;   // score loads in flight per thread
-    for (uint32_t t0 = 0; t0 < n; t0 += EB * 512) {   // (uniform: every lane calls the exp)
+    for (uint32_t t0 = 0; t0 < n; t0 += EB * NT) {   // (uniform: every lane calls the exp)
         float sv[EB];
 #pragma unroll
-        for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(t0 + u * 512 + (uint32_t)tid, n - 1)];
+        for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(t0 + u * NT + (uint32_t)tid, n - 1)];
 #pragma unroll
         for (uint32_t u = 0; u < EB; ++u) {
-            const uint32_t t = t0 + u * 512 + (uint32_t)tid;
-            if (t0 + u * 512 < n) {
+            const uint32_t t = t0 + u * NT + (uint32_t)tid;
+            if (t0 + u * NT < n) {
                 const float ev = hg_expf_l(sv[u] - m, tab);
                 if (t < n) e[t] = ev;
             }
@@ -538,7 +540,7 @@ __global__ __launch_bounds__(512) void k_b_softmax(float *scores, uint32_t sc_st
             const float r = n <= 2048 ? block_seq_sum<4, 8>(e, n, xs, wave, lane) : block_seq_sum<4, 12>(e, n, xs, wave, lane);
             if (tid == 0) s_inv = 1.0f / r;
         }
-    } else if (n <= 16384) {
+    } else if (NT == 512 && n <= 16384) {
         const float r = block_seq_sum<8, 32>(e, n, xs, wave, lane);
         if (tid == 0) s_inv = 1.0f / r;
     } else if (tid == 0) {
@@ -546,7 +548,7 @@ __global__ __launch_bounds__(512) void k_b_softmax(float *scores, uint32_t sc_st
     }
     __syncthreads();
     const float inv = s_inv;
-    for (uint32_t t = tid; t < n; t += 512) sc[t] = e[t] * inv;   // p_t (x *= inv, ops.rs:124-126)
+    for (uint32_t t = tid; t < n; t += NT) sc[t] = e[t] * inv;   // p_t (x *= inv, ops.rs:124-126)
 }
 
 // ------------------------------------------------------------------ paged attention: P.V
@@ -1123,7 +1125,7 @@ __global__ void k_b_step_advance(uint32_t *step) {
 bool batch_ctx_ok(uint32_t max_ctx) { return bsm_lds(max_ctx) <= BSM_LDS_MAX && pv2_lds(max_ctx) <= PV2_LDS_MAX; }
 
 hipError_t init_batch_kernel_attributes() {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_b_softmax),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_b_softmax<512>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)BSM_LDS_MAX);
     if (e == hipSuccess)
         e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_b_pv2<64>), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1210,7 +1212,7 @@ bool launch_b_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t 
         BLAUNCH(k_b_scores<64>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, kv, scores, ss, pmax, nch);
     else
         BLAUNCH(k_b_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, kv, scores, ss, pmax, nch);
-    BLAUNCH(k_b_softmax, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
+    BLAUNCH(k_b_softmax<512>, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
     if (hd == 64)
         BLAUNCH(k_b_pv2<64>, gp, dim3(64 * (PV2_NP + 1)), pv2_lds(max_ctx), st, scores, ss, pos, order, kv, n, o, err);
     else
@@ -1469,7 +1471,10 @@ bool launch_p_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t 
         BLAUNCH(k_p_scores<64>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
     else
         BLAUNCH(k_p_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
-    BLAUNCH(k_b_softmax, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
+    if (max_ctx <= 3072)   // (a prompt chunk's window: bsm_lds fits the default limit)
+        BLAUNCH(k_b_softmax<256>, gm, dim3(256), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
+    else
+        BLAUNCH(k_b_softmax<512>, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
     const dim3 gp(div_up(n, 4u), kv.n_kv);
 #define PPV(H, P) BLAUNCH((k_p_pv<H, P>), gp, dim3(256), 0, st, scores, ss, pos, n, kv, o)
     if (hd == 64) {
