@@ -265,11 +265,19 @@ __global__ __launch_bounds__(256) void k_gemm_p(GemmArgs g) {
     const uint32_t nc = M[0].nc, nb = M[0].nb, ne = tile.count;
     const uint32_t qst = pgemm_qstride(nc), sst = pgemm_sstride(nc);
     float *xds = reinterpret_cast<float *>(xs + (size_t)TT * qst);
-    for (uint32_t i = tid; i < TT * nc * 8; i += 256) {   // 16-byte pieces: entry i / (8 nc)
-        const uint32_t e = i / (nc * 8), p = i % (nc * 8);
-        v4i v = {0, 0, 0, 0};
-        if (e < ne) v = *reinterpret_cast<const v4i *>(g.aq + (size_t)g.act_row[tile.entry0 + e] * g.aqs + p * 16);
-        *reinterpret_cast<v4i *>(xs + (size_t)e * qst + p * 16) = v;
+    // 32-byte groups (a chunk's K group g: the lanes 2g and 2g + 1 of its 4 blocks), stored with
+    // each block's two words side by side, so that the B operand of block t is one aligned pair
+    for (uint32_t i = tid; i < TT * nc * 4; i += 256) {   // entry i / (4 nc)
+        const uint32_t e = i / (nc * 4), p = i % (nc * 4);
+        v4i a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+        if (e < ne) {
+            const v4i *src = reinterpret_cast<const v4i *>(g.aq + (size_t)g.act_row[tile.entry0 + e] * g.aqs + p * 32);
+            a = src[0];
+            b = src[1];
+        }
+        v4i *dst = reinterpret_cast<v4i *>(xs + (size_t)e * qst + p * 32);
+        dst[0] = v4i{a.x, b.x, a.y, b.y};
+        dst[1] = v4i{a.z, b.z, a.w, b.w};
     }
     for (uint32_t i = tid; i < TT * nc; i += 256) {   // block scales: entry i / nc, chunk i % nc
         const uint32_t e = i / nc, c = i % nc;
@@ -293,15 +301,18 @@ __global__ __launch_bounds__(256) void k_gemm_p(GemmArgs g) {
             srow[m][v] = reinterpret_cast<const SV *>(row_sc<SCF32>(M[m], min(gbase + r0 + 4 * gq + v, rlim)));
     }
     struct Ch {
-        v4i w[NM][2];
+        long A[NM][4];   // the A operand of each block of the chunk (paired at load time)
         SV s[NM][4];
     };
     auto load = [&](Ch &d, uint32_t c) {
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
             const v4i *wp = reinterpret_cast<const v4i *>(wrow[m] + (size_t)c * CHUNK_BYTES);
-            d.w[m][0] = wp[0];
-            d.w[m][1] = wp[1];
+            const v4i w0 = wp[0], w1 = wp[1];
+            d.A[m][0] = (long)((uint64_t)(uint32_t)w0.x | (uint64_t)(uint32_t)w1.x << 32);
+            d.A[m][1] = (long)((uint64_t)(uint32_t)w0.y | (uint64_t)(uint32_t)w1.y << 32);
+            d.A[m][2] = (long)((uint64_t)(uint32_t)w0.z | (uint64_t)(uint32_t)w1.z << 32);
+            d.A[m][3] = (long)((uint64_t)(uint32_t)w0.w | (uint64_t)(uint32_t)w1.w << 32);
 #pragma unroll
             for (int v = 0; v < 4; ++v) d.s[m][v] = srow[m][v][c];
         }
@@ -325,21 +336,17 @@ __global__ __launch_bounds__(256) void k_gemm_p(GemmArgs g) {
         for (int q = 0; q < NG; ++q) {
             if ((uint32_t)q < ngr) {   // (uniform)
                 const uint8_t *bp = xb + (size_t)q * 16 * qst + (size_t)c * CHUNK_BYTES;
-                const v4i b0 = *reinterpret_cast<const v4i *>(bp), b1 = *reinterpret_cast<const v4i *>(bp + 16);
+                const v2l b0 = *reinterpret_cast<const v2l *>(bp), b1 = *reinterpret_cast<const v2l *>(bp + 16);
                 const v4f dx4 = *reinterpret_cast<const v4f *>(xd + (size_t)q * 16 * sst + 4 * c);
-                const int bl[4] = {b0.x, b0.y, b0.z, b0.w}, bh[4] = {b1.x, b1.y, b1.z, b1.w};
+                const long Bt[4] = {b0.x, b0.y, b1.x, b1.y};
                 const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     if (FULLK || 4 * c + t < nb) {   // (uniform; padding blocks of a partial last chunk: no add)
-                        const long B = (long)((uint64_t)(uint32_t)bl[t] | (uint64_t)(uint32_t)bh[t] << 32);
 #pragma unroll
                         for (int m = 0; m < NM; ++m) {
-                            const int lo = t == 0 ? d.w[m][0].x : t == 1 ? d.w[m][0].y : t == 2 ? d.w[m][0].z : d.w[m][0].w;
-                            const int hi = t == 0 ? d.w[m][1].x : t == 1 ? d.w[m][1].y : t == 2 ? d.w[m][1].z : d.w[m][1].w;
-                            const long A = (long)((uint64_t)(uint32_t)lo | (uint64_t)(uint32_t)hi << 32);
                             const v4i z = {0, 0, 0, 0};
-                            const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, z, 0, 0, 0);
+                            const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(d.A[m][t], Bt[t], z, 0, 0, 0);
 #pragma unroll
                             for (int v = 0; v < 4; ++v) {
                                 const float dd = sw[m][v][t] * dxs[t];
@@ -994,58 +1001,67 @@ __global__ void k_b_order(const uint32_t *__restrict__ pos, uint32_t n, uint32_t
 // sequence (its quantized h), out_row = sequence * n_slots + slot (its row of a and y).
 // Column tiles of at most TT entries cover each expert's entries (matrix group e of set 0; the
 // shared expert's tiles use group 0 of set 1).  One workgroup.
-__global__ __launch_bounds__(256) void k_b_group(const uint32_t *__restrict__ topk_idx, uint32_t n, uint32_t top_k,
-                                                 uint32_t E, uint32_t n_slots, uint32_t TT,
-                                                 uint32_t *act_row, uint32_t *out_row, GemmTile *tiles,
-                                                 uint32_t *n_tiles) {
+__global__ __launch_bounds__(1024) void k_b_group(const uint32_t *__restrict__ topk_idx, uint32_t n, uint32_t top_k,
+                                                  uint32_t E, uint32_t n_slots, uint32_t TT,
+                                                  uint32_t *act_row, uint32_t *out_row, GemmTile *tiles,
+                                                  uint32_t *n_tiles) {
     __shared__ uint32_t cnt[MAX_GROUPS], base[MAX_GROUPS], wa[4], wt[4];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NP = n * top_k;
     const uint32_t NG = E + (n_slots > top_k ? 1 : 0);
-    cnt[tid] = 0;   // (256 threads = MAX_GROUPS)
+    if (tid < MAX_GROUPS) cnt[tid] = 0;
     __syncthreads();
-    for (uint32_t i = tid; i < NP; i += 256) {
+#pragma unroll 4
+    for (uint32_t i = tid; i < NP; i += 1024) {
         const uint32_t e = topk_idx[i];   // (< E: the router's output; anything else is dropped)
         if (e < E) atomicAdd(&cnt[e], 1u);
     }
     __syncthreads();
-    // exclusive scans of the entry and tile counts over the groups (thread = group)
-    const uint32_t c = tid < E ? cnt[tid] : tid < NG ? n : 0u, tc = div_up(c, TT);
-    cnt[tid] = 0;   // (now the fill count of the placement below)
-    const uint32_t ia = wave_scan_u(c), it = wave_scan_u(tc);
-    if (lane == 63) {
-        wa[wave] = ia;
-        wt[wave] = it;
-    }
-    __syncthreads();
-    uint32_t ba = 0, bt = 0;
-    for (uint32_t w = 0; w < wave; ++w) {
-        ba += wa[w];
-        bt += wt[w];
-    }
-    const uint32_t off = ba + ia - c, toff = bt + it - tc;
-    base[tid] = off;
-    if (tid == 255) *n_tiles = bt + it;
-    if (tid < NG) {
-        for (uint32_t q = 0; q < tc; ++q) {
-            GemmTile tl;
-            tl.grp = tid < E ? tid : 0u;
-            tl.entry0 = off + q * TT;
-            tl.count = min(TT, c - q * TT);
-            tl.mat = tid < E ? 0u : 1u;
-            tiles[toff + q] = tl;
+    // exclusive scans of the entry and tile counts over the groups (threads 0 .. 255 = groups)
+    uint32_t c = 0, tc = 0, ia = 0, it = 0;
+    if (tid < MAX_GROUPS) {   // (whole waves)
+        c = tid < E ? cnt[tid] : tid < NG ? n : 0u;
+        tc = div_up(c, TT);
+        ia = wave_scan_u(c);
+        it = wave_scan_u(tc);
+        if (lane == 63) {
+            wa[wave] = ia;
+            wt[wave] = it;
         }
     }
     __syncthreads();
-    if (NG > E) {   // the shared expert: every sequence, slot top_k
+    if (tid < MAX_GROUPS) {
+        uint32_t ba = 0, bt = 0;
+        for (uint32_t w = 0; w < wave; ++w) {
+            ba += wa[w];
+            bt += wt[w];
+        }
+        const uint32_t off = ba + ia - c, toff = bt + it - tc;
+        base[tid] = off;
+        cnt[tid] = 0;   // (now the fill count of the placement below)
+        if (tid == MAX_GROUPS - 1) *n_tiles = bt + it;
+        if (tid < NG) {
+            for (uint32_t q = 0; q < tc; ++q) {
+                GemmTile tl;
+                tl.grp = tid < E ? tid : 0u;
+                tl.entry0 = off + q * TT;
+                tl.count = min(TT, c - q * TT);
+                tl.mat = tid < E ? 0u : 1u;
+                tiles[toff + q] = tl;
+            }
+        }
+    }
+    __syncthreads();
+    if (NG > E) {   // the shared expert: every row, slot top_k
         const uint32_t sb = base[E];
-        for (uint32_t sq = tid; sq < n; sq += 256) {
+        for (uint32_t sq = tid; sq < n; sq += 1024) {
             act_row[sb + sq] = sq;
             out_row[sb + sq] = sq * n_slots + top_k;
         }
     }
     // the routed picks: a pick's entry is its expert's base + a slot taken with an LDS atomic
     // (the order of an expert's entries is arbitrary: each entry's GEMM column is its own)
-    for (uint32_t i = tid; i < NP; i += 256) {
+#pragma unroll 4
+    for (uint32_t i = tid; i < NP; i += 1024) {
         const uint32_t e = topk_idx[i];
         if (e < E) {
             const uint32_t at = base[e] + atomicAdd(&cnt[e], 1u);
@@ -1223,7 +1239,7 @@ bool launch_b_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t 
 void launch_b_group(hipStream_t st, const uint32_t *topk_idx, uint32_t n, uint32_t top_k, uint32_t E,
                     uint32_t n_slots, uint32_t tt, uint32_t *act_row, uint32_t *out_row, GemmTile *tiles,
                     uint32_t *n_tiles) {
-    BLAUNCH(k_b_group, dim3(1), dim3(256), 0, st, topk_idx, n, top_k, E, n_slots, tt, act_row, out_row, tiles,
+    BLAUNCH(k_b_group, dim3(1), dim3(1024), 0, st, topk_idx, n, top_k, E, n_slots, tt, act_row, out_row, tiles,
             n_tiles);
 }
 

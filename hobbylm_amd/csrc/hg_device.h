@@ -100,6 +100,7 @@ __device__ inline void stage_act(const uint8_t *gq, const float *gd, uint32_t nc
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef long v2l __attribute__((ext_vector_type(2)));
 
 // Storage vector of the four scales of one chunk: f32 (16 B) or f16 (8 B).
 template <bool SCF32> struct ScaleVec { typedef v2u T; };
