@@ -37,6 +37,12 @@ _u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _vp = C.c_void_p
 
 
+class GenOpts(C.Structure):
+    """hg_gen_opts: GenOpts (lib.rs:29-41)."""
+    _fields_ = [("max_new", C.c_uint32), ("temp", C.c_float), ("top_p", C.c_float), ("seed", C.c_uint64),
+                ("rep_penalty", C.c_float)]
+
+
 class HgConfig(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in (
         "d_model", "n_layers", "n_dense", "n_heads", "n_kv_heads", "head_dim", "dense_ffn",
@@ -70,6 +76,9 @@ SIGNATURES = {
     "hg_decode_greedy": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, _u32p]),
     "hg_generate_greedy": (C.c_int, [_vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32,
                                      _u32p, C.POINTER(C.c_uint32)]),
+    "hg_generate": (C.c_int, [_vp, _vp, _u32p, C.c_uint32, _vp, C.c_uint32, _u32p, C.POINTER(C.c_uint32)]),
+    "hg_sample": (C.c_int, [_f32p, C.c_uint32, C.c_float, C.c_float, C.POINTER(C.c_uint64),
+                            C.POINTER(C.c_uint32)]),
     "hg_last_routing": (C.c_int, [_vp, _u32p, _f32p]),
     "hg_seq_sum": (C.c_int, [_f32p, C.c_uint32, C.c_uint32, _f32p]),
     "hg_profile_step": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, _f32p, _u32p]),
@@ -204,6 +213,17 @@ class Model:
         cnt = np.zeros(n, np.uint32)
         _check(lib().hg_profile_step(self.h, cache.h, token, reps, us, cnt))
         return {lib().hg_profile_class(c).decode(): (float(us[c]), int(cnt[c])) for c in range(n) if cnt[c]}
+
+    def generate(self, prompt, max_new: int, cache: "KvCache", temp: float = 0.0, top_p: float = 0.95,
+                 seed: int = 1234, rep_penalty: float = 1.0, eos: int = 50256) -> np.ndarray:
+        """Engine::generate (lib.rs:107-162) with GenOpts {max_new, temp, top_p, seed, rep_penalty},
+        sampling on the device."""
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.empty(max(max_new, 1), np.uint32)
+        n = C.c_uint32()
+        opts = GenOpts(max_new, temp, top_p, seed, rep_penalty)
+        _check(lib().hg_generate(self.h, cache.h, p, p.size, C.cast(C.pointer(opts), _vp), eos, out, C.byref(n)))
+        return out[: n.value].copy()
 
     def generate_greedy(self, prompt, max_new: int, cache: "KvCache", rep_penalty: float = 1.0,
                         eos: int = 50256) -> np.ndarray:
@@ -429,6 +449,15 @@ def gguf_load_tensor(path: str, name: str) -> np.ndarray:
     out = np.empty(n.value, np.float32)
     _check(lib().hg_gguf_load_tensor(str(path).encode(), name.encode(), _ptr(out), out.size, C.byref(n)))
     return out
+
+
+def sample(logits, temp: float, top_p: float, state: int):
+    """sample::sample (sample.rs:66-112) on the device: (pick, the advanced RNG state)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    st = C.c_uint64(state)
+    out = C.c_uint32()
+    _check(lib().hg_sample(lg, lg.size, temp, top_p, C.byref(st), C.byref(out)))
+    return int(out.value), int(st.value)
 
 
 def seq_sum(x, method: int = 1) -> np.float32:

@@ -23,6 +23,7 @@
 #include "hg_kernels.h"
 #include "hg_model.h"
 #include "hg_prefill.h"
+#include "hg_sample.h"
 
 using namespace hg;
 
@@ -144,6 +145,8 @@ struct hg_kv {
     bool use_graph = true;
     LaunchTimer *timer = nullptr;  // hg_profile_step: per-dispatch timing
     std::unique_ptr<PrefillWork> pw;   // the batched prompt path's buffers (on first use)
+    std::unique_ptr<SampleWork> sw;    // the device sampler's buffers (on first use)
+    DevBuf picks;                      // sampled ids of hg_generate
     ~hg_kv();
 };
 
@@ -791,6 +794,93 @@ int hg_decode_greedy(const hg_model *m, hg_kv *kv, uint32_t first_token, uint32_
         HIP_TRY(hipStreamSynchronize(kv->st));
         memcpy(out_ids, kv->h_ids, (size_t)n_steps * 4);
         kv->len = pos + n_steps;
+        return HG_OK;
+    });
+}
+
+int hg_generate(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uint32_t n_prompt, const hg_gen_opts *opts,
+                uint32_t eos, uint32_t *out_ids, uint32_t *n_out) {
+    return guard([&]() -> int {
+        if (!m || !kv || !opts || !n_out) return fail(HG_ERR_ARG, "NULL argument");
+        *n_out = 0;
+        if (n_prompt > 0 && !prompt) return fail(HG_ERR_ARG, "prompt is NULL");
+        if (opts->max_new > 0 && !out_ids) return fail(HG_ERR_ARG, "out_ids is NULL");
+        if (kv->m != m) return fail(HG_ERR_ARG, "cache does not belong to this model");
+        if (n_prompt == 0) return HG_OK;
+        const hg_config &c = m->c;
+        const uint32_t d = c.d_model, V = c.vocab_size, valid = V < 50257 ? V : 50257, max_new = opts->max_new;
+        std::vector<float> in((size_t)n_prompt * d);
+        int rc;
+        for (uint32_t i = 0; i < n_prompt; ++i)
+            if ((rc = hg_token_embedding(m, prompt[i], in.data() + (size_t)i * d))) return rc;
+        uint32_t first = 0;
+        if ((rc = hg_prefill(m, kv, in.data(), n_prompt, nullptr, &first))) return rc;   // logits stay on the device
+        if (max_new == 0) return HG_OK;
+        if (!kv->sw) kv->sw = std::make_unique<SampleWork>();
+        if ((rc = sample_init(*kv->sw, V))) return rc;
+        const uint64_t seed = opts->seed > 1 ? opts->seed : 1;   // Rng::new (sample.rs:6-8)
+        HIP_TRY(hipMemcpy(kv->sw->rng.p, &seed, 8, hipMemcpyHostToDevice));
+        if (kv->picks.n < (size_t)max_new * 4 && (rc = kv->picks.alloc((size_t)max_new * 4))) return rc;
+        uint32_t *picks = kv->picks.as<uint32_t>();
+        const uint32_t p0 = kv->len, stop = std::min(c.context_length, kv->cap);
+        uint32_t pos = p0, n = 0, fw = 0;
+        bool done = false;
+        if ((rc = set_params(kv, 0, pos, 1, 1, pos))) return rc;
+        // steps in chunks between host checks of the picks: per step the draw from the logits on
+        // the device (it sets the token of the next step), then the decode step at pos
+        constexpr uint32_t CH = 16;
+        for (uint32_t it = 0; it < max_new && !done;) {
+            const uint32_t j0 = it;
+            uint32_t fw_chunk = 0;
+            bool ctx_stop = false;
+            for (; it < max_new && it < j0 + CH; ++it) {
+                (void)take_launch_error_reset();
+                if (!enqueue_sample(kv->st, *kv->sw, kv->logits.as<float>(), valid, opts->temp, opts->top_p,
+                                    opts->rep_penalty, picks + it, kv->params.as<StepParams>()))
+                    return fail(HG_ERR_DEVICE, "sampling launch failed");
+                if (pos + 1 >= stop) {   // lib.rs:155-157: the token is kept, not forwarded
+                    ctx_stop = true;
+                    ++it;
+                    break;
+                }
+                if ((rc = run(kv, graph_for(kv, kv->g_decode, pos), enqueue_decode))) return rc;
+                ++pos;
+                ++fw_chunk;
+            }
+            HIP_TRY(hipMemcpyAsync(kv->h_ids, picks + j0, (size_t)(it - j0) * 4, hipMemcpyDeviceToHost, kv->st));
+            HIP_TRY(hipStreamSynchronize(kv->st));
+            for (uint32_t j = 0; j < it - j0; ++j) {
+                const uint32_t t = kv->h_ids[j];
+                if (t == eos) {   // lib.rs:143-145
+                    done = true;
+                    break;
+                }
+                out_ids[n++] = t;
+                if (j < fw_chunk) ++fw;
+            }
+            if (ctx_stop) done = true;
+        }
+        kv->len = p0 + fw;   // the forwarded rows (a step past an eos leaves rows beyond len)
+        *n_out = n;
+        return HG_OK;
+    });
+}
+
+int hg_sample(const float *logits, uint32_t n, float temp, float top_p, uint64_t *rng_state, uint32_t *out) {
+    return guard([&]() -> int {
+        if (!logits || !rng_state || !out) return fail(HG_ERR_ARG, "NULL argument");
+        if (n == 0) return fail(HG_ERR_ARG, "no logits");
+        int rc = check_device();
+        if (rc) return rc;
+        SampleWork w;
+        DevBuf lg, pick;
+        if ((rc = sample_init(w, n)) || (rc = lg.alloc((size_t)n * 4)) || (rc = pick.alloc(4))) return rc;
+        HIP_TRY(hipMemcpy(lg.p, logits, (size_t)n * 4, hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpy(w.rng.p, rng_state, 8, hipMemcpyHostToDevice));
+        if (!enqueue_sample(nullptr, w, lg.as<float>(), n, temp, top_p, 1.0f, pick.as<uint32_t>(), nullptr))
+            return fail(HG_ERR_DEVICE, "sampling launch failed");
+        HIP_TRY(hipMemcpy(out, pick.p, 4, hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(rng_state, w.rng.p, 8, hipMemcpyDeviceToHost));
         return HG_OK;
     });
 }

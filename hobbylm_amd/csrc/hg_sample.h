@@ -1,0 +1,27 @@
+// hg_sample.h -- sample::sample (sample.rs:66-112) on the device (hg_sample.hip): the token of a
+// generation step is drawn from logits that never leave the GPU.
+#pragma once
+#include "hg_model.h"
+
+namespace hg {
+
+// Device buffers of the sampler for a vocabulary of V ids, and its RNG state.
+struct SampleWork {
+    uint32_t V = 0;
+    size_t sort_bytes = 0;
+    DevBuf p, keys, ids, keys_out, ids_out, sort_tmp, counts, rng;
+};
+
+// Allocates w for V ids (keeps it when V is unchanged) and zeroes the occurrence counts.
+int sample_init(SampleWork &w, uint32_t V);
+
+// One draw of Engine::generate's sampling step (lib.rs:132-142): logits[0 .. V) (device) with
+// ids >= valid masked to -inf and, when rep_penalty != 1, the repetition penalty applied once
+// per earlier occurrence (w.counts), then sample::sample with temperature temp and nucleus
+// top_p using the device RNG state w.rng (xorshift64*, sample.rs:3-29).  The pick goes to
+// *pick; with p, p->token = pick; its occurrence count is incremented.  false if a launch was
+// refused.  Equal probabilities in the nucleus order by ascending id.
+bool enqueue_sample(hipStream_t st, SampleWork &w, const float *logits, uint32_t valid, float temp, float top_p,
+                    float rep_penalty, uint32_t *pick, StepParams *p);
+
+}  // namespace hg

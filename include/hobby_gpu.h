@@ -140,6 +140,27 @@ int hg_decode_greedy(const hg_model *m, hg_kv *kv, uint32_t first_token, uint32_
 int hg_generate_greedy(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uint32_t n_prompt,
                        uint32_t max_new, float rep_penalty, uint32_t eos, uint32_t *out_ids,
                        uint32_t *n_out);
+/* GenOpts (lib.rs:29-41): temp <= 0 is greedy; top_p outside (0, 1) disables the nucleus;
+ * rep_penalty 1.0 is off. */
+typedef struct hg_gen_opts {
+    uint32_t max_new;
+    float temp;
+    float top_p;
+    uint64_t seed;
+    float rep_penalty;
+} hg_gen_opts;
+/* Engine::generate (lib.rs:107-162) over token ids with sampling on the device: prefill of the
+ * prompt, then per step the 50257 mask, the repetition penalty once per earlier occurrence,
+ * sample::sample (sample.rs:66-112) with the xorshift64* Rng seeded by opts->seed, the EOS stop
+ * and the context stop.  The logits never leave the GPU; the host reads the picks every 16
+ * steps.  Writes at most max_new ids; *n_out receives the count; the cache then holds the
+ * prompt and the forwarded ids.  Equal probabilities in the nucleus order by ascending id
+ * (sample.rs:86's sort_unstable_by leaves that order unspecified). */
+int hg_generate(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uint32_t n_prompt, const hg_gen_opts *opts,
+                uint32_t eos, uint32_t *out_ids, uint32_t *n_out);
+/* sample::sample (sample.rs:66-112) of host logits[0 .. n) on the device, with the RNG state
+ * *rng_state (Rng's u64: the seed clamped to >= 1), which it advances; the pick in *out. */
+int hg_sample(const float *logits, uint32_t n, float temp, float top_p, uint64_t *rng_state, uint32_t *out);
 /* Routing of the last processed row, per layer in rank order (model.rs:282-293):
  * idx[L*top_k] (UINT32_MAX for dense layers) and the scaled weights w[L*top_k]. */
 int hg_last_routing(const hg_kv *kv, uint32_t *idx, float *w);

@@ -94,6 +94,12 @@ def lib():
             "orc_last_routing": (C.c_int, [C.c_void_p, _u32p, _f32p, _f32p]),
             "orc_generate_greedy": (C.c_int, [C.c_void_p, C.c_void_p, _u32p, C.c_uint32, C.c_uint32,
                                               C.c_float, C.c_uint32, _u32p, C.POINTER(C.c_uint32)]),
+            "orc_generate": (C.c_int, [C.c_void_p, C.c_void_p, _u32p, C.c_uint32, C.c_uint32, C.c_float,
+                                       C.c_float, C.c_uint64, C.c_float, C.c_uint32, _u32p,
+                                       C.POINTER(C.c_uint32)]),
+            "orc_rng_next_u64": (C.c_uint64, [C.POINTER(C.c_uint64)]),
+            "orc_rng_next_f32": (C.c_float, [C.POINTER(C.c_uint64)]),
+            "orc_sample": (C.c_uint32, [_f32p, C.c_size_t, C.c_float, C.c_float, C.POINTER(C.c_uint64)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -121,6 +127,25 @@ def threads() -> int:
 
 
 # ---- op level ----
+class Rng:
+    """sample::Rng (sample.rs:3-29): xorshift64*, the seed clamped to at least 1."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(max(int(seed), 1))
+
+    def next_u64(self) -> int:
+        return int(lib().orc_rng_next_u64(C.byref(self.state)))
+
+    def next_f32(self) -> float:
+        return float(lib().orc_rng_next_f32(C.byref(self.state)))
+
+
+def sample(logits: np.ndarray, temp: float, top_p: float, rng: Rng) -> int:
+    """sample::sample (sample.rs:66-112); ties in the nucleus order by ascending token id."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    return int(lib().orc_sample(lg, lg.size, temp, top_p, C.byref(rng.state)))
+
+
 def half_to_f32(h: int) -> float:
     return float(lib().orc_half_to_f32(h))
 
@@ -313,6 +338,16 @@ class Model:
         lg = np.empty(self.cfg.vocab_size, np.float32)
         _check(lib().orc_prefill(self.h, cache.h, inputs.reshape(-1), inputs.shape[0], lg))
         return lg
+
+    def generate(self, prompt, max_new: int, cache: "KvCache", temp: float = 0.0, top_p: float = 0.95,
+                 seed: int = 1234, rep_penalty: float = 1.0, eos: int = 50256) -> np.ndarray:
+        """Engine::generate (lib.rs:107-162) with GenOpts {max_new, temp, top_p, seed, rep_penalty}."""
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.empty(max(max_new, 1), np.uint32)
+        n = C.c_uint32()
+        _check(lib().orc_generate(self.h, cache.h, p, p.size, max_new, temp, top_p, seed, rep_penalty, eos, out,
+                                  C.byref(n)))
+        return out[: n.value].copy()
 
     def generate_greedy(self, prompt, max_new: int, cache: "KvCache", rep_penalty: float = 1.0,
                         eos: int = 50256) -> np.ndarray:

@@ -585,6 +585,89 @@ uint32_t orc_argmax(const float *logits, size_t n) {
 }
 
 /* ======================================================================
+ * sample.rs
+ * ====================================================================== */
+
+/* Rng::next_u64 (sample.rs:10-17): xorshift64* on the state; Rng::new (sample.rs:6-8) clamps a
+ * zero seed to 1. */
+uint64_t orc_rng_next_u64(uint64_t *state) {
+    uint64_t x = *state;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *state = x;
+    return x * 0x2545F4914F6CDD1DULL;
+}
+
+/* Rng::next_f32 (sample.rs:18-20): the top 24 bits over 2^24 (both steps exact). */
+float orc_rng_next_f32(uint64_t *state) {
+    return (float)(orc_rng_next_u64(state) >> 40) / (float)(1ull << 24);
+}
+
+typedef struct {
+    float p;
+    uint32_t i;
+} prob_t;
+
+/* The nucleus order: probability descending.  sample.rs:86 sorts with sort_unstable_by, whose
+ * order among equal probabilities is unspecified; here equal probabilities keep ascending
+ * token ids (the order a stable sort of the id-ordered list gives). */
+static int prob_desc(const void *a, const void *b) {
+    const prob_t *x = (const prob_t *)a, *y = (const prob_t *)b;
+    if (x->p > y->p) return -1;
+    if (x->p < y->p) return 1;
+    return x->i < y->i ? -1 : x->i > y->i;
+}
+
+/* sample::sample (sample.rs:66-112): temperature softmax (v / temp, max, exp(v - m), a sum in id
+ * order, p /= sum), then with 0 < top_p < 1 the nucleus (descending order, cumulative sum until
+ * it reaches top_p, renormalized by the kept sum); one uniform draw r, the first entry whose
+ * cumulative probability exceeds r, else the last.  temp <= 0: argmax. */
+uint32_t orc_sample(const float *logits, size_t n, float temp, float top_p, uint64_t *state) {
+    if (!(temp > 0.0f)) return orc_argmax(logits, n);
+    prob_t *pr = (prob_t *)malloc(n * sizeof(prob_t));
+    float m = -INFINITY;
+    for (size_t i = 0; i < n; i++) {
+        pr[i].p = logits[i] / temp;
+        pr[i].i = (uint32_t)i;
+        m = fmaxf(m, pr[i].p);
+    }
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        pr[i].p = expf(pr[i].p - m);
+        sum += pr[i].p;
+    }
+    for (size_t i = 0; i < n; i++) pr[i].p /= sum;
+    size_t cut = n;
+    if (top_p > 0.0f && top_p < 1.0f) {
+        qsort(pr, n, sizeof(prob_t), prob_desc);
+        float cum = 0.0f;
+        for (size_t i = 0; i < n; i++) {
+            cum += pr[i].p;
+            if (cum >= top_p) {
+                cut = i + 1;
+                break;
+            }
+        }
+        float s = -0.0f;   /* <f32 as Sum>::sum */
+        for (size_t i = 0; i < cut; i++) s += pr[i].p;
+        for (size_t i = 0; i < cut; i++) pr[i].p /= s;
+    }
+    const float r = orc_rng_next_f32(state);
+    float cum = 0.0f;
+    uint32_t pick = cut ? pr[cut - 1].i : 0u;
+    for (size_t i = 0; i < cut; i++) {
+        cum += pr[i].p;
+        if (r < cum) {
+            pick = pr[i].i;
+            break;
+        }
+    }
+    free(pr);
+    return pick;
+}
+
+/* ======================================================================
  * quant.rs
  * ====================================================================== */
 
@@ -1337,6 +1420,45 @@ int orc_last_routing(const orc_kv *kv, uint32_t *idx, float *weight, float *gap)
     if (idx) memcpy(idx, kv->r_idx, n * 4);
     if (weight) memcpy(weight, kv->r_w, n * 4);
     if (gap) memcpy(gap, kv->r_gap, (size_t)kv->L * 4);
+    return 0;
+}
+
+/* Engine::generate (lib.rs:107-162): prefill, then per step the ids >= 50257 masked, the
+ * repetition penalty once per earlier occurrence of a token, sample::sample with the seeded Rng
+ * (lib.rs:115), a stop at eos or at the context length. */
+int orc_generate(const orc_model *m, orc_kv *kv, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_new,
+                 float temp, float top_p, uint64_t seed, float rep_penalty, uint32_t eos, uint32_t *out_ids,
+                 uint32_t *n_out) {
+    *n_out = 0;
+    if (n_prompt == 0) return 0;
+    const orc_config *c = &m->c;
+    size_t d = c->d_model, V = c->vocab_size;
+    uint64_t rng = seed > 1 ? seed : 1;
+    float *in = (float *)malloc((size_t)n_prompt * d * 4);
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (orc_token_embedding(m, prompt[i], in + (size_t)i * d)) { free(in); return -1; }
+    float *logits = (float *)malloc(V * 4);
+    uint32_t pos = n_prompt + kv->len;
+    if (orc_prefill(m, kv, in, n_prompt, logits)) { free(in); free(logits); return -1; }
+    free(in);
+    size_t valid = V < 50257 ? V : 50257;
+    uint32_t n = 0;
+    for (uint32_t it = 0; it < max_new; it++) {
+        for (size_t i = valid; i < V; i++) logits[i] = -INFINITY;
+        if (rep_penalty != 1.0f)
+            for (uint32_t q = 0; q < n; q++) {
+                float *l = &logits[out_ids[q]];
+                *l = *l > 0.0f ? *l / rep_penalty : *l * rep_penalty;
+            }
+        uint32_t next = orc_sample(logits, V, temp, top_p, &rng);
+        if (next == eos) break;
+        out_ids[n++] = next;
+        if (pos + 1 >= c->context_length) break;
+        if (orc_forward(m, kv, next, pos, logits)) { free(logits); *n_out = n; return -1; }
+        pos++;
+    }
+    free(logits);
+    *n_out = n;
     return 0;
 }
 

@@ -72,6 +72,9 @@ void orc_rope_table(size_t head_dim, size_t max_pos, float theta, float *cos_t, 
 /* Rope::apply (ops.rs:155-166) */
 void orc_rope_apply(const float *cos_t, const float *sin_t, size_t head_dim, float *v, size_t pos);
 uint32_t orc_argmax(const float *logits, size_t n);                 /* sample.rs:53-63 */
+uint64_t orc_rng_next_u64(uint64_t *state);                         /* sample.rs:10-17 */
+float orc_rng_next_f32(uint64_t *state);                            /* sample.rs:18-20 */
+uint32_t orc_sample(const float *logits, size_t n, float temp, float top_p, uint64_t *state); /* sample.rs:66-112 */
 /* Router decision of one row (model.rs:270-293): sigmoid (or softmax) gate, sel = score +
  * bias, descending sort, top_k ids in rank order, their un-biased scores (renormalised when
  * weights_norm), and gap = sel[k-th] - sel[(k+1)-th]. */
@@ -109,6 +112,9 @@ int orc_last_routing(const orc_kv *kv, uint32_t *idx, float *weight, float *gap)
 /* Engine::generate at temp 0 (lib.rs:107-162) over token ids: prefill, then greedy
  * steps with the id>=min(50257,vocab) mask, optional repetition penalty, EOS and
  * context stops.  Returns the number of generated ids written to out_ids. */
+int orc_generate(const orc_model *m, orc_kv *kv, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_new,
+                 float temp, float top_p, uint64_t seed, float rep_penalty, uint32_t eos, uint32_t *out_ids,
+                 uint32_t *n_out);                                  /* lib.rs:107-162 */
 int orc_generate_greedy(const orc_model *m, orc_kv *kv, const uint32_t *prompt, uint32_t n_prompt,
                         uint32_t max_new, float rep_penalty, uint32_t eos, uint32_t *out_ids,
                         uint32_t *n_out);
