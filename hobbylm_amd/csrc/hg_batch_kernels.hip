@@ -1205,6 +1205,7 @@ bool launch_b_qk_rope_append(hipStream_t st, uint32_t hd, float *qkv, uint32_t q
                              const PagedKV &kv, uint32_t n) {
     const dim3 grid(kv.n_heads + 2 * kv.n_kv, n);
     switch (hd) {
+    case 32: BLAUNCH(k_b_qk_rope_append<32>, grid, dim3(64), 0, st, qkv, qkv_stride, qn, kn, eps, cs, sn, pos, kv); break;
     case 64: BLAUNCH(k_b_qk_rope_append<64>, grid, dim3(64), 0, st, qkv, qkv_stride, qn, kn, eps, cs, sn, pos, kv); break;
     case 128: BLAUNCH(k_b_qk_rope_append<128>, grid, dim3(64), 0, st, qkv, qkv_stride, qn, kn, eps, cs, sn, pos, kv); break;
     default: return false;
@@ -1405,8 +1406,10 @@ __global__ __launch_bounds__(256) void k_p_scores(const float *__restrict__ qkv,
 template <int HD, int REP>
 __global__ __launch_bounds__(256) void k_p_pv(const float *__restrict__ probs, uint32_t ss,
                                               const uint32_t *__restrict__ pos, uint32_t R, PagedKV kv, float *o) {
-    constexpr int EPL = HD / 64, PB = 64 / REP;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int EPL = HD >= 64 ? HD / 64 : 1, PB = 64 / REP;   // (heads of 32: lanes 32 .. 63 idle)
+    const int lane_ = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool act = HD >= 64 || lane_ < HD;
+    const int lane = act ? lane_ : HD - 1;   // (idle lanes load in bounds and store nothing)
     const uint32_t ngrp = div_up(R, 4u), g = blockIdx.y;
     const uint32_t r = (ngrp - 1 - blockIdx.x) * 4 + (uint32_t)wave;
     if (r >= R) return;   // (uniform per wave)
@@ -1467,23 +1470,26 @@ __global__ __launch_bounds__(256) void k_p_pv(const float *__restrict__ probs, u
             }
         }
     }
+    if (act)
 #pragma unroll
-    for (int c = 0; c < REP; ++c)
+        for (int c = 0; c < REP; ++c)
 #pragma unroll
-        for (int q = 0; q < EPL; ++q) o[((size_t)r * n_heads + g * REP + c) * HD + lane + 64 * q] = acc[c][q];
+            for (int q = 0; q < EPL; ++q) o[((size_t)r * n_heads + g * REP + c) * HD + lane + 64 * q] = acc[c][q];
 }
 
 bool launch_p_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t qkv_stride, const uint32_t *pos,
                         const uint32_t *order, const PagedKV &kv, uint32_t n, uint32_t max_ctx, float *scores,
                         float *pmax, float *o, uint32_t *err) {
-    if (!batch_ctx_ok(max_ctx) || (hd != 64 && hd != 128)) return false;
+    if (!batch_ctx_ok(max_ctx) || (hd != 32 && hd != 64 && hd != 128)) return false;
     const uint32_t rep = kv.n_heads / kv.n_kv;
     if (rep != 1 && rep != 2 && rep != 4 && rep != 8)   // other groupings: the decode step's P.V kernel
-        return launch_b_attention(st, hd, qkv, qkv_stride, pos, order, kv, n, max_ctx, scores, pmax, o, err);
+        return hd != 32 && launch_b_attention(st, hd, qkv, qkv_stride, pos, order, kv, n, max_ctx, scores, pmax, o, err);
     const uint32_t nch = div_up(max_ctx, ACH);
     const dim3 gs(nch, kv.n_kv, div_up(n, PRB)), gm(n * kv.n_heads);
     const uint32_t ss = b_sc_stride(max_ctx);
-    if (hd == 64)
+    if (hd == 32)
+        BLAUNCH(k_p_scores<32>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
+    else if (hd == 64)
         BLAUNCH(k_p_scores<64>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
     else
         BLAUNCH(k_p_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
@@ -1493,7 +1499,12 @@ bool launch_p_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t 
         BLAUNCH(k_b_softmax<512>, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
     const dim3 gp(div_up(n, 4u), kv.n_kv);
 #define PPV(H, P) BLAUNCH((k_p_pv<H, P>), gp, dim3(256), 0, st, scores, ss, pos, n, kv, o)
-    if (hd == 64) {
+    if (hd == 32) {
+        if (rep == 1) PPV(32, 1);
+        else if (rep == 2) PPV(32, 2);
+        else if (rep == 4) PPV(32, 4);
+        else PPV(32, 8);
+    } else if (hd == 64) {
         if (rep == 1) PPV(64, 1);
         else if (rep == 2) PPV(64, 2);
         else if (rep == 4) PPV(64, 4);

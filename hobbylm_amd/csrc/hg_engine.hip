@@ -566,14 +566,15 @@ int finish(hg_kv *kv, float *logits, uint32_t *next) {
     return HG_OK;
 }
 
-// The prompt path: all rows at once (default), or with HG_PREFILL=rows one replayed decode-shaped
-// step per row (the reference-order kernels of the decode step in prompt order).
-bool batched_prefill() {
-    static const bool rows = [] {
-        const char *e = getenv("HG_PREFILL");
-        return e && strcmp(e, "rows") == 0;
-    }();
-    return !rows;
+// The prompt path: all rows at once (default; shapes it does not take fall back), with
+// HG_PREFILL=rows one replayed decode-shaped step per row (the reference-order kernels of the
+// decode step in prompt order), with HG_PREFILL=batched all rows at once or an error.
+enum { PF_AUTO, PF_ROWS, PF_BATCHED };
+int prefill_mode() {
+    const char *e = getenv("HG_PREFILL");
+    if (e && strcmp(e, "rows") == 0) return PF_ROWS;
+    if (e && strcmp(e, "batched") == 0) return PF_BATCHED;
+    return PF_AUTO;
 }
 
 int check_step(const hg_model *m, const hg_kv *kv, uint32_t pos, uint32_t n) {
@@ -756,7 +757,10 @@ int hg_prefill(const hg_model *m, hg_kv *kv, const float *inputs, uint32_t tn, f
                 if (g.second) (void)hipGraphExecDestroy(g.second);
             kv->g_body.clear();
         }
-        if (kv->exact && batched_prefill() && prefill_batched_ok(m, base + tn)) {
+        const int mode = prefill_mode();
+        const bool ok = kv->exact && prefill_batched_ok(m, base + tn);
+        if (mode == PF_BATCHED && !ok) return fail(HG_ERR_UNSUPPORTED, "HG_PREFILL=batched: shape or cache not supported");
+        if (mode != PF_ROWS && ok) {
             if (!kv->pw) kv->pw = std::make_unique<PrefillWork>();
             if ((rc = prefill_batched(m, *kv->pw, kv->st, inputs, base, tn, kv->kc.as<float>(), kv->vc.as<float>(),
                                       kv->cap, kv->x.as<float>(), kv->rec_idx.as<uint32_t>(), kv->rec_w.as<float>())))
@@ -881,6 +885,242 @@ int hg_sample(const float *logits, uint32_t n, float temp, float top_p, uint64_t
             return fail(HG_ERR_DEVICE, "sampling launch failed");
         HIP_TRY(hipMemcpy(out, pick.p, 4, hipMemcpyDeviceToHost));
         HIP_TRY(hipMemcpy(rng_state, w.rng.p, 8, hipMemcpyDeviceToHost));
+        return HG_OK;
+    });
+}
+
+int hg_run_block(const hg_model *m, hg_kv *kv, const float *block, uint32_t b, uint32_t base, int append,
+                 float *logits, float *bk, float *bv) {
+    return guard([&]() -> int {
+        if (!m || !kv || !block) return fail(HG_ERR_ARG, "NULL argument");
+        if (kv->m != m) return fail(HG_ERR_ARG, "cache does not belong to this model");
+        if (b == 0) return fail(HG_ERR_ARG, "run_block needs at least one row");
+        if (base > kv->len) return fail(HG_ERR_ARG, "base beyond the cache length");
+        if (append && base != kv->len) return fail(HG_ERR_ARG, "append needs base == the cache length");
+        if ((uint64_t)base + b > kv->cap) return fail(HG_ERR_ARG, "block beyond the cache capacity");
+        if (!prefill_batched_ok(m, base + b)) return fail(HG_ERR_UNSUPPORTED, "run_block: shape not supported");
+        const hg_config &c = m->c;
+        const size_t kvd = (size_t)c.n_kv_heads * c.head_dim, lb = (size_t)c.vocab_size * b * 4;
+        const size_t kb = (size_t)c.n_layers * b * kvd * 4;
+        DevBuf dl, dk, dv;
+        int rc;
+        if ((logits && (rc = dl.alloc(lb))) || (bk && (rc = dk.alloc(kb))) || (bv && (rc = dv.alloc(kb)))) return rc;
+        if (!kv->pw) kv->pw = std::make_unique<PrefillWork>();
+        if ((rc = run_block_batched(m, *kv->pw, kv->st, block, nullptr, base, b, kv->kc.as<float>(), kv->vc.as<float>(),
+                                    kv->cap, append != 0, dl.as<float>(), dk.as<float>(), dv.as<float>())))
+            return rc;
+        if (logits) HIP_TRY(hipMemcpy(logits, dl.p, lb, hipMemcpyDeviceToHost));
+        if (bk) HIP_TRY(hipMemcpy(bk, dk.p, kb, hipMemcpyDeviceToHost));
+        if (bv) HIP_TRY(hipMemcpy(bv, dv.p, kb, hipMemcpyDeviceToHost));
+        if (append) kv->len = base + b;
+        return HG_OK;
+    });
+}
+
+int hg_forward_bidir(const hg_model *m, const float *inputs, uint32_t tn, float *logits) {
+    return guard([&]() -> int {
+        if (!m || !inputs || !logits) return fail(HG_ERR_ARG, "NULL argument");
+        hg_kv *kv = nullptr;
+        int rc = hg_kv_new(m, tn, 0, &kv);
+        if (rc) return rc;
+        rc = hg_run_block(m, kv, inputs, tn, 0, 0, logits, nullptr, nullptr);
+        hg_kv_free(kv);
+        return rc;
+    });
+}
+
+namespace {
+
+// The scoring state of one Engine::generate_diffusion call (lib.rs:214-495).
+struct Diffusion {
+    const hg_model *m = nullptr;
+    const hg_diff_opts *o = nullptr;
+    hg_kv *kv = nullptr;          // cached: the persistent prefix cache; uncached: a scratch cache
+    std::vector<uint32_t> canvas; // uncached: the canvas; cached: the committed ids
+    size_t committed = 0;
+    uint32_t valid = 0, mask = 0;
+    DevBuf logits, ids, present, cur, pred, pconf, cconf;
+    std::vector<uint8_t> h_present;
+    ~Diffusion() {
+        if (kv) hg_kv_free(kv);
+    }
+
+    // Engine::score_block / diffusion_block's scoring (lib.rs:171-205, 226-262) of the block
+    // [b0, b0 + len) whose current ids are blk: run_block of the block over the cache (cached) or
+    // forward_bidir of canvas[0 .. b0 + len) (uncached), then the rows scored on the device.
+    int score(const uint32_t *blk, size_t b0, size_t len, uint32_t *h_pred, float *h_pconf, float *h_cconf) {
+        const hg_config &c = m->c;
+        const uint32_t V = c.vocab_size;
+        hipStream_t st = kv->st;
+        const bool cached = o->cached != 0;
+        const size_t rows = cached ? len : b0 + len;
+        const uint32_t *src = cached ? blk : canvas.data();
+        HIP_TRY(hipMemcpyAsync(ids.p, src, rows * 4, hipMemcpyHostToDevice, st));
+        int rc = run_block_batched(m, *kv->pw, st, nullptr, ids.as<uint32_t>(), cached ? (uint32_t)b0 : 0u,
+                                   (uint32_t)rows, kv->kc.as<float>(), kv->vc.as<float>(), kv->cap, false,
+                                   logits.as<float>(), nullptr, nullptr);
+        if (rc) return rc;
+        const bool pen = o->rep_penalty != 1.0f;
+        if (pen) {   // the present ids: committed (or the canvas up to b1) and the block, mask excluded
+            std::fill(h_present.begin(), h_present.end(), 0);
+            auto mark = [&](uint32_t id) {
+                if (id != mask && id < valid) h_present[id] = 1;
+            };
+            if (cached) {
+                for (size_t i = 0; i < committed; ++i) mark(canvas[i]);
+                for (size_t i = 0; i < len; ++i) mark(blk[i]);
+            } else {
+                for (size_t i = 0; i < b0 + len; ++i) mark(canvas[i]);
+            }
+            HIP_TRY(hipMemcpyAsync(present.p, h_present.data(), valid, hipMemcpyHostToDevice, st));
+        }
+        HIP_TRY(hipMemcpyAsync(cur.p, blk, len * 4, hipMemcpyHostToDevice, st));
+        const float *lg = logits.as<float>() + (cached ? 0 : b0 * (size_t)V);
+        if (!enqueue_score_rows(st, lg, (uint32_t)len, V, valid, pen ? present.as<uint8_t>() : nullptr, o->rep_penalty,
+                                cur.as<uint32_t>(), pred.as<uint32_t>(), pconf.as<float>(), cconf.as<float>()))
+            return fail(HG_ERR_DEVICE, "scoring launch failed");
+        HIP_TRY(hipMemcpyAsync(h_pred, pred.p, len * 4, hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipMemcpyAsync(h_pconf, pconf.p, len * 4, hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipMemcpyAsync(h_cconf, cconf.p, len * 4, hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipStreamSynchronize(st));
+        return HG_OK;
+    }
+};
+
+}  // namespace
+
+int hg_generate_diffusion(const hg_model *m, const uint32_t *prompt, uint32_t n_prompt, const hg_diff_opts *opts,
+                          uint32_t eos, uint32_t *out_ids, uint32_t *n_out) {
+    return guard([&]() -> int {
+        if (!m || !opts || !n_out) return fail(HG_ERR_ARG, "NULL argument");
+        *n_out = 0;
+        if (n_prompt > 0 && !prompt) return fail(HG_ERR_ARG, "prompt is NULL");
+        if (n_prompt == 0) return HG_OK;
+        if (opts->block == 0 || opts->steps == 0) return fail(HG_ERR_ARG, "block and steps must be positive");
+        if (opts->temp > 0.0f) return fail(HG_ERR_UNSUPPORTED, "diffusion decoding with temp > 0 (Gumbel draws)");
+        if (!out_ids && opts->gen_len > 0) return fail(HG_ERR_ARG, "out_ids is NULL");
+        const hg_config &c = m->c;
+        const size_t p = n_prompt, V = c.vocab_size, ctx = c.context_length;
+        for (size_t i = 0; i < p; ++i)
+            if (prompt[i] >= V) return fail(HG_ERR_ARG, "token out of range");
+        if (c.mask_token_id >= V) return fail(HG_ERR_UNSUPPORTED, "the mask id is outside the vocabulary");
+        Diffusion D;
+        D.m = m;
+        D.o = opts;
+        D.valid = (uint32_t)std::min<size_t>(V, 50257);
+        D.mask = c.mask_token_id;
+        const bool cached = opts->cached != 0;
+        const size_t room = cached ? (ctx > p + opts->block ? ctx - (p + opts->block) : 0) : (ctx > p ? ctx - p : 0);
+        const size_t gen_len = std::min<size_t>(opts->gen_len, std::max<size_t>(room, 1));
+        const size_t span = cached ? std::max<size_t>(opts->block, p) : p + gen_len;
+        int rc = hg_kv_new(m, (uint32_t)std::min<size_t>(ctx, p + gen_len + opts->block), 0, &D.kv);
+        if (rc) return rc;
+        D.kv->pw = std::make_unique<PrefillWork>();
+        if ((rc = D.logits.alloc(span * V * 4)) || (rc = D.ids.alloc(span * 4)) || (rc = D.present.alloc(D.valid)) ||
+            (rc = D.cur.alloc(opts->block * 4)) || (rc = D.pred.alloc(opts->block * 4)) ||
+            (rc = D.pconf.alloc(opts->block * 4)) || (rc = D.cconf.alloc(opts->block * 4)))
+            return rc;
+        D.h_present.assign(D.valid, 0);
+        D.canvas.assign(prompt, prompt + p);
+        if (cached) {   // the bidirectional prompt encode seeds the cache (lib.rs:281-289)
+            HIP_TRY(hipMemcpy(D.ids.p, prompt, p * 4, hipMemcpyHostToDevice));
+            if ((rc = run_block_batched(m, *D.kv->pw, D.kv->st, nullptr, D.ids.as<uint32_t>(), 0, (uint32_t)p,
+                                        D.kv->kc.as<float>(), D.kv->vc.as<float>(), D.kv->cap, true, nullptr, nullptr,
+                                        nullptr)))
+                return rc;
+            D.kv->len = (uint32_t)p;
+            D.committed = p;
+        } else {
+            D.canvas.resize(p + gen_len, D.mask);
+        }
+        std::vector<uint32_t> blk(opts->block), pred(opts->block);
+        std::vector<float> pconf(opts->block), cconf(opts->block);
+        size_t result = gen_len;
+        for (size_t b0 = p; b0 < p + gen_len;) {
+            const size_t b1 = std::min<size_t>(b0 + opts->block, p + gen_len), len = b1 - b0;
+            uint32_t *cur = cached ? blk.data() : D.canvas.data() + b0;
+            if (cached) std::fill(blk.begin(), blk.begin() + len, D.mask);
+            auto any_mask = [&] {
+                for (size_t i = 0; i < len; ++i)
+                    if (cur[i] == D.mask) return true;
+                return false;
+            };
+            auto score = [&] { return D.score(cur, b0, len, pred.data(), pconf.data(), cconf.data()); };
+            if (cached && opts->threshold > 0.0f) {   // confidence-threshold decode (lib.rs:302-327)
+                for (size_t it = 0; it < std::max<size_t>(len, 1); ++it) {
+                    if (!any_mask()) break;
+                    if ((rc = score())) return rc;
+                    bool any = false, have = false;
+                    size_t best = 0;
+                    for (size_t i = 0; i < len; ++i)   // Iterator::max_by: the last of equal maxima
+                        if (cur[i] == D.mask && (!have || !(pconf[i] < pconf[best]))) {
+                            best = i;
+                            have = true;
+                        }
+                    for (size_t i = 0; i < len; ++i)
+                        if (cur[i] == D.mask && pconf[i] >= opts->threshold) {
+                            cur[i] = pred[i];
+                            any = true;
+                        }
+                    if (!any) cur[best] = pred[best];
+                }
+            } else {   // the num_transfer schedule (lib.rs:329-352, 420-451)
+                size_t sb = (size_t)roundf((float)(opts->steps * len) / (float)gen_len);
+                sb = std::max<size_t>(sb, 1);
+                const size_t base_n = len / sb;
+                for (size_t s = 0; s < sb; ++s) {
+                    const size_t k_step = base_n + (s < len - base_n * sb ? 1 : 0);   // num_transfer (lib.rs:68-76)
+                    if ((rc = score())) return rc;
+                    std::vector<std::pair<size_t, float>> cand;
+                    for (size_t i = 0; i < len; ++i)
+                        if (cur[i] == D.mask) cand.emplace_back(i, pconf[i]);
+                    if (cand.empty()) break;
+                    std::stable_sort(cand.begin(), cand.end(), [](const auto &a, const auto &b) { return a.second > b.second; });
+                    for (size_t q = 0; q < std::min(k_step, cand.size()); ++q) cur[cand[q].first] = pred[cand[q].first];
+                }
+                if (any_mask()) {
+                    if ((rc = score())) return rc;
+                    for (size_t i = 0; i < len; ++i)
+                        if (cur[i] == D.mask) cur[i] = pred[i];
+                }
+            }
+            for (uint32_t rs = 0; rs < opts->remask_steps; ++rs) {   // re-mask the least confident (lib.rs:354-371)
+                if ((rc = score())) return rc;
+                size_t r = std::max<size_t>((size_t)((float)len * opts->remask_frac), 1);
+                std::vector<std::pair<size_t, float>> idx;
+                for (size_t i = 0; i < len; ++i) idx.emplace_back(i, cconf[i]);
+                std::stable_sort(idx.begin(), idx.end(), [](const auto &a, const auto &b) { return a.second < b.second; });
+                for (size_t q = 0; q < std::min(r, len); ++q) cur[idx[q].first] = D.mask;
+                if ((rc = score())) return rc;
+                for (size_t i = 0; i < len; ++i)
+                    if (cur[i] == D.mask) cur[i] = pred[i];
+            }
+            if (cached) {   // finalize: the block's K/V into the cache (lib.rs:374-381)
+                HIP_TRY(hipMemcpy(D.ids.p, blk.data(), len * 4, hipMemcpyHostToDevice));
+                if ((rc = run_block_batched(m, *D.kv->pw, D.kv->st, nullptr, D.ids.as<uint32_t>(), (uint32_t)b0,
+                                            (uint32_t)len, D.kv->kc.as<float>(), D.kv->vc.as<float>(), D.kv->cap, true,
+                                            nullptr, nullptr, nullptr)))
+                    return rc;
+                D.kv->len = (uint32_t)b1;
+                D.canvas.insert(D.canvas.end(), blk.begin(), blk.begin() + len);
+                D.committed = b1;
+            }
+            size_t endpos = b1;
+            bool hit = false;
+            for (size_t i = p; i < b1; ++i)
+                if (D.canvas[i] == eos) {
+                    endpos = i;
+                    hit = true;
+                    break;
+                }
+            if (hit) {
+                result = endpos - p;
+                break;
+            }
+            b0 = b1;
+        }
+        memcpy(out_ids, D.canvas.data() + p, result * 4);
+        *n_out = (uint32_t)result;
         return HG_OK;
     });
 }

@@ -420,6 +420,7 @@ int config_from_gguf(const Gguf &g, hg_config &c, std::string &err) {
     if (!g.get_f32(key("expert_weights_scale"), c.expert_weights_scale)) c.expert_weights_scale = 1.0f;
     bool b;
     c.expert_weights_norm = g.get_bool(key("expert_weights_norm"), b) ? b : 0;
+    if (!g.get_u32("diffusion.mask_token_id", c.mask_token_id)) c.mask_token_id = 50257;   // config.rs:93
     return HG_OK;
 }
 

@@ -41,10 +41,11 @@ uint32_t chunk_rows(const hg_config &c, uint32_t win, uint32_t tn) {
 // Per chunk of n rows at positions base0 ..: pos[i] = base0 + i, order[i] = n - 1 - i (longest
 // context first) and the plain column tiles of 16, 32 and 64 entries (tables at k tmax, counts
 // at counts[k]).
-__global__ void k_p_setup(uint32_t n, uint32_t base0, uint32_t tmax, uint32_t *pos, uint32_t *order,
-                          GemmTile *tiles, uint32_t *counts) {
+__global__ void k_p_setup(uint32_t n, uint32_t base0, uint32_t tmax, uint32_t *pos, uint32_t *apos, uint32_t bidir,
+                          uint32_t *order, GemmTile *tiles, uint32_t *counts) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
         pos[i] = base0 + i;
+        apos[i] = bidir ? base0 + n - 1 : base0 + i;   // the last position each row attends to
         order[i] = n - 1 - i;
 #pragma unroll
         for (uint32_t k = 0; k < 3; ++k) {
@@ -60,6 +61,16 @@ __global__ void k_p_setup(uint32_t n, uint32_t base0, uint32_t tmax, uint32_t *p
         }
     }
     if (blockIdx.x == 0 && threadIdx.x < 3) counts[threadIdx.x] = div_up(n, 16u << threadIdx.x);
+}
+
+// Rows r = blockIdx.y of the chunk's k and v (normed and rotated) into bk / bv [R][kvd].
+__global__ void k_p_rows_out(const float *__restrict__ qkv, uint32_t qw, uint32_t qd, uint32_t kvd, float *bk,
+                             float *bv) {
+    const uint32_t r = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= kvd) return;
+    const float *row = qkv + (size_t)r * qw + qd;
+    if (bk) bk[(size_t)r * kvd + i] = row[i];
+    if (bv) bv[(size_t)r * kvd + i] = row[kvd + i];
 }
 
 __global__ void k_p_iota(uint32_t n, uint32_t *out) {
@@ -133,7 +144,7 @@ int grow(PrefillWork &w, const hg_model *m, const Shapes &s, uint32_t R, uint32_
         const uint32_t tk = std::max(c.top_k, 1u), ns = s.ns, tmax = div_up(R, 16);
         const uint32_t max_te = c.n_experts + 1 + div_up(R * ns, std::max(s.tt_e, 16u));
         const size_t arows = std::max((size_t)ns * s.f, (size_t)s.df), qrows = std::max((size_t)ns * s.ncf, (size_t)s.ncdf);
-        if ((rc = w.pos.alloc((size_t)R * 4)) || (rc = w.order.alloc((size_t)R * 4)) ||
+        if ((rc = w.pos.alloc((size_t)R * 4)) || (rc = w.apos.alloc((size_t)R * 4)) || (rc = w.order.alloc((size_t)R * 4)) ||
             (rc = w.ptiles.alloc((size_t)3 * tmax * sizeof(GemmTile))) || (rc = w.pn.alloc(3 * 4)) ||
             (rc = w.xq.alloc((size_t)R * s.ncd * CHUNK_BYTES)) || (rc = w.xd.alloc((size_t)R * s.ncd * 16)) ||
             (rc = w.qkv.alloc((size_t)R * s.qw * 4)) || (rc = w.o.alloc((size_t)R * s.qd * 4)) ||
@@ -177,14 +188,23 @@ void gemm(hipStream_t st, int mode, const GemmArgs &g, uint32_t max_tiles, uint3
     if (!launch_p_gemm(st, mode, g, max_tiles, tt)) note_launch_error(hipErrorInvalidConfiguration, what);
 }
 
+// What a chunk does besides the layers: prompt rows (causal, appended to the cache) or a
+// run_block block (every row attends to all block rows; appended only when finalizing; its K/V
+// rows per layer to bk / bv [L][R][kvd]; logits of every row).
+struct ChunkMode {
+    bool bidir = false, store = true;
+    float *bk = nullptr, *bv = nullptr, *logits = nullptr;
+};
+
 // The layers over one chunk of R rows at positions base0 .. base0 + R - 1 (x: their residuals).
 void enqueue_chunk(const hg_model *m, PrefillWork &w, const Shapes &s, hipStream_t st, float *x, uint32_t base0,
-                   uint32_t R, float *kc, float *vc, uint32_t cap) {
+                   uint32_t R, float *kc, float *vc, uint32_t cap, const ChunkMode &cm = ChunkMode()) {
     const hg_config &c = m->c;
     const uint32_t win = window_for(base0 + R), d = s.d, hd = s.hd, nkv = c.n_kv_heads;
     const uint32_t tmax = div_up(w.rows, 16);
     hipLaunchKernelGGL(k_p_setup, dim3(div_up(R, 256)), dim3(256), 0, st, R, base0, tmax, w.pos.as<uint32_t>(),
-                       w.order.as<uint32_t>(), w.ptiles.as<GemmTile>(), w.pn.as<uint32_t>());
+                       w.apos.as<uint32_t>(), cm.bidir ? 1u : 0u, w.order.as<uint32_t>(), w.ptiles.as<GemmTile>(),
+                       w.pn.as<uint32_t>());
     const hipError_t le = hipGetLastError();
     if (le != hipSuccess) note_launch_error(le, "k_p_setup");
     PagedKV kvp;
@@ -209,8 +229,15 @@ void enqueue_chunk(const hg_model *m, PrefillWork &w, const Shapes &s, hipStream
         if (!launch_b_qk_rope_append(st, hd, w.qkv.as<float>(), s.qw, L.q_norm.as<float>(), L.k_norm.as<float>(),
                                      c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), pos, kvp, R))
             note_launch_error(hipErrorInvalidConfiguration, "QK-norm / RoPE");
-        launch_p_kv_store(st, w.qkv.as<float>(), s.qw, s.qd, s.kvd, hd, nkv, base0, R, cap, Lk, Lv);
-        if (!launch_p_attention(st, hd, w.qkv.as<float>(), s.qw, pos, w.order.as<uint32_t>(), kvp, R, win,
+        if (cm.store) launch_p_kv_store(st, w.qkv.as<float>(), s.qw, s.qd, s.kvd, hd, nkv, base0, R, cap, Lk, Lv);
+        if (cm.bk || cm.bv) {
+            hipLaunchKernelGGL(k_p_rows_out, dim3(div_up(s.kvd, 256), R), dim3(256), 0, st, w.qkv.as<float>(), s.qw,
+                               s.qd, s.kvd, cm.bk ? cm.bk + (size_t)l * R * s.kvd : nullptr,
+                               cm.bv ? cm.bv + (size_t)l * R * s.kvd : nullptr);
+            const hipError_t e2 = hipGetLastError();
+            if (e2 != hipSuccess) note_launch_error(e2, "k_p_rows_out");
+        }
+        if (!launch_p_attention(st, hd, w.qkv.as<float>(), s.qw, w.apos.as<uint32_t>(), w.order.as<uint32_t>(), kvp, R, win,
                                 w.scores.as<float>(), w.pmax.as<float>(), w.o.as<float>(), w.err.as<uint32_t>()))
             note_launch_error(hipErrorInvalidConfiguration, "causal attention");
         launch_b_quant_rows(st, w.o.as<float>(), s.qd, s.qd, R, w.oq.as<uint8_t>(), s.ncq * CHUNK_BYTES,
@@ -280,13 +307,20 @@ void enqueue_chunk(const hg_model *m, PrefillWork &w, const Shapes &s, hipStream
                  div_up(R, s.tt_df), s.tt_df, "dense down GEMM");
         }
     }
+    if (cm.logits) {   // every row's logits: output_norm rows, output.matmul (model.rs:504-507)
+        launch_rmsnorm_quant_rows(st, true, R, x, m->output_norm.as<float>(), c.rms_eps, d, nullptr, xq, xd);
+        gemm(st, GM_STORE, plain(w, m->output.m, xq, xd, cm.logits, c.vocab_size, s.tt_d), nt_d, s.tt_d,
+             "lm_head GEMM");
+    }
 }
 
 }  // namespace
 
 bool prefill_batched_ok(const hg_model *m, uint32_t cap) {
     const hg_config &c = m->c;
-    if (c.head_dim != 64 && c.head_dim != 128) return false;
+    if (c.head_dim != 32 && c.head_dim != 64 && c.head_dim != 128) return false;
+    const uint32_t rep = c.n_heads / c.n_kv_heads;
+    if (c.head_dim == 32 && rep != 1 && rep != 2 && rep != 4 && rep != 8) return false;
     if (c.n_experts + 1 > MAX_GROUPS) return false;
     if (!batch_ctx_ok(window_for(cap))) return false;
     const Shapes s = shapes_of(m);
@@ -294,6 +328,42 @@ bool prefill_batched_ok(const hg_model *m, uint32_t cap) {
     if (has_moe(m) && !s.tt_e) return false;
     if (has_dense(m) && !s.tt_df) return false;
     return true;
+}
+
+int run_block_batched(const hg_model *m, PrefillWork &w, hipStream_t st, const float *block, const uint32_t *ids,
+                      uint32_t base, uint32_t b, float *kc, float *vc, uint32_t cap, bool append, float *logits,
+                      float *bk, float *bv) {
+    const hg_config &c = m->c;
+    const Shapes s = shapes_of(m);
+    const uint32_t win = window_for(base + b);
+    const uint32_t R = chunk_rows(c, win, b);
+    if (R < b) return fail(HG_ERR_UNSUPPORTED, "run_block: a block of " + std::to_string(b) + " rows at this context");
+    HIP_TRY(hipStreamSynchronize(st));
+    int rc = grow(w, m, s, b, win, b);
+    if (rc) return rc;
+    std::string msg;
+    (void)take_launch_error(msg);
+    if (block) HIP_TRY(hipMemcpyAsync(w.xall.p, block, (size_t)b * s.d * 4, hipMemcpyHostToDevice, st));
+    else launch_b_embed(st, m->token_embd.as<float>(), s.d, ids, b, w.xall.as<float>());
+    ChunkMode cm;
+    cm.bidir = true;
+    cm.store = append;
+    cm.bk = bk;
+    cm.bv = bv;
+    cm.logits = logits;
+    enqueue_chunk(m, w, s, st, w.xall.as<float>(), base, b, kc, vc, cap, cm);
+    if (take_launch_error(msg) != hipSuccess) {
+        (void)hipStreamSynchronize(st);
+        return fail(HG_ERR_DEVICE, "run_block: " + msg);
+    }
+    uint32_t e = 0;
+    HIP_TRY(hipMemcpyAsync(&e, w.err.p, 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    if (e) {
+        HIP_TRY(hipMemset(w.err.p, 0, 4));
+        return fail(HG_ERR_DEVICE, "run_block: an attention hand-off wait exceeded its bound");
+    }
+    return HG_OK;
 }
 
 int prefill_batched(const hg_model *m, PrefillWork &w, hipStream_t st, const float *inputs, uint32_t base,

@@ -24,4 +24,11 @@ int sample_init(SampleWork &w, uint32_t V);
 bool enqueue_sample(hipStream_t st, SampleWork &w, const float *logits, uint32_t valid, float temp, float top_p,
                     float rep_penalty, uint32_t *pick, StepParams *p);
 
+// Engine::score_block at temperature 0 (lib.rs:226-262) of `rows` logit rows [rows][V] (device):
+// per row the ids >= valid masked, the presence penalty (present: valid bytes, nonzero = present;
+// nullptr = off), pred = the argmax, pconf / cconf = the row's softmax at pred and at cur[row].
+bool enqueue_score_rows(hipStream_t st, const float *logits, uint32_t rows, uint32_t V, uint32_t valid,
+                        const uint8_t *present, float rp, const uint32_t *cur, uint32_t *pred, float *pconf,
+                        float *cconf);
+
 }  // namespace hg

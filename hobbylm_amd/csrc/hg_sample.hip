@@ -243,7 +243,82 @@ __global__ __launch_bounds__(NT) void k_s_pick(const float *__restrict__ q, cons
     }
 }
 
+// Engine::score_block at temp 0 (lib.rs:226-262): row r = blockIdx.x of logits [rows][V] with the
+// ids >= valid masked and, when present != nullptr, the presence penalty once per present id;
+// pred = the argmax (gumbel_argmax at temp 0, sample.rs:36-38), then ops::softmax of the row
+// (ops.rs:112-128: m, e = exp(v - m), the id-order sum, x * (1 / sum)) read at pred and at the
+// row's current id.  One workgroup per row.
+__global__ __launch_bounds__(NT) void k_d_score(const float *__restrict__ logits, uint32_t V, uint32_t valid,
+                                                const uint8_t *__restrict__ present, float rp,
+                                                const uint32_t *__restrict__ cur, uint32_t *pred, float *pconf,
+                                                float *cconf) {
+    __shared__ SegLds L;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t r = blockIdx.x;
+    const float *row = logits + (size_t)r * V;
+    auto pen = [&](uint32_t i) {
+        float l = i < valid ? row[i] : -__builtin_huge_valf();
+        if (present && i < valid && present[i]) l = l > 0.0f ? l / rp : l * rp;
+        return l;
+    };
+    const WaveExpTab tab = WaveExpTab::load(lane);
+    float mv = -__builtin_huge_valf();
+    uint32_t mi = 0xffffffffu;
+    for (uint32_t i = tid; i < V; i += NT) {
+        const float v = pen(i);
+        if (v > mv) {
+            mv = v;
+            mi = i;
+        }
+    }
+    for (int m = 1; m < 64; m <<= 1) {
+        const float ov = shfl_xor(mv, m);
+        const uint32_t oi = (uint32_t)shfl_xor_i((int)mi, m);
+        if (ov > mv || (ov == mv && oi < mi)) {
+            mv = ov;
+            mi = oi;
+        }
+    }
+    if (lane == 0) {
+        L.red[wave] = mv;
+        L.redi[wave] = mi;
+    }
+    __syncthreads();
+    float m = L.red[0];
+    uint32_t pk = L.redi[0];
+    for (uint32_t w = 1; w < NT / 64; ++w)
+        if (L.red[w] > m || (L.red[w] == m && L.redi[w] < pk)) {
+            m = L.red[w];
+            pk = L.redi[w];
+        }
+    if (pk == 0xffffffffu) pk = 0;   // sample::argmax: 0 when nothing exceeds -inf
+    float sum = 0.0f;
+    for (uint32_t s0 = 0; s0 < V; s0 += SEG - 1) {   // sum += exp(v - m) in id order
+        const uint32_t cnt = min(SEG - 1, V - s0);
+        if (tid == 0) L.a[0] = sum;
+        for (uint32_t k0 = 0; k0 < cnt; k0 += NT) {   // (uniform: every lane calls the exp)
+            const uint32_t k = k0 + tid;
+            const float e = hg_expf_l((k < cnt ? pen(s0 + k) : m) - m, tab);
+            if (k < cnt) L.a[1 + k] = e;
+        }
+        sum = seg_sum(L, cnt + 1, wave, lane);
+    }
+    if (tid == 0) {
+        const float inv = 1.0f / sum;
+        pred[r] = pk;
+        pconf[r] = hg_expf(pen(pk) - m) * inv;
+        cconf[r] = hg_expf(pen(cur[r]) - m) * inv;
+    }
+}
+
 }  // namespace
+
+bool enqueue_score_rows(hipStream_t st, const float *logits, uint32_t rows, uint32_t V, uint32_t valid,
+                        const uint8_t *present, float rp, const uint32_t *cur, uint32_t *pred, float *pconf,
+                        float *cconf) {
+    hipLaunchKernelGGL(k_d_score, dim3(rows), dim3(NT), 0, st, logits, V, valid, present, rp, cur, pred, pconf, cconf);
+    return hipGetLastError() == hipSuccess;
+}
 
 int sample_init(SampleWork &w, uint32_t V) {
     int rc;

@@ -70,6 +70,9 @@ PRESETS: Dict[str, Shape] = {
     # small shapes that keep every feature (dense layer, routed + shared experts, GQA,
     # a K that is not a multiple of 128) and run in milliseconds on the CPU oracle
     "tiny": Shape(128, 3, 1, 4, 2, 32, 256, 96, 8, 2, 1, 1000, context_length=512),
+    # the tiny shape with the GPT-2 vocabulary padded to 50304: the diffusion [MASK] id 50257
+    # (config.rs:93's default) is a real row, and ids >= 50257 are masked out of every draw
+    "tiny_diff": Shape(128, 3, 1, 4, 2, 32, 256, 96, 8, 2, 1, 50304, context_length=512),
     # the tiny shape with room for prompts of thousands of rows
     "tiny_long": Shape(128, 3, 1, 4, 2, 32, 256, 96, 8, 2, 1, 1000, context_length=4096),
     "tiny_noshared": Shape(64, 2, 1, 2, 1, 32, 128, 64, 6, 3, 0, 300, context_length=256,

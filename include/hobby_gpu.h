@@ -59,6 +59,7 @@ typedef struct hg_config {
     uint32_t vocab_size, context_length;
     float rms_eps, rope_theta, expert_weights_scale;
     int32_t expert_weights_norm, gating_sigmoid;
+    uint32_t mask_token_id;   /* the diffusion canvas's [MASK] id (config.rs:93, default 50257) */
 } hg_config;
 
 /* Message of the last failing call on this thread ("" if none). */
@@ -161,6 +162,38 @@ int hg_generate(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uint32_t n
 /* sample::sample (sample.rs:66-112) of host logits[0 .. n) on the device, with the RNG state
  * *rng_state (Rng's u64: the seed clamped to >= 1), which it advances; the pick in *out. */
 int hg_sample(const float *logits, uint32_t n, float temp, float top_p, uint64_t *rng_state, uint32_t *out);
+/* ---- the diffusion block path (model.rs:440-651, lib.rs:164-495) ---------------------- */
+
+/* Model::run_block (model.rs:471-585): the b block rows (residual inputs, b x d_model floats)
+ * at positions base .. base + b - 1 attend to the cache's rows 0 .. base - 1 and to every block
+ * row (bidirectional within the block).  logits [b][vocab] and the block's K/V rows bk / bv
+ * [n_layers][b][kv_dim] when not NULL.  append == 0 leaves the cache as it was (run_block is
+ * non-destructive); append != 0 (base must equal the cache length) also appends the block's
+ * rows, as lib.rs:374-381 does when a block is finalized. */
+int hg_run_block(const hg_model *m, hg_kv *kv, const float *block, uint32_t b, uint32_t base, int append,
+                 float *logits, float *bk, float *bv);
+/* Model::forward_bidir (model.rs:443-468): all tn rows with full bidirectional attention and no
+ * cache; logits [tn][vocab]. */
+int hg_forward_bidir(const hg_model *m, const float *inputs, uint32_t tn, float *logits);
+/* DiffOpts (lib.rs:45-65). */
+typedef struct hg_diff_opts {
+    uint32_t gen_len, block, steps;
+    float temp, rep_penalty;
+    uint32_t remask_steps;
+    float remask_frac;
+    uint64_t seed;
+    uint32_t cached;
+    float threshold;
+} hg_diff_opts;
+/* Engine::generate_diffusion (lib.rs:214-495) over token ids: the prefix-cached (cached != 0,
+ * lib.rs:269-407) or the uncached (lib.rs:410-495) semi-autoregressive denoising of gen_len ids
+ * after the prompt, with the block's logits scored on the device (the mask, the presence
+ * penalty, the pick and its softmax confidences; only those cross PCIe).  Writes the generated
+ * ids up to the first eos (at most gen_len); *n_out receives the count.  temp > 0 (Gumbel
+ * draws, sample.rs:32-50) returns HG_ERR_UNSUPPORTED. */
+int hg_generate_diffusion(const hg_model *m, const uint32_t *prompt, uint32_t n_prompt, const hg_diff_opts *opts,
+                          uint32_t eos, uint32_t *out_ids, uint32_t *n_out);
+
 /* Routing of the last processed row, per layer in rank order (model.rs:282-293):
  * idx[L*top_k] (UINT32_MAX for dense layers) and the scaled weights w[L*top_k]. */
 int hg_last_routing(const hg_kv *kv, uint32_t *idx, float *w);

@@ -25,7 +25,19 @@ class OrcConfig(C.Structure):
         "d_model", "n_layers", "n_dense", "n_heads", "n_kv_heads", "head_dim", "dense_ffn",
         "expert_ffn", "n_experts", "top_k", "n_shared", "vocab_size", "context_length")] + [
         ("rms_eps", C.c_float), ("rope_theta", C.c_float), ("expert_weights_scale", C.c_float),
-        ("expert_weights_norm", C.c_int32), ("gating_sigmoid", C.c_int32)]
+        ("expert_weights_norm", C.c_int32), ("gating_sigmoid", C.c_int32), ("mask_token_id", C.c_uint32)]
+
+
+class DiffOpts(C.Structure):
+    """orc_diff_opts: DiffOpts (lib.rs:45-65); defaults as DiffOpts::default (lib.rs:59-64)."""
+    _fields_ = [("gen_len", C.c_uint32), ("block", C.c_uint32), ("steps", C.c_uint32), ("temp", C.c_float),
+                ("rep_penalty", C.c_float), ("remask_steps", C.c_uint32), ("remask_frac", C.c_float),
+                ("seed", C.c_uint64), ("cached", C.c_uint32), ("threshold", C.c_float)]
+
+    @classmethod
+    def make(cls, gen_len=128, block=32, steps=32, temp=0.0, rep_penalty=1.4, remask_steps=0, remask_frac=0.3,
+             seed=1234, cached=True, threshold=0.0):
+        return cls(gen_len, block, steps, temp, rep_penalty, remask_steps, remask_frac, seed, int(cached), threshold)
 
 
 def build(force: bool = False) -> str:
@@ -97,6 +109,12 @@ def lib():
             "orc_generate": (C.c_int, [C.c_void_p, C.c_void_p, _u32p, C.c_uint32, C.c_uint32, C.c_float,
                                        C.c_float, C.c_uint64, C.c_float, C.c_uint32, _u32p,
                                        C.POINTER(C.c_uint32)]),
+            "orc_run_block": (C.c_int, [C.c_void_p, C.c_void_p, _f32p, C.c_uint32, C.c_uint32, C.c_void_p,
+                                        C.c_void_p, C.c_void_p]),
+            "orc_forward_bidir": (C.c_int, [C.c_void_p, _f32p, C.c_uint32, _f32p]),
+            "orc_generate_diffusion": (C.c_int, [C.c_void_p, _u32p, C.c_uint32, C.c_void_p, C.c_uint32, _u32p,
+                                                 C.POINTER(C.c_uint32)]),
+            "orc_gumbel_argmax": (C.c_uint32, [_f32p, C.c_size_t, C.c_float, C.POINTER(C.c_uint64)]),
             "orc_rng_next_u64": (C.c_uint64, [C.POINTER(C.c_uint64)]),
             "orc_rng_next_f32": (C.c_float, [C.POINTER(C.c_uint64)]),
             "orc_sample": (C.c_uint32, [_f32p, C.c_size_t, C.c_float, C.c_float, C.POINTER(C.c_uint64)]),
@@ -347,6 +365,35 @@ class Model:
         n = C.c_uint32()
         _check(lib().orc_generate(self.h, cache.h, p, p.size, max_new, temp, top_p, seed, rep_penalty, eos, out,
                                   C.byref(n)))
+        return out[: n.value].copy()
+
+    def run_block(self, block: np.ndarray, cache: "KvCache", base: int, want_kv: bool = False):
+        """Model::run_block (model.rs:471-585): (logits [b][V], bk, bv [L][b][kv_dim] or None)."""
+        c = self.cfg
+        blk = np.ascontiguousarray(block, np.float32)
+        b = blk.shape[0]
+        lg = np.empty((b, c.vocab_size), np.float32)
+        kvd = c.n_kv_heads * c.head_dim
+        bk = np.empty((c.n_layers, b, kvd), np.float32) if want_kv else None
+        bv = np.empty((c.n_layers, b, kvd), np.float32) if want_kv else None
+        p = lambda a: a.ctypes.data_as(C.c_void_p) if a is not None else None
+        _check(lib().orc_run_block(self.h, cache.h, blk.reshape(-1), b, base, p(lg), p(bk), p(bv)))
+        return lg, bk, bv
+
+    def forward_bidir(self, inputs: np.ndarray) -> np.ndarray:
+        """Model::forward_bidir (model.rs:443-468): logits [tn][V]."""
+        x = np.ascontiguousarray(inputs, np.float32)
+        lg = np.empty((x.shape[0], self.cfg.vocab_size), np.float32)
+        _check(lib().orc_forward_bidir(self.h, x.reshape(-1), x.shape[0], lg.reshape(-1)))
+        return lg
+
+    def generate_diffusion(self, prompt, opts: "DiffOpts", eos: int = 50256) -> np.ndarray:
+        """Engine::generate_diffusion (lib.rs:214-495) over ids."""
+        pr = np.ascontiguousarray(prompt, np.uint32)
+        out = np.empty(max(opts.gen_len, 1), np.uint32)
+        n = C.c_uint32()
+        _check(lib().orc_generate_diffusion(self.h, pr, pr.size, C.cast(C.pointer(opts), C.c_void_p), eos, out,
+                                            C.byref(n)))
         return out[: n.value].copy()
 
     def generate_greedy(self, prompt, max_new: int, cache: "KvCache", rep_penalty: float = 1.0,

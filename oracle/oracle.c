@@ -667,6 +667,27 @@ uint32_t orc_sample(const float *logits, size_t n, float temp, float top_p, uint
     return pick;
 }
 
+/* sample::gumbel_argmax (sample.rs:32-50): argmax_i of l_i / temp - ln(-ln(u_i)), one draw u_i
+ * (clamped to [1e-9, 1 - 1e-9]) per finite logit in id order; temp <= 0: argmax. */
+uint32_t orc_gumbel_argmax(const float *logits, size_t n, float temp, uint64_t *state) {
+    if (!(temp > 0.0f)) return orc_argmax(logits, n);
+    size_t best = 0;
+    float bv = -INFINITY;
+    const float lo = 1e-9f, hi = 1.0f - 1e-9f;
+    for (size_t i = 0; i < n; i++) {
+        const float l = logits[i];
+        if (!isfinite(l)) continue;
+        float u = orc_rng_next_f32(state);
+        u = u < lo ? lo : u > hi ? hi : u;
+        const float val = l / temp + -logf(-logf(u));
+        if (val > bv) {
+            bv = val;
+            best = i;
+        }
+    }
+    return (uint32_t)best;
+}
+
 /* ======================================================================
  * quant.rs
  * ====================================================================== */
@@ -879,6 +900,7 @@ static int config_from_gguf(const gguf_t *g, orc_config *c) {
     if (!get_f32(g, K("expert_weights_scale"), &c->expert_weights_scale)) c->expert_weights_scale = 1.0f;
     int b;
     c->expert_weights_norm = get_bool(g, K("expert_weights_norm"), &b) ? b : 0;
+    if (!get_u32(g, "diffusion.mask_token_id", &c->mask_token_id)) c->mask_token_id = 50257;
 #undef K
 #undef REQ
 #undef OPT
@@ -1421,6 +1443,297 @@ int orc_last_routing(const orc_kv *kv, uint32_t *idx, float *weight, float *gap)
     if (weight) memcpy(weight, kv->r_w, n * 4);
     if (gap) memcpy(gap, kv->r_gap, (size_t)kv->L * 4);
     return 0;
+}
+
+/* Model::run_block (model.rs:471-508) with attn_block_cached (model.rs:512-585): the b block rows
+ * (residual inputs) at positions base .. base + b - 1 attend to the cache's rows 0 .. base - 1
+ * and to every block row (bidirectional within the block); the cache rows are not changed.
+ * logits [b][V] (output.matmul), bk / bv [L][b][kv_dim] when not NULL.  The routing records of
+ * kv take the block's last row. */
+int orc_run_block(const orc_model *m, orc_kv *kv, const float *block, uint32_t b, uint32_t base, float *logits,
+                  float *bk, float *bv) {
+    if (b == 0) return fail("run_block needs at least one row");
+    if (base > kv->len) return fail("base %u beyond the cache (len %u)", base, kv->len);
+    const orc_config *c = &m->c;
+    size_t d = c->d_model, hd = c->head_dim, qd = (size_t)c->n_heads * hd, kvd = (size_t)c->n_kv_heads * hd;
+    size_t qw = qd + 2 * kvd, n = (size_t)base + b;
+    float *x = (float *)malloc((size_t)b * d * 4), *h = (float *)malloc((size_t)b * d * 4);
+    float *t = (float *)malloc((size_t)b * d * 4), *qkv = (float *)malloc((size_t)b * qw * 4);
+    float *o = (float *)malloc((size_t)b * qd * 4);
+    float *ka = (float *)malloc(n * kvd * 4), *va = (float *)malloc(n * kvd * 4);
+    memcpy(x, block, (size_t)b * d * 4);
+    for (uint32_t li = 0; li < c->n_layers; li++) {
+        const layer_t *L = &m->layers[li];
+        for (size_t r = 0; r < b; r++) orc_rmsnorm(x + r * d, L->attn_norm, c->rms_eps, h + r * d, d);
+        mat_matmul(&L->qkv, h, qkv, b);
+        for (size_t r = 0; r < b; r++) qk_norm_rope(m, L, qkv + r * qw, qkv + r * qw + qd, base + r);
+        memcpy(ka, kv->k[li], (size_t)base * kvd * 4);
+        memcpy(va, kv->v[li], (size_t)base * kvd * 4);
+        for (size_t r = 0; r < b; r++) {
+            memcpy(ka + (base + r) * kvd, qkv + r * qw + qd, kvd * 4);
+            memcpy(va + (base + r) * kvd, qkv + r * qw + qd + kvd, kvd * 4);
+            if (bk) memcpy(bk + ((size_t)li * b + r) * kvd, qkv + r * qw + qd, kvd * 4);
+            if (bv) memcpy(bv + ((size_t)li * b + r) * kvd, qkv + r * qw + qd + kvd, kvd * 4);
+        }
+#pragma omp parallel for schedule(static)
+        for (size_t r = 0; r < b; r++) {
+            float *scores = (float *)malloc(n * 4);
+            attend(c, qkv + r * qw, ka, va, n, o + r * qd, scores);
+            free(scores);
+        }
+        mat_matmul(&L->o, o, t, b);
+        for (size_t i = 0; i < (size_t)b * d; i++) x[i] += t[i];
+        for (size_t r = 0; r < b; r++) orc_rmsnorm(x + r * d, L->ffn_norm, c->rms_eps, h + r * d, d);
+        ffn_prefill(m, L, h, b, t, kv, li);
+        for (size_t i = 0; i < (size_t)b * d; i++) x[i] += t[i];
+    }
+    if (logits) {
+        for (size_t r = 0; r < b; r++) orc_rmsnorm(x + r * d, m->output_norm, c->rms_eps, h + r * d, d);
+        mat_matmul(&m->output, h, logits, b);
+    }
+    free(x); free(h); free(t); free(qkv); free(o); free(ka); free(va);
+    return 0;
+}
+
+/* Model::forward_bidir (model.rs:443-468): run_block over an empty prefix (attn_bidir,
+ * model.rs:589-651, is attn_block_cached with base 0). */
+int orc_forward_bidir(const orc_model *m, const float *inputs, uint32_t tn, float *logits) {
+    orc_kv *kv;
+    if (orc_kv_new(m, &kv)) return -1;
+    int rc = orc_run_block(m, kv, inputs, tn, 0, logits, NULL, NULL);
+    orc_kv_free(kv);
+    return rc;
+}
+
+/* Engine::score_block (lib.rs:226-262), also the scoring of diffusion_block (lib.rs:167-205):
+ * per row the ids >= valid masked, the presence penalty once per present id, the Gumbel pick,
+ * softmax of the penalized row, the pick's probability and the current id's. */
+static void score_rows(const orc_config *c, const float *all, size_t rows, size_t valid, const uint8_t *present,
+                       float rp, float temp, uint64_t *rng, const uint32_t *cur, uint32_t *pred, float *pconf,
+                       float *cconf) {
+    size_t V = c->vocab_size;
+    float *row = (float *)malloc(V * 4);
+    for (size_t i = 0; i < rows; i++) {
+        memcpy(row, all + i * V, V * 4);
+        for (size_t l = valid; l < V; l++) row[l] = -INFINITY;
+        if (rp != 1.0f)
+            for (size_t t = 0; t < valid; t++)
+                if (present[t]) row[t] = row[t] > 0.0f ? row[t] / rp : row[t] * rp;
+        const uint32_t pk = orc_gumbel_argmax(row, V, temp, rng);
+        orc_softmax(row, V);
+        pred[i] = pk;
+        pconf[i] = row[pk];
+        cconf[i] = row[cur[i]];
+    }
+    free(row);
+}
+
+/* num_transfer (lib.rs:68-76) */
+static void num_transfer(size_t n, size_t steps, size_t *out) {
+    size_t base = n / steps;
+    for (size_t i = 0; i < steps; i++) out[i] = base + (i < n - base * steps ? 1 : 0);
+}
+
+typedef struct {
+    size_t i;
+    float v;
+} conf_t;
+static int conf_desc(const void *a, const void *b) {   /* stable by index among equals */
+    const conf_t *x = (const conf_t *)a, *y = (const conf_t *)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return x->i < y->i ? -1 : x->i > y->i;
+}
+static int conf_asc(const void *a, const void *b) {
+    const conf_t *x = (const conf_t *)a, *y = (const conf_t *)b;
+    if (x->v < y->v) return -1;
+    if (x->v > y->v) return 1;
+    return x->i < y->i ? -1 : x->i > y->i;
+}
+
+/* The scoring of one block [b0, b0 + len) of ids `ids` (the canvas's, or the active block's):
+ * cached: run_block of the block over the cache; uncached: forward_bidir of canvas[0 .. b0 + len). */
+typedef struct {
+    const orc_model *m;
+    const orc_diff_opts *o;
+    orc_kv *kv;           /* cached path: the persistent prefix cache */
+    uint32_t *canvas;     /* uncached path: the whole canvas; cached: committed ids */
+    size_t committed;     /* cached path: ids in canvas[] so far */
+    uint64_t rng;
+    size_t valid;
+    uint32_t mask;
+    float *all, *emb;
+    uint8_t *present;
+} diff_t;
+
+static int diff_score(diff_t *D, const uint32_t *blk, size_t b0, size_t len, uint32_t *pred, float *pconf,
+                      float *cconf) {
+    const orc_config *c = &D->m->c;
+    size_t d = c->d_model, V = c->vocab_size;
+    memset(D->present, 0, D->valid);
+    if (D->o->cached) {
+        for (size_t i = 0; i < len; i++)
+            if (orc_token_embedding(D->m, blk[i], D->emb + i * d)) return -1;
+        if (orc_run_block(D->m, D->kv, D->emb, (uint32_t)len, (uint32_t)b0, D->all, NULL, NULL)) return -1;
+        if (D->o->rep_penalty != 1.0f) {
+            for (size_t i = 0; i < D->committed; i++)
+                if (D->canvas[i] != D->mask && D->canvas[i] < D->valid) D->present[D->canvas[i]] = 1;
+            for (size_t i = 0; i < len; i++)
+                if (blk[i] != D->mask && blk[i] < D->valid) D->present[blk[i]] = 1;
+        }
+        score_rows(c, D->all, len, D->valid, D->present, D->o->rep_penalty, D->o->temp, &D->rng, blk, pred, pconf,
+                   cconf);
+    } else {
+        size_t b1 = b0 + len;
+        for (size_t i = 0; i < b1; i++)
+            if (orc_token_embedding(D->m, D->canvas[i], D->emb + i * d)) return -1;
+        if (orc_forward_bidir(D->m, D->emb, (uint32_t)b1, D->all)) return -1;
+        if (D->o->rep_penalty != 1.0f)
+            for (size_t i = 0; i < b1; i++)
+                if (D->canvas[i] != D->mask && D->canvas[i] < D->valid) D->present[D->canvas[i]] = 1;
+        score_rows(c, D->all + b0 * V, len, D->valid, D->present, D->o->rep_penalty, D->o->temp, &D->rng, blk, pred,
+                   pconf, cconf);
+    }
+    return 0;
+}
+
+/* Engine::generate_diffusion (lib.rs:214-224): the prefix-cached (lib.rs:269-407) or the
+ * uncached (lib.rs:410-495) semi-autoregressive denoising of gen_len ids after the prompt; the
+ * generated ids up to the first eos in out_ids, their count in *n_out. */
+int orc_generate_diffusion(const orc_model *m, const uint32_t *prompt, uint32_t n_prompt, const orc_diff_opts *o,
+                           uint32_t eos, uint32_t *out_ids, uint32_t *n_out) {
+    *n_out = 0;
+    const orc_config *c = &m->c;
+    size_t p = n_prompt, d = c->d_model, V = c->vocab_size, ctx = c->context_length;
+    if (p == 0) return 0;
+    if (o->block == 0 || o->steps == 0) return fail("block and steps must be positive");
+    diff_t D;
+    memset(&D, 0, sizeof D);
+    D.m = m;
+    D.o = o;
+    D.rng = o->seed > 1 ? o->seed : 1;
+    D.valid = V < 50257 ? V : 50257;
+    D.mask = c->mask_token_id;
+    size_t gen_len;
+    if (o->cached) {
+        size_t room = ctx > p + o->block ? ctx - (p + o->block) : 0;
+        gen_len = o->gen_len < (room > 1 ? room : 1) ? o->gen_len : (room > 1 ? room : 1);
+    } else {
+        size_t room = ctx > p ? ctx - p : 0;
+        gen_len = o->gen_len < (room > 1 ? room : 1) ? o->gen_len : (room > 1 ? room : 1);
+    }
+    size_t span = o->cached ? (o->block > p ? o->block : p) : p + gen_len;
+    D.all = (float *)malloc(span * V * 4);
+    D.emb = (float *)malloc(span * d * 4);
+    D.present = (uint8_t *)malloc(D.valid);
+    D.canvas = (uint32_t *)malloc((p + gen_len) * 4);
+    memcpy(D.canvas, prompt, p * 4);
+    uint32_t *blk = (uint32_t *)malloc(o->block * 4), *pred = (uint32_t *)malloc(o->block * 4);
+    float *pconf = (float *)malloc(o->block * 4), *cconf = (float *)malloc(o->block * 4);
+    conf_t *cand = (conf_t *)malloc(o->block * sizeof(conf_t));
+    size_t *sched = NULL;
+    int rc = 0;
+    float *bk = NULL, *bv = NULL;
+    size_t kvd = (size_t)c->n_kv_heads * c->head_dim, result = gen_len;
+    if (o->cached) {
+        if (orc_kv_new(m, &D.kv)) { rc = -1; goto out; }
+        for (size_t i = 0; i < p; i++)
+            if (orc_token_embedding(m, prompt[i], D.emb + i * d)) { rc = -1; goto out; }
+        bk = (float *)malloc((size_t)c->n_layers * span * kvd * 4);
+        bv = (float *)malloc((size_t)c->n_layers * span * kvd * 4);
+        if (orc_run_block(m, D.kv, D.emb, (uint32_t)p, 0, NULL, bk, bv)) { rc = -1; goto out; }
+        for (uint32_t li = 0; li < c->n_layers; li++) {
+            memcpy(D.kv->k[li], bk + (size_t)li * p * kvd, p * kvd * 4);
+            memcpy(D.kv->v[li], bv + (size_t)li * p * kvd, p * kvd * 4);
+        }
+        D.kv->len = (uint32_t)p;
+        D.committed = p;
+    } else {
+        for (size_t i = p; i < p + gen_len; i++) D.canvas[i] = D.mask;
+    }
+    for (size_t b0 = p; b0 < p + gen_len;) {
+        size_t b1 = b0 + o->block < p + gen_len ? b0 + o->block : p + gen_len, len = b1 - b0;
+        uint32_t *cur = o->cached ? blk : D.canvas + b0;   /* the active block's ids */
+        if (o->cached)
+            for (size_t i = 0; i < len; i++) blk[i] = D.mask;
+        if (o->cached && o->threshold > 0.0f) {   /* lib.rs:302-327 */
+            for (size_t it = 0; it < (len > 1 ? len : 1); it++) {
+                int anym = 0;
+                for (size_t i = 0; i < len; i++) anym |= cur[i] == D.mask;
+                if (!anym) break;
+                if (diff_score(&D, cur, b0, len, pred, pconf, cconf)) { rc = -1; goto out; }
+                int any = 0;
+                size_t best = 0;
+                float bvv = 0.0f;
+                int have = 0;
+                for (size_t i = 0; i < len; i++) {
+                    if (cur[i] != D.mask) continue;
+                    /* Iterator::max_by: the last of equal maxima */
+                    if (!have || !(pconf[i] < bvv)) { best = i; bvv = pconf[i]; have = 1; }
+                }
+                for (size_t i = 0; i < len; i++)
+                    if (cur[i] == D.mask && pconf[i] >= o->threshold) { cur[i] = pred[i]; any = 1; }
+                if (!any) cur[best] = pred[best];
+            }
+        } else {   /* the num_transfer schedule (lib.rs:329-352, 428-451) */
+            size_t sb = (size_t)roundf((float)(o->steps * len) / (float)gen_len);
+            if (sb < 1) sb = 1;
+            sched = (size_t *)realloc(sched, sb * sizeof(size_t));
+            num_transfer(len, sb, sched);
+            for (size_t s = 0; s < sb; s++) {
+                if (diff_score(&D, cur, b0, len, pred, pconf, cconf)) { rc = -1; goto out; }
+                size_t nc = 0;
+                for (size_t i = 0; i < len; i++)
+                    if (cur[i] == D.mask) { cand[nc].i = i; cand[nc].v = pconf[i]; nc++; }
+                if (nc == 0) break;
+                qsort(cand, nc, sizeof(conf_t), conf_desc);
+                for (size_t q = 0; q < (sched[s] < nc ? sched[s] : nc); q++) cur[cand[q].i] = pred[cand[q].i];
+            }
+            int anym = 0;
+            for (size_t i = 0; i < len; i++) anym |= cur[i] == D.mask;
+            if (anym) {
+                if (diff_score(&D, cur, b0, len, pred, pconf, cconf)) { rc = -1; goto out; }
+                for (size_t i = 0; i < len; i++)
+                    if (cur[i] == D.mask) cur[i] = pred[i];
+            }
+        }
+        for (uint32_t rs = 0; rs < o->remask_steps; rs++) {   /* lib.rs:354-371, 453-468 */
+            if (diff_score(&D, cur, b0, len, pred, pconf, cconf)) { rc = -1; goto out; }
+            size_t r = (size_t)((float)len * o->remask_frac);
+            if (r < 1) r = 1;
+            for (size_t i = 0; i < len; i++) { cand[i].i = i; cand[i].v = cconf[i]; }
+            qsort(cand, len, sizeof(conf_t), conf_asc);
+            for (size_t q = 0; q < (r < len ? r : len); q++) cur[cand[q].i] = D.mask;
+            if (diff_score(&D, cur, b0, len, pred, pconf, cconf)) { rc = -1; goto out; }
+            for (size_t i = 0; i < len; i++)
+                if (cur[i] == D.mask) cur[i] = pred[i];
+        }
+        if (o->cached) {   /* finalize: the block's K/V into the cache (lib.rs:374-381) */
+            for (size_t i = 0; i < len; i++)
+                if (orc_token_embedding(m, blk[i], D.emb + i * d)) { rc = -1; goto out; }
+            if (orc_run_block(m, D.kv, D.emb, (uint32_t)len, (uint32_t)b0, NULL, bk, bv)) { rc = -1; goto out; }
+            for (uint32_t li = 0; li < c->n_layers; li++) {
+                memcpy(D.kv->k[li] + b0 * kvd, bk + (size_t)li * len * kvd, len * kvd * 4);
+                memcpy(D.kv->v[li] + b0 * kvd, bv + (size_t)li * len * kvd, len * kvd * 4);
+            }
+            D.kv->len = (uint32_t)b1;
+            memcpy(D.canvas + b0, blk, len * 4);
+            D.committed = b1;
+        }
+        size_t endpos = b1;   /* the first eos of the generated region ends the generation */
+        int hit = 0;
+        for (size_t i = p; i < b1; i++)
+            if (D.canvas[i] == eos) { endpos = i; hit = 1; break; }
+        if (hit) { result = endpos - p; break; }
+        b0 = b1;
+    }
+    memcpy(out_ids, D.canvas + p, result * 4);
+    *n_out = (uint32_t)result;
+out:
+    if (D.kv) orc_kv_free(D.kv);
+    free(D.all); free(D.emb); free(D.present); free(D.canvas); free(blk); free(pred); free(pconf); free(cconf);
+    free(cand); free(sched); free(bk); free(bv);
+    return rc;
 }
 
 /* Engine::generate (lib.rs:107-162): prefill, then per step the ids >= 50257 masked, the

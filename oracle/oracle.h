@@ -25,6 +25,7 @@ typedef struct orc_config {
     uint32_t vocab_size, context_length;
     float rms_eps, rope_theta, expert_weights_scale;
     int32_t expert_weights_norm, gating_sigmoid;
+    uint32_t mask_token_id;
 } orc_config;
 
 typedef struct orc_model orc_model;
@@ -112,6 +113,22 @@ int orc_last_routing(const orc_kv *kv, uint32_t *idx, float *weight, float *gap)
 /* Engine::generate at temp 0 (lib.rs:107-162) over token ids: prefill, then greedy
  * steps with the id>=min(50257,vocab) mask, optional repetition penalty, EOS and
  * context stops.  Returns the number of generated ids written to out_ids. */
+/* DiffOpts (lib.rs:45-65) */
+typedef struct orc_diff_opts {
+    uint32_t gen_len, block, steps;
+    float temp, rep_penalty;
+    uint32_t remask_steps;
+    float remask_frac;
+    uint64_t seed;
+    uint32_t cached;
+    float threshold;
+} orc_diff_opts;
+uint32_t orc_gumbel_argmax(const float *logits, size_t n, float temp, uint64_t *state); /* sample.rs:32-50 */
+int orc_run_block(const orc_model *m, orc_kv *kv, const float *block, uint32_t b, uint32_t base, float *logits,
+                  float *bk, float *bv);                            /* model.rs:471-585 */
+int orc_forward_bidir(const orc_model *m, const float *inputs, uint32_t tn, float *logits); /* model.rs:443-468 */
+int orc_generate_diffusion(const orc_model *m, const uint32_t *prompt, uint32_t n_prompt, const orc_diff_opts *o,
+                           uint32_t eos, uint32_t *out_ids, uint32_t *n_out); /* lib.rs:214-495 */
 int orc_generate(const orc_model *m, orc_kv *kv, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_new,
                  float temp, float top_p, uint64_t seed, float rep_penalty, uint32_t eos, uint32_t *out_ids,
                  uint32_t *n_out);                                  /* lib.rs:107-162 */

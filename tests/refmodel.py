@@ -126,6 +126,59 @@ class RefModel:
         z = (v[:half] + 1j * v[half:]) * (c + 1j * s)
         return np.concatenate([z.real, z.imag])
 
+    def block(self, tokens, base):
+        """Model::run_block in float64: rows at positions base + r, each attending to the prefix
+        rows 0 .. base - 1 already in the cache and to every block row; the cache is unchanged."""
+        W = self.w
+        b = len(tokens)
+        X = np.stack([W["token_embd.weight"][t].copy() for t in tokens])
+        qd, kvd, rep = self.nh * self.hd, self.nkv * self.hd, self.nh // self.nkv
+        for li in range(self.L):
+            p = f"blk.{li}."
+            qs, ks, vs = [], [], []
+            for r in range(b):
+                h = self.rms(X[r], W[p + "attn_norm.weight"])
+                qkv = self.mv(W[p + "attn_qkv.weight"], h)
+                q = qkv[:qd].reshape(self.nh, self.hd)
+                k = qkv[qd:qd + kvd].reshape(self.nkv, self.hd)
+                qs.append(np.stack([self.rope(self.rms(qh, W[p + "attn_q_norm.weight"]), base + r) for qh in q]))
+                ks.append(np.stack([self.rope(self.rms(kh, W[p + "attn_k_norm.weight"]), base + r) for kh in k]))
+                vs.append(qkv[qd + kvd:].reshape(self.nkv, self.hd))
+            K = np.stack(self.k[li][:base] + ks)
+            V = np.stack(self.v[li][:base] + vs)
+            for r in range(b):
+                o = np.empty((self.nh, self.hd))
+                for hq in range(self.nh):
+                    s = K[:, hq // rep, :] @ qs[r][hq] / np.sqrt(self.hd)
+                    pr = np.exp(s - s.max())
+                    pr /= pr.sum()
+                    o[hq] = pr @ V[:, hq // rep, :]
+                X[r] = X[r] + self.mv(W[p + "attn_output.weight"], o.reshape(-1))
+            for r in range(b):
+                X[r] = X[r] + self._ffn(li, self.rms(X[r], W[p + "ffn_norm.weight"]))
+        return np.stack([self.mv(W["output.weight"], self.rms(X[r], W["output_norm.weight"])) for r in range(b)])
+
+    def _ffn(self, li, h):
+        W, p = self.w, f"blk.{li}."
+        if li < self.n_dense:
+            gg = self.mv(W[p + "ffn_gate.weight"], h)
+            uu = self.mv(W[p + "ffn_up.weight"], h)
+            return self.mv(W[p + "ffn_down.weight"], gg / (1 + np.exp(-gg)) * uu)
+        logits = W[p + "ffn_gate_inp.weight"] @ h
+        sc = 1 / (1 + np.exp(-logits))
+        sel = sc + W[p + "exp_probs_b.bias"]
+        top = np.argsort(-sel, kind="stable")[: self.top_k]
+        out = np.zeros(self.d)
+        for e in top:
+            gg = self.mv(W[p + "ffn_gate_exps.weight"][e], h)
+            uu = self.mv(W[p + "ffn_up_exps.weight"][e], h)
+            out += sc[e] * self.mv(W[p + "ffn_down_exps.weight"][e], gg / (1 + np.exp(-gg)) * uu)
+        if self.n_shared:
+            gg = self.mv(W[p + "ffn_gate_shexp.weight"], h)
+            uu = self.mv(W[p + "ffn_up_shexp.weight"], h)
+            out += self.mv(W[p + "ffn_down_shexp.weight"], gg / (1 + np.exp(-gg)) * uu)
+        return out
+
     def forward(self, token, pos):
         x = self.w["token_embd.weight"][token].copy()
         W = self.w

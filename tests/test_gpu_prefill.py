@@ -20,6 +20,12 @@ def hg():
     return hobbylm_amd
 
 
+@pytest.fixture(autouse=True)
+def _batched_only(monkeypatch):
+    """Every prompt here must take the batched path (an unsupported shape is an error)."""
+    monkeypatch.setenv("HG_PREFILL", "batched")
+
+
 def _bits_equal(a, b):
     return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
