@@ -48,6 +48,7 @@ class Gguf {
             std::string &err) const;
     // Gguf::load (gguf.rs:250-269): the tensor as f32, dequantized from any supported type.
     int load(const std::string &name, std::vector<float> &out, std::string &err) const;
+    const std::unordered_map<std::string, TensorInfo> &tensors() const { return tensors_; }
 
   private:
     const uint8_t *map_ = nullptr;
