@@ -941,6 +941,11 @@ struct Diffusion {
     uint32_t valid = 0, mask = 0;
     DevBuf logits, ids, present, cur, pred, pconf, cconf;
     std::vector<uint8_t> h_present;
+    // Gumbel draws (temp > 0): the RNG state (host), the jump matrices, the -ln(-ln(u)) table
+    uint64_t rng = 1;
+    std::vector<uint64_t> M;
+    DevBuf dM, G, count;
+    std::vector<uint32_t> h_count;
     ~Diffusion() {
         if (kv) hg_kv_free(kv);
     }
@@ -976,13 +981,22 @@ struct Diffusion {
         }
         HIP_TRY(hipMemcpyAsync(cur.p, blk, len * 4, hipMemcpyHostToDevice, st));
         const float *lg = logits.as<float>() + (cached ? 0 : b0 * (size_t)V);
+        const bool gumbel = o->temp > 0.0f;
+        GumbelDraws gd{o->temp, rng, dM.as<uint64_t>(), G.as<float>(), count.as<uint32_t>()};
         if (!enqueue_score_rows(st, lg, (uint32_t)len, V, valid, pen ? present.as<uint8_t>() : nullptr, o->rep_penalty,
-                                cur.as<uint32_t>(), pred.as<uint32_t>(), pconf.as<float>(), cconf.as<float>()))
+                                cur.as<uint32_t>(), pred.as<uint32_t>(), pconf.as<float>(), cconf.as<float>(),
+                                gumbel ? &gd : nullptr))
             return fail(HG_ERR_DEVICE, "scoring launch failed");
         HIP_TRY(hipMemcpyAsync(h_pred, pred.p, len * 4, hipMemcpyDeviceToHost, st));
         HIP_TRY(hipMemcpyAsync(h_pconf, pconf.p, len * 4, hipMemcpyDeviceToHost, st));
         HIP_TRY(hipMemcpyAsync(h_cconf, cconf.p, len * 4, hipMemcpyDeviceToHost, st));
+        if (gumbel) HIP_TRY(hipMemcpyAsync(h_count.data(), count.p, len * 4, hipMemcpyDeviceToHost, st));
         HIP_TRY(hipStreamSynchronize(st));
+        if (gumbel) {   // the rows' draws advance the one Rng (lib.rs:275, 312-370)
+            uint64_t total = 0;
+            for (size_t i = 0; i < len; ++i) total += h_count[i];
+            rng = rng_jump_host(rng, total, M.data());
+        }
         return HG_OK;
     }
 };
@@ -997,7 +1011,6 @@ int hg_generate_diffusion(const hg_model *m, const uint32_t *prompt, uint32_t n_
         if (n_prompt > 0 && !prompt) return fail(HG_ERR_ARG, "prompt is NULL");
         if (n_prompt == 0) return HG_OK;
         if (opts->block == 0 || opts->steps == 0) return fail(HG_ERR_ARG, "block and steps must be positive");
-        if (opts->temp > 0.0f) return fail(HG_ERR_UNSUPPORTED, "diffusion decoding with temp > 0 (Gumbel draws)");
         if (!out_ids && opts->gen_len > 0) return fail(HG_ERR_ARG, "out_ids is NULL");
         const hg_config &c = m->c;
         const size_t p = n_prompt, V = c.vocab_size, ctx = c.context_length;
@@ -1022,6 +1035,16 @@ int hg_generate_diffusion(const hg_model *m, const uint32_t *prompt, uint32_t n_
             return rc;
         D.h_present.assign(D.valid, 0);
         D.canvas.assign(prompt, prompt + p);
+        if (opts->temp > 0.0f) {   // Rng::new (sample.rs:6-8), the jump matrices and the draw table
+            D.rng = opts->seed > 1 ? opts->seed : 1;
+            D.M.resize(32 * 64);
+            rng_jump_matrices(D.M.data());
+            const std::vector<float> &tab = gumbel_table();
+            if ((rc = D.dM.upload(D.M.data(), D.M.size() * 8)) || (rc = D.G.upload(tab.data(), tab.size() * 4)) ||
+                (rc = D.count.alloc(opts->block * 4 + 4)))
+                return rc;
+            D.h_count.assign(opts->block + 1, 0);
+        }
         if (cached) {   // the bidirectional prompt encode seeds the cache (lib.rs:281-289)
             HIP_TRY(hipMemcpy(D.ids.p, prompt, p * 4, hipMemcpyHostToDevice));
             if ((rc = run_block_batched(m, *D.kv->pw, D.kv->st, nullptr, D.ids.as<uint32_t>(), 0, (uint32_t)p,

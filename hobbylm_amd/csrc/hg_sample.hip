@@ -11,6 +11,11 @@
 // the earlier segments as its first term (0 + s = s, so the chain of segment sums is the one
 // sequential sum); the segment where a running sum crosses a threshold is then replayed by one
 // lane from its exact start.
+#include <math.h>
+
+#include <mutex>
+#include <vector>
+
 #include <rocprim/device/device_radix_sort.hpp>
 
 #include "hg_common.h"
@@ -248,27 +253,104 @@ __global__ __launch_bounds__(NT) void k_s_pick(const float *__restrict__ q, cons
 // pred = the argmax (gumbel_argmax at temp 0, sample.rs:36-38), then ops::softmax of the row
 // (ops.rs:112-128: m, e = exp(v - m), the id-order sum, x * (1 / sum)) read at pred and at the
 // row's current id.  One workgroup per row.
+// The xorshift64* state after n steps (sample.rs:10-17): the state step is linear over GF(2), so
+// n steps are the product of the matrices T^(2^j) of n's set bits (M: [32][64] columns).
+__device__ inline uint64_t rng_jump(uint64_t s, uint64_t n, const uint64_t *M) {
+    for (uint32_t j = 0; n; ++j, n >>= 1)
+        if (n & 1) {
+            uint64_t r = 0;
+            for (uint32_t i = 0; i < 64; ++i)
+                if ((s >> i) & 1) r ^= M[j * 64 + i];
+            s = r;
+        }
+    return s;
+}
+
+__device__ inline uint64_t rng_step(uint64_t x) {
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    return x;
+}
+
+__device__ inline float pen_logit(const float *row, uint32_t i, uint32_t valid, const uint8_t *present, float rp) {
+    float l = i < valid ? row[i] : -__builtin_huge_valf();
+    if (present && i < valid && present[i]) l = l > 0.0f ? l / rp : l * rp;
+    return l;
+}
+
+// Finite (drawn) entries per row of the masked, penalized logits.  One workgroup per row.
+__global__ __launch_bounds__(NT) void k_d_count(const float *__restrict__ logits, uint32_t V, uint32_t valid,
+                                                const uint8_t *__restrict__ present, float rp, uint32_t *count) {
+    __shared__ uint32_t red[NT / 64];
+    const uint32_t tid = threadIdx.x, r = blockIdx.x;
+    const float *row = logits + (size_t)r * V;
+    uint32_t c = 0;
+    for (uint32_t i = tid; i < V; i += NT) c += __builtin_isfinite(pen_logit(row, i, valid, present, rp)) ? 1u : 0u;
+    for (int m = 32; m >= 1; m >>= 1) c += (uint32_t)shfl_xor_i((int)c, m);
+    if ((tid & 63) == 0) red[tid >> 6] = c;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t t = 0;
+        for (uint32_t w = 0; w < NT / 64; ++w) t += red[w];
+        count[r] = t;
+    }
+}
+
+// Engine::score_block (lib.rs:226-262): row r = blockIdx.x of logits [rows][V] with the ids >=
+// valid masked and, when present != nullptr, the presence penalty once per present id; the pick
+// (GUMBEL: sample::gumbel_argmax, sample.rs:32-50 -- one draw per finite entry in id order, the
+// rows' draws consecutive from state s0, g = -ln(-ln(u)) read from the table G of the 2^24
+// possible u; else the argmax), then ops::softmax of the row (ops.rs:112-128: m, e = exp(v - m),
+// the id-order sum, x * (1 / sum)) read at the pick and at the row's current id.  One
+// workgroup per row; a thread's draws start from s0 advanced past the earlier rows' and threads'
+// finite entries (rng_jump).
+template <bool GUMBEL>
 __global__ __launch_bounds__(NT) void k_d_score(const float *__restrict__ logits, uint32_t V, uint32_t valid,
                                                 const uint8_t *__restrict__ present, float rp,
                                                 const uint32_t *__restrict__ cur, uint32_t *pred, float *pconf,
-                                                float *cconf) {
+                                                float *cconf, float temp, uint64_t s0,
+                                                const uint64_t *__restrict__ M, const float *__restrict__ G,
+                                                const uint32_t *__restrict__ count) {
     __shared__ SegLds L;
+    __shared__ uint64_t Ms[GUMBEL ? 32 * 64 : 1];
+    __shared__ uint32_t tcnt[NT];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t r = blockIdx.x;
     const float *row = logits + (size_t)r * V;
-    auto pen = [&](uint32_t i) {
-        float l = i < valid ? row[i] : -__builtin_huge_valf();
-        if (present && i < valid && present[i]) l = l > 0.0f ? l / rp : l * rp;
-        return l;
-    };
+    auto pen = [&](uint32_t i) { return pen_logit(row, i, valid, present, rp); };
     const WaveExpTab tab = WaveExpTab::load(lane);
     float mv = -__builtin_huge_valf();
     uint32_t mi = 0xffffffffu;
-    for (uint32_t i = tid; i < V; i += NT) {
-        const float v = pen(i);
-        if (v > mv) {
-            mv = v;
-            mi = i;
+    if constexpr (GUMBEL) {   // a contiguous run of ids per thread, its draws in id order
+        for (uint32_t i = tid; i < 32 * 64; i += NT) Ms[i] = M[i];
+        const uint32_t K = div_up(V, NT), i0 = min(tid * K, V), i1 = min(i0 + K, V);
+        uint32_t c = 0;
+        for (uint32_t i = i0; i < i1; ++i) c += __builtin_isfinite(pen(i)) ? 1u : 0u;
+        tcnt[tid] = c;
+        __syncthreads();
+        uint64_t off = 0;   // draws before this thread's: the earlier rows', then the earlier threads'
+        for (uint32_t q = 0; q < r; ++q) off += count[q];
+        for (uint32_t t = 0; t < (uint32_t)tid; ++t) off += tcnt[t];
+        uint64_t st = rng_jump(s0, off, Ms);
+        for (uint32_t i = i0; i < i1; ++i) {
+            const float l = pen(i);
+            if (!__builtin_isfinite(l)) continue;
+            st = rng_step(st);
+            const uint32_t k = (uint32_t)((st * 0x2545F4914F6CDD1DULL) >> 40);   // u = k / 2^24 (next_f32)
+            const float val = l / temp + G[k];
+            if (val > mv) {
+                mv = val;
+                mi = i;
+            }
+        }
+    } else {
+        for (uint32_t i = tid; i < V; i += NT) {
+            const float v = pen(i);
+            if (v > mv) {
+                mv = v;
+                mi = i;
+            }
         }
     }
     for (int m = 1; m < 64; m <<= 1) {
@@ -291,7 +373,17 @@ __global__ __launch_bounds__(NT) void k_d_score(const float *__restrict__ logits
             m = L.red[w];
             pk = L.redi[w];
         }
-    if (pk == 0xffffffffu) pk = 0;   // sample::argmax: 0 when nothing exceeds -inf
+    if (pk == 0xffffffffu) pk = 0;   // no finite candidate: sample.rs's best = 0
+    if constexpr (GUMBEL) {   // the softmax's maximum is the penalized row's own
+        __syncthreads();
+        float mx = -__builtin_huge_valf();
+        for (uint32_t i = tid; i < V; i += NT) mx = fmaxf(mx, pen(i));
+        for (int q = 32; q >= 1; q >>= 1) mx = fmaxf(mx, shfl_xor(mx, q));
+        if (lane == 0) L.red[wave] = mx;
+        __syncthreads();
+        m = L.red[0];
+        for (uint32_t w = 1; w < NT / 64; ++w) m = fmaxf(m, L.red[w]);
+    }
     float sum = 0.0f;
     for (uint32_t s0 = 0; s0 < V; s0 += SEG - 1) {   // sum += exp(v - m) in id order
         const uint32_t cnt = min(SEG - 1, V - s0);
@@ -315,9 +407,63 @@ __global__ __launch_bounds__(NT) void k_d_score(const float *__restrict__ logits
 
 bool enqueue_score_rows(hipStream_t st, const float *logits, uint32_t rows, uint32_t V, uint32_t valid,
                         const uint8_t *present, float rp, const uint32_t *cur, uint32_t *pred, float *pconf,
-                        float *cconf) {
-    hipLaunchKernelGGL(k_d_score, dim3(rows), dim3(NT), 0, st, logits, V, valid, present, rp, cur, pred, pconf, cconf);
+                        float *cconf, const GumbelDraws *gd) {
+    if (!gd) {
+        hipLaunchKernelGGL(k_d_score<false>, dim3(rows), dim3(NT), 0, st, logits, V, valid, present, rp, cur, pred, pconf,
+                           cconf, 1.0f, (uint64_t)1, nullptr, nullptr, nullptr);
+        return hipGetLastError() == hipSuccess;
+    }
+    hipLaunchKernelGGL(k_d_count, dim3(rows), dim3(NT), 0, st, logits, V, valid, present, rp, gd->count);
+    if (hipGetLastError() != hipSuccess) return false;
+    hipLaunchKernelGGL(k_d_score<true>, dim3(rows), dim3(NT), 0, st, logits, V, valid, present, rp, cur, pred, pconf,
+                       cconf, gd->temp, gd->state, gd->M, gd->G, gd->count);
     return hipGetLastError() == hipSuccess;
+}
+
+// The xorshift state step as GF(2) matrices T^(2^j), j < 32, column i = the image of bit i.
+void rng_jump_matrices(uint64_t *M) {
+    for (uint32_t i = 0; i < 64; ++i) {
+        uint64_t x = 1ull << i;
+        x ^= x >> 12;
+        x ^= x << 25;
+        x ^= x >> 27;
+        M[i] = x;
+    }
+    for (uint32_t j = 1; j < 32; ++j)
+        for (uint32_t i = 0; i < 64; ++i) {
+            uint64_t s = M[(j - 1) * 64 + i], r = 0;
+            for (uint32_t b = 0; b < 64; ++b)
+                if ((s >> b) & 1) r ^= M[(j - 1) * 64 + b];
+            M[j * 64 + i] = r;
+        }
+}
+
+uint64_t rng_jump_host(uint64_t s, uint64_t n, const uint64_t *M) {
+    for (uint32_t j = 0; n; ++j, n >>= 1)
+        if (n & 1) {
+            uint64_t r = 0;
+            for (uint32_t i = 0; i < 64; ++i)
+                if ((s >> i) & 1) r ^= M[j * 64 + i];
+            s = r;
+        }
+    return s;
+}
+
+// g(k) = -ln(-ln(u)) for u = k / 2^24 clamped to [1e-9, 1 - 1e-9] (sample.rs:42-43), with the
+// host libm's logf -- the function Rust's f32::ln calls.  Computed once per process.
+const std::vector<float> &gumbel_table() {
+    static std::vector<float> t;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        t.resize((size_t)1 << 24);
+        const float lo = 1e-9f, hi = 1.0f - 1e-9f;
+        for (uint32_t k = 0; k < (1u << 24); ++k) {
+            float u = (float)k / (float)(1u << 24);
+            u = u < lo ? lo : u > hi ? hi : u;
+            t[k] = -logf(-logf(u));
+        }
+    });
+    return t;
 }
 
 int sample_init(SampleWork &w, uint32_t V) {

@@ -189,8 +189,10 @@ typedef struct hg_diff_opts {
  * lib.rs:269-407) or the uncached (lib.rs:410-495) semi-autoregressive denoising of gen_len ids
  * after the prompt, with the block's logits scored on the device (the mask, the presence
  * penalty, the pick and its softmax confidences; only those cross PCIe).  Writes the generated
- * ids up to the first eos (at most gen_len); *n_out receives the count.  temp > 0 (Gumbel
- * draws, sample.rs:32-50) returns HG_ERR_UNSUPPORTED. */
+ * ids up to the first eos (at most gen_len); *n_out receives the count.  temp > 0 draws the
+ * picks as sample::gumbel_argmax (sample.rs:32-50) with the seeded Rng: -ln(-ln(u)) comes from a
+ * table of the Rng's 2^24 possible u computed with the host libm's logf (64 MB on the device,
+ * built once per process), each lane's draws from a GF(2) jump of the xorshift state. */
 int hg_generate_diffusion(const hg_model *m, const uint32_t *prompt, uint32_t n_prompt, const hg_diff_opts *opts,
                           uint32_t eos, uint32_t *out_ids, uint32_t *n_out);
 

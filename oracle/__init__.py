@@ -158,6 +158,12 @@ class Rng:
         return float(lib().orc_rng_next_f32(C.byref(self.state)))
 
 
+def gumbel_argmax(logits: np.ndarray, temp: float, rng: Rng) -> int:
+    """sample::gumbel_argmax (sample.rs:32-50)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    return int(lib().orc_gumbel_argmax(lg, lg.size, temp, C.byref(rng.state)))
+
+
 def sample(logits: np.ndarray, temp: float, top_p: float, rng: Rng) -> int:
     """sample::sample (sample.rs:66-112); ties in the nucleus order by ascending token id."""
     lg = np.ascontiguousarray(logits, np.float32)

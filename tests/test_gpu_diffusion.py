@@ -2,7 +2,7 @@
 oracle: run_block's logits for every block row and its K/V rows over a prefix cache (the tiny
 diffusion shape, the 500M model, heads of 128), forward_bidir, appending a finalized block, and
 whole cached and uncached denoising runs (the num_transfer schedule, the confidence threshold,
-re-masking, the presence penalty, an EOS stop)."""
+re-masking, the presence penalty, Gumbel draws at temperature > 0, an EOS stop)."""
 import numpy as np
 import pytest
 
@@ -67,6 +67,8 @@ CASES = [
     dict(gen_len=48, block=16, steps=8, rep_penalty=1.4, cached=True, threshold=0.05),
     dict(gen_len=32, block=8, steps=16, rep_penalty=1.4, cached=False),
     dict(gen_len=24, block=12, steps=6, rep_penalty=1.2, cached=False, remask_steps=1, remask_frac=0.5),
+    dict(gen_len=40, block=16, steps=20, rep_penalty=1.4, cached=True, temp=0.8, seed=77),
+    dict(gen_len=24, block=8, steps=12, rep_penalty=1.0, cached=False, temp=1.2, seed=5, remask_steps=1),
 ]
 
 

@@ -122,3 +122,23 @@ def test_draw_frequencies():
     q = np.sqrt([0.1, 0.2, 0.3, 0.4])
     expect = q / q.sum() * n
     assert np.all(np.abs(counts - expect) < 5 * np.sqrt(expect)), counts
+
+
+def test_gumbel_argmax_draws_and_distribution():
+    """gumbel_argmax: temp 0 is the argmax with no draw; one draw per finite logit; the picks of
+    argmax(l / temp - ln(-ln u)) follow softmax(l / temp) (the Gumbel-max identity)."""
+    lg = np.array([0.3, -np.inf, 1.0, np.nan, 0.5, 0.0], np.float32)
+    r = oracle.Rng(9)
+    assert oracle.gumbel_argmax(lg, 0.0, r) == 2
+    assert r.next_u64() == oracle.Rng(9).next_u64()
+    r, ref = oracle.Rng(9), oracle.Rng(9)
+    oracle.gumbel_argmax(lg, 1.0, r)
+    for _ in range(4):   # four finite entries, four draws
+        ref.next_u64()
+    assert r.next_u64() == ref.next_u64()
+    p = np.array([0.1, 0.2, 0.3, 0.4])
+    lg = (np.log(p) * 0.7).astype(np.float32)   # at temp 0.7: softmax(l / 0.7) = p
+    r = oracle.Rng(31)
+    n = 20000
+    counts = np.bincount([oracle.gumbel_argmax(lg, 0.7, r) for _ in range(n)], minlength=4)
+    assert np.all(np.abs(counts - p * n) < 5 * np.sqrt(p * n)), counts
