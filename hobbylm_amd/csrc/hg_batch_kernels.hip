@@ -236,12 +236,13 @@ __global__ __launch_bounds__(256) void k_gemm16(GemmArgs g) {
 // 16 entries with no masking: lane l supplies A row l % 16 and B column (entry) l % 16 for K
 // group g = l / 16 (block elements 8g .. 8g + 7: word t of the 16-byte halves at 32 g and
 // 32 g + 16 of a chunk, t the block within the chunk); C register v of lane l is row 4 g + v,
-// column l % 16.  Workgroup = 4 waves over 64 rows (blockIdx.x) of one column tile of at most
-// 16 NG entries (blockIdx.y; tiles past *n_tiles exit).  The tile's activations are staged in
+// column l % 16.  Workgroup = PG_WAVES waves over 16 PG_WAVES rows (blockIdx.x) of one column
+// tile of at most 16 NG entries (blockIdx.y; tiles past *n_tiles exit).  The tile's activations are staged in
 // LDS with entry strides of an odd number of 16-byte units, so the 16 entries read at one chunk
 // offset fall in distinct banks; each wave owns 16 rows and all of the tile's entries and streams
 // its rows' chunks through a register ring of D chunks.  The epilogue is 4 VALU operations per
 // (row, entry, block) against one MFMA per 256 of them, so the kernel is VALU-bound.
+constexpr uint32_t PG_WAVES = 8;   // waves (of 16 rows each) per workgroup: 128 rows share a staged tile
 __host__ __device__ inline uint32_t pgemm_qstride(uint32_t nc) { return nc * CHUNK_BYTES + 16; }
 __host__ __device__ inline uint32_t pgemm_sstride(uint32_t nc) { return nc * 4 + 4; }
 __host__ __device__ inline size_t pgemm_lds(uint32_t nc, uint32_t tt) {
@@ -249,7 +250,7 @@ __host__ __device__ inline size_t pgemm_lds(uint32_t nc, uint32_t tt) {
 }
 
 template <bool SCF32, int MODE, int D, bool FULLK, int NG>
-__global__ __launch_bounds__(256) void k_gemm_p(GemmArgs g) {
+__global__ __launch_bounds__(64 * PG_WAVES) void k_gemm_p(GemmArgs g) {
     static_assert(FULLK || D == 1, "a partial last chunk: one chunk per group");
     constexpr int NM = MODE == GM_GATEUP ? 2 : 1;   // matrices per wave
     constexpr uint32_t TT = 16 * NG;                // entries per column tile
@@ -267,7 +268,7 @@ __global__ __launch_bounds__(256) void k_gemm_p(GemmArgs g) {
     float *xds = reinterpret_cast<float *>(xs + (size_t)TT * qst);
     // 32-byte groups (a chunk's K group g: the lanes 2g and 2g + 1 of its 4 blocks), stored with
     // each block's two words side by side, so that the B operand of block t is one aligned pair
-    for (uint32_t i = tid; i < TT * nc * 4; i += 256) {   // entry i / (4 nc)
+    for (uint32_t i = tid; i < TT * nc * 4; i += 64 * PG_WAVES) {   // entry i / (4 nc)
         const uint32_t e = i / (nc * 4), p = i % (nc * 4);
         v4i a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
         if (e < ne) {
@@ -279,14 +280,14 @@ __global__ __launch_bounds__(256) void k_gemm_p(GemmArgs g) {
         dst[0] = v4i{a.x, b.x, a.y, b.y};
         dst[1] = v4i{a.z, b.z, a.w, b.w};
     }
-    for (uint32_t i = tid; i < TT * nc; i += 256) {   // block scales: entry i / nc, chunk i % nc
+    for (uint32_t i = tid; i < TT * nc; i += 64 * PG_WAVES) {   // block scales: entry i / nc, chunk i % nc
         const uint32_t e = i / nc, c = i % nc;
         v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
         if (e < ne) v = *reinterpret_cast<const v4f *>(g.ad + (size_t)g.act_row[tile.entry0 + e] * g.ads + 4 * c);
         *reinterpret_cast<v4f *>(xds + (size_t)e * sst + 4 * c) = v;
     }
     __syncthreads();
-    const uint32_t r0 = blockIdx.x * 64 + (uint32_t)wave * 16;   // this wave's rows within the group
+    const uint32_t r0 = blockIdx.x * 16 * PG_WAVES + (uint32_t)wave * 16;   // this wave's rows within the group
     if (r0 >= g.rows) return;   // (uniform per wave; after the workgroup's only barrier)
     const WaveExpTab tab = WaveExpTab::load(lane);
     const uint32_t gq = (uint32_t)lane >> 4, cc = (uint32_t)lane & 15;
@@ -505,8 +506,8 @@ __global__ __launch_bounds__(256) void k_b_scores(const float *__restrict__ qkv,
 // chunk maxima (order-free); e_t = exp(s_t - m) with the reference expf, into LDS; sum = the
 // index-order sum of e_t (block_seq_sum: 4 waves up to 3072 terms, 8 waves x 32 up to 16384,
 // else one lane); p_t = e_t * (1 / sum) written over the scores.  Workgroups are dealt longest
-// sequence first (order[] ranks the sequences by length).  NT = 512 threads, or 256 for
-// contexts of at most 3072 positions (the 4-wave sums; twice the workgroups per CU).
+// sequence first (order[] ranks the sequences by length).  NT = 512 threads, or 256 / 128 for
+// contexts of at most 3072 positions (4- or 2-wave sums; more workgroups per CU).
 __host__ __device__ inline size_t bsm_lds(uint32_t max_ctx) { return ((size_t)div_up(max_ctx, 4) * 4 + 64) * 4; }
 
 template <int NT>
@@ -543,8 +544,13 @@ __global__ __launch_bounds__(NT) void k_b_softmax(float *scores, uint32_t sc_str
     if (tid < 4) e[n + tid] = 0.0f;   // readable up to a multiple of 4 past n
     __syncthreads();
     if (n <= 3072) {   // sum += e_t in index order (ops.rs:119-122)
-        if (wave < 4) {
-            const float r = n <= 2048 ? block_seq_sum<4, 8>(e, n, xs, wave, lane) : block_seq_sum<4, 12>(e, n, xs, wave, lane);
+        if constexpr (NT >= 256) {
+            if (wave < 4) {
+                const float r = n <= 2048 ? block_seq_sum<4, 8>(e, n, xs, wave, lane) : block_seq_sum<4, 12>(e, n, xs, wave, lane);
+                if (tid == 0) s_inv = 1.0f / r;
+            }
+        } else {   // two waves, 16 or 24 terms per lane
+            const float r = n <= 2048 ? block_seq_sum<2, 16>(e, n, xs, wave, lane) : block_seq_sum<2, 24>(e, n, xs, wave, lane);
             if (tid == 0) s_inv = 1.0f / r;
         }
     } else if (NT == 512 && n <= 16384) {
@@ -1494,7 +1500,7 @@ bool launch_p_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t 
     else
         BLAUNCH(k_p_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
     if (max_ctx <= 3072)   // (a prompt chunk's window: bsm_lds fits the default limit)
-        BLAUNCH(k_b_softmax<256>, gm, dim3(256), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
+        BLAUNCH(k_b_softmax<128>, gm, dim3(128), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
     else
         BLAUNCH(k_b_softmax<512>, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
     const dim3 gp(div_up(n, 4u), kv.n_kv);
@@ -1547,7 +1553,7 @@ bool launch_p_gemm(hipStream_t st, int mode, const GemmArgs &a, uint32_t max_til
     if (tt != 16 && tt != 32 && tt != 64) return false;
     const size_t lds = pgemm_lds(M.nc, tt);
     if (lds > PGEMM_LDS_MAX || max_tiles == 0) return false;
-    const dim3 grid(div_up(a.rows, 64), max_tiles);
+    const dim3 grid(div_up(a.rows, 16 * PG_WAVES), max_tiles);
     // (each instantiation raises its dynamic LDS limit on first use)
 #define PG_L(S, MD, DD, FK, N)                                                                               \
     do {                                                                                                     \
@@ -1559,7 +1565,7 @@ bool launch_p_gemm(hipStream_t st, int mode, const GemmArgs &a, uint32_t max_til
             note_launch_error(ae_, "k_gemm_p LDS limit");                                                    \
             return false;                                                                                    \
         }                                                                                                    \
-        BLAUNCH(kf_, grid, dim3(256), lds, st, a);                                                           \
+        BLAUNCH(kf_, grid, dim3(64 * PG_WAVES), lds, st, a);                                                 \
     } while (0)
 #define PG_N(S, MD, DD, FK)                                                                                  \
     if (tt == 64) PG_L(S, MD, DD, FK, 4);                                                                    \
