@@ -492,7 +492,7 @@ __global__ __launch_bounds__(256) void k_b_scores(const float *__restrict__ qkv,
                 mx = sv;
             }
         }
-        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, shfl_xor(mx, o));
+        mx = wave_max_f(mx);
         if (lane == 0) wm[wave][r] = mx;
     }
     __syncthreads();
@@ -1392,7 +1392,7 @@ __global__ __launch_bounds__(256) void k_p_scores(const float *__restrict__ qkv,
                     mx = sv;
                 }
             }
-            for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, shfl_xor(mx, o));
+            mx = wave_max_f(mx);
             if (lane == 0) wm[wave][k * rep + r] = mx;
         }
     }

@@ -44,6 +44,21 @@ template <int CTRL>
 __device__ inline uint32_t dpp_u(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xf, 0xf, false);
 }
+// The maximum over the 64 lanes, in every lane: within each row of 16 by DPP (lane ^ 1, lane ^ 2,
+// then rotations by 4 and 8), then the four rows' maxima read as scalars.  No LDS round trip.
+// Every lane must be active.
+__device__ inline float wave_max_f(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x128>(v));
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
 // max over the 8 aligned lanes of a quantization block (lane j = lane & 7); every lane of the
 // group must be active.
 __device__ inline float max8_lanes(float m, int j) {
