@@ -565,203 +565,11 @@ __global__ __launch_bounds__(NT) void k_b_softmax(float *scores, uint32_t sc_str
 }
 
 // ------------------------------------------------------------------ paged attention: P.V
-// o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ... (model.rs:227-232).  One wave per (kv head,
-// group of HPW query heads sharing it, slice of EW = 64 / HPW elements): lane = (head, element),
-// each lane running its chain itself (a rounded product, then the add).  Packing the heads of a
-// kv head into one wave lets the lanes of one element share each V load, so a sequence's V is
-// streamed once per kv head by hd / EW waves, each on its own CU (a wave's stream rate is
-// bounded by the loads it keeps in flight).  A lane's 16 values of a page are four 16-byte
-// loads (v_el), pages prefetched 11 ahead in a register ring of 12 (constant slot indices: the
-// body is unrolled over a 192-position block).  Each head's probabilities of a block are loaded
-// one block ahead, one per lane per 64 positions, and broadcast through the wave's LDS rows.
-// Positions past the context contribute a product of +0 (the chain never holds -0: it starts
-// at +0 and x + (-x) rounds to +0), so o + 0 = o keeps the chain exact.  One wave per
-// workgroup; the waves of one (sequence, kv head) get ids equal mod 8 (one XCD's L2), and
-// workgroups are dealt longest sequence first.
-// o = (((o + p0 v0) + p1 v1) + ...) + p7 v7 with each product rounded (no FMA): the products are
-// interleaved with the adds (mul, mul, add, mul, add, ...) so that no add waits on the one
-// before it with nothing issued in between.
-__device__ __forceinline__ float chain8(float o, v4f pa, v4f pb, v4f va, v4f vb) {
-    float t0, t1;
-    asm("v_mul_f32 %[t0], %[p0], %[v0]\n\t"
-        "v_mul_f32 %[t1], %[p1], %[v1]\n\t"
-        "v_add_f32 %[o], %[o], %[t0]\n\t"
-        "v_mul_f32 %[t0], %[p2], %[v2]\n\t"
-        "v_add_f32 %[o], %[o], %[t1]\n\t"
-        "v_mul_f32 %[t1], %[p3], %[v3]\n\t"
-        "v_add_f32 %[o], %[o], %[t0]\n\t"
-        "v_mul_f32 %[t0], %[p4], %[v4]\n\t"
-        "v_add_f32 %[o], %[o], %[t1]\n\t"
-        "v_mul_f32 %[t1], %[p5], %[v5]\n\t"
-        "v_add_f32 %[o], %[o], %[t0]\n\t"
-        "v_mul_f32 %[t0], %[p6], %[v6]\n\t"
-        "v_add_f32 %[o], %[o], %[t1]\n\t"
-        "v_mul_f32 %[t1], %[p7], %[v7]\n\t"
-        "v_add_f32 %[o], %[o], %[t0]\n\t"
-        "v_add_f32 %[o], %[o], %[t1]"
-        : [o] "+v"(o), [t0] "=&v"(t0), [t1] "=&v"(t1)
-        : [p0] "v"(pa.x), [p1] "v"(pa.y), [p2] "v"(pa.z), [p3] "v"(pa.w), [p4] "v"(pb.x), [p5] "v"(pb.y),
-          [p6] "v"(pb.z), [p7] "v"(pb.w), [v0] "v"(va.x), [v1] "v"(va.y), [v2] "v"(va.z), [v3] "v"(va.w),
-          [v4] "v"(vb.x), [v5] "v"(vb.y), [v6] "v"(vb.z), [v7] "v"(vb.w));
-    return o;
-}
-
-template <int HD, int HPW>
-__global__ __launch_bounds__(64) void k_b_pv(const float *__restrict__ probs, uint32_t sc_stride,
-                                             const uint32_t *__restrict__ pos, const uint32_t *__restrict__ order,
-                                             PagedKV kv, uint32_t n_seq, float *o_out) {
-    // EW elements per wave, WPE waves per head group, LPP 16-byte loads per lane per page
-    constexpr uint32_t EW = 64 / HPW, WPE = HD / EW, LPP = 4 / HPW;
-    // a register ring of R pages (24 loads in flight), probabilities in blocks of half a ring
-    constexpr uint32_t R = 24 / LPP, NPB = R / 2, PB = NPB * PAGE, SB = R * PAGE;
-    constexpr uint32_t PV4 = HPW * PB / 4, PU = (PV4 + 63) / 64;   // 16-byte probability loads per block, per lane
-    constexpr uint32_t PLS = PB + 4;   // LDS row of one head (padded: the heads' rows on other banks)
-    __shared__ __align__(16) float pw[HPW * PLS];
-    __shared__ __align__(16) v4f stg[2][4 * EW];   // a page slice, [quad][element]
-    extern __shared__ uint32_t btl[];             // [pages of the longest context]
-    const int lane = threadIdx.x;
-    const uint32_t n_heads = kv.n_heads, n_kv = kv.n_kv, rep = n_heads / n_kv;
-    const uint32_t wpk = div_up(rep, HPW) * WPE;   // waves per (sequence, kv head)
-    uint32_t key, w;
-    {
-        const uint32_t L = blockIdx.x, nkeys = n_seq * n_kv;
-        if (nkeys % 8 == 0) {
-            const uint32_t slot = L / 8;
-            key = L % 8 + 8 * (slot / wpk);
-            w = slot % wpk;
-        } else {
-            key = L / wpk;
-            w = L % wpk;
-        }
-    }
-    const uint32_t s = order[key / n_kv], g = key % n_kv, n = pos[s] + 1, npg = div_up(n, PAGE);
-    const uint32_t *bts = kv.bt + (size_t)s * kv.bt_stride;
-    for (uint32_t i = lane; i < npg; i += 64) btl[i] = bts[i];   // the block table
-    __syncthreads();
-    const uint32_t hb = (w / WPE) * HPW, es = (w % WPE) * EW;   // head group, element slice
-    const uint32_t hl = (uint32_t)lane / EW, el = (uint32_t)lane % EW, hr = hb + hl;   // hr >= rep: idle lanes
-    const float *prb = probs + ((size_t)s * n_heads + g * rep) * sc_stride;
-    const float *vg = kv.v + kv_tile(0, g, n_kv, HD);   // (uniform) + page * pstride
-    const size_t pstride = (size_t)n_kv * HD * PAGE;
-    v4f vr[R][LPP];
-    // the slice of a page: load u of lane l is entry c = 64 u + l of [quad][element] (64
-    // lanes: contiguous runs of EW * 16 bytes)
-    auto load_page = [&](v4f (&d)[LPP], uint32_t page) {
-        const v4f *src = reinterpret_cast<const v4f *>(vg + (size_t)page * pstride);
-#pragma unroll
-        for (uint32_t u = 0; u < LPP; ++u) {
-            const uint32_t c = 64 * u + (uint32_t)lane;
-            d[u] = src[(c / EW) * HD + es + c % EW];
-        }
-    };
-    auto stage = [&](const v4f (&d)[LPP], uint32_t buf) {
-#pragma unroll
-        for (uint32_t u = 0; u < LPP; ++u) stg[buf][64 * u + lane] = d[u];
-    };
-    auto id_of = [&](uint32_t p) { return btl[min(p, npg - 1)]; };   // (clamped to the sequence's pages)
-    // probabilities of block B: entry c = 64 u + lane is head c / (PB / 4), positions
-    // B PB + 4 (c % (PB / 4)) .. + 3 (clamped into the row; past the context they are masked)
-    v4f pn[2][PU];
-    auto load_probs = [&](v4f (&d)[PU], uint32_t B) {
-#pragma unroll
-        for (uint32_t u = 0; u < PU; ++u) {
-            const uint32_t c = PV4 % 64 == 0 ? 64 * u + (uint32_t)lane : min(64 * u + (uint32_t)lane, PV4 - 1);
-            const uint32_t r = c / (PB / 4), i = c % (PB / 4);
-            d[u] = *reinterpret_cast<const v4f *>(prb + (size_t)min(hb + r, rep - 1) * sc_stride +
-                                                  min(B * PB + 4 * i, sc_stride - 4));
-        }
-    };
-    auto stage_probs = [&](const v4f (&d)[PU]) {
-#pragma unroll
-        for (uint32_t u = 0; u < PU; ++u) {
-            const uint32_t c = 64 * u + (uint32_t)lane;
-            if (PV4 % 64 == 0 || c < PV4)   // (all lanes when the block fills them)
-                *reinterpret_cast<v4f *>(pw + (c / (PB / 4)) * PLS + 4 * (c % (PB / 4))) = d[u];
-        }
-    };
-    // a page's operands in registers: probabilities of the lane's head, values of its element
-    struct Ops {
-        v4f p[4], v[4];
-    };
-    auto read_ops = [&](Ops &d, uint32_t k) {   // page k (its slice staged in stg[k & 1])
-        const v4f *pj = reinterpret_cast<const v4f *>(pw + hl * PLS + 16 * (k % NPB));
-        const v4f *vj = stg[k & 1] + el;
-#pragma unroll
-        for (uint32_t q = 0; q < 4; ++q) {
-            d.p[q] = pj[q];
-            d.v[q] = vj[q * EW];
-        }
-    };
-    // Pipeline over pages k (ring slot k % R holds page k, loaded R pages ahead).  Step k:
-    // stage page k + 2 into stg[k & 1] and reload its slot with page k + 2 + R; stage the
-    // probabilities if page k + 1 starts a block; read page k + 1's operands from LDS; run the
-    // chain over page k (operands read in the step before).  No fences: the LDS executes one
-    // wave's operations in order, so each write lands after the reads of the data it replaces
-    // and each read sees the writes before it (the compiler keeps the order of accesses to the
-    // same buffer).  Page ids of the pages a
-    // superblock (R pages) loads come from the LDS table one superblock ahead (lane j: page
-    // (sb + 1) R + j + 2).  The probabilities of block B are loaded two blocks ahead into
-    // pn[B & 1] (loads retire in order: the wait for them leaves the newer page loads in flight).
-    const uint32_t ids0 = id_of(min((uint32_t)lane, R + 1));   // pages 0 .. R + 1
-    load_probs(pn[0], 0);
-    load_probs(pn[1], 1);
-    uint32_t ids_nx = id_of(R + 2 + (uint32_t)lane);
-#pragma unroll
-    for (uint32_t j = 0; j < R; ++j) load_page(vr[j], __builtin_amdgcn_readlane(ids0, j));
-    stage_probs(pn[0]);
-    load_probs(pn[0], 2);
-    stage(vr[0], 0);
-    load_page(vr[0], __builtin_amdgcn_readlane(ids0, R));
-    stage(vr[1], 1);
-    load_page(vr[1], __builtin_amdgcn_readlane(ids0, R + 1));
-    Ops ops[2];
-    read_ops(ops[0], 0);
-    float o = 0.0f;
-    const uint32_t nfull = n / SB, nsb = div_up(n, SB);
-    auto step = [&](uint32_t sb, uint32_t j, uint32_t ids, auto full_tag) {
-        constexpr bool full = decltype(full_tag)::value;
-        stage(vr[(j + 2) % R], j & 1);
-        if constexpr (full) load_page(vr[(j + 2) % R], __builtin_amdgcn_readlane(ids, j));
-        if ((j + 1) % NPB == 0) {
-            const uint32_t nb = (j + 1) / NPB;   // block 2 sb + nb starts at page j + 1
-            stage_probs(pn[nb & 1]);
-            if constexpr (full) load_probs(pn[nb & 1], 2 * sb + nb + 2);
-        }
-        read_ops(ops[(j + 1) & 1], j + 1);
-        const Ops &c = ops[j & 1];
-        if constexpr (full) {
-            o = chain8(o, c.p[0], c.p[1], c.v[0], c.v[1]);
-            o = chain8(o, c.p[2], c.p[3], c.v[2], c.v[3]);
-        } else {   // positions t = sb SB + 16 j + 4 q + u < n only
-#pragma unroll
-            for (uint32_t q = 0; q < 4; ++q) {
-                const uint32_t t = sb * SB + 16 * j + 4 * q;
-                o = o + (t < n ? c.p[q].x * c.v[q].x : 0.0f);
-                o = o + (t + 1 < n ? c.p[q].y * c.v[q].y : 0.0f);
-                o = o + (t + 2 < n ? c.p[q].z * c.v[q].z : 0.0f);
-                o = o + (t + 3 < n ? c.p[q].w * c.v[q].w : 0.0f);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);   // keep the step's order
-    };
-    // full superblocks: a straight-line body; then the last one, masked and loading nothing
-    for (uint32_t sb = 0; sb < nfull; ++sb) {
-        const uint32_t ids = ids_nx;
-        ids_nx = id_of((sb + 2) * R + 2 + (uint32_t)lane);
-#pragma unroll
-        for (uint32_t j = 0; j < R; ++j) step(sb, j, ids, std::true_type{});
-    }
-    if (nfull < nsb) {
-#pragma unroll
-        for (uint32_t j = 0; j < R; ++j) step(nfull, j, 0u, std::false_type{});
-    }
-    if (hr < rep) o_out[((size_t)s * n_heads + g * rep + hr) * HD + es + el] = o;
-}
-
-// ------------------------------------------------------------------ paged attention: P.V, split
-// The same chains as k_b_pv with the rounded products formed by a second wave: workgroup = 2
-// waves for one (sequence, kv head, group of 4 query heads, slice of 16 elements).  The
-// producer (wave 1, lane = (slot quad q, element e)) loads each page's V slice (one 16-byte load:
+// o[di] = ((0 + p_0 v_0[di]) + p_1 v_1[di]) + ... (model.rs:227-232): every (head, element) is a
+// one-lane chain of rounded products added in position order, and the products are formed by
+// other waves than the chain's: workgroup = a chain wave and PV2_NP producer waves for one
+// (sequence, kv head, group of 4 query heads, slice of 16 elements).  A
+// producer (lane = (slot quad q, element e)) loads each page's V slice (one 16-byte load:
 // 4 positions of element e) and the 4 heads' probabilities of those positions, and writes the
 // 16 products p * v (+0 past the context) into an LDS ring of PV2_NS slots of PV2_G pages, laid
 // out [q][head][element][4 positions]; the chain wave (lane = (head, element)) reads 16
@@ -770,7 +578,8 @@ __global__ __launch_bounds__(64) void k_b_pv(const float *__restrict__ probs, ui
 // the LDS executes one wave's operations in order, so a flag written after the data (and read
 // before it) orders them without waits; only the compiler is fenced.  Every wait is bounded and
 // reports *err.  Workgroups are dealt longest sequence first; the slices of one (sequence,
-// kv head) get ids equal mod 8.
+// kv head) get ids equal mod 8.  Positions past the context contribute +0, which leaves the
+// chain unchanged: it never holds -0 (it starts at +0, and x + (-x) rounds to +0).
 constexpr uint32_t PV2_G = 4, PV2_NS = 4, PV2_R = 32;   // pages per slot, ring slots, producer V ring (pages)
 constexpr uint32_t PV2_NP = 3;                          // producer waves
 constexpr size_t PV2_LDS_MAX = 96 * 1024;
@@ -983,9 +792,6 @@ __global__ __launch_bounds__(64 * (PV2_NP + 1)) void k_b_pv2(const float *__rest
     }
     if (hb + hl < rep) o_out[((size_t)s * n_heads + g * rep + hb + hl) * HD + es + (uint32_t)lane % 16] = o;
 }
-
-// Heads per P.V wave for rep query heads per kv head.
-inline uint32_t pv_hpw(uint32_t rep) { return rep >= 4 ? 4u : rep >= 2 ? 2u : 1u; }
 
 // Sequences ranked by length, longest first (equal lengths: lower index first).  One workgroup.
 __global__ void k_b_order(const uint32_t *__restrict__ pos, uint32_t n, uint32_t *order) {
