@@ -36,7 +36,7 @@ CTX_END = 2048          # the timed window ends at position CTX_END - 1
 N_PROMPT = 16
 PEAK_HBM = 8.0e12       # MI355X HBM3E, bytes/s
 METRIC = "500M Q8_0 decode tok/s (bs1, ctx2k) + achieved HBM GB/s vs peak"
-DOM_KERNEL = "k_attn_softmax_pv_res<64>"
+DOM_KERNEL = "k_attn_softmax_pv_res<64, false>"
 
 
 def algorithmic_bytes(cfg, ctx):
@@ -183,7 +183,7 @@ def op_attention():
     and fp32 cache, append at pos = ctx - 1.  Bytes ~ 2 ctx 256 4 + 2 KB + 8 KB."""
     import hobbylm_amd as hg
     rows = []
-    for ctx in (512, 2048, 8192):
+    for ctx in (512, 2048, 4096, 7168, 8192):
         nbytes = 2 * ctx * 256 * 4 + 2048 + 8192
         for fast in (False, True):
             s_us, p_us = hg.attention_time(16, 4, 64, ctx, reps=50, fast=fast)

@@ -593,7 +593,8 @@ __host__ __device__ inline size_t pv2_lds(uint32_t max_ctx) {
 template <int HD>
 __global__ __launch_bounds__(64 * (PV2_NP + 1)) void k_b_pv2(const float *__restrict__ probs, uint32_t sc_stride,
                                                const uint32_t *__restrict__ pos, const uint32_t *__restrict__ order,
-                                               PagedKV kv, uint32_t n_seq, float *o_out, uint32_t *err) {
+                                               PagedKV kv, uint32_t n_seq, float *o_out, uint32_t *err,
+                                               uint32_t flip) {
     constexpr uint32_t EW = 16, WPE = HD / EW, G = PV2_G, NS = PV2_NS, R = PV2_R;
     static_assert(R % G == 0, "whole slots per register ring");
     extern __shared__ __align__(16) float lds[];
@@ -606,7 +607,11 @@ __global__ __launch_bounds__(64 * (PV2_NP + 1)) void k_b_pv2(const float *__rest
     const uint32_t wpk = div_up(rep, 4) * WPE;   // workgroups per (sequence, kv head)
     uint32_t key, w;
     {
-        const uint32_t L = blockIdx.x, nkeys = n_seq * n_kv;
+        // second round of the dispatch (ids >= flip) in reverse rank order, so the CU that holds
+        // a long sequence's workgroup also holds a short one
+        const uint32_t W = gridDim.x, L0 = blockIdx.x;
+        const uint32_t L = (flip && L0 >= flip && W <= 2 * flip) ? flip + (W - 1 - L0) : L0;
+        const uint32_t nkeys = n_seq * n_kv;
         if (nkeys % 8 == 0) {
             const uint32_t slot = L / 8;
             key = L % 8 + 8 * (slot / wpk);
@@ -1042,10 +1047,20 @@ bool launch_b_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t 
     else
         BLAUNCH(k_b_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, kv, scores, ss, pmax, nch);
     BLAUNCH(k_b_softmax<512>, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
+    // workgroups of the first dispatch round: one per CU
+    static const uint32_t n_cu = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            v = 0;
+        return (uint32_t)v;
+    }();
+    const uint32_t flip = n_cu;
     if (hd == 64)
-        BLAUNCH(k_b_pv2<64>, gp, dim3(64 * (PV2_NP + 1)), pv2_lds(max_ctx), st, scores, ss, pos, order, kv, n, o, err);
+        BLAUNCH(k_b_pv2<64>, gp, dim3(64 * (PV2_NP + 1)), pv2_lds(max_ctx), st, scores, ss, pos, order, kv, n, o, err,
+                flip);
     else
-        BLAUNCH(k_b_pv2<128>, gp, dim3(64 * (PV2_NP + 1)), pv2_lds(max_ctx), st, scores, ss, pos, order, kv, n, o, err);
+        BLAUNCH(k_b_pv2<128>, gp, dim3(64 * (PV2_NP + 1)), pv2_lds(max_ctx), st, scores, ss, pos, order, kv, n, o, err,
+                flip);
     return true;
 }
 

@@ -1070,10 +1070,15 @@ __device__ __forceinline__ void pv_adds64(float &o, const v4f a) {
 //   others, flagging them; wave 0 then runs the D sequential chains, a row's lanes holding a
 //   group's products and its first lane adding them in order through DPP row rotations
 //   (pv_adds64), waiting only for each block of 4 groups' flags.
+// LONG = false serves windows up to SHORT positions (one 64-bit ready word, each producer's
+// groups in one batch); LONG = true up to MAXR (two ready words, batches of 7 groups, the sum
+// as 16 or 28 terms per lane).
 struct PvResCfg {
     static constexpr uint32_t D = 4;      // output elements per workgroup (4 or 8)
     static constexpr uint32_t G = 64;     // positions per product group (16 lanes x 4)
-    static constexpr uint32_t NG = 64;    // product groups: one bit each of the ready mask
+    static constexpr uint32_t NG = 128;   // product groups: one bit each of the ready mask (2 words)
+    static constexpr uint32_t MAXR = 7168;   // positions: the exact sum as 4 waves x 64 lanes x 28 terms
+    static constexpr uint32_t SHORT = 3072;  // up to here: 12 terms per lane, one ready word (LONG = false)
     static constexpr uint32_t VB = 8;     // V loads in flight per V thread
 };
 
@@ -1085,10 +1090,10 @@ __host__ __device__ inline size_t pv_res_lds(uint32_t cap) {   // e, P, the sum'
 }
 __host__ __device__ bool pv_res_fits(uint32_t cap) {
     return cap >= 1 && pv_res_lds(cap) <= PV_LDS_BUDGET && pv_res_rows(cap) / PvResCfg::G <= PvResCfg::NG &&
-           pv_res_rows(cap) <= 3072;
+           pv_res_rows(cap) <= PvResCfg::MAXR;
 }
 
-template <int HD>
+template <int HD, bool LONG>
 __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__restrict__ scores,
                                                              const float *__restrict__ pmax,
                                                              const float *__restrict__ qkv, const StepParams *p,
@@ -1097,7 +1102,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     using C = PvResCfg;
     constexpr uint32_t D = C::D, G = C::G, EB = 8;
     extern __shared__ __align__(16) float lds[];
-    __shared__ uint64_t ready;           // bit g: products of group g written
+    __shared__ uint64_t ready[LONG ? 2 : 1];   // bit g % 64 of word g / 64: products of group g written
     __shared__ uint32_t vdone[4];        // V rounds written by V wave 4 + i (its groups i, i + 4, ...)
     __shared__ uint32_t arrived;         // waves whose e_t are written
     __shared__ uint32_t inv_ready;
@@ -1122,7 +1127,8 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(u * 512 + tid, n - 1)];
     const WaveExpTab tab = WaveExpTab::load(lane);
     if (tid == 0) {
-        ready = 0;
+        ready[0] = 0;
+        if constexpr (LONG) ready[LONG ? 1 : 0] = 0;
         arrived = 0;
         inv_ready = 0;
         xs.sync = 0;
@@ -1178,7 +1184,14 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
         while (__hip_atomic_load(&arrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 8u)
             __builtin_amdgcn_s_sleep(1);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        const float r = n <= 2048 ? block_seq_sum<4, 8>(e, n, xs, wave, lane) : block_seq_sum<4, 12>(e, n, xs, wave, lane);
+        // terms per lane by context (4 waves x 64 lanes x EPT >= n; a longer sum would fall back
+        // to the one-lane chain inside block_seq_sum).  Two layouts per instantiation: more
+        // inlined layouts made the kernel measurably slower.
+        float r;
+        if constexpr (LONG)
+            r = n <= 4096 ? block_seq_sum<4, 16>(e, n, xs, wave, lane) : block_seq_sum<4, 28>(e, n, xs, wave, lane);
+        else
+            r = n <= 2048 ? block_seq_sum<4, 8>(e, n, xs, wave, lane) : block_seq_sum<4, 12>(e, n, xs, wave, lane);
         inv0 = 1.0f / r;
         if (tid == 0) {
             s_inv = inv0;
@@ -1220,9 +1233,9 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
             v4f *pv = reinterpret_cast<v4f *>(P + di * TPC + t);
             *pv = prod(t, *reinterpret_cast<const v4f *>(e + t), *pv);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-            if (lane == 0) __hip_atomic_fetch_or(&ready, 1ull << pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) __hip_atomic_fetch_or(&ready[0], 1ull << pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        if (pw + 6 < ngp) {
+        if (!LONG && pw + 6 < ngp) {
             constexpr uint32_t KM = 8;   // groups per wave: 4 nblk <= 48
             vwait(div_up(ng, 4) - 1, 0, 3);   // every V round in
             v4f ev[KM], vv[KM];
@@ -1242,7 +1255,38 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
                 }
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-            if (lane == 0) __hip_atomic_fetch_or(&ready, mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) __hip_atomic_fetch_or(&ready[0], mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        if (LONG && pw + 6 < ngp) {
+            // the wave's other groups pw + 6 k (k >= 1) in batches of KB: the batch's reads first,
+            // then its products, one release and one flag update per ready word
+            constexpr uint32_t KB = 7;
+            vwait(div_up(ng, 4) - 1, 0, 3);   // every V round in
+            for (uint32_t k0 = 1; pw + 6 * k0 < ngp; k0 += KB) {
+                v4f ev[KB], vv[KB];
+#pragma unroll
+                for (uint32_t k = 0; k < KB; ++k) {
+                    const uint32_t gi = min(pw + 6 * (k0 + k), ngp - 1), t = G * gi + 4 * tq;
+                    ev[k] = *reinterpret_cast<const v4f *>(e + t);
+                    vv[k] = *reinterpret_cast<const v4f *>(P + di * TPC + t);
+                }
+                uint64_t m0 = 0, m1 = 0;
+#pragma unroll
+                for (uint32_t k = 0; k < KB; ++k) {
+                    const uint32_t gi = pw + 6 * (k0 + k), t = G * gi + 4 * tq;
+                    if (gi < ngp) {
+                        *reinterpret_cast<v4f *>(P + di * TPC + t) = prod(t, ev[k], vv[k]);
+                        if (gi < 64) m0 |= 1ull << gi;
+                        else m1 |= 1ull << (gi - 64);
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                if (lane == 0) {
+                    if (m0) __hip_atomic_fetch_or(&ready[0], m0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    if (m1)
+                        __hip_atomic_fetch_or(&ready[LONG ? 1 : 0], m1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+            }
         }
     }
     if (wave == 0) {   // the first block's products (groups 0..3), by the chain wave itself
@@ -1285,11 +1329,17 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
         // the current group's adds; the product flags are checked once per block of 4 groups.
         const uint32_t r4 = (uint32_t)lane >> 4, li = (uint32_t)lane & 15;
         const float *prow = P + r4 * TPC + 4 * li;
-        uint64_t known = 0xf;   // ready bits seen so far (block 0: this wave's own products)
-        auto block_wait = [&](uint32_t b) {   // groups 4 b .. 4 b + 3
-            while (((known >> (4 * b)) & 0xf) != 0xf) {
-                known = __hip_atomic_load(&ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-                if (((known >> (4 * b)) & 0xf) != 0xf) __builtin_amdgcn_s_sleep(1);
+        uint64_t known = 0xf;   // ready word kw as last read (block 0: this wave's own products)
+        uint32_t kw = 0;
+        auto block_wait = [&](uint32_t b) {   // groups 4 b .. 4 b + 3: bits 4 b % 64 .. of word b / 16
+            const uint32_t wd = LONG ? b >> 4 : 0, sh = (4 * b) & 63;
+            if (LONG && wd != kw) {
+                kw = wd;
+                known = 0;
+            }
+            while (((known >> sh) & 0xf) != 0xf) {
+                known = __hip_atomic_load(&ready[wd], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (((known >> sh) & 0xf) != 0xf) __builtin_amdgcn_s_sleep(1);
             }
         };
         const uint32_t ngp = 4 * nblk;
@@ -2015,7 +2065,10 @@ hipError_t init_kernel_attributes() {
 #undef PV_ATTR
 #define PVR_ATTR(HD)                                                                                        \
     if (e == hipSuccess)                                                                                    \
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_softmax_pv_res<HD>),                 \
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_softmax_pv_res<HD, false>),          \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_LDS_BUDGET);            \
+    if (e == hipSuccess)                                                                                    \
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_softmax_pv_res<HD, true>),           \
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_LDS_BUDGET);
     PVR_ATTR(32) PVR_ATTR(64) PVR_ATTR(128)
 #undef PVR_ATTR
@@ -2203,8 +2256,12 @@ static void attn_exact_launch(hipStream_t st, int which, const float *qkv, const
         return;
     }
     if (pv_res_fits(win)) {
-        LAUNCH(k_attn_softmax_pv_res<HD>, dim3(n_heads * (HD / PvResCfg::D)), dim3(512), pv_res_lds(win), st, scratch,
-               part, qkv, p, vc, cap, win, S, n_heads, n_kv, o_out);
+        if (pv_res_rows(win) <= PvResCfg::SHORT)
+            LAUNCH((k_attn_softmax_pv_res<HD, false>), dim3(n_heads * (HD / PvResCfg::D)), dim3(512), pv_res_lds(win),
+                   st, scratch, part, qkv, p, vc, cap, win, S, n_heads, n_kv, o_out);
+        else
+            LAUNCH((k_attn_softmax_pv_res<HD, true>), dim3(n_heads * (HD / PvResCfg::D)), dim3(512), pv_res_lds(win),
+                   st, scratch, part, qkv, p, vc, cap, win, S, n_heads, n_kv, o_out);
     } else {
         const size_t shm = (size_t)div_up(win, 4) * 16 + (size_t)pv_ring_slots(win) * PvCfg::SLOT * 4;
         LAUNCH(k_attn_softmax_pv<HD>, dim3(n_heads * (HD / PvCfg::D)), dim3(PvCfg::NW * 64), shm, st, scratch, part, qkv,

@@ -153,12 +153,13 @@ def test_joint12_shape_bit_exact(hg, orc):
         assert _bits_equal(gk, ok) and _bits_equal(gv, ov), layer
 
 
-@pytest.mark.parametrize("start", [3050, 8176])
+@pytest.mark.parametrize("start", [3050, 7150, 8176])
 def test_default_capacity_cache_bit_exact(hg, orc, start):
     """The drop-in cache (max_ctx = 0: capacity = context_length = 8192) on the 500M model,
     seeded with the same KV rows on both paths, decoding forced tokens across attention
-    windows: from the LDS-resident softmax/P.V kernel (<= 3072 positions) into the ring kernel
-    (start 3050), and up to the last position of the cache (start 8176)."""
+    windows: across the resident softmax/P.V kernel's sum layouts (start 3050: 12 to 16 terms
+    per lane), from that kernel (<= 7168 positions) into the ring kernel (start 7150), and up to
+    the last position of the cache (start 8176)."""
     path = gs.synth_path("500M", 1)
     gm, om = hg.Model(path), orc.Model(path)
     c = gm.cfg

@@ -117,18 +117,20 @@ def test_attention_fast_within_tolerance(hg, orc, ctx):
     assert np.max(np.abs(got - want)) <= 1e-4
 
 
-# 512 / 2048 / 8192: the attention layer's contexts; 2049 and 3072: the resident kernel's
-# 12-terms-per-lane sum and its longest window; 3073 and 8192: the LDS product ring
-@pytest.mark.parametrize("ctx", [1, 300, 512, 2048, 2049, 3072, 3073, 8192])
+# 512 / 2048 / 8192: the attention layer's contexts.  The resident kernel holds windows up to
+# 7168 positions, its exact sum as 4 waves x 64 lanes x 8, 12, ..., 28 terms: 2048 / 2049,
+# 3072 / 3073, 4096 / 4097, 5120, 6145 and 7168 are the edges of those layouts; 7169 and 8192
+# run the LDS product ring.
+@pytest.mark.parametrize("ctx", [1, 300, 512, 2048, 2049, 3072, 3073, 4096, 4097, 5120, 6145, 7168, 7169, 8192])
 def test_attention_exact_bit_exact(hg, orc, ctx):
     got, want = _attn_case(orc, hg, ctx, exact=True)
     assert _bits_equal(got, want)
 
 
-@pytest.mark.parametrize("hd,nh,nkv", [(128, 12, 3), (32, 4, 2)])
-def test_attention_other_head_dims(hg, orc, hd, nh, nkv):
+@pytest.mark.parametrize("hd,nh,nkv,ctx", [(128, 12, 3, 777), (32, 4, 2, 777), (128, 12, 3, 5000)])
+def test_attention_other_head_dims(hg, orc, hd, nh, nkv, ctx):
     for exact in (False, True):
-        got, want = _attn_case(orc, hg, 777, exact=exact, nh=nh, nkv=nkv, hd=hd, theta=1e6)
+        got, want = _attn_case(orc, hg, ctx, exact=exact, nh=nh, nkv=nkv, hd=hd, theta=1e6)
         if exact:
             assert _bits_equal(got, want)
         else:
