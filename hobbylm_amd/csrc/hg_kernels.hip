@@ -819,9 +819,10 @@ struct PvCfg {
     static constexpr uint32_t RMAX = 16;
 };
 constexpr size_t PV_LDS_BUDGET = 156 * 1024;
+constexpr size_t XSUM_FLOATS = (sizeof(xsum::Scratch) + 15) / 16 * 4;   // the exact sum's LDS tables
 
 __host__ __device__ uint32_t pv_ring_slots(uint32_t cap) {
-    const size_t e_bytes = (size_t)div_up(cap, 4) * 16;
+    const size_t e_bytes = (size_t)div_up(cap, 4) * 16 + XSUM_FLOATS * 4;
     const size_t left = PV_LDS_BUDGET > e_bytes ? PV_LDS_BUDGET - e_bytes : 0;
     const uint32_t r = (uint32_t)(left / (PvCfg::SLOT * 4));
     return r > PvCfg::RMAX ? PvCfg::RMAX : r;
@@ -848,6 +849,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
     const uint32_t R = pv_ring_slots(win);
     float *e = lds;                                     // [win] e_t, then p_t
     float *ring = lds + (size_t)div_up(win, 4) * 4;     // [R][D][TP]
+    xsum::Scratch &xs = *reinterpret_cast<xsum::Scratch *>(ring + (size_t)R * C::SLOT);
     const float *sc = scores + (size_t)h * cap;
     const uint32_t qd = n_heads * HD, kvd = n_kv * HD;
     const float *vcg = vc + (size_t)g * cap * HD + q * D;
@@ -894,9 +896,16 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
             }
     }
     if (tid < (int)C::RMAX) ready[tid] = 0;
-    if (tid == 0) done = 0;
+    if (tid == 0) {
+        done = 0;
+        xs.sync = 0;
+    }
     __syncthreads();
-    if (tid == 0) s_inv = 1.0f / seq_sum_lds(e, n, 0.0f);   // sum += e_t in index order
+    {   // sum += e_t in index order, formed by all 8 waves (16 or 32 terms per lane; past 16384
+        // terms block_seq_sum runs the one-lane chain itself)
+        const float r = n <= 8192 ? block_seq_sum<8, 16>(e, n, xs, wave, lane) : block_seq_sum<8, 32>(e, n, xs, wave, lane);
+        if (tid == 0) s_inv = 1.0f / r;
+    }
     __syncthreads();
     const float inv = s_inv;   // p_t = e_t * inv, formed by the producers
     if (pw >= 0) {
@@ -1083,7 +1092,6 @@ struct PvResCfg {
 };
 
 __host__ __device__ inline uint32_t pv_res_rows(uint32_t cap) { return div_up(cap, 256) * 256; }   // chain blocks
-constexpr size_t XSUM_FLOATS = (sizeof(xsum::Scratch) + 15) / 16 * 4;
 __host__ __device__ inline size_t pv_res_lds(uint32_t cap) {   // e, P, the sum's scratch
     const uint32_t rc = pv_res_rows(cap);
     return ((size_t)rc + (size_t)PvResCfg::D * (rc + 4) + XSUM_FLOATS) * 4;
@@ -2263,7 +2271,7 @@ static void attn_exact_launch(hipStream_t st, int which, const float *qkv, const
             LAUNCH((k_attn_softmax_pv_res<HD, true>), dim3(n_heads * (HD / PvResCfg::D)), dim3(512), pv_res_lds(win),
                    st, scratch, part, qkv, p, vc, cap, win, S, n_heads, n_kv, o_out);
     } else {
-        const size_t shm = (size_t)div_up(win, 4) * 16 + (size_t)pv_ring_slots(win) * PvCfg::SLOT * 4;
+        const size_t shm = (size_t)div_up(win, 4) * 16 + (size_t)pv_ring_slots(win) * PvCfg::SLOT * 4 + XSUM_FLOATS * 4;
         LAUNCH(k_attn_softmax_pv<HD>, dim3(n_heads * (HD / PvCfg::D)), dim3(PvCfg::NW * 64), shm, st, scratch, part, qkv,
                p, vc, cap, win, S, n_heads, n_kv, o_out, q_out, d_out);
     }
