@@ -13,7 +13,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhobby_gpu.so")
-SOURCES = ["hg_kernels.hip", "hg_batch_kernels.hip", "hg_engine.hip", "hg_batch.hip", "hg_prefill.hip", "hg_sample.hip", "hg_gguf.cpp"]
+SOURCES = ["hg_kernels.hip", "hg_batch_kernels.hip", "hg_engine.hip", "hg_batch.hip", "hg_prefill.hip", "hg_sample.hip",
+           "hg_f32.hip", "hg_gguf.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: no implicit FMA; the kernels call fmaf() exactly where hobby-rs fuses.

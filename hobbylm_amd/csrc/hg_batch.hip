@@ -278,6 +278,7 @@ int hg_batch_new(const hg_model *m, uint32_t max_seqs, uint32_t max_ctx, uint32_
         const hg_config &c = m->c;
         if (max_seqs == 0 || max_seqs > 8 * PT_MAX) return fail(HG_ERR_ARG, "max_seqs out of range (1..512)");
         if (max_ctx == 0 || max_ctx > c.context_length) max_ctx = c.context_length;
+        if (m->f32) return fail(HG_ERR_UNSUPPORTED, "batched decode needs Q8 matrices (load with quant = true)");
         if (c.head_dim != 64 && c.head_dim != 128) return fail(HG_ERR_UNSUPPORTED, "batched decode: head_dim 64 or 128");
         if (c.n_experts + 1 > MAX_GROUPS) return fail(HG_ERR_UNSUPPORTED, "batched decode: too many experts");
         if (!batch_ctx_ok(max_ctx))

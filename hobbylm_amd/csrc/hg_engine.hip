@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "../../include/hobby_gpu.h"
+#include "hg_batch.h"
 #include "hg_common.h"
 #include "hg_gguf.h"
 #include "hg_kernels.h"
@@ -110,16 +111,23 @@ namespace {
 
 // The model as parsed and packed on the host, before any device call: every format error of
 // the file surfaces here, in the reference's load order (model.rs:79-131).
+// A matrix as the load keeps it: packed Q8 (quant = true) or f32 rows in F32Mat's layout.
+struct HostMat {
+    PackedQ8 q8;
+    std::vector<float> f32;
+    uint32_t N = 0, K = 0;
+};
 struct HostLayer {
     bool moe = false;
     std::vector<float> attn_norm, q_norm, k_norm, ffn_norm, router, router_p, bias;
-    PackedQ8 qkv, o, gate, up, down, gate_e, up_e, down_e, gate_sh, up_sh, down_sh;
+    HostMat qkv, o, gate, up, down, gate_e, up_e, down_e, gate_sh, up_sh, down_sh;
 };
 struct HostModel {
     hg_config c{};
+    bool quant = true;
     std::vector<HostLayer> layers;
     std::vector<float> token_embd, output_norm, rope_cos, rope_sin;
-    PackedQ8 output;
+    HostMat output;
     uint64_t ref_bytes = 0;
 };
 
@@ -135,6 +143,7 @@ struct hg_kv {
     DevBuf kc, vc;          // [L][n_kv][cap][hd]; V: each layer also [n_kv][hd][vt_stride(cap)]
     DevBuf x, qkv, o, part, scores, a, logits, pv, pi, qa, da, topk_idx, topk_w, order, rec_idx, rec_w, params,
         out_ids, inputs;
+    DevBuf h, y;            // F32 mode: the normed activation, the expert slots' down outputs
     uint32_t inputs_rows = 0;
     StepParams *h_params = nullptr;
     uint32_t *h_ids = nullptr;
@@ -170,8 +179,9 @@ int load_norm(const Gguf &g, const std::string &name, size_t want, std::vector<f
     return HG_OK;
 }
 
-// Gguf::load + Mat::build(.., quant = true) (model.rs:87-89, 121): requantize and pack.
-int load_q8(const Gguf &g, const std::string &name, uint32_t N, uint32_t K, PackedQ8 &dst, HostModel &hm) {
+// Gguf::load + Mat::build(.., quant) (model.rs:87-89, 121, quant.rs:213-222): requantize and
+// pack (quant = true), or keep the (dequantized) f32 rows (quant = false).
+int load_q8(const Gguf &g, const std::string &name, uint32_t N, uint32_t K, HostMat &dst, HostModel &hm) {
     const TensorInfo *t;
     const uint8_t *raw;
     size_t nbytes;
@@ -180,15 +190,24 @@ int load_q8(const Gguf &g, const std::string &name, uint32_t N, uint32_t K, Pack
     if (t->n_elems() != (uint64_t)N * K)
         return fail(HG_ERR_FORMAT, "tensor `" + name + "` has " + std::to_string(t->n_elems()) + " elements, expected " +
                                        std::to_string((uint64_t)N * K));
+    dst.N = N;
+    dst.K = K;
+    if (!hm.quant) {
+        std::vector<float> w;
+        if ((rc = g.load(name, w, g_err))) return rc;
+        permute_f32_rows(w.data(), N, K, dst.f32);
+        hm.ref_bytes += (uint64_t)N * K * 4;
+        return HG_OK;
+    }
     if (K % QK) return fail(HG_ERR_UNSUPPORTED, "Q8_0 needs in_ divisible by 32 (got " + std::to_string(K) + ")");
-    if (t->type == GGML_Q8_0) pack_q8_from_q8_0(raw, N, K, dst);
+    if (t->type == GGML_Q8_0) pack_q8_from_q8_0(raw, N, K, dst.q8);
     else {
         std::vector<float> w;
         rc = g.load(name, w, g_err);
         if (rc) return rc;
-        pack_q8_from_f32(w.data(), N, K, dst);
+        pack_q8_from_f32(w.data(), N, K, dst.q8);
     }
-    hm.ref_bytes += dst.ref_bytes();
+    hm.ref_bytes += dst.q8.ref_bytes();
     return HG_OK;
 }
 
@@ -200,7 +219,7 @@ int validate(const hg_config &c) {
         return bad("head_dim " + std::to_string(c.head_dim) + " not in {32, 64, 128}");
     if (c.n_heads / c.n_kv_heads > 8) return bad("more than 8 query heads per kv head");
     if (c.d_model % QK || c.expert_ffn % QK || c.dense_ffn % QK)
-        return bad("Q8_0 needs in_ divisible by 32");
+        return bad("Q8_0 and the F32 kernels need in_ divisible by 32");
     if (c.n_experts > 256 || c.top_k > 64 || c.top_k > c.n_experts) return bad("expert count out of range");
     if (c.n_dense < c.n_layers && (slots_of(c) == 0 || slots_of(c) > 16)) return bad("more than 16 expert slots");
     if (!c.context_length) return bad("context_length is 0");
@@ -209,7 +228,8 @@ int validate(const hg_config &c) {
 }
 
 // Gguf::open + Config::from_gguf + Model::load on the host (no device call).
-int parse_model(const char *path, HostModel &hm) {
+int parse_model(const char *path, bool quant, HostModel &hm) {
+    hm.quant = quant;
     Gguf g;
     int rc = g.open(path, g_err);
     if (rc) return rc;
@@ -262,25 +282,32 @@ int parse_model(const char *path, HostModel &hm) {
 
 int upload_vec(const std::vector<float> &v, DevBuf &dst) { return dst.upload(v.data(), v.size() * 4); }
 
-// Device residency of a parsed model.  Matrices keep f16 scales if every scale of every matrix
-// is an exact f16 value (GGUF Q8_0 files: the on-disk 34 bytes per block), else all f32.
+// Device residency of a parsed model.  Q8 matrices keep f16 scales if every scale of every
+// matrix is an exact f16 value (GGUF Q8_0 files: the on-disk 34 bytes per block), else all f32.
 int upload_model(HostModel &hm, hg_model *m) {
     m->c = hm.c;
+    m->f32 = !hm.quant;
     m->n_slots = slots_of(hm.c);
     m->ref_bytes = hm.ref_bytes;
-    std::vector<std::pair<PackedQ8 *, DevQ8 *>> mats;
+    std::vector<std::pair<HostMat *, DevQ8 *>> mats;
+    std::vector<std::pair<HostMat *, DevF32 *>> fmats;
     m->layers.resize(hm.layers.size());
     for (size_t i = 0; i < hm.layers.size(); ++i) {
         HostLayer &H = hm.layers[i];
         m->layers[i] = std::make_unique<Layer>();
         Layer &L = *m->layers[i];
         L.moe = H.moe;
-        PackedQ8 *hp[] = {&H.qkv, &H.o, &H.gate, &H.up, &H.down, &H.gate_e, &H.up_e, &H.down_e, &H.gate_sh,
-                          &H.up_sh, &H.down_sh};
+        HostMat *hp[] = {&H.qkv, &H.o, &H.gate, &H.up, &H.down, &H.gate_e, &H.up_e, &H.down_e, &H.gate_sh,
+                         &H.up_sh, &H.down_sh};
         DevQ8 *dp[] = {&L.qkv, &L.o, &L.gate, &L.up, &L.down, &L.gate_e, &L.up_e, &L.down_e, &L.gate_sh,
                        &L.up_sh, &L.down_sh};
-        for (size_t k = 0; k < sizeof hp / sizeof hp[0]; ++k)
-            if (hp[k]->N) mats.emplace_back(hp[k], dp[k]);
+        DevF32 *fp[] = {&L.fqkv, &L.fo, &L.fgate, &L.fup, &L.fdown, &L.fgate_e, &L.fup_e, &L.fdown_e, &L.fgate_sh,
+                        &L.fup_sh, &L.fdown_sh};
+        for (size_t k = 0; k < sizeof hp / sizeof hp[0]; ++k) {
+            if (!hp[k]->N) continue;
+            if (hm.quant) mats.emplace_back(hp[k], dp[k]);
+            else fmats.emplace_back(hp[k], fp[k]);
+        }
         int rc;
         if ((rc = upload_vec(H.attn_norm, L.attn_norm)) || (rc = upload_vec(H.q_norm, L.q_norm)) ||
             (rc = upload_vec(H.k_norm, L.k_norm)) || (rc = upload_vec(H.ffn_norm, L.ffn_norm)) ||
@@ -288,15 +315,22 @@ int upload_model(HostModel &hm, hg_model *m) {
             (rc = upload_vec(H.bias, L.bias)))
             return rc;
     }
-    mats.emplace_back(&hm.output, &m->output);
+    if (hm.quant) mats.emplace_back(&hm.output, &m->output);
+    else fmats.emplace_back(&hm.output, &m->foutput);
     bool all_f16 = true;
-    for (auto &pm : mats) all_f16 = all_f16 && pm.first->f16_exact;
+    for (auto &pm : mats) all_f16 = all_f16 && pm.first->q8.f16_exact;
     for (auto &pm : mats) {
-        pm.first->set_scale_storage(!all_f16);
-        int rc = pm.second->upload(*pm.first);
+        pm.first->q8.set_scale_storage(!all_f16);
+        int rc = pm.second->upload(pm.first->q8);
         if (rc) return rc;
         m->dev_bytes += pm.second->dev_bytes();
-        *pm.first = PackedQ8();
+        pm.first->q8 = PackedQ8();
+    }
+    for (auto &pm : fmats) {
+        int rc = pm.second->upload(pm.first->f32, pm.first->N, pm.first->K);
+        if (rc) return rc;
+        m->dev_bytes += pm.second->w.n;
+        std::vector<float>().swap(pm.first->f32);
     }
     int rc;
     if ((rc = upload_vec(hm.token_embd, m->token_embd)) || (rc = upload_vec(hm.output_norm, m->output_norm)) ||
@@ -317,10 +351,8 @@ int hg_model_load(const char *path, int quant, hg_model **out) {
         if (!out) return fail(HG_ERR_ARG, "out is NULL");
         *out = nullptr;
         if (!path) return fail(HG_ERR_ARG, "path is NULL");
-        if (!quant)
-            return fail(HG_ERR_UNSUPPORTED, "F32 matrices (quant = false) are not supported by the GPU backend");
         auto hm = std::make_unique<HostModel>();
-        int rc = parse_model(path, *hm);
+        int rc = parse_model(path, quant != 0, *hm);
         if (rc) return rc;
         if ((rc = check_device())) return rc;
         auto m = std::make_unique<hg_model>();
@@ -397,7 +429,68 @@ float *layer_v(const hg_kv *kv, uint32_t l) {
     return kv->vc.as<float>() + (size_t)l * v_layer_floats(kv->cap, c.n_kv_heads, c.head_dim);
 }
 
+// The F32 mode's layers (model.rs:164-184 with every Mat::matvec an ops::matvec): the norms,
+// QK-norm + RoPE + append, attention, router and combine of the Q8 step, the products in
+// ops::dot's order.  order: ORDER_DECODE adds the routed experts in rank order (Model::ffn,
+// model.rs:299-311), ORDER_PREFILL in expert-id order (ffn_prefill, model.rs:707-731).
+void enqueue_layers_f32(hg_kv *kv, int order) {
+    const hg_model *m = kv->m;
+    const hg_config &c = m->c;
+    hipStream_t st = kv->st;
+    const uint32_t d = c.d_model;
+    float *x = kv->x.as<float>(), *h = kv->h.as<float>(), *qkv = kv->qkv.as<float>();
+    uint8_t *qa = kv->qa.as<uint8_t>();
+    float *da = kv->da.as<float>();
+    StepParams *p = kv->params.as<StepParams>();
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        const Layer &L = *m->layers[l];
+        mark(kv, P_QKV);   // attn_norm, qkv, QK-norm + RoPE + append (model.rs:164-165, 194-211)
+        launch_rmsnorm_quant(st, true, x, L.attn_norm.as<float>(), c.rms_eps, d, h, qa, da);
+        launch_f32_matvec(st, EPI_STORE, L.fqkv.m, h, qkv, 0, nullptr, nullptr);
+        launch_qk_rope_append(st, c.head_dim, qkv, L.q_norm.as<float>(), L.k_norm.as<float>(), c.rms_eps,
+                              m->rope_cos.as<float>(), m->rope_sin.as<float>(), p, c.n_heads, c.n_kv_heads,
+                              layer_k(kv, l), layer_v(kv, l), kv->cap);
+        for (int part = 0; part < 2; ++part) {
+            mark(kv, part == 0 ? P_ATTN_A : P_ATTN_B);
+            launch_attn(st, true, part, c.head_dim, qkv, L.q_norm.as<float>(), L.k_norm.as<float>(), c.rms_eps,
+                        m->rope_cos.as<float>(), m->rope_sin.as<float>(), p, layer_k(kv, l), layer_v(kv, l), kv->cap,
+                        kv->win, c.n_heads, c.n_kv_heads, attn_splits(kv->win), kv->part.as<float>(),
+                        kv->scores.as<float>(), kv->o.as<float>(), nullptr, da);
+        }
+        mark(kv, P_OPROJ);   // x += attn_output(o) (model.rs:168-171, 233)
+        launch_f32_matvec(st, EPI_RESID, L.fo.m, kv->o.as<float>(), x, 0, nullptr, nullptr);
+        mark(kv, P_ROUTER);
+        launch_rmsnorm_quant(st, true, x, L.ffn_norm.as<float>(), c.rms_eps, d, h, qa, da);
+        if (L.moe) {   // router + top-k (model.rs:270-293), the slots' experts, the combine (model.rs:295-324)
+            launch_ffn_router(st, true, x, L.ffn_norm.as<float>(), c.rms_eps, d, L.router.as<float>(),
+                              L.router_p.as<float>(), L.bias.as<float>(), c.n_experts, c.top_k, c.gating_sigmoid,
+                              c.expert_weights_norm, c.expert_weights_scale, qa, da, kv->topk_idx.as<uint32_t>(),
+                              kv->topk_w.as<float>(), kv->order.as<uint32_t>(),
+                              kv->rec_idx.as<uint32_t>() + (size_t)l * c.top_k,
+                              kv->rec_w.as<float>() + (size_t)l * c.top_k);
+            mark(kv, P_GATEUP);
+            launch_f32_gateup(st, L.fgate_e.m, L.fup_e.m, L.fgate_sh.m, L.fup_sh.m, kv->topk_idx.as<uint32_t>(),
+                              c.top_k, m->n_slots, c.expert_ffn, h, kv->a.as<float>());
+            mark(kv, P_DOWN);
+            launch_f32_down(st, L.fdown_e.m, L.fdown_sh.m, kv->topk_idx.as<uint32_t>(), c.top_k, m->n_slots, d,
+                            c.expert_ffn, kv->a.as<float>(), kv->y.as<float>());
+            launch_b_combine(st, kv->y.as<float>(), kv->topk_w.as<float>(),
+                             order == ORDER_PREFILL ? kv->order.as<uint32_t>() : nullptr, c.top_k, m->n_slots, d, 1, x);
+        } else {   // the dense SwiGLU (model.rs:243-255), x += down(silu(g) * u)
+            mark(kv, P_GATEUP);
+            launch_f32_gateup(st, L.fgate.m, L.fup.m, L.fgate.m, L.fup.m, nullptr, 0, 1, c.dense_ffn, h,
+                              kv->a.as<float>());
+            mark(kv, P_DOWN);
+            launch_f32_matvec(st, EPI_RESID, L.fdown.m, kv->a.as<float>(), x, 0, nullptr, nullptr);
+        }
+    }
+}
+
 void enqueue_layers(hg_kv *kv, int order) {
+    if (kv->m->f32) {
+        enqueue_layers_f32(kv, order);
+        return;
+    }
     const hg_model *m = kv->m;
     const hg_config &c = m->c;
     hipStream_t st = kv->st;
@@ -469,10 +562,14 @@ void enqueue_tail(hg_kv *kv) {
     const uint32_t valid = c.vocab_size < 50257 ? c.vocab_size : 50257;
     mark(kv, P_NORM);
     launch_rmsnorm_quant(kv->st, kv->exact, kv->x.as<float>(), m->output_norm.as<float>(), c.rms_eps, c.d_model,
-                         nullptr, kv->qa.as<uint8_t>(), kv->da.as<float>());
+                         m->f32 ? kv->h.as<float>() : nullptr, kv->qa.as<uint8_t>(), kv->da.as<float>());
     mark(kv, P_LMHEAD);
-    launch_matvec(kv->st, ORDER_DECODE, EPI_LOGITS, m->output.m, kv->qa.as<uint8_t>(), kv->da.as<float>(),
-                  kv->logits.as<float>(), kv->lm_threads, valid, kv->pv.as<float>(), kv->pi.as<uint32_t>());
+    if (m->f32)
+        launch_f32_matvec(kv->st, EPI_LOGITS, m->foutput.m, kv->h.as<float>(), kv->logits.as<float>(), valid,
+                          kv->pv.as<float>(), kv->pi.as<uint32_t>());
+    else
+        launch_matvec(kv->st, ORDER_DECODE, EPI_LOGITS, m->output.m, kv->qa.as<uint8_t>(), kv->da.as<float>(),
+                      kv->logits.as<float>(), kv->lm_threads, valid, kv->pv.as<float>(), kv->pi.as<uint32_t>());
     mark(kv, P_ARGMAX);
     launch_argmax_final(kv->st, kv->pv.as<float>(), kv->pi.as<uint32_t>(), kv->n_part, kv->params.as<StepParams>(),
                         kv->out_ids.as<uint32_t>());
@@ -621,6 +718,8 @@ int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out) 
         kv->win = kv->cap;
         if (kv->exact && pv_ring_slots(kv->cap) < 2)
             return fail(HG_ERR_UNSUPPORTED, "a reference-order cache holds at most 32768 positions");
+        if (m->f32 && !kv->exact)
+            return fail(HG_ERR_UNSUPPORTED, "the F32 mode runs the reference-order attention only (no HG_KV_FAST)");
         HIP_TRY(hipStreamCreateWithFlags(&kv->st, hipStreamNonBlocking));
         const size_t kvsz = (size_t)c.n_layers * c.n_kv_heads * kv->cap * c.head_dim * 4;
         int rc;
@@ -631,7 +730,10 @@ int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out) 
         const uint32_t maxk = std::max(std::max(c.d_model, qd), std::max(c.dense_ffn, c.expert_ffn));
         const uint32_t maxnc = div_up(maxk / QK, 4);
         const uint32_t ffw = std::max(c.dense_ffn, c.expert_ffn) * std::max(m->n_slots, 1u);
-        kv->n_part = matvec_blocks(c.vocab_size, kv->lm_threads);
+        kv->n_part = m->f32 ? f32_matvec_blocks(c.vocab_size) : matvec_blocks(c.vocab_size, kv->lm_threads);
+        if (m->f32 && ((rc = kv->h.alloc((size_t)c.d_model * 4)) ||
+                       (rc = kv->y.alloc((size_t)std::max(m->n_slots, 1u) * c.d_model * 4))))
+            return rc;
         if ((rc = kv->x.alloc(c.d_model * 4)) || (rc = kv->qkv.alloc((size_t)(qd + 2 * kvd) * 4)) ||
             (rc = kv->o.alloc((size_t)qd * 4)) ||
             (rc = kv->part.alloc((size_t)c.n_heads * attn_splits(kv->cap) * (c.head_dim + 2) * 4)) ||
@@ -1007,6 +1109,7 @@ int hg_generate_diffusion(const hg_model *m, const uint32_t *prompt, uint32_t n_
                           uint32_t eos, uint32_t *out_ids, uint32_t *n_out) {
     return guard([&]() -> int {
         if (!m || !opts || !n_out) return fail(HG_ERR_ARG, "NULL argument");
+        if (m->f32) return fail(HG_ERR_UNSUPPORTED, "diffusion decoding needs Q8 matrices (load with quant = true)");
         *n_out = 0;
         if (n_prompt > 0 && !prompt) return fail(HG_ERR_ARG, "prompt is NULL");
         if (n_prompt == 0) return HG_OK;

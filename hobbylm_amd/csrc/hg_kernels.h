@@ -15,6 +15,7 @@ struct LaunchTimer {
     void add(hipEvent_t a, hipEvent_t b) { ev.emplace_back(a, b); tags.push_back(cls); }
 };
 void set_launch_timer(LaunchTimer *t);
+LaunchTimer *launch_timer();   // this thread's, or null
 // First launch error recorded on this thread since the last take (hipSuccess if none), with
 // the kernel it concerns; taking clears it.
 hipError_t take_launch_error(std::string &msg);

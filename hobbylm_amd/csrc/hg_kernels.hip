@@ -2025,6 +2025,7 @@ __global__ __launch_bounds__(1024) void k_ffn_down(Q8Mat Wd, Q8Mat Sd, const uin
 // pair recorded by its own dispatch (hipExtLaunchKernelGGL): the kernel's execution time.
 thread_local LaunchTimer *g_timer = nullptr;
 void set_launch_timer(LaunchTimer *t) { g_timer = t; }
+LaunchTimer *launch_timer() { return g_timer; }
 
 // The first launch error since the last take: a launch HIP rejected (its error code) or one
 // the launch helpers refused on the host (hipErrorInvalidConfiguration).

@@ -11,6 +11,7 @@
 
 #include "../../include/hobby_gpu.h"
 #include "hg_common.h"
+#include "hg_f32.h"
 #include "hg_gguf.h"
 
 namespace hg {
@@ -80,10 +81,26 @@ struct DevQ8 {
     uint64_t dev_bytes() const { return qs.n + sc.n; }
 };
 
+// An F32 matrix (the F32 mode's Mat::Owned) in F32Mat's permuted row layout.
+struct DevF32 {
+    DevBuf w;
+    F32Mat m{};
+    int upload(const std::vector<float> &perm, uint32_t N, uint32_t K) {
+        int rc = w.upload(perm.data(), perm.size() * 4);
+        if (rc) return rc;
+        m.w = w.as<float>();
+        m.N = N;
+        m.K = K;
+        return HG_OK;
+    }
+};
+
 struct Layer {
     bool moe = false;
     DevBuf attn_norm, q_norm, k_norm, ffn_norm, router, router_p, bias;
     DevQ8 qkv, o, gate, up, down, gate_e, up_e, down_e, gate_sh, up_sh, down_sh;
+    // the F32 mode's matrices (loaded with quant = false; the Q8 ones are then empty)
+    DevF32 fqkv, fo, fgate, fup, fdown, fgate_e, fup_e, fdown_e, fgate_sh, fup_sh, fdown_sh;
 };
 
 }  // namespace hg
@@ -93,6 +110,8 @@ struct hg_model {
     std::vector<std::unique_ptr<hg::Layer>> layers;
     hg::DevBuf token_embd, output_norm, rope_cos, rope_sin;
     hg::DevQ8 output;
+    hg::DevF32 foutput;
+    bool f32 = false;   // loaded with quant = false: F32 matrices, ops::dot arithmetic
     uint64_t ref_bytes = 0, dev_bytes = 0;
     uint32_t n_slots = 0;  // routed top-k + shared expert slot
 };

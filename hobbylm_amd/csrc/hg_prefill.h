@@ -14,7 +14,7 @@ struct PrefillWork {
 };
 
 // Whether the batched prompt path runs prompts of a cache of `cap` positions with this model
-// (head size, expert count, attention window and GEMM tile limits).
+// (Q8 matrices, head size, expert count, attention window and GEMM tile limits).
 bool prefill_batched_ok(const hg_model *m, uint32_t cap);
 
 // Prompt rows inputs[0 .. tn) (host, d floats each) at positions base .. base + tn - 1 of a

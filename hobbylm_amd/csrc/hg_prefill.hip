@@ -318,6 +318,7 @@ void enqueue_chunk(const hg_model *m, PrefillWork &w, const Shapes &s, hipStream
 
 bool prefill_batched_ok(const hg_model *m, uint32_t cap) {
     const hg_config &c = m->c;
+    if (m->f32) return false;   // the prompt GEMMs are Q8 (the F32 mode runs one step per row)
     if (c.head_dim != 32 && c.head_dim != 64 && c.head_dim != 128) return false;
     const uint32_t rep = c.n_heads / c.n_kv_heads;
     if (c.head_dim == 32 && rep != 1 && rep != 2 && rep != 4 && rep != 8) return false;

@@ -77,6 +77,9 @@ PRESETS: Dict[str, Shape] = {
     "tiny_long": Shape(128, 3, 1, 4, 2, 32, 256, 96, 8, 2, 1, 1000, context_length=4096),
     "tiny_noshared": Shape(64, 2, 1, 2, 1, 32, 128, 64, 6, 3, 0, 300, context_length=256,
                            rope_theta=1e6),
+    # one routed expert and no shared one: the decode step's rank-order and the prompt path's
+    # expert-id-order accumulations coincide
+    "tiny_top1": Shape(64, 2, 1, 2, 1, 32, 128, 64, 6, 1, 0, 300, context_length=256),
     # the other router forms: softmax gating with renormalized weights, and sigmoid gating with
     # renormalized and scaled weights
     "tiny_softmax": Shape(128, 2, 1, 4, 2, 32, 256, 96, 8, 2, 1, 1000, context_length=512,

@@ -71,7 +71,12 @@ const char *hg_last_error(void);
  * Config::from_gguf (config.rs:35-97), Model::load (model.rs:79-131).  quant != 0 keeps
  * every matrix as Q8_0 after the load-time requantization of Q8Tensor::quantize
  * (quant.rs:78-102), from any matrix type Gguf::load reads (F32, F16, Q5_0, Q8_0, Q4_K,
- * Q6_K); quant == 0 (F32 matrices) returns HG_ERR_UNSUPPORTED.  The file is parsed and
+ * Q6_K); quant == 0 keeps every matrix as f32 (Mat::Owned, quant.rs:198-222) and applies it
+ * with ops::matvec / ops::matmul (ops.rs:40-71: ops::dot per output, ops.rs:7-36) -- in that
+ * mode hg_forward, hg_forward_x, hg_prefill (one step per prompt row), the generate entry
+ * points and hg_last_routing work, with reference-order caches only (HG_KV_FAST is refused),
+ * while the batched prompt path (hg_run_block, hg_forward_bidir, hg_generate_diffusion) and
+ * batched decode (hg_batch_*) return HG_ERR_UNSUPPORTED.  The file is parsed and
  * checked on the host before any device call, so format errors are reported (HG_ERR_IO,
  * HG_ERR_FORMAT, HG_ERR_UNSUPPORTED) on a machine without a GPU too.  The tokenizer is not
  * built: token ids cross this boundary. */

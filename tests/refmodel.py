@@ -91,9 +91,10 @@ def actq(x: np.ndarray) -> np.ndarray:
 
 
 class RefModel:
-    def __init__(self, path):
+    def __init__(self, path, quant=True):
         g = GGUF(path)
         self.g = g
+        self.quant = quant   # False: Mat::Owned, no activation quantization before a product
         a = g.meta["general.architecture"]
         m = lambda k, d=None: g.meta.get(f"{a}.{k}", d)
         self.d = m("embedding_length")
@@ -116,7 +117,7 @@ class RefModel:
         return x / np.sqrt(np.mean(x * x) + self.eps) * w
 
     def mv(self, W, x):
-        return W @ actq(x)
+        return W @ (actq(x) if self.quant else x)
 
     def rope(self, v, pos):
         half = self.hd // 2

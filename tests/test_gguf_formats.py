@@ -151,10 +151,10 @@ def _write(tmp_path, name, data):
     return str(p)
 
 
-def _load_rc(hg, path):
+def _load_rc(hg, path, quant=1):
     import ctypes as C
     h = C.c_void_p()
-    rc = hg.lib().hg_model_load(str(path).encode(), 1, C.byref(h))
+    rc = hg.lib().hg_model_load(str(path).encode(), quant, C.byref(h))
     if rc == 0:
         hg.lib().hg_model_free(h)
     return rc, hg.lib().hg_last_error().decode()
@@ -199,6 +199,8 @@ def test_product_load_errors_match_reference_messages(orc, tmp_path):
         path = _write(tmp_path, name, data)
         rc, err = _load_rc(hg, path)
         assert rc == code and re.search(msg, err), (name, rc, err)
+        rc, err = _load_rc(hg, path, quant=0)   # the F32 mode parses the same file first
+        assert rc == code and re.search(msg, err), (name, "quant=0", rc, err)
         # the oracle (the reference's messages) fails on the same file
         with pytest.raises(orc.OracleError, match=msg):
             orc.Model(path)
@@ -210,4 +212,6 @@ def test_product_load_errors_match_reference_messages(orc, tmp_path):
     # arguments
     import ctypes as C
     assert hg.lib().hg_model_load(None, 1, C.byref(C.c_void_p())) == -4
-    assert hg.lib().hg_model_load(tiny.encode(), 0, C.byref(C.c_void_p())) == -3
+    # the F32 mode (quant = 0) parses the same well-formed file and then needs the device too
+    rc, err = _load_rc(hg, tiny, quant=0)
+    assert rc == 0 or (rc == -5 and "device" in err.lower()), (rc, err)

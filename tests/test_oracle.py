@@ -371,6 +371,50 @@ def test_weight_bytes(orc, tiny_path):
     mats += c.n_dense * 3 * c.dense_ffn * c.d_model
     mats += (c.n_layers - c.n_dense) * (c.n_experts + 1) * 3 * c.expert_ffn * c.d_model
     assert m.weight_bytes() == mats + mats // 32 * 4  # 1 B per weight + one f32 scale per 32
+    assert orc.Model(tiny_path, quant=False).weight_bytes() == 4 * mats  # Mat::Owned: f32 per weight
+
+
+# ---------------------------------------------------------------- F32 mode (quant = false)
+def test_f32_mode_vs_float64(orc, tiny_path):
+    """Engine::load(path, quant = false): every product is ops::dot over the dequantized f32
+    weights, with no activation quantization.  The F32 oracle follows the float64 model without
+    activation quantization to ~1e-7 of the logit range, and stays far (~1e-2) from the one
+    that quantizes activations before each product."""
+    from refmodel import RefModel
+    toks = gs.prompt_ids(14, 10, 1000)
+    devs = {}
+    for ref_quant in (False, True):
+        m = orc.Model(tiny_path, quant=False)
+        kv = m.new_cache()
+        ref = RefModel(tiny_path, quant=ref_quant)
+        dev = 0.0
+        for pos, t in enumerate(toks):
+            got = m.forward(int(t), pos, kv)
+            want = ref.forward(int(t), pos)
+            dev = max(dev, float(np.max(np.abs(got - want))) / float(want.max() - want.min()))
+        devs[ref_quant] = dev
+    assert devs[False] <= 2e-6, devs
+    assert devs[True] > 1000 * devs[False], devs
+
+
+def test_f32_mode_prompt_equals_steps_with_one_expert(orc):
+    """With one routed expert and no shared one, ffn_prefill's expert-id order and ffn's rank
+    order add the same single term, and in the F32 mode Mat::matmul is Mat::matvec per row
+    (ops.rs:57-71 against 40-53): the prompt's logits and cache rows equal stepwise forwards
+    bit for bit.  (The Q8 mode differs: Q8Tensor::matmul's order is not matvec's.)"""
+    path = gs.synth_path("tiny_top1", 15, norm_jitter=0.1)
+    toks = gs.prompt_ids(16, 11, 300)
+    same = {}
+    for quant in (False, True):
+        m = orc.Model(path, quant=quant)
+        kv1, kv2 = m.new_cache(), m.new_cache()
+        emb = np.stack([m.token_embedding(int(t)) for t in toks])
+        lp = m.prefill(emb, kv1)
+        for pos, t in enumerate(toks):
+            lf = m.forward(int(t), pos, kv2)
+        same[quant] = (lp.view(np.uint32) == lf.view(np.uint32)).all() and all(
+            (kv1.read(l)[0].view(np.uint32) == kv2.read(l)[0].view(np.uint32)).all() for l in range(m.cfg.n_layers))
+    assert same[False] and not same[True], same
 
 
 # ---------------------------------------------------------------- load errors (gguf.rs / config.rs)
