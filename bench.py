@@ -39,16 +39,16 @@ METRIC = "500M Q8_0 decode tok/s (bs1, ctx2k) + achieved HBM GB/s vs peak"
 DOM_KERNEL = "k_attn_softmax_pv_res<64, false>"
 
 
-def algorithmic_bytes(cfg, ctx):
+def algorithmic_bytes(cfg, ctx, f32=False):
     """HBM bytes one decode step must read/write at context length ctx (positions 0..ctx-1).
 
-    Matrices at 34 B per 32 Q8_0 weights: QKV and attn_output every layer, the dense FFN in
-    the leading dense layers, top_k routed + the shared expert's gate/up/down in MoE layers,
-    the lm_head; the F32 router and bias, the norm gains, one F32 embedding row, the K/V row
-    appended per layer and the K/V rows read per layer."""
+    Matrices at 34 B per 32 Q8_0 weights (4 B per weight in the F32 mode): QKV and attn_output
+    every layer, the dense FFN in the leading dense layers, top_k routed + the shared expert's
+    gate/up/down in MoE layers, the lm_head; the F32 router and bias, the norm gains, one F32
+    embedding row, the K/V row appended per layer and the K/V rows read per layer."""
     d, L, hd = cfg.d_model, cfg.n_layers, cfg.head_dim
     qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
-    q8 = lambda n, k: n * k // 32 * 34
+    q8 = (lambda n, k: n * k * 4) if f32 else (lambda n, k: n * k // 32 * 34)
     b = L * (q8(qd + 2 * kvd, d) + q8(d, qd))
     b += cfg.n_dense * (2 * q8(cfg.dense_ffn, d) + q8(d, cfg.dense_ffn))
     n_moe = L - cfg.n_dense
@@ -365,6 +365,67 @@ def prefill_bench(args):
     print(json.dumps(out))
 
 
+def f32_bench(args):
+    """The F32 matrix mode (Engine::load(path, quant = false): f32 matrices, ops::dot) on the
+    default workload's window: the 500M model, a 16-row prompt, greedy decode to position 1791,
+    `warmup` steps, then `steps` timed greedy steps (median of `repeats`).  Parity: the oracle's
+    F32 model continues from the GPU's cache at the window's start and must pick the same
+    greedy tokens for the first --f32-parity-steps steps."""
+    import torch
+    import hobbylm_amd as hg
+    from hobbylm_amd import gguf_synth as gs
+    steps, warmup = args.steps, args.warmup
+    start = CTX_END - steps
+    path = gs.synth_path("500M", 1)
+    m = hg.Model(path, quant=False)
+    cfg = m.cfg
+    kv = m.new_cache()
+    emb = np.stack([m.token_embedding(int(t)) for t in gs.prompt_ids(1, N_PROMPT, 50257)])
+    _, first = m.prefill(emb, kv)
+    pre = m.decode_greedy(first, start - warmup - N_PROMPT, kv)
+    warm = m.decode_greedy(int(pre[-1]), warmup, kv)
+    snap = [kv.read(l) for l in range(cfg.n_layers)]
+    times = []
+    for r in range(max(1, args.repeats)):
+        if r:
+            kv.truncate(start)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ids_r = m.decode_greedy(int(warm[-1]), steps, kv)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        if r == 0:
+            ids = ids_r
+        elif list(ids_r) != list(ids):
+            sys.exit("repeated window produced different tokens")
+    dt = float(np.median(times))
+    import oracle
+    om = oracle.Model(path, quant=False)
+    okv = om.new_cache()
+    okv.load(np.stack([s_[0] for s_ in snap]), np.stack([s_[1] for s_ in snap]))
+    del snap
+    tok, ok, n_chk = int(warm[-1]), 0, min(steps, args.f32_parity_steps)
+    for i in range(n_chk):
+        lg = om.forward(tok, start + i, okv)
+        tok = int(np.argmax(lg[:50257]))
+        ok += tok == int(ids[i])
+    by = algorithmic_bytes(cfg, CTX_END - steps / 2.0, f32=True)
+    out = {
+        "metric": "F32-mode decode tok/s (500M, f32 matrices, bs1, ctx 2k) + achieved HBM GB/s vs peak",
+        "value": round(steps / dt, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(dt * 1e3 / steps, 4), "higher_is_better": True,
+        "repeats_ms_per_step": [round(t * 1e3 / steps, 4) for t in times], "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 (ops::dot order)", "data": "synthetic: random-init 500M-shaped Q8_0 GGUF (seed 1) loaded as f32",
+        "config": {"workload": "greedy decode positions 1792..2047 after a 16-token prompt, default cache",
+                   "model": "hobbylm-500M-synthetic", "global_batch": 1, "seq_len": 2048, "parallelism": "none (1 GPU)"},
+        "step_bandwidth": {"algorithmic_bytes_per_token": by, "achieved_GBps": round(by * steps / dt / 1e9, 1),
+                           "peak_GBps": PEAK_HBM / 1e9, "frac": round(by * steps / dt / PEAK_HBM, 4)},
+        "parity": {"greedy_tokens_identical": f"{ok}/{n_chk}",
+                   "oracle": "C restatement of hobby-rs's F32 decode path, continuing from the GPU's cache"},
+    }
+    print(json.dumps(out))
+
+
 COPY_BYTES = 256 * 2**20
 
 
@@ -450,6 +511,8 @@ def main():
                     help="the batched workload: 32 ragged sequences over a paged cache (its own JSON line)")
     ap.add_argument("--batch", type=int, default=32, help="sequences of --batched")
     ap.add_argument("--prefill", type=int, metavar="ROWS", help="prompt-processing measurement of ROWS rows instead")
+    ap.add_argument("--f32", action="store_true", help="the F32 matrix mode (quant = false) on the decode window instead")
+    ap.add_argument("--f32-parity-steps", type=int, default=8, help="oracle-checked steps of --f32")
     ap.add_argument("--prefill-cpu-rows", type=int, default=128, help="oracle-timed rows of --prefill")
     ap.add_argument("--parity-steps", type=int, default=3, help="oracle-checked steps per sequence (--batched)")
     ap.add_argument("--contiguous-pages", action="store_true",
@@ -483,6 +546,11 @@ def main():
         if args.gpus != 1:
             sys.exit("bench.py measures one GPU")
         batched(args)
+        return
+    if args.f32:
+        if args.gpus != 1:
+            sys.exit("bench.py measures one GPU")
+        f32_bench(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this decode path does not shard (--gpus {args.gpus} requested)",
