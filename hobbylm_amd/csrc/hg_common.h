@@ -37,8 +37,10 @@ struct StepParams {
     uint32_t feedback;  // 1: argmax writes token = next and pos += 1 for the next replay
     uint32_t embed;     // 1: x = token_embd[token]; 0: x already holds the input row
     uint32_t base;      // first position of the current prefill batch
-    uint32_t pad[2];
+    uint32_t err;       // set by a bounded wait of the attention kernels that ran out (host: HG_ERR_DEVICE)
+    uint32_t spin_cap;  // polls a bounded wait makes before giving up (0: SPIN_CAP_DEFAULT)
 };
+constexpr uint32_t SPIN_CAP_DEFAULT = 1u << 22;
 
 // Per-row pointer offsets of a batched launch of a one-row kernel (blockIdx.x = row), in
 // elements: x / h rows, quantized chunk bytes, scales, top-k entries, routing records.  All

@@ -648,7 +648,21 @@ int set_params(hg_kv *kv, uint32_t token, uint32_t pos, uint32_t feedback, uint3
     hp.feedback = feedback;
     hp.embed = embed;
     hp.base = base;
+    const char *sc = getenv("HG_SPIN_CAP");   // (tests: a tiny cap drives the bounded waits' error path)
+    hp.spin_cap = sc ? (uint32_t)strtoul(sc, nullptr, 10) : 0u;
     HIP_TRY(hipMemcpyAsync(kv->params.p, kv->h_params, sizeof(StepParams), hipMemcpyHostToDevice, kv->st));
+    return HG_OK;
+}
+
+// Enqueue the read-back of the step parameters (before the stream sync that ends a call) and,
+// after it, the verdict of the attention kernels' bounded waits (StepParams::err).
+int fetch_params(hg_kv *kv) {
+    HIP_TRY(hipMemcpyAsync(kv->h_params, kv->params.p, sizeof(StepParams), hipMemcpyDeviceToHost, kv->st));
+    return HG_OK;
+}
+int waits_ok(const hg_kv *kv) {
+    if (kv->h_params->err)
+        return fail(HG_ERR_DEVICE, "a softmax/P.V kernel's wait ran out of polls: the step's results are void");
     return HG_OK;
 }
 
@@ -657,7 +671,10 @@ int finish(hg_kv *kv, float *logits, uint32_t *next) {
     if (logits)
         HIP_TRY(hipMemcpyAsync(kv->h_logits, kv->logits.p, (size_t)c.vocab_size * 4, hipMemcpyDeviceToHost, kv->st));
     HIP_TRY(hipMemcpyAsync(kv->h_ids, kv->out_ids.p, 4, hipMemcpyDeviceToHost, kv->st));
+    int rc = fetch_params(kv);
+    if (rc) return rc;
     HIP_TRY(hipStreamSynchronize(kv->st));
+    if ((rc = waits_ok(kv))) return rc;
     if (logits) memcpy(logits, kv->h_logits, (size_t)c.vocab_size * 4);
     if (next) *next = kv->h_ids[0];
     return HG_OK;
@@ -897,7 +914,9 @@ int hg_decode_greedy(const hg_model *m, hg_kv *kv, uint32_t first_token, uint32_
         for (uint32_t i = 0; i < n_steps; ++i)
             if ((rc = run(kv, graph_for(kv, kv->g_decode, pos + i), enqueue_decode))) return rc;
         HIP_TRY(hipMemcpyAsync(kv->h_ids, kv->out_ids.p, (size_t)n_steps * 4, hipMemcpyDeviceToHost, kv->st));
+        if ((rc = fetch_params(kv))) return rc;
         HIP_TRY(hipStreamSynchronize(kv->st));
+        if ((rc = waits_ok(kv))) return rc;
         memcpy(out_ids, kv->h_ids, (size_t)n_steps * 4);
         kv->len = pos + n_steps;
         return HG_OK;
@@ -954,7 +973,9 @@ int hg_generate(const hg_model *m, hg_kv *kv, const uint32_t *prompt, uint32_t n
                 ++fw_chunk;
             }
             HIP_TRY(hipMemcpyAsync(kv->h_ids, picks + j0, (size_t)(it - j0) * 4, hipMemcpyDeviceToHost, kv->st));
+            if ((rc = fetch_params(kv))) return rc;
             HIP_TRY(hipStreamSynchronize(kv->st));
+            if ((rc = waits_ok(kv))) return rc;
             for (uint32_t j = 0; j < it - j0; ++j) {
                 const uint32_t t = kv->h_ids[j];
                 if (t == eos) {   // lib.rs:143-145
@@ -1629,6 +1650,9 @@ int hg_attention_decode(const float *q, const float *k, const float *v, const fl
                 return fail(HG_ERR_UNSUPPORTED, "head_dim not supported");
         HIP_TRY(hipGetLastError());
         HIP_TRY(hipDeviceSynchronize());
+        StepParams back{};
+        HIP_TRY(hipMemcpy(&back, dp.p, sizeof back, hipMemcpyDeviceToHost));
+        if (back.err) return fail(HG_ERR_DEVICE, "a softmax/P.V kernel's wait ran out of polls");
         HIP_TRY(hipMemcpy(out, dout.p, (size_t)qd * 4, hipMemcpyDeviceToHost));
         HIP_TRY(hipMemcpy(kh.data(), dk.p, kh.size() * 4, hipMemcpyDeviceToHost));
         HIP_TRY(hipMemcpy(vh.data(), dv.p, vh.size() * 4, hipMemcpyDeviceToHost));

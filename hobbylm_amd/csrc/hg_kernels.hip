@@ -785,6 +785,27 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
 // is bounded: tile k waits only for tile k - R to be consumed, the chain only for tile k to be
 // produced.  Producers start their first V fetch before the sum.  Also writes o and its
 // quantization for attn_output (quant.rs:111-123).
+// The bounded LDS waits of the softmax + P.V kernels: a wait polls at most cap times
+// (StepParams::spin_cap, 0 = SPIN_CAP_DEFAULT, ~0.1 s of s_sleep), then records the failure in
+// StepParams::err (a vector atomic) and gives up; the kernel runs on to its normal exit with
+// whatever the LDS holds, and the host reports HG_ERR_DEVICE for the step.
+struct SpinGuard {
+    uint32_t cap;
+    uint32_t *err;
+    __device__ explicit SpinGuard(const StepParams *p)
+        : cap(p->spin_cap ? p->spin_cap : SPIN_CAP_DEFAULT), err(const_cast<uint32_t *>(&p->err)) {}
+    // One more poll of a wait that has polled `it` times: true after a sleep, false (error
+    // recorded) once the cap is reached.
+    __device__ bool more(uint32_t &it) const {
+        if (++it <= cap) {
+            __builtin_amdgcn_s_sleep(1);
+            return true;
+        }
+        atomicOr(err, 1u);
+        return false;
+    }
+};
+
 // Workgroup -> (head h, output quarter q) of the softmax + P.V kernels (1-D grid of
 // n_heads * nq).  Workgroups are dealt to the 8 XCDs round-robin by linear id, each XCD with its
 // own L2; the rep query heads of a kv group read the same V slice, so the rep workgroups of one
@@ -846,6 +867,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
     pv_head_quarter(blockIdx.x, n_heads, n_kv, HD / D, &h, &q);
     const uint32_t rep = n_heads / n_kv, g = h / rep;
     const uint32_t pos = p->pos, n = pos + 1;
+    const SpinGuard sg(p);
     const uint32_t R = pv_ring_slots(win);
     float *e = lds;                                     // [win] e_t, then p_t
     float *ring = lds + (size_t)div_up(win, 4) * 4;     // [R][D][TP]
@@ -911,9 +933,11 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
     if (pw >= 0) {
         for (uint32_t k = pw; k < ntiles; k += C::NP) {
             if (k != (uint32_t)pw) fetch(k);
-            if (k >= R)
+            if (k >= R) {
+                uint32_t it = 0;
                 while (__hip_atomic_load(&done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < k - R + 1)
-                    __builtin_amdgcn_s_sleep(1);
+                    if (!sg.more(it)) break;
+            }
             float *slot = ring + (size_t)(k % R) * C::SLOT;
 #pragma unroll
             for (uint32_t i = 0; i < C::NI; ++i) {
@@ -937,8 +961,9 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv(const float *__restrict
         float o = 0.0f;
         const uint32_t di = lane;
         auto ready_wait = [&](uint32_t k) {
+            uint32_t it = 0;
             while (__hip_atomic_load(&ready[k % R], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != k + 1)
-                __builtin_amdgcn_s_sleep(1);
+                if (!sg.more(it)) break;
         };
         auto rowp = [&](uint32_t k) {
             return reinterpret_cast<const v4f *>(ring + (size_t)(k % R) * C::SLOT + di * TP);
@@ -1120,6 +1145,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     pv_head_quarter(blockIdx.x, n_heads, n_kv, HD / D, &h, &q);
     const uint32_t rep = n_heads / n_kv, g = h / rep;
     const uint32_t pos = p->pos, n = pos + 1;
+    const SpinGuard sg(p);
     const uint32_t rc = pv_res_rows(win), TPC = rc + 4;   // row stride 4 mod 32 banks
     float *e = lds;                                         // [rc]  e_t
     float *P = lds + rc;                                    // [D][TPC]  V, then the products
@@ -1189,8 +1215,9 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     }
     float inv0 = 0.0f;   // wave 0: 1 / sum
     if (wave < 4) {   // sum += e_t in index order, once every wave's e_t are written
+        uint32_t it = 0;
         while (__hip_atomic_load(&arrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 8u)
-            __builtin_amdgcn_s_sleep(1);
+            if (!sg.more(it)) break;
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         // terms per lane by context (4 waves x 64 lanes x EPT >= n; a longer sum would fall back
         // to the one-lane chain inside block_seq_sum).  Two layouts per instantiation: more
@@ -1211,18 +1238,19 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
         // groups pw, pw + 6, ... (pw = 0..5) past the first block; lane l -> element l / 16,
         // positions 4 (l % 16) .. + 3 of the group.  The first group alone (the chain needs it
         // soon), then the others together: their reads first, one release, one flag update.
+        uint32_t it = 0;
         while (__hip_atomic_load(&inv_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0u)
-            __builtin_amdgcn_s_sleep(1);
+            if (!sg.more(it)) break;
         const float inv = s_inv;
         const uint32_t di = (uint32_t)lane >> 4, tq = (uint32_t)lane & 15;
         const uint32_t pw = (uint32_t)wave - (wave < 4 ? 1 : 2), ngp = 4 * nblk;   // (past the context: -0)
         auto vwait = [&](uint32_t r, uint32_t w0, uint32_t w1) {   // V waves w0..w1 past round r
+            uint32_t it = 0;
             for (;;) {
                 uint32_t v0 = __hip_atomic_load(&vdone[w0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 for (uint32_t w = w0 + 1; w <= w1; ++w)
                     v0 = min(v0, __hip_atomic_load(&vdone[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-                if (v0 > r) break;
-                __builtin_amdgcn_s_sleep(1);
+                if (v0 > r || !sg.more(it)) break;
             }
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         };
@@ -1299,13 +1327,13 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     }
     if (wave == 0) {   // the first block's products (groups 0..3), by the chain wave itself
         const uint32_t di = (uint32_t)lane >> 4, tq = (uint32_t)lane & 15;
+        uint32_t it = 0;
         for (;;) {   // round 0 of every V wave in
             uint32_t v0 = __hip_atomic_load(&vdone[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             v0 = min(v0, __hip_atomic_load(&vdone[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
             v0 = min(v0, __hip_atomic_load(&vdone[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
             v0 = min(v0, __hip_atomic_load(&vdone[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-            if (v0 > 0) break;
-            __builtin_amdgcn_s_sleep(1);
+            if (v0 > 0 || !sg.more(it)) break;
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         v4f ev[4], vv[4];
@@ -1339,6 +1367,9 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
         const float *prow = P + r4 * TPC + 4 * li;
         uint64_t known = 0xf;   // ready word kw as last read (block 0: this wave's own products)
         uint32_t kw = 0;
+        // (not polled against the cap: ready bits are only ever set, and every producer wave
+        // runs to its end through bounded waits setting all of its groups' bits, so this wait
+        // always ends; a cap here cost 0.8 us per launch)
         auto block_wait = [&](uint32_t b) {   // groups 4 b .. 4 b + 3: bits 4 b % 64 .. of word b / 16
             const uint32_t wd = LONG ? b >> 4 : 0, sh = (4 * b) & 63;
             if (LONG && wd != kw) {

@@ -185,3 +185,34 @@ def test_default_capacity_cache_bit_exact(hg, orc, start):
     gk, gv = gkv.read(c.n_layers - 1)
     ok, ov = okv.read(c.n_layers - 1)
     assert _bits_equal(gk, ok) and _bits_equal(gv, ov)
+
+
+def test_bounded_waits_report_an_error(hg, orc, monkeypatch):
+    """The softmax/P.V kernels' LDS waits are bounded (StepParams::spin_cap polls, HG_SPIN_CAP
+    overrides the default for tests).  With a cap of one poll the V waves' wait for the exact
+    sum (~1 us) gives up: the kernels still run to their normal exit and the call returns
+    HG_ERR_DEVICE (-5) instead of results.  With the default cap the same model then decodes
+    bit-identically to the oracle on a fresh cache."""
+    path = gs.synth_path("tiny", 31, norm_jitter=0.1)
+    gm, om = hg.Model(path), orc.Model(path)
+    toks = gs.prompt_ids(32, 6, 1000)
+    emb = np.stack([om.token_embedding(int(t)) for t in toks])
+    monkeypatch.setenv("HG_SPIN_CAP", "1")
+    kv = gm.new_cache()
+    codes = []
+    for i, t in enumerate(toks):
+        try:
+            gm.forward(int(t), kv.len, kv)
+            codes.append(0)
+        except hg.HgError as e:
+            codes.append(e.code)
+    assert codes and set(codes) <= {0, -5} and -5 in codes, codes
+    monkeypatch.delenv("HG_SPIN_CAP")
+    gkv, okv = gm.new_cache(), om.new_cache()
+    gl, _ = gm.prefill(emb, gkv)
+    ol = om.prefill(emb, okv)
+    assert _bits_equal(gl, ol)
+    for i in range(4):
+        gl, _ = gm.forward(int(toks[i]), len(toks) + i, gkv)
+        ol = om.forward(int(toks[i]), len(toks) + i, okv)
+        assert _bits_equal(gl, ol), i
