@@ -503,7 +503,8 @@ __global__ __launch_bounds__(256) void k_b_scores(const float *__restrict__ qkv,
 
 // ------------------------------------------------------------------ paged attention: softmax
 // The softmax of one (sequence, query head) row of scores (ops.rs:112-128): m = max of the
-// chunk maxima (order-free); e_t = exp(s_t - m) with the reference expf, into LDS; sum = the
+// chunk maxima, or with pmax == nullptr the max of the row itself (the scores staged in LDS
+// first; the max is order-free); e_t = exp(s_t - m) with the reference expf, into LDS; sum = the
 // index-order sum of e_t (block_seq_sum: 4 waves up to 3072 terms, 8 waves x 32 up to 16384,
 // else one lane); p_t = e_t * (1 / sum) written over the scores.  Workgroups are dealt longest
 // sequence first (order[] ranks the sequences by length).  NT = 512 threads, or 256 / 128 for
@@ -524,14 +525,37 @@ __global__ __launch_bounds__(NT) void k_b_softmax(float *scores, uint32_t sc_str
     const float *pm = pmax + ((size_t)s * n_heads + h) * pm_stride;
     const WaveExpTab tab = WaveExpTab::load(lane);
     float m = -__builtin_huge_valf();
-    for (uint32_t c = lane; c < nch; c += 64) m = fmaxf(m, pm[c]);
-    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
-    if (tid == 0) xs.sync = 0;
     constexpr uint32_t EB = 8;   // score loads in flight per thread
+    if (pmax) {
+        for (uint32_t c = lane; c < nch; c += 64) m = fmaxf(m, pm[c]);
+        for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
+    } else {   // the row into LDS and its max
+        __shared__ float wmax[NT / 64];
+        for (uint32_t t0 = 0; t0 < n; t0 += EB * NT) {
+            float sv[EB];
+#pragma unroll
+            for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(t0 + u * NT + (uint32_t)tid, n - 1)];
+#pragma unroll
+            for (uint32_t u = 0; u < EB; ++u) {
+                const uint32_t t = t0 + u * NT + (uint32_t)tid;
+                m = fmaxf(m, sv[u]);   // (clamped lanes repeat s_{n-1})
+                if (t < n) e[t] = sv[u];
+            }
+        }
+        m = wave_max_f(m);
+        if (lane == 0) wmax[wave] = m;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < NT / 64; ++w) m = fmaxf(m, wmax[w]);
+    }
+    if (tid == 0) xs.sync = 0;
     for (uint32_t t0 = 0; t0 < n; t0 += EB * NT) {   // (uniform: every lane calls the exp)
         float sv[EB];
 #pragma unroll
-        for (uint32_t u = 0; u < EB; ++u) sv[u] = sc[min(t0 + u * NT + (uint32_t)tid, n - 1)];
+        for (uint32_t u = 0; u < EB; ++u) {
+            const uint32_t t = min(t0 + u * NT + (uint32_t)tid, n - 1);
+            sv[u] = pmax ? sc[t] : e[t];   // (each thread reads back only the entries it wrote)
+        }
 #pragma unroll
         for (uint32_t u = 0; u < EB; ++u) {
             const uint32_t t = t0 + u * NT + (uint32_t)tid;
@@ -1158,24 +1182,24 @@ __global__ void k_p_rev(uint32_t n, uint32_t *order) {
 // Scores of prompt rows (model.rs:386-391): s_t = dot(q_{r,h}, K_t) * (1/sqrt(hd)) in ops::dot's
 // order, as k_b_scores, for a block of PRB consecutive rows (blockIdx.z, longest block first)
 // and the rep query heads of kv head g (blockIdx.y) over positions [256 c, 256 c + 256)
-// (c = blockIdx.x; chunks past the block's longest row exit), and each (row, head)'s chunk
-// maximum.  Lane = position: its K row is read once and dotted with the block's rep PRB query
-// heads (scalar operands), so K is read once per block of rows instead of once per row.
+// (c = blockIdx.x; chunks past the block's longest row exit).  Lane = position: its K row is
+// read once and dotted with the block's rep PRB query heads (scalar operands), so K is read once
+// per block of rows instead of once per row.  The row maxima are left to the softmax, which
+// reads every score anyway (a wave maximum per row and head here cost ~15 % of this kernel).
 constexpr uint32_t PRB = 16;
 template <int HD>
 __global__ __launch_bounds__(256) void k_p_scores(const float *__restrict__ qkv, uint32_t qkv_stride,
                                                   const uint32_t *__restrict__ pos, uint32_t R, PagedKV kv,
-                                                  float *scores, uint32_t sc_stride, float *pmax, uint32_t pm_stride) {
-    constexpr int MAXREP = 8;
-    __shared__ float wm[4][PRB * MAXREP];
+                                                  float *scores, uint32_t sc_stride) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t c = blockIdx.x, g = blockIdx.y, rb0 = (gridDim.z - 1 - blockIdx.z) * PRB;
     const uint32_t nrow = min(PRB, R - rb0), nlast = pos[rb0 + nrow - 1] + 1, t0 = c * ACH;
     if (t0 >= nlast) return;   // (uniform)
     const uint32_t n_heads = kv.n_heads, rep = n_heads / kv.n_kv;
     const uint32_t t = t0 + 64 * (uint32_t)wave + (uint32_t)lane, tw = t0 + 64 * (uint32_t)wave;
+    if (tw >= nlast) return;   // (uniform per wave: a wave past every row of the block)
     v4f kt[HD / 4];
-    if (tw < nlast) {
+    {
         const uint32_t tc = min(t, nlast - 1);
         const v4f *kp = reinterpret_cast<const v4f *>(kv.k + kv_tile(kv.bt[tc / PAGE], g, kv.n_kv, HD)) + tc % PAGE;
 #pragma unroll
@@ -1184,43 +1208,32 @@ __global__ __launch_bounds__(256) void k_p_scores(const float *__restrict__ qkv,
     const float scale = 1.0f / sqrtf((float)HD);
     for (uint32_t k = 0; k < nrow; ++k) {
         const uint32_t n = pos[rb0 + k] + 1;
+        if (tw >= n) continue;   // (uniform per wave)
         float *scb = scores + ((size_t)(rb0 + k) * n_heads + g * rep) * sc_stride;
         for (uint32_t r = 0; r < rep; ++r) {
-            float mx = -__builtin_huge_valf();
-            if (tw < n) {   // (uniform per wave)
-                // (a wave-uniform address of read-only memory: the query comes in scalar loads)
-                const float *qr = qkv + (size_t)(rb0 + k) * qkv_stride + (size_t)(g * rep + r) * HD;
-                float acc[4][8];   // ops::dot: four 8-lane FMA accumulators over 32-wide steps
+            // (a wave-uniform address of read-only memory: the query comes in scalar loads)
+            const float *qr = qkv + (size_t)(rb0 + k) * qkv_stride + (size_t)(g * rep + r) * HD;
+            float acc[4][8];   // ops::dot: four 8-lane FMA accumulators over 32-wide steps
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int l = 0; l < 8; ++l) acc[a][l] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < HD; i += 32)
 #pragma unroll
                 for (int a = 0; a < 4; ++a)
 #pragma unroll
-                    for (int l = 0; l < 8; ++l) acc[a][l] = 0.0f;
+                    for (int l = 0; l < 8; ++l) {
+                        const int e = i + 8 * a + l;
+                        acc[a][l] = fmaf(qr[e], kt[e / 4][e % 4], acc[a][l]);
+                    }
+            float v[8];
 #pragma unroll
-                for (int i = 0; i < HD; i += 32)
-#pragma unroll
-                    for (int a = 0; a < 4; ++a)
-#pragma unroll
-                        for (int l = 0; l < 8; ++l) {
-                            const int e = i + 8 * a + l;
-                            acc[a][l] = fmaf(qr[e], kt[e / 4][e % 4], acc[a][l]);
-                        }
-                float v[8];
-#pragma unroll
-                for (int l = 0; l < 8; ++l) v[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
-                const float sv = (((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]))) * scale;
-                if (t < n) {
-                    scb[(size_t)r * sc_stride + t] = sv;
-                    mx = sv;
-                }
-            }
-            mx = wave_max_f(mx);
-            if (lane == 0) wm[wave][k * rep + r] = mx;
+            for (int l = 0; l < 8; ++l) v[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+            const float sv = (((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]))) * scale;
+            if (t < n) scb[(size_t)r * sc_stride + t] = sv;
         }
     }
-    __syncthreads();
-    for (uint32_t i = tid; i < nrow * rep; i += 256)
-        pmax[((size_t)(rb0 + i / rep) * n_heads + g * rep + i % rep) * pm_stride + c] =
-            fmaxf(fmaxf(wm[0][i], wm[1][i]), fmaxf(wm[2][i], wm[3][i]));
 }
 
 // P.V of prompt rows (model.rs:392-397): o[r][h][e] = ((0 + p_0 v_0[e]) + p_1 v_1[e]) + ... over
@@ -1315,15 +1328,18 @@ bool launch_p_attention(hipStream_t st, uint32_t hd, const float *qkv, uint32_t 
     const dim3 gs(nch, kv.n_kv, div_up(n, PRB)), gm(n * kv.n_heads);
     const uint32_t ss = b_sc_stride(max_ctx);
     if (hd == 32)
-        BLAUNCH(k_p_scores<32>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
+        BLAUNCH(k_p_scores<32>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss);
     else if (hd == 64)
-        BLAUNCH(k_p_scores<64>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
+        BLAUNCH(k_p_scores<64>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss);
     else
-        BLAUNCH(k_p_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss, pmax, nch);
+        BLAUNCH(k_p_scores<128>, gs, dim3(256), 0, st, qkv, qkv_stride, pos, n, kv, scores, ss);
+    // (the softmax forms each row's maximum itself: pmax = nullptr)
     if (max_ctx <= 3072)   // (a prompt chunk's window: bsm_lds fits the default limit)
-        BLAUNCH(k_b_softmax<128>, gm, dim3(128), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
+        BLAUNCH(k_b_softmax<128>, gm, dim3(128), bsm_lds(max_ctx), st, scores, ss, nullptr, nch, pos, order,
+                kv.n_heads);
     else
-        BLAUNCH(k_b_softmax<512>, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, pmax, nch, pos, order, kv.n_heads);
+        BLAUNCH(k_b_softmax<512>, gm, dim3(512), bsm_lds(max_ctx), st, scores, ss, nullptr, nch, pos, order,
+                kv.n_heads);
     const dim3 gp(div_up(n, 4u), kv.n_kv);
 #define PPV(H, P) BLAUNCH((k_p_pv<H, P>), gp, dim3(256), 0, st, scores, ss, pos, n, kv, o)
     if (hd == 32) {

@@ -73,6 +73,12 @@ def test_f32_heads_of_128(hg, orc):
     _pair(hg, orc, gs.synth_path("joint12", 3), 5, 4, 13)
 
 
+def test_f32_from_kquant_file(hg, orc):
+    """Q5_0 / Q4_K / Q6_K / Q8_0 / F16 tensors dequantized at load (gguf.rs:361-468) and kept
+    as f32 (Src::Owned -> Mat::Owned, quant.rs:213-222)."""
+    _pair(hg, orc, gs.synth_path("tiny", 31, norm_jitter=0.1, qtype="kquant"), 7, 6, 17)
+
+
 def test_f32_greedy_generation(hg, orc):
     path = gs.synth_path("tiny", 22, norm_jitter=0.1)
     gm, om = hg.Model(path, quant=False), orc.Model(path, quant=False)
