@@ -655,6 +655,23 @@ __device__ inline void norm_rope_head(const float *u, float *o, const HeadConst<
 }
 
 
+// dot_wide_serial(a, b, 64) by the lanes of one wave: lane 8 r + l (and its mirror 32 + 8 r + l)
+// holds accumulator (r, l), fmaf(a[32 + e], b[32 + e], fmaf(a[e], b[e], 0)); the butterflies
+// then form (acc0 + acc1) + (acc2 + acc3) and ((v0 + v4) + (v2 + v6)) + ((v1 + v5) + (v3 + v7)),
+// the same additions as the serial form (each IEEE addition is commutative).  Every lane
+// returns the sum.
+// (a0, b0, a1, b1: lane e's elements e % 32 and 32 + e % 32 of a and b)
+__device__ inline float dot64_lanes(float a0, float b0, float a1, float b1) {
+    float acc = fmaf(a0, b0, 0.0f);
+    acc = fmaf(a1, b1, acc);
+    acc = acc + shfl_xor(acc, 8);
+    acc = acc + shfl_xor(acc, 16);
+    acc = acc + shfl_xor(acc, 4);
+    acc = acc + shfl_xor(acc, 2);
+    acc = acc + shfl_xor(acc, 1);
+    return acc;
+}
+
 // ops::dot (ops.rs:7-36) of two hd-vectors in the reference order: four 8-lane FMA
 // accumulators over 32-wide steps, 8-wide tail on accumulator 0, then
 // ((a0+a1)+(a2+a3)) reduced as ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)), then a scalar tail.

@@ -152,6 +152,7 @@ struct hg_kv {
     std::map<uint32_t, hipGraphExec_t> g_decode, g_body;
     hipGraphExec_t g_tail = nullptr;
     bool use_graph = true;
+    bool no_fuse = false;          // HG_QKV_SCORES=0: scores in their own launch (the unfused kernels)
     LaunchTimer *timer = nullptr;  // hg_profile_step: per-dispatch timing
     std::unique_ptr<PrefillWork> pw;   // the batched prompt path's buffers (on first use)
     std::unique_ptr<SampleWork> sw;    // the device sampler's buffers (on first use)
@@ -499,13 +500,29 @@ void enqueue_layers(hg_kv *kv, int order) {
     uint8_t *qa = kv->qa.as<uint8_t>();
     float *da = kv->da.as<float>();
     StepParams *p = kv->params.as<StepParams>();
+    const bool fused =
+        !kv->no_fuse && qkv_scores_ok(kv->exact, c.head_dim, kv->win, c.n_heads, c.n_kv_heads, c.d_model);
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const Layer &L = *m->layers[l];
         mark(kv, P_QKV);   // attn_norm + attn_qkv + QK-norm + RoPE + append (model.rs:164-165, 194-211)
-        launch_qkv_head(st, kv->exact, order, c.head_dim, L.qkv.m, x, L.attn_norm.as<float>(), c.rms_eps,
-                        L.q_norm.as<float>(), L.k_norm.as<float>(), m->rope_cos.as<float>(), m->rope_sin.as<float>(), p,
-                        c.n_heads, c.n_kv_heads, layer_k(kv, l), layer_v(kv, l), kv->cap, kv->qkv.as<float>());
-        for (int part = 0; part < 2; ++part) {
+        // + the attention scores where the launch takes them (the softmax + P.V then forms the
+        // score at pos)
+        const bool fz = fused && launch_qkv_scores(st, order, L.qkv.m, x, L.attn_norm.as<float>(), c.rms_eps,
+                                                   L.q_norm.as<float>(), L.k_norm.as<float>(),
+                                                   m->rope_cos.as<float>(), m->rope_sin.as<float>(), p, c.n_heads,
+                                                   c.n_kv_heads, layer_k(kv, l), layer_v(kv, l), kv->cap, kv->win,
+                                                   kv->qkv.as<float>(), kv->scores.as<float>(), kv->part.as<float>());
+        if (fz) {
+            mark(kv, P_ATTN_B);
+            launch_attn_pv_self(st, kv->qkv.as<float>(), p, layer_v(kv, l), kv->cap, kv->win, c.n_heads,
+                                c.n_kv_heads, kv->part.as<float>(), kv->scores.as<float>(), kv->o.as<float>());
+        } else {
+            launch_qkv_head(st, kv->exact, order, c.head_dim, L.qkv.m, x, L.attn_norm.as<float>(), c.rms_eps,
+                            L.q_norm.as<float>(), L.k_norm.as<float>(), m->rope_cos.as<float>(),
+                            m->rope_sin.as<float>(), p, c.n_heads, c.n_kv_heads, layer_k(kv, l), layer_v(kv, l),
+                            kv->cap, kv->qkv.as<float>());
+        }
+        for (int part = 0; part < 2 && !fz; ++part) {
             mark(kv, part == 0 ? P_ATTN_A : P_ATTN_B);
             launch_attn(st, kv->exact, part, c.head_dim, kv->qkv.as<float>(), L.q_norm.as<float>(),
                         L.k_norm.as<float>(), c.rms_eps, m->rope_cos.as<float>(), m->rope_sin.as<float>(), p,
@@ -732,6 +749,8 @@ int hg_kv_new(const hg_model *m, uint32_t max_ctx, uint32_t flags, hg_kv **out) 
         kv->exact = (flags & HG_KV_FAST) == 0;
         const char *ge = getenv("HG_GRAPH");
         kv->use_graph = !(ge && ge[0] == '0');
+        const char *qs = getenv("HG_QKV_SCORES");
+        kv->no_fuse = qs && qs[0] == '0';
         kv->win = kv->cap;
         if (kv->exact && pv_ring_slots(kv->cap) < 2)
             return fail(HG_ERR_UNSUPPORTED, "a reference-order cache holds at most 32768 positions");

@@ -46,6 +46,21 @@ bool launch_qkv_head(hipStream_t st, bool exact, int order, uint32_t hd, const Q
                      const float *w, float eps, const float *qn, const float *kn, const float *cs, const float *sn,
                      const StepParams *p, uint32_t n_heads, uint32_t n_kv, float *kc, float *vc, uint32_t cap,
                      float *out);
+// Reference order, head_dim 64, a window the LDS-resident softmax + P.V kernel takes: the QKV
+// step and the attention scores in one launch (workgroups that each form one q head and score
+// one split of at most QKV_SCORE_POS positions, t < pos; qkv_score_splits splits), then
+// launch_attn_pv_self for the softmax + P.V, which forms the score at pos itself.
+// launch_qkv_scores returns false, launching nothing, where qkv_scores_ok does not hold;
+// scores and pmax as launch_attn's scratch and part.
+constexpr uint32_t QKV_SCORE_POS = 256;
+uint32_t qkv_score_splits(uint32_t win, uint32_t n_heads, uint32_t n_kv);
+bool qkv_scores_ok(bool exact, uint32_t hd, uint32_t win, uint32_t n_heads, uint32_t n_kv, uint32_t d);
+bool launch_qkv_scores(hipStream_t st, int order, const Q8Mat &W, const float *x, const float *w, float eps,
+                       const float *qn, const float *kn, const float *cs, const float *sn, const StepParams *p,
+                       uint32_t n_heads, uint32_t n_kv, float *kc, float *vc, uint32_t cap, uint32_t win, float *out,
+                       float *scores, float *pmax);
+void launch_attn_pv_self(hipStream_t st, const float *qkv, const StepParams *p, float *vc, uint32_t cap, uint32_t win,
+                         uint32_t n_heads, uint32_t n_kv, float *part, float *scratch, float *o_out);
 // The same head steps for a q | k | v vector computed elsewhere (rewritten in place).
 bool launch_qk_rope_append(hipStream_t st, uint32_t hd, float *qkv, const float *qn, const float *kn, float eps,
                            const float *cs, const float *sn, const StepParams *p, uint32_t n_heads, uint32_t n_kv,

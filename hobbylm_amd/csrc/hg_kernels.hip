@@ -8,6 +8,8 @@
 // hg_common.h for the device row layout).
 #include <hip/hip_ext.h>
 
+#include <algorithm>
+
 #include "hg_common.h"
 #include "hg_device.h"
 #include "hg_expf.h"
@@ -356,20 +358,31 @@ struct GroupRaw {
 // hh*HD .. hh*HD + HD - 1).  Every workgroup forms the norm of the whole x itself, in the
 // reference's order; a separate chain wave (HD <= 64) runs it while the row waves fetch their
 // weights.  Writes q, k (normed and rotated) and v into out (the q | k | v layout).
+// SC (reference order, HD = 64): the attention scores join this launch.  Workgroups
+// 0 .. n_heads S2 - 1 each form one q head and the scores s[h][t] = dot(q_h, K_t) / sqrt(HD)
+// (model.rs:213-218, ops::dot's order) of split s of the window (positions [s c, s c + c),
+// c = ceil(win / S2) <= 256, one position per row thread, the split's K rows fetched into LDS
+// behind the weights), for t < pos only, and the split's maximum into pmax[h S2 + s]; the
+// score at pos needs this step's k, so the softmax + P.V kernel forms it.  Placement: the rep
+// heads of one (kv group, split) share an XCD (one L2 for their K rows) and each kv group's
+// splits stay on 8 / n_kv XCDs (its q weights reach that many L2s).  The k and v workgroups
+// follow.  Every q head is formed alike by its S2 workgroups; split 0's writes it to out.
 template <int HD> struct QkvCfg {
     static constexpr int CW = HD <= 64 ? 64 : 0;   // wave 0: the head's epilogue
     static constexpr int RE = CW + 8 * HD;         // + 8 lanes per row
     static constexpr int SW = HD <= 64 ? 192 : 0;  // + waves that only sum (no weight loads)
     static constexpr int NT = RE + SW;
 };
-template <bool EXACT, int ORDER, bool SCF32, int NCT, int HD>
+template <bool EXACT, int ORDER, bool SCF32, int NCT, int HD, bool SC = false>
 __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const float *__restrict__ x,
                                                             const float *__restrict__ w, float eps,
                                                             const float *__restrict__ qn, const float *__restrict__ kn,
                                                             const float *__restrict__ cs, const float *__restrict__ sn,
                                                             const StepParams *p, uint32_t n_heads, uint32_t n_kv,
-                                                            float *kc, float *vc, uint32_t cap, float *out) {
+                                                            float *kc, float *vc, uint32_t cap, float *out,
+                                                            uint32_t win, uint32_t S2, float *scores, float *pmax) {
     constexpr int CW = QkvCfg<HD>::CW, RE = QkvCfg<HD>::RE, NT = QkvCfg<HD>::NT;
+    static_assert(!SC || (EXACT && HD == 64), "scores join the exact head-64 launch only");
     extern __shared__ __align__(16) uint8_t smem[];
     uint8_t *sq = smem;
     float *sd = reinterpret_cast<float *>(smem + W.nc * CHUNK_BYTES);
@@ -380,7 +393,33 @@ __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const floa
     __shared__ xsum::Scratch xs;
     const int tid = threadIdx.x, lane = tid & 63, j = tid & 7;
     const bool rowt = tid >= CW && tid < RE;
-    const uint32_t hh = blockIdx.x, d = W.K, ng = d / 4;
+    uint32_t hh = blockIdx.x, spl = 0;   // head, split (SC)
+    if constexpr (SC) {
+        const uint32_t nsc = n_heads * S2, rep = n_heads / n_kv, L = blockIdx.x;
+        if (L < nsc) {
+            uint32_t key, r;
+            const uint32_t xq = n_kv <= 8 && 8 % n_kv == 0 ? 8 / n_kv : 0;   // XCDs per kv group
+            if (xq && S2 % xq == 0) {
+                // XCD x serves kv group x / xq, splits x % xq, + xq, ...: each q head's weights
+                // reach xq L2s, each split's K rows one
+                const uint32_t x = L % 8, loc = L / 8, gg = x / xq;
+                r = loc % rep;
+                key = gg * S2 + (loc / rep) * xq + x % xq;
+            } else if ((n_kv * S2) % 8 == 0) {
+                const uint32_t slot = L / 8;
+                key = L % 8 + 8 * (slot / rep);
+                r = slot % rep;
+            } else {
+                key = L / rep;
+                r = L % rep;
+            }
+            hh = (key / S2) * rep + r;
+            spl = key % S2;
+        } else {
+            hh = n_heads + (L - nsc);
+        }
+    }
+    const uint32_t d = W.K, ng = d / 4;
     // the waves of the index-order sum: wave 0 and the waves past the rows (or, without those,
     // the first four waves)
     const int wave = tid >> 6,
@@ -415,11 +454,26 @@ __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const floa
     for (uint32_t u = 0; u < RQ; ++u)
         if (tid + NT * u < ng) squares(xv[u], tid + NT * u);
     for (uint32_t g = tid + NT * RQ; g < ng; g += NT) squares(reinterpret_cast<const v4f *>(x)[g], g);
+    // (SC) the split's K rows, fetched straight into LDS behind the weights: 16-byte piece m of
+    // local row i at slot 16 i + (m + i) % 16, so a row read by its thread is bank-conflict free
+    float *kbuf = ps + d;
     if (EXACT) {
         if (tid == 0) xs.sync = 0;
         __syncthreads();
         // the row waves issue their weights now (arriving during the sum)
         if (rowt) rd.begin(row_qs(W, row), row_sc<SCF32>(W, row), W.nb, W.nc, j);
+        if constexpr (SC) {
+            const uint32_t c = div_up(win, S2), t0 = spl * c, t1 = min(win, t0 + c);
+            if (kind == 0 && rowt) {   // row wave rw issues 1 KB instructions rw, rw + 8, ... (64 slots each)
+                const float *kcg = kc + (size_t)(hh / (n_heads / n_kv)) * cap * HD;
+                const uint32_t rw = (uint32_t)(tid - CW) >> 6, ni = div_up(c, 4);
+                for (uint32_t I = rw; I < ni; I += (RE - CW) / 64) {
+                    const uint32_t sl = I * 64 + (uint32_t)lane, i = sl / 16, m = (sl - i) & 15;
+                    const uint32_t tr = min(t0 + i, t1 - 1);   // (rows past the split: its last row)
+                    __builtin_amdgcn_global_load_lds(kcg + (size_t)tr * HD + 4 * m, kbuf + (size_t)I * 256, 16, 0, 0);
+                }
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
         if (sp >= 0) {
             const float r = block_seq_sum<4, 4>(ps, d, xs, sp, lane);   // ss += v * v in index order
@@ -456,27 +510,55 @@ __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const floa
         if (j == 0) hv[(tid - CW) >> 3] = v;
     }
     __syncthreads();
-    if (tid >= 64) return;
-    float *dst = out + (size_t)hh * HD;   // q | k | v regions are contiguous in head order
-    if (kind == 2) {
-        const uint32_t g = hh - n_heads - n_kv;
-        float *vcr = vc + ((size_t)g * cap + pos) * HD;
-        float *vtr = vc + (size_t)n_kv * cap * HD + (size_t)g * HD * vt_stride(cap) + pos;
-        for (uint32_t i = lane; i < HD; i += 64) {
-            dst[i] = hv[i];
-            vcr[i] = hv[i];
-            vtr[(size_t)i * vt_stride(cap)] = hv[i];
+    const bool scw = SC && kind == 0;   // (uniform) a score workgroup: every thread stays
+    if (!scw && tid >= 64) return;
+    if (tid < 64) {
+        float *dst = out + (size_t)hh * HD;   // q | k | v regions are contiguous in head order
+        if (kind == 2) {
+            const uint32_t g = hh - n_heads - n_kv;
+            float *vcr = vc + ((size_t)g * cap + pos) * HD;
+            float *vtr = vc + (size_t)n_kv * cap * HD + (size_t)g * HD * vt_stride(cap) + pos;
+            for (uint32_t i = lane; i < HD; i += 64) {
+                dst[i] = hv[i];
+                vcr[i] = hv[i];
+                vtr[(size_t)i * vt_stride(cap)] = hv[i];
+            }
+            return;
         }
-        return;
+        norm_rope_head<HD>(hv, ho, hc, kind == 0, eps, tmp, lane);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (!scw || spl == 0)
+            for (uint32_t i = lane; i < HD; i += 64) dst[i] = ho[i];
+        if (kind == 1) {
+            float *kcr = kc + ((size_t)(hh - n_heads) * cap + pos) * HD;
+            for (uint32_t i = lane; i < HD; i += 64) kcr[i] = ho[i];
+        }
     }
-    norm_rope_head<HD>(hv, ho, hc, kind == 0, eps, tmp, lane);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (uint32_t i = lane; i < HD; i += 64) dst[i] = ho[i];
-    if (kind == 1) {
-        float *kcr = kc + ((size_t)(hh - n_heads) * cap + pos) * HD;
-        for (uint32_t i = lane; i < HD; i += 64) kcr[i] = ho[i];
+    if constexpr (SC) {
+        if (!scw) return;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's K pieces are in LDS
+        __syncthreads();   // q_h (ho) and every K piece in LDS
+        const uint32_t c = div_up(win, S2), t0 = spl * c, t1 = min(win, t0 + c);
+        const uint32_t i = (uint32_t)(tid - CW), t = t0 + i;
+        float mx = -__builtin_huge_valf();
+        if (rowt && t < t1 && t < pos) {   // (position pos: the softmax + P.V kernel)
+            float kt[HD];
+#pragma unroll
+            for (uint32_t m = 0; m < HD / 4; ++m)
+                *reinterpret_cast<v4f *>(kt + 4 * m) = *reinterpret_cast<const v4f *>(kbuf + 4 * (16 * i + ((m + i) & 15)));
+            const float v = dot_wide_serial(ho, kt, HD) * (1.0f / sqrtf((float)HD));
+            scores[(size_t)hh * cap + t] = v;
+            mx = v;
+        }
+        for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, shfl_xor(mx, m));   // max is order-free
+        if (lane == 0) red[tid >> 6] = mx;
+        __syncthreads();
+        if (tid == 0) {
+            for (int i = 1; i < NT / 64; ++i) mx = fmaxf(mx, red[i]);
+            pmax[(size_t)hh * S2 + spl] = mx;
+        }
     }
 }
 
@@ -1106,7 +1188,9 @@ __device__ __forceinline__ void pv_adds64(float &o, const v4f a) {
 //   (pv_adds64), waiting only for each block of 4 groups' flags.
 // LONG = false serves windows up to SHORT positions (one 64-bit ready word, each producer's
 // groups in one batch); LONG = true up to MAXR (two ready words, batches of 7 groups, the sum
-// as 16 or 28 terms per lane).
+// as 16 or 28 terms per lane).  SELF (head 64, after the QKV launch that also scores): the
+// scores row stops short of pos; wave 0 forms the score at pos from this step's q and k
+// (dot64_lanes, ops::dot's order) and the maximum and exps take it in place of the row's.
 struct PvResCfg {
     static constexpr uint32_t D = 4;      // output elements per workgroup (4 or 8)
     static constexpr uint32_t G = 64;     // positions per product group (16 lanes x 4)
@@ -1126,7 +1210,7 @@ __host__ __device__ bool pv_res_fits(uint32_t cap) {
            pv_res_rows(cap) <= PvResCfg::MAXR;
 }
 
-template <int HD, bool LONG>
+template <int HD, bool LONG, bool SELF = false>
 __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__restrict__ scores,
                                                              const float *__restrict__ pmax,
                                                              const float *__restrict__ qkv, const StepParams *p,
@@ -1139,7 +1223,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     __shared__ uint32_t vdone[4];        // V rounds written by V wave 4 + i (its groups i, i + 4, ...)
     __shared__ uint32_t arrived;         // waves whose e_t are written
     __shared__ uint32_t inv_ready;
-    __shared__ float s_inv;
+    __shared__ float s_inv, s_pos;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t h, q;
     pv_head_quarter(blockIdx.x, n_heads, n_kv, HD / D, &h, &q);
@@ -1154,7 +1238,19 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
     static_assert(D == 4, "a lane moves 16 bytes of one element's row");
     const float *vtg = vc + (size_t)n_kv * cap * HD + ((size_t)g * HD + q * D) * vt_stride(cap);   // rows q D ..
     const uint32_t ng = div_up(n, G), nblk = div_up(n, 4 * G);   // V groups, chain blocks of 4 groups
-    // loads in issue order: the split maxima, this thread's first scores, the exp table
+    // loads in issue order: (SELF, wave 0) this step's q and k elements, the split maxima, this
+    // thread's first scores, the exp table
+    float qk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (SELF) {
+        if (wave == 0) {
+            const float *qh = qkv + (size_t)h * HD, *kp = qkv + (size_t)(n_heads + g) * HD;
+            const uint32_t e = (uint32_t)lane & 31;
+            qk[0] = qh[e];
+            qk[1] = kp[e];
+            qk[2] = qh[32 + e];
+            qk[3] = kp[32 + e];
+        }
+    }
     float m = pmax[(size_t)h * S + min((uint32_t)lane, S - 1)];
     float sv[EB];
 #pragma unroll
@@ -1167,8 +1263,19 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
         inv_ready = 0;
         xs.sync = 0;
     }
+    if constexpr (SELF) {
+        // the score at pos, s = dot(q_h, k_pos) / sqrt(HD) (model.rs:213-218, ops::dot's order),
+        // from this step's q and k as the QKV launch wrote them (the scores row stops short of pos)
+        static_assert(!SELF || HD == 64, "one wave's dot");
+        if (wave == 0) {
+            const float v = dot64_lanes(qk[0], qk[1], qk[2], qk[3]) * (1.0f / sqrtf((float)HD));
+            if (lane == 0) s_pos = v;
+        }
+    }
     if (tid < 4) vdone[tid] = 0;
     __syncthreads();
+    const float spos = SELF ? s_pos : 0.0f;
+    if constexpr (SELF) m = fmaxf(m, spos);
     for (uint32_t s = lane + 64; s < S; s += 64) m = fmaxf(m, pmax[(size_t)h * S + s]);
     for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));   // max is order-free
     for (uint32_t t0 = 0; t0 < n; t0 += EB * 512) {
@@ -1179,7 +1286,7 @@ __global__ __launch_bounds__(512) void k_attn_softmax_pv_res(const float *__rest
         for (uint32_t u = 0; u < EB; ++u)
             if (t0 + u * 512 < n) {                      // uniform: every lane calls the exp
                 const uint32_t t = t0 + u * 512 + tid;
-                const float ev = hg_expf_l(sv[u] - m, tab);
+                const float ev = hg_expf_l(((SELF && t == n - 1) ? spos : sv[u]) - m, tab);
                 if (t < n) e[t] = ev;
             }
     }
@@ -2112,6 +2219,21 @@ hipError_t init_kernel_attributes() {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_LDS_BUDGET);
     PVR_ATTR(32) PVR_ATTR(64) PVR_ATTR(128)
 #undef PVR_ATTR
+#define QKS_ATTR(O, S, N)                                                                                    \
+    if (e == hipSuccess)                                                                                     \
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_qkv_head<true, O, S, N, 64, true>),        \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_LDS_BUDGET);
+#define QKS_ATTR_N(O, S) QKS_ATTR(O, S, 1) QKS_ATTR(O, S, 2) QKS_ATTR(O, S, 4) QKS_ATTR(O, S, 8)
+    QKS_ATTR_N(ORDER_DECODE, false) QKS_ATTR_N(ORDER_DECODE, true) QKS_ATTR_N(ORDER_PREFILL, false)
+    QKS_ATTR_N(ORDER_PREFILL, true)
+#undef QKS_ATTR_N
+#undef QKS_ATTR
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_softmax_pv_res<64, false, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_LDS_BUDGET);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_attn_softmax_pv_res<64, true, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_LDS_BUDGET);
     if (e == hipSuccess)
         e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_seq_sum), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)((SEQSUM_MAX + 4) * sizeof(float)));
@@ -2210,7 +2332,7 @@ bool launch_qkv_head(hipStream_t st, bool exact, int order, uint32_t hd, const Q
     const size_t shm = (size_t)W.nc * CHUNK_BYTES + (size_t)W.nc * 4 * sizeof(float) + (size_t)W.K * sizeof(float);
 #define QKH(E, O, S, N, HD)                                                                                     \
     LAUNCH((k_qkv_head<E, O, S, N, HD>), grid, dim3(QkvCfg<HD>::NT), shm, st, W, x, w, eps, qn, kn, cs, sn, p, \
-           n_heads, n_kv, kc, vc, cap, out)
+           n_heads, n_kv, kc, vc, cap, out, 0u, 0u, nullptr, nullptr)
 #define QKH_S(E, O, N, HD)                  \
     do {                                    \
         if (W.sc_f32) QKH(E, O, true, N, HD);  \
@@ -2243,6 +2365,67 @@ bool launch_qkv_head(hipStream_t st, bool exact, int order, uint32_t hd, const Q
 #undef QKH_O
 #undef QKH_S
 #undef QKH
+    return true;
+}
+
+// Score splits of a window: at most QKV_SCORE_POS positions each, and as many more (down to 64
+// positions each) as keep the launch within one workgroup per CU; a multiple of the XCDs per kv
+// group.
+uint32_t qkv_score_splits(uint32_t win, uint32_t n_heads, uint32_t n_kv) {
+    static const uint32_t n_cu = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            v = 0;
+        return (uint32_t)v;
+    }();
+    const uint32_t xq = n_kv && n_kv <= 8 && 8 % n_kv == 0 ? 8 / n_kv : 1;
+    const uint32_t need = div_up(div_up(win, QKV_SCORE_POS), xq) * xq;
+    const uint32_t fill = n_heads && n_cu > 2 * n_kv ? (n_cu - 2 * n_kv) / n_heads / xq * xq : 0;
+    const uint32_t most = div_up(div_up(win, 64), xq) * xq;
+    return std::max(need, std::min(fill, most));
+}
+// k_qkv_head's dynamic LDS with SC: the activation, its scales, the squares, the split's K rows
+static size_t qkv_scores_lds(uint32_t d, uint32_t win, uint32_t n_heads, uint32_t n_kv) {
+    const size_t nc = div_up(d / 32, 4), c = div_up(win, qkv_score_splits(win, n_heads, n_kv));
+    return nc * CHUNK_BYTES + nc * 4 * sizeof(float) + (size_t)d * sizeof(float) + div_up(c, 4) * 4 * 64 * sizeof(float);
+}
+bool qkv_scores_ok(bool exact, uint32_t hd, uint32_t win, uint32_t n_heads, uint32_t n_kv, uint32_t d) {
+    return exact && hd == 64 && n_kv && n_heads % n_kv == 0 && pv_res_fits(win) && d % 32 == 0 &&
+           qkv_scores_lds(d, win, n_heads, n_kv) <= PV_LDS_BUDGET;
+}
+
+bool launch_qkv_scores(hipStream_t st, int order, const Q8Mat &W, const float *x, const float *w, float eps,
+                       const float *qn, const float *kn, const float *cs, const float *sn, const StepParams *p,
+                       uint32_t n_heads, uint32_t n_kv, float *kc, float *vc, uint32_t cap, uint32_t win, float *out,
+                       float *scores, float *pmax) {
+    if (!qkv_scores_ok(true, 64, win, n_heads, n_kv, W.K) || win > cap || W.nc != div_up(W.K / 32, 4)) return false;
+    const uint32_t S2 = qkv_score_splits(win, n_heads, n_kv);
+    static_assert(QKV_SCORE_POS <= 8 * 64, "one position per row thread");
+    const dim3 grid(n_heads * S2 + 2 * n_kv);
+    const size_t shm = qkv_scores_lds(W.K, win, n_heads, n_kv);
+#define QKS(O, S, N)                                                                                               \
+    LAUNCH((k_qkv_head<true, O, S, N, 64, true>), grid, dim3(QkvCfg<64>::NT), shm, st, W, x, w, eps, qn, kn, cs, sn, \
+           p, n_heads, n_kv, kc, vc, cap, out, win, S2, scores, pmax)
+#define QKS_S(O, N)                  \
+    do {                             \
+        if (W.sc_f32) QKS(O, true, N);  \
+        else QKS(O, false, N);          \
+    } while (0)
+#define QKS_O(N)                                          \
+    do {                                                  \
+        if (order == ORDER_DECODE) QKS_S(ORDER_DECODE, N); \
+        else QKS_S(ORDER_PREFILL, N);                      \
+    } while (0)
+    switch (nct_of(W.nc)) {
+    case 8: QKS_O(8); break;
+    case 4: QKS_O(4); break;
+    case 2: QKS_O(2); break;
+    default: QKS_O(1); break;
+    }
+#undef QKS_O
+#undef QKS_S
+#undef QKS
     return true;
 }
 
@@ -2322,6 +2505,18 @@ static void attn_fast_launch(hipStream_t st, int which, const float *qkv, const 
         return;
     }
     LAUNCH(k_attn_combine<HD>, dim3(n_heads), dim3(256), 0, st, part, n_heads, S, o_out, q_out, d_out);
+}
+
+void launch_attn_pv_self(hipStream_t st, const float *qkv, const StepParams *p, float *vc, uint32_t cap, uint32_t win,
+                         uint32_t n_heads, uint32_t n_kv, float *part, float *scratch, float *o_out) {
+    constexpr int HD = 64;
+    const uint32_t S2 = qkv_score_splits(win, n_heads, n_kv);
+    if (pv_res_rows(win) <= PvResCfg::SHORT)
+        LAUNCH((k_attn_softmax_pv_res<HD, false, true>), dim3(n_heads * (HD / PvResCfg::D)), dim3(512), pv_res_lds(win),
+               st, scratch, part, qkv, p, vc, cap, win, S2, n_heads, n_kv, o_out);
+    else
+        LAUNCH((k_attn_softmax_pv_res<HD, true, true>), dim3(n_heads * (HD / PvResCfg::D)), dim3(512), pv_res_lds(win),
+               st, scratch, part, qkv, p, vc, cap, win, S2, n_heads, n_kv, o_out);
 }
 
 bool launch_attn(hipStream_t st, bool exact, int which, uint32_t hd, const float *qkv, const float *qn,

@@ -216,3 +216,56 @@ def test_bounded_waits_report_an_error(hg, orc, monkeypatch):
         gl, _ = gm.forward(int(toks[i]), len(toks) + i, gkv)
         ol = om.forward(int(toks[i]), len(toks) + i, okv)
         assert _bits_equal(gl, ol), i
+
+
+@pytest.mark.parametrize("preset,start,rows", [("500M", 2040, False), ("tiny_wnorm", 0, True), ("130M", 0, True)])
+def test_scores_in_qkv_launch(hg, orc, monkeypatch, preset, start, rows):
+    """Head-64 reference-order steps form the attention scores inside the QKV launch (each score
+    workgroup forms its own q head; the softmax + P.V kernel forms the score at pos).  Logits,
+    routing and KV rows must equal both the oracle's and those of the separate scores launch
+    (HG_QKV_SCORES=0), bit for bit: for the 500M model from seeded KV rows across the windows
+    of 2048 and 2304 positions, and for the head-64 presets through a prompt run as one
+    replayed step per row (prompt order, HG_PREFILL=rows) followed by decode steps."""
+    path = gs.synth_path(preset, 5, norm_jitter=0.1)
+    gm, om = hg.Model(path), orc.Model(path)
+    c = gm.cfg
+    assert c.head_dim == 64
+    valid = min(c.vocab_size, 50257)
+    rng = np.random.default_rng(start + 1)
+    kvd = c.n_kv_heads * c.head_dim
+    k = v = None
+    if start:
+        k = rng.standard_normal((c.n_layers, start, kvd), dtype=np.float32)
+        v = rng.standard_normal((c.n_layers, start, kvd), dtype=np.float32)
+    prompt = gs.prompt_ids(start + 2, 0 if start else 11, valid)
+    toks = gs.prompt_ids(start + 3, 16, valid)
+    if rows:
+        monkeypatch.setenv("HG_PREFILL", "rows")
+
+    def run(env, dev):
+        if env is None:
+            monkeypatch.delenv("HG_QKV_SCORES", raising=False)
+        else:
+            monkeypatch.setenv("HG_QKV_SCORES", env)
+        m = gm if dev else om
+        kv = m.new_cache()
+        if start:
+            kv.load(k, v)
+        out = []
+        if len(prompt):
+            emb = np.stack([om.token_embedding(int(t)) for t in prompt])
+            r = m.prefill(emb, kv)
+            out.append(r[0] if dev else r)
+        for i, t in enumerate(toks):
+            r = m.forward(int(t), start + len(prompt) + i, kv)
+            out.append(r[0] if dev else r)
+        return out, kv.routing()[0], kv.read(c.n_layers - 1)
+
+    fused, sep, ref = run(None, True), run("0", True), run(None, False)
+    for i, (a, b, o) in enumerate(zip(fused[0], sep[0], ref[0])):
+        assert _bits_equal(a, o), f"logits differ from the oracle at step {i}"
+        assert _bits_equal(a, b), f"fused and separate scores differ at step {i}"
+    nd = c.n_dense
+    assert np.array_equal(fused[1][nd:], ref[1][nd:]) and np.array_equal(sep[1][nd:], ref[1][nd:])
+    for a, b, o in zip(fused[2], sep[2], ref[2]):
+        assert _bits_equal(a, o) and _bits_equal(b, o)
