@@ -36,7 +36,9 @@ CTX_END = 2048          # the timed window ends at position CTX_END - 1
 N_PROMPT = 16
 PEAK_HBM = 8.0e12       # MI355X HBM3E, bytes/s
 METRIC = "500M Q8_0 decode tok/s (bs1, ctx2k) + achieved HBM GB/s vs peak"
-DOM_KERNEL = "k_attn_softmax_pv_res<64, false>"
+DOM_KERNEL = "k_attn_softmax_pv_res<64, false, true>"   # softmax + P.V after the QKV + scores launch
+SCORES_KERNEL = "k_qkv_head<true, 0, false, 8, 64, true>"   # QKV rows + the attention scores
+N_CALIB_STEPS = 2   # --pmc-calib decode steps at context 2049 (24 layers each)
 
 
 def algorithmic_bytes(cfg, ctx, f32=False):
@@ -431,9 +433,9 @@ COPY_BYTES = 256 * 2**20
 
 def pmc_calib():
     """For rocprofv3 --pmc runs: 4 device copies of COPY_BYTES (the calibration of the byte
-    counters); the attention layer of the timed window (16 q / 4 kv heads, context 2049,
-    reference order) 10 times; then prefill + 16 decode steps of the bench model (the other
-    kernels' shapes do not depend on the context)."""
+    counters); N_CALIB_STEPS decode steps of the bench model at context 2049 on the default
+    cache (seeded KV rows; the '@ctx2049' dispatches of the attention kernels); then prefill +
+    16 decode steps on a small cache (the other kernels' shapes do not depend on the context)."""
     import torch
     import hobbylm_amd as hg
     from hobbylm_amd import gguf_synth as gs
@@ -442,8 +444,16 @@ def pmc_calib():
     for _ in range(4):
         b.copy_(a)
     torch.cuda.synchronize()
-    hg.attention_time(16, 4, 64, CTX_END + 1, reps=10)
     m = hg.Model(gs.synth_path("500M", 1))
+    c = m.cfg
+    kv = m.new_cache()
+    rng = np.random.default_rng(CTX_END)
+    rows = rng.standard_normal((c.n_layers, CTX_END, c.n_kv_heads * c.head_dim), dtype=np.float32)
+    kv.load(rows, rows[::-1].copy())
+    del rows
+    for i in range(N_CALIB_STEPS):
+        m.forward(int(gs.prompt_ids(2, 1, 50257)[0]), CTX_END + i, kv)
+    torch.cuda.synchronize()
     kv = m.new_cache(max_ctx=64)
     prompt = gs.prompt_ids(1, N_PROMPT, 50257)
     emb = np.stack([m.token_embedding(int(t)) for t in prompt])
@@ -482,11 +492,12 @@ def pmc_stats(fetch_dir, write_dir):
             if k.startswith("void hg::") or k.startswith("hg::"):
                 name = k.split("(")[0].replace("void ", "").replace("hg::", "")
                 agg.setdefault(name, []).append(v * 1024 * f)
-        # the first 13 attention dispatches are the context-2049 layer of --pmc-calib
-        for name in ("k_attn_scores<64>", DOM_KERNEL):
+        # the first N_CALIB_STEPS x n_layers dispatches of the attention kernels are --pmc-calib's
+        # steps at context 2049
+        for name in (SCORES_KERNEL, DOM_KERNEL):
             if name in agg:
-                agg[name + " @ctx2049"] = agg[name][:13]
-                agg[name] = agg[name][13:]
+                agg[name + " @ctx2049"] = agg[name][:N_CALIB_STEPS * 24]
+                agg[name] = agg[name][N_CALIB_STEPS * 24:]
         for name, vals in agg.items():
             if vals:
                 res.setdefault(name, {})[counter.lower() + "_bytes"] = float(np.mean(vals))
