@@ -509,9 +509,20 @@ __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const floa
         const float v = rd.finish(sq, sd);
         if (j == 0) hv[(tid - CW) >> 3] = v;
     }
-    __syncthreads();
     const bool scw = SC && kind == 0;   // (uniform) a score workgroup: every thread stays
+    if (scw) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's K pieces are in LDS
+    __syncthreads();
     if (!scw && tid >= 64) return;
+    // (SC) each row thread takes its K row into registers while wave 0 forms the q head
+    float kt[SC ? HD : 1];
+    if constexpr (SC) {
+        const uint32_t i = (uint32_t)(tid - CW);
+        if (rowt && i < div_up(win, S2)) {
+#pragma unroll
+            for (uint32_t m = 0; m < HD / 4; ++m)
+                *reinterpret_cast<v4f *>(kt + 4 * m) = *reinterpret_cast<const v4f *>(kbuf + 4 * (16 * i + ((m + i) & 15)));
+        }
+    }
     if (tid < 64) {
         float *dst = out + (size_t)hh * HD;   // q | k | v regions are contiguous in head order
         if (kind == 2) {
@@ -538,16 +549,11 @@ __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const floa
     }
     if constexpr (SC) {
         if (!scw) return;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's K pieces are in LDS
-        __syncthreads();   // q_h (ho) and every K piece in LDS
+        __syncthreads();   // q_h (ho)
         const uint32_t c = div_up(win, S2), t0 = spl * c, t1 = min(win, t0 + c);
-        const uint32_t i = (uint32_t)(tid - CW), t = t0 + i;
+        const uint32_t t = t0 + (uint32_t)(tid - CW);
         float mx = -__builtin_huge_valf();
         if (rowt && t < t1 && t < pos) {   // (position pos: the softmax + P.V kernel)
-            float kt[HD];
-#pragma unroll
-            for (uint32_t m = 0; m < HD / 4; ++m)
-                *reinterpret_cast<v4f *>(kt + 4 * m) = *reinterpret_cast<const v4f *>(kbuf + 4 * (16 * i + ((m + i) & 15)));
             const float v = dot_wide_serial(ho, kt, HD) * (1.0f / sqrtf((float)HD));
             scores[(size_t)hh * cap + t] = v;
             mx = v;
@@ -2391,8 +2397,10 @@ static size_t qkv_scores_lds(uint32_t d, uint32_t win, uint32_t n_heads, uint32_
     return nc * CHUNK_BYTES + nc * 4 * sizeof(float) + (size_t)d * sizeof(float) + div_up(c, 4) * 4 * 64 * sizeof(float);
 }
 bool qkv_scores_ok(bool exact, uint32_t hd, uint32_t win, uint32_t n_heads, uint32_t n_kv, uint32_t d) {
+    // (the split maxima fit the attention partials buffer, attn_splits(cap) (hd + 2) floats a head)
     return exact && hd == 64 && n_kv && n_heads % n_kv == 0 && pv_res_fits(win) && d % 32 == 0 &&
-           qkv_scores_lds(d, win, n_heads, n_kv) <= PV_LDS_BUDGET;
+           qkv_scores_lds(d, win, n_heads, n_kv) <= PV_LDS_BUDGET &&
+           qkv_score_splits(win, n_heads, n_kv) <= attn_splits(win) * (hd + 2);
 }
 
 bool launch_qkv_scores(hipStream_t st, int order, const Q8Mat &W, const float *x, const float *w, float eps,
