@@ -604,7 +604,7 @@ __global__ __launch_bounds__(NT) void k_b_softmax(float *scores, uint32_t sc_str
 // reports *err.  Workgroups are dealt longest sequence first; the slices of one (sequence,
 // kv head) get ids equal mod 8.  Positions past the context contribute +0, which leaves the
 // chain unchanged: it never holds -0 (it starts at +0, and x + (-x) rounds to +0).
-constexpr uint32_t PV2_G = 4, PV2_NS = 4, PV2_R = 32;   // pages per slot, ring slots, producer V ring (pages)
+constexpr uint32_t PV2_G = 4, PV2_NS = 4, PV2_R = 24;   // pages per slot, ring slots, producer V ring (pages)
 constexpr uint32_t PV2_NP = 3;                          // producer waves
 constexpr size_t PV2_LDS_MAX = 96 * 1024;
 constexpr uint32_t PV_SPIN_CAP = 1u << 22;
@@ -700,7 +700,7 @@ __global__ __launch_bounds__(64 * (PV2_NP + 1)) void k_b_pv2(const float *__rest
         uint32_t ids_nx = id_of(R + lane);
         stage_probs(pn[0], 0);
         load_probs(pn[0], 2);
-        v4f pc[4], pn4[4];
+        v4f pc[4], pn4[4], pr[G][4];   // (pr: the current group's products)
         read_probs(pc, 0);
         // local pages in blocks of R (the ring's loads run past the producer's last group; those
         // pages are not written)
@@ -719,31 +719,38 @@ __global__ __launch_bounds__(64 * (PV2_NP + 1)) void k_b_pv2(const float *__rest
                 }
                 read_probs(pn4, k + 1);
                 if (gi < ngr) {   // (uniform; pages of groups past the last one are only loaded)
-                    if (u % G == 0 && gi >= NS && dc < gi - NS + 1) {   // the slot's previous group consumed
-                        uint32_t it = 0;   // (dc: the last count read; read again only when it is too low)
-                        while ((dc = __hip_atomic_load(&done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < gi - NS + 1) {
-                            if (++it > PV_SPIN_CAP) {
-                                if (lane == 0) atomicOr(err, 1u);
-                                break;
-                            }
-                            __builtin_amdgcn_s_sleep(1);
-                        }
-                        PV2_COMPILER_FENCE();
-                    }
-                    v4f *dst = ring + (size_t)(sl * G + u % G) * 256 + q * 64 + e;
+                    // the page's 16 products into registers; the group's G pages go to its ring
+                    // slot together once the slot is free, so the wait for the chain overlaps
+                    // the group's V waits and multiplies
                     const v4f vv = vr[u];
                     if (16 * kg + 16 <= n) {   // (uniform) a full page
 #pragma unroll
                         for (uint32_t h = 0; h < 4; ++h)
-                            dst[h * 16] = v4f{pc[h].x * vv.x, pc[h].y * vv.y, pc[h].z * vv.z, pc[h].w * vv.w};
+                            pr[u % G][h] = v4f{pc[h].x * vv.x, pc[h].y * vv.y, pc[h].z * vv.z, pc[h].w * vv.w};
                     } else {   // positions t = 16 k + 4 q + c < n only
                         const uint32_t t = 16 * kg + 4 * q;
 #pragma unroll
                         for (uint32_t h = 0; h < 4; ++h)
-                            dst[h * 16] = v4f{t < n ? pc[h].x * vv.x : 0.0f, t + 1 < n ? pc[h].y * vv.y : 0.0f,
-                                              t + 2 < n ? pc[h].z * vv.z : 0.0f, t + 3 < n ? pc[h].w * vv.w : 0.0f};
+                            pr[u % G][h] = v4f{t < n ? pc[h].x * vv.x : 0.0f, t + 1 < n ? pc[h].y * vv.y : 0.0f,
+                                               t + 2 < n ? pc[h].z * vv.z : 0.0f, t + 3 < n ? pc[h].w * vv.w : 0.0f};
                     }
                     if (u % G == G - 1) {
+                        if (gi >= NS && dc < gi - NS + 1) {   // the slot's previous group consumed
+                            uint32_t it = 0;   // (dc: the last count read; read again only when it is too low)
+                            while ((dc = __hip_atomic_load(&done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < gi - NS + 1) {
+                                if (++it > PV_SPIN_CAP) {
+                                    if (lane == 0) atomicOr(err, 1u);
+                                    break;
+                                }
+                                __builtin_amdgcn_s_sleep(1);
+                            }
+                            PV2_COMPILER_FENCE();
+                        }
+                        v4f *dst = ring + (size_t)sl * G * 256 + q * 64 + e;
+#pragma unroll
+                        for (uint32_t pg = 0; pg < G; ++pg)
+#pragma unroll
+                            for (uint32_t h = 0; h < 4; ++h) dst[pg * 256 + h * 16] = pr[pg][h];
                         PV2_COMPILER_FENCE();   // (the slot's data written before its flag)
                         if (lane == 0)
                             __hip_atomic_store(&ready[sl], gi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
