@@ -398,7 +398,7 @@ __global__ __launch_bounds__(QkvCfg<HD>::NT) void k_qkv_head(Q8Mat W, const floa
         const uint32_t nsc = n_heads * S2, rep = n_heads / n_kv, L = blockIdx.x;
         if (L < nsc) {
             uint32_t key, r;
-            const uint32_t xq = n_kv <= 8 && 8 % n_kv == 0 ? 8 / n_kv : 0;   // XCDs per kv group
+            const uint32_t xq = n_kv && n_kv <= 8 && 8 % n_kv == 0 ? 8 / n_kv : 0;   // XCDs per kv group
             if (xq && S2 % xq == 0) {
                 // XCD x serves kv group x / xq, splits x % xq, + xq, ...: each q head's weights
                 // reach xq L2s, each split's K rows one
